@@ -1,0 +1,665 @@
+// C ABI of libferrum_kv.so (declared in include/ferrum_kv.h).
+//
+// Host-side state (block allocator, sequence bookkeeping of the compat pool,
+// validation, error strings) is C++ here; all K/V bytes live in device memory
+// and are touched only by the HIP kernels in fkv_kernels.hip.
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/ferrum_kv.h"
+#include "fkv_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+// FerrumError Display forms (crates/core-types/src/error.rs:21-46).
+int32_t fail(int32_t code, const std::string& msg) {
+  switch (code) {
+    case FKV_ERR_CACHE: g_last_error = "cache: " + msg; break;
+    case FKV_ERR_KERNEL: g_last_error = "kernel: " + msg; break;
+    default: g_last_error = msg; break;
+  }
+  return code;
+}
+
+int32_t ok() {
+  g_last_error.clear();
+  return FKV_OK;
+}
+
+int32_t hip_fail(hipError_t e, const char* what) {
+  return fail(FKV_ERR_INTERNAL, std::string("hip: ") + what + ": " + hipGetErrorString(e));
+}
+
+#define FKV_HIP(call, what)                       \
+  do {                                            \
+    hipError_t e_ = (call);                       \
+    if (e_ != hipSuccess) return hip_fail(e_, what); \
+  } while (0)
+
+// Makes `device` current for the lifetime of the guard.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = false;
+  explicit DeviceGuard(int device) {
+    if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+    ok = hipSetDevice(device) == hipSuccess;
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+bool mul_ovf(uint64_t a, uint64_t b, uint64_t* r) { return __builtin_mul_overflow(a, b, r); }
+
+}  // namespace
+
+struct fkv_pool {
+  fkv_paged_config cfg{};
+  fkv::Geom geom{};
+  uint8_t* dev = nullptr;
+  uint8_t* host = nullptr;
+  uint32_t* fault = nullptr;
+  std::vector<int32_t> free_list;  // stack; LIFO reuse, as a fragmented pool would see
+  std::vector<uint32_t> refcount;
+};
+
+struct fkv_kvpool {
+  fkv_kvpool_config cfg{};
+  fkv_pool* paged = nullptr;  // block_size = max_seq_len, one block per slot
+  std::vector<uint8_t> free_;
+  std::vector<uint64_t> seq_len;
+  std::vector<uint64_t> layers_appended;
+  float* stage = nullptr;     // device: k row, v row
+  int64_t* slot_dev = nullptr;
+  hipStream_t stream = nullptr;
+};
+
+extern "C" {
+
+int32_t fkv_abi_version(void) { return FKV_ABI_VERSION; }
+
+const char* fkv_last_error(void) { return g_last_error.c_str(); }
+
+int32_t fkv_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+// ---------------------------------------------------------------------------
+// Paged pool
+// ---------------------------------------------------------------------------
+
+int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
+  if (!config || !out) return fail(FKV_ERR_INVALID, "null argument");
+  *out = nullptr;
+  const fkv_paged_config& c = *config;
+  if (!c.n_layers || !c.n_kv_heads || !c.head_dim || !c.block_size || !c.num_blocks)
+    return fail(FKV_ERR_CACHE, "kv pool dimension is zero");
+  if (c.kv_dtype != FKV_DTYPE_F32 && c.kv_dtype != FKV_DTYPE_F16 && c.kv_dtype != FKV_DTYPE_Q8_0)
+    return fail(FKV_ERR_KERNEL, "unsupported dtype");
+  if (c.kv_dtype == FKV_DTYPE_Q8_0 && c.head_dim % 32 != 0)
+    return fail(FKV_ERR_KERNEL, "q8_0 k is not a multiple of 32");
+  if (c.f16_rounding != FKV_ROUND_NEAREST_EVEN && c.f16_rounding != FKV_ROUND_HALF_AWAY)
+    return fail(FKV_ERR_INVALID, "unknown f16 rounding mode");
+  if (c.num_blocks > 0x7fffffffull) return fail(FKV_ERR_CACHE, "kv pool size overflow");
+  const uint64_t tile = fkv::tile_bytes_for(c.kv_dtype, c.block_size, c.head_dim);
+  uint64_t block = 0, total = 0, host_total = 0;
+  if (mul_ovf((uint64_t)c.n_layers * 2u, (uint64_t)c.n_kv_heads, &block) ||
+      mul_ovf(block, tile, &block) || mul_ovf(block, c.num_blocks, &total) ||
+      mul_ovf(block, c.num_host_blocks, &host_total))
+    return fail(FKV_ERR_CACHE, "kv pool size overflow");
+  if ((uint64_t)c.num_blocks * c.block_size > 0x7fffffffffffffffull)
+    return fail(FKV_ERR_CACHE, "kv pool size overflow");
+
+  DeviceGuard dg(c.device);
+  if (!dg.ok) return fail(FKV_ERR_INTERNAL, "hip: cannot select device");
+  auto* p = new fkv_pool();
+  p->cfg = c;
+  hipError_t e = hipMalloc((void**)&p->dev, total);
+  if (e != hipSuccess) {
+    delete p;
+    return fail(FKV_ERR_UNAVAILABLE, "no device memory for kv pool");
+  }
+  e = hipMalloc((void**)&p->fault, sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemset(p->fault, 0, sizeof(uint32_t));
+  if (e == hipSuccess && host_total) e = hipHostMalloc((void**)&p->host, host_total, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    (void)hipFree(p->dev);
+    if (p->fault) (void)hipFree(p->fault);
+    delete p;
+    return hip_fail(e, "pool allocation");
+  }
+  p->geom.base = p->dev;
+  p->geom.tile_bytes = tile;
+  p->geom.block_bytes = block;
+  p->geom.num_blocks = c.num_blocks;
+  p->geom.n_layers = c.n_layers;
+  p->geom.n_kv_heads = c.n_kv_heads;
+  p->geom.head_dim = c.head_dim;
+  p->geom.block_size = c.block_size;
+  p->geom.dtype = c.kv_dtype;
+  p->geom.rounding = c.f16_rounding;
+  p->geom.fault = p->fault;
+  p->free_list.resize(c.num_blocks);
+  for (uint64_t i = 0; i < c.num_blocks; i++)
+    p->free_list[i] = (int32_t)(c.num_blocks - 1 - i);  // pop order 0, 1, 2, ...
+  p->refcount.assign(c.num_blocks, 0);
+  *out = p;
+  return ok();
+}
+
+int32_t fkv_paged_destroy(fkv_pool* pool) {
+  if (!pool) return ok();
+  DeviceGuard dg(pool->cfg.device);
+  (void)hipDeviceSynchronize();
+  if (pool->dev) (void)hipFree(pool->dev);
+  if (pool->fault) (void)hipFree(pool->fault);
+  if (pool->host) (void)hipHostFree(pool->host);
+  delete pool;
+  return ok();
+}
+
+int32_t fkv_paged_get_info(const fkv_pool* pool, fkv_paged_info* out) {
+  if (!pool || !out) return fail(FKV_ERR_INVALID, "null argument");
+  out->tile_bytes = pool->geom.tile_bytes;
+  out->block_bytes = pool->geom.block_bytes;
+  out->pool_bytes = pool->geom.block_bytes * pool->geom.num_blocks;
+  out->free_blocks = pool->free_list.size();
+  out->device_base = pool->dev;
+  out->host_base = pool->host;
+  return ok();
+}
+
+int32_t fkv_paged_take_fault_flags(fkv_pool* pool, uint32_t* flags_out) {
+  if (!pool || !flags_out) return fail(FKV_ERR_INVALID, "null argument");
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(hipDeviceSynchronize(), "synchronize");
+  uint32_t f = 0;
+  FKV_HIP(hipMemcpy(&f, pool->fault, sizeof f, hipMemcpyDeviceToHost), "read fault flags");
+  FKV_HIP(hipMemset(pool->fault, 0, sizeof f), "clear fault flags");
+  *flags_out = f;
+  return ok();
+}
+
+int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(fkv::launch_fill(pool->dev, byte, pool->geom.block_bytes * pool->geom.num_blocks,
+                           (hipStream_t)stream),
+          "fill");
+  return ok();
+}
+
+static int32_t check_range(const fkv_pool* pool, uint64_t offset, uint64_t bytes) {
+  const uint64_t total = pool->geom.block_bytes * pool->geom.num_blocks;
+  if (offset > total || bytes > total - offset) return fail(FKV_ERR_INVALID, "range outside the pool");
+  return FKV_OK;
+}
+
+int32_t fkv_paged_read(fkv_pool* pool, uint64_t offset, uint64_t bytes, void* host_dst) {
+  if (!pool || (bytes && !host_dst)) return fail(FKV_ERR_INVALID, "null argument");
+  if (check_range(pool, offset, bytes)) return FKV_ERR_INVALID;
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(hipDeviceSynchronize(), "synchronize");
+  FKV_HIP(hipMemcpy(host_dst, pool->dev + offset, bytes, hipMemcpyDeviceToHost), "pool read");
+  return ok();
+}
+
+int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const void* host_src) {
+  if (!pool || (bytes && !host_src)) return fail(FKV_ERR_INVALID, "null argument");
+  if (check_range(pool, offset, bytes)) return FKV_ERR_INVALID;
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(hipDeviceSynchronize(), "synchronize");
+  FKV_HIP(hipMemcpy(pool->dev + offset, host_src, bytes, hipMemcpyHostToDevice), "pool write");
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Block allocator
+// ---------------------------------------------------------------------------
+
+int32_t fkv_block_alloc(fkv_pool* pool, uint32_t n, int32_t* ids_out) {
+  if (!pool || (n && !ids_out)) return fail(FKV_ERR_INVALID, "null argument");
+  if (pool->free_list.size() < n) return fail(FKV_ERR_UNAVAILABLE, "no free kv blocks");
+  for (uint32_t i = 0; i < n; i++) {
+    int32_t id = pool->free_list.back();
+    pool->free_list.pop_back();
+    pool->refcount[(size_t)id] = 1;
+    ids_out[i] = id;
+  }
+  return ok();
+}
+
+int32_t fkv_block_free(fkv_pool* pool, uint32_t n, const int32_t* ids) {
+  if (!pool || (n && !ids)) return fail(FKV_ERR_INVALID, "null argument");
+  // Validate first (ids repeated in one call count once per occurrence) so a bad
+  // id leaves the allocator unchanged.
+  std::vector<int32_t> sorted(ids, ids + n);
+  std::sort(sorted.begin(), sorted.end());
+  for (size_t i = 0; i < sorted.size();) {
+    size_t j = i;
+    while (j < sorted.size() && sorted[j] == sorted[i]) j++;
+    int32_t id = sorted[i];
+    if (id < 0 || (uint64_t)id >= pool->cfg.num_blocks || pool->refcount[(size_t)id] < j - i)
+      return fail(FKV_ERR_CACHE, "free of unallocated block");
+    i = j;
+  }
+  for (uint32_t i = 0; i < n; i++) {
+    uint32_t& rc = pool->refcount[(size_t)ids[i]];
+    if (--rc == 0) pool->free_list.push_back(ids[i]);
+  }
+  return ok();
+}
+
+int32_t fkv_block_ref(fkv_pool* pool, uint32_t n, const int32_t* ids) {
+  if (!pool || (n && !ids)) return fail(FKV_ERR_INVALID, "null argument");
+  for (uint32_t i = 0; i < n; i++) {
+    int32_t id = ids[i];
+    if (id < 0 || (uint64_t)id >= pool->cfg.num_blocks || pool->refcount[(size_t)id] == 0)
+      return fail(FKV_ERR_CACHE, "reference to unallocated block");
+  }
+  for (uint32_t i = 0; i < n; i++) pool->refcount[(size_t)ids[i]]++;
+  return ok();
+}
+
+int32_t fkv_block_refcount(const fkv_pool* pool, int32_t id, uint32_t* out) {
+  if (!pool || !out) return fail(FKV_ERR_INVALID, "null argument");
+  if (id < 0 || (uint64_t)id >= pool->cfg.num_blocks) return fail(FKV_ERR_CACHE, "unknown block");
+  *out = pool->refcount[(size_t)id];
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Device operations
+// ---------------------------------------------------------------------------
+
+int32_t fkv_append(fkv_pool* pool, uint32_t layer, const float* k, const float* v,
+                   const int64_t* slot_mapping, uint32_t n_tokens, void* stream) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
+  if (n_tokens == 0) return ok();
+  if (!k || !v || !slot_mapping) return fail(FKV_ERR_INVALID, "null argument");
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(fkv::launch_append(pool->geom, layer, k, v, slot_mapping, n_tokens, (hipStream_t)stream),
+          "append");
+  return ok();
+}
+
+static int32_t check_format(int32_t format) {
+  if (format != FKV_GATHER_F32 && format != FKV_GATHER_RAW)
+    return fail(FKV_ERR_INVALID, "unknown gather format");
+  return FKV_OK;
+}
+
+int32_t fkv_gather_slots(fkv_pool* pool, uint32_t layer, const int64_t* slot_mapping,
+                         uint32_t n_tokens, int32_t format, void* out_k, void* out_v,
+                         void* stream) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
+  if (check_format(format)) return FKV_ERR_INVALID;
+  if (n_tokens == 0) return ok();
+  if (!slot_mapping || !out_k || !out_v) return fail(FKV_ERR_INVALID, "null argument");
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(fkv::launch_gather_slots(pool->geom, layer, slot_mapping, n_tokens, format, out_k, out_v,
+                                   (hipStream_t)stream),
+          "gather");
+  return ok();
+}
+
+int32_t fkv_gather_tables(fkv_pool* pool, uint32_t layer, const int32_t* block_tables,
+                          uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                          const int64_t* out_offsets, uint32_t n_seqs, uint32_t max_ctx_len,
+                          int32_t format, void* out_k, void* out_v, void* stream) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
+  if (check_format(format)) return FKV_ERR_INVALID;
+  if (n_seqs == 0) return ok();
+  if (n_seqs > 65535) return fail(FKV_ERR_INVALID, "too many sequences in one gather");
+  if (!block_tables || !ctx_lens || !out_offsets || !out_k || !out_v)
+    return fail(FKV_ERR_INVALID, "null argument");
+  if ((uint64_t)max_ctx_len > (uint64_t)max_blocks_per_seq * pool->cfg.block_size)
+    return fail(FKV_ERR_INVALID, "max_ctx_len exceeds the block table");
+  if (pool->cfg.kv_dtype != FKV_DTYPE_Q8_0 && pool->cfg.head_dim % 8 != 0)
+    return fail(FKV_ERR_KERNEL, "gather_tables needs head_dim % 8 == 0");
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(fkv::launch_gather_tables(pool->geom, layer, block_tables, max_blocks_per_seq, ctx_lens,
+                                    out_offsets, n_seqs, max_ctx_len, format, out_k, out_v,
+                                    (hipStream_t)stream),
+          "gather_tables");
+  return ok();
+}
+
+int32_t fkv_copy_blocks(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void* stream) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (n_pairs == 0) return ok();
+  if (!pairs) return fail(FKV_ERR_INVALID, "null argument");
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(fkv::launch_copy_blocks(pool->geom, pairs, n_pairs, (hipStream_t)stream), "copy_blocks");
+  return ok();
+}
+
+static int32_t swap(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void* stream,
+                    bool out) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (n_pairs == 0) return ok();
+  if (!pairs) return fail(FKV_ERR_INVALID, "null argument");
+  if (!pool->host) return fail(FKV_ERR_CACHE, "pool has no host swap space");
+  const uint64_t nb = pool->cfg.num_blocks, nh = pool->cfg.num_host_blocks;
+  for (uint32_t i = 0; i < n_pairs; i++) {
+    int64_t a = pairs[2 * i], b = pairs[2 * i + 1];
+    int64_t dev = out ? a : b, host = out ? b : a;
+    if (dev < 0 || (uint64_t)dev >= nb) return fail(FKV_ERR_CACHE, "unknown block");
+    if (host < 0 || (uint64_t)host >= nh) return fail(FKV_ERR_CACHE, "unknown host block");
+  }
+  DeviceGuard dg(pool->cfg.device);
+  const uint64_t bb = pool->geom.block_bytes;
+  // Merge runs that are consecutive on both sides into one copy each.
+  uint32_t i = 0;
+  while (i < n_pairs) {
+    uint32_t j = i + 1;
+    while (j < n_pairs && pairs[2 * j] == pairs[2 * (j - 1)] + 1 &&
+           pairs[2 * j + 1] == pairs[2 * (j - 1) + 1] + 1)
+      j++;
+    const uint64_t bytes = (uint64_t)(j - i) * bb;
+    if (out) {
+      FKV_HIP(hipMemcpyAsync(pool->host + (uint64_t)pairs[2 * i + 1] * bb,
+                             pool->dev + (uint64_t)pairs[2 * i] * bb, bytes,
+                             hipMemcpyDeviceToHost, (hipStream_t)stream),
+              "swap_out");
+    } else {
+      FKV_HIP(hipMemcpyAsync(pool->dev + (uint64_t)pairs[2 * i + 1] * bb,
+                             pool->host + (uint64_t)pairs[2 * i] * bb, bytes,
+                             hipMemcpyHostToDevice, (hipStream_t)stream),
+              "swap_in");
+    }
+    i = j;
+  }
+  return ok();
+}
+
+int32_t fkv_swap_out(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void* stream) {
+  return swap(pool, pairs, n_pairs, stream, true);
+}
+
+int32_t fkv_swap_in(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void* stream) {
+  return swap(pool, pairs, n_pairs, stream, false);
+}
+
+static int32_t check_attention(const fkv_pool* pool, uint32_t n_heads, uint32_t max_ctx_len) {
+  const fkv_paged_config& c = pool->cfg;
+  if (n_heads == 0 || n_heads % c.n_kv_heads != 0) return fail(FKV_ERR_KERNEL, "length mismatch");
+  if (c.block_size != (uint32_t)fkv::kAttnBlock ||
+      !fkv::attention_supported(c.kv_dtype, c.head_dim, n_heads / c.n_kv_heads))
+    return fail(FKV_ERR_KERNEL, "unsupported attention shape");
+  uint64_t parts = ((uint64_t)max_ctx_len + fkv::kAttnPartTokens - 1) / fkv::kAttnPartTokens;
+  if (parts > 65535) return fail(FKV_ERR_KERNEL, "context too long");
+  return FKV_OK;
+}
+
+int32_t fkv_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                            uint32_t n_seqs, uint32_t max_ctx_len,
+                                            uint64_t* bytes_out) {
+  if (!pool || !bytes_out) return fail(FKV_ERR_INVALID, "null argument");
+  int32_t st = check_attention(pool, n_heads, max_ctx_len);
+  if (st) return st;
+  *bytes_out = fkv::attention_workspace_bytes(n_heads, pool->cfg.head_dim, n_seqs, max_ctx_len);
+  return ok();
+}
+
+int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,
+                             float* out, const int32_t* block_tables,
+                             uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                             uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                             void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
+  int32_t st = check_attention(pool, n_heads, max_ctx_len);
+  if (st) return st;
+  if (n_seqs == 0) return ok();
+  if (!q || !out || !block_tables || !ctx_lens) return fail(FKV_ERR_INVALID, "null argument");
+  if ((uintptr_t)q % 16 != 0) return fail(FKV_ERR_INVALID, "q must be 16-byte aligned");
+  if ((uint64_t)n_seqs * pool->cfg.n_kv_heads > 0x7fffffffull)
+    return fail(FKV_ERR_INVALID, "too many sequences");
+  if ((uint64_t)max_ctx_len > (uint64_t)max_blocks_per_seq * pool->cfg.block_size)
+    return fail(FKV_ERR_INVALID, "max_ctx_len exceeds the block table");
+  const uint64_t need =
+      fkv::attention_workspace_bytes(n_heads, pool->cfg.head_dim, n_seqs, max_ctx_len);
+  if (workspace_bytes < need || (need && !workspace))
+    return fail(FKV_ERR_INVALID, "attention workspace too small");
+  DeviceGuard dg(pool->cfg.device);
+  FKV_HIP(fkv::launch_decode_attention(pool->geom, layer, n_heads, q, out, block_tables,
+                                       max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale,
+                                       workspace, (hipStream_t)stream),
+          "decode_attention");
+  return ok();
+}
+
+int32_t fkv_device_copy(void* dst, const void* src, uint64_t bytes, void* stream) {
+  if (bytes && (!dst || !src)) return fail(FKV_ERR_INVALID, "null argument");
+  if (((uintptr_t)dst | (uintptr_t)src) % 16 != 0)
+    return fail(FKV_ERR_INVALID, "device_copy needs 16-byte aligned pointers");
+  FKV_HIP(fkv::launch_device_copy(dst, src, bytes, (hipStream_t)stream), "device_copy");
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Revision-1 compat pool (crates/kvcache/src/pool.rs), device storage
+// ---------------------------------------------------------------------------
+
+int32_t fkv_kvpool_new(const fkv_kvpool_config* config, int32_t device, fkv_kvpool** out) {
+  if (!config || !out) return fail(FKV_ERR_INVALID, "null argument");
+  *out = nullptr;
+  const fkv_kvpool_config& c = *config;
+  // pool.rs:22-29
+  if (!c.n_layers || !c.n_kv_heads || !c.head_dim || !c.max_seq_len || !c.max_slots)
+    return fail(FKV_ERR_CACHE, "kv pool dimension is zero");
+  // pool.rs:30-38 (plus the 32-bit fields of the paged geometry)
+  uint64_t block = 0, per_slot = 0, total = 0;
+  if (mul_ovf(c.n_kv_heads, c.head_dim, &block) || mul_ovf(block, 2, &block) ||
+      mul_ovf(c.n_layers, c.max_seq_len, &per_slot) || mul_ovf(per_slot, block, &per_slot) ||
+      mul_ovf(per_slot, c.max_slots, &total) || mul_ovf(total, 4, &total) ||
+      c.n_layers > 0xffffffffull || c.n_kv_heads > 0xffffffffull ||
+      c.head_dim > 0xffffffffull || c.max_seq_len > 0xffffffffull)
+    return fail(FKV_ERR_CACHE, "kv pool size overflow");
+  fkv_paged_config pc{};
+  pc.n_layers = (uint32_t)c.n_layers;
+  pc.n_kv_heads = (uint32_t)c.n_kv_heads;
+  pc.head_dim = (uint32_t)c.head_dim;
+  pc.block_size = (uint32_t)c.max_seq_len;
+  pc.num_blocks = c.max_slots;
+  pc.kv_dtype = FKV_DTYPE_F32;
+  pc.f16_rounding = FKV_ROUND_NEAREST_EVEN;
+  pc.device = device;
+  fkv_pool* paged = nullptr;
+  int32_t st = fkv_paged_create(&pc, &paged);
+  if (st) return st;
+  auto* p = new fkv_kvpool();
+  p->cfg = c;
+  p->paged = paged;
+  p->free_.assign(c.max_slots, 1);
+  p->seq_len.assign(c.max_slots, 0);
+  p->layers_appended.assign(c.max_slots, 0);
+  DeviceGuard dg(device);
+  const uint64_t row = c.n_kv_heads * c.head_dim;
+  hipError_t e = hipMalloc((void**)&p->stage, row * 2 * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc((void**)&p->slot_dev, sizeof(int64_t));
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    fkv_kvpool_destroy(p);
+    return hip_fail(e, "kv pool allocation");
+  }
+  *out = p;
+  return ok();
+}
+
+int32_t fkv_kvpool_destroy(fkv_kvpool* pool) {
+  if (!pool) return ok();
+  {
+    DeviceGuard dg(pool->paged ? pool->paged->cfg.device : 0);
+    if (pool->stream) (void)hipStreamSynchronize(pool->stream);
+    if (pool->stage) (void)hipFree(pool->stage);
+    if (pool->slot_dev) (void)hipFree(pool->slot_dev);
+    if (pool->stream) (void)hipStreamDestroy(pool->stream);
+  }
+  fkv_paged_destroy(pool->paged);
+  delete pool;
+  return ok();
+}
+
+int32_t fkv_kvpool_get_config(const fkv_kvpool* pool, fkv_kvpool_config* out) {
+  if (!pool || !out) return fail(FKV_ERR_INVALID, "null argument");
+  *out = pool->cfg;
+  return ok();
+}
+
+int32_t fkv_kvpool_storage_len(const fkv_kvpool* pool, uint64_t* out) {
+  if (!pool || !out) return fail(FKV_ERR_INVALID, "null argument");
+  *out = pool->paged->geom.block_bytes * pool->paged->geom.num_blocks / sizeof(float);
+  return ok();
+}
+
+// alloc, pool.rs:83-101: first free slot; the whole slot is zero-filled.
+int32_t fkv_kvpool_alloc(fkv_kvpool* pool, uint32_t* slot_out) {
+  if (!pool || !slot_out) return fail(FKV_ERR_INVALID, "null argument");
+  for (uint64_t i = 0; i < pool->cfg.max_slots; i++) {
+    if (!pool->free_[i]) continue;
+    DeviceGuard dg(pool->paged->cfg.device);
+    const uint64_t bb = pool->paged->geom.block_bytes;
+    FKV_HIP(fkv::launch_fill(pool->paged->dev + i * bb, 0, bb, pool->stream), "alloc zero-fill");
+    FKV_HIP(hipStreamSynchronize(pool->stream), "alloc zero-fill");
+    pool->free_[i] = 0;
+    pool->seq_len[i] = 0;
+    pool->layers_appended[i] = 0;
+    *slot_out = (uint32_t)i;
+    return ok();
+  }
+  return fail(FKV_ERR_UNAVAILABLE, "no free kv slots");
+}
+
+// free, pool.rs:103-112.
+int32_t fkv_kvpool_free(fkv_kvpool* pool, uint32_t slot) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (slot >= pool->cfg.max_slots || pool->free_[slot])
+    return fail(FKV_ERR_CACHE, "free of unallocated slot");
+  pool->free_[slot] = 1;
+  pool->seq_len[slot] = 0;
+  pool->layers_appended[slot] = 0;
+  return ok();
+}
+
+// seq_len, pool.rs:114-120.
+int32_t fkv_kvpool_seq_len(const fkv_kvpool* pool, uint32_t slot, uint64_t* out) {
+  if (!pool || !out) return fail(FKV_ERR_INVALID, "null argument");
+  if (slot >= pool->cfg.max_slots) return fail(FKV_ERR_CACHE, "unknown slot");
+  *out = pool->seq_len[slot];
+  return ok();
+}
+
+// append_layer, pool.rs:122-153: same checks, same order. An out-of-range slot
+// (a panic in the reference, which indexes `free[index]` unchecked) is
+// "unknown slot" here.
+int32_t fkv_kvpool_append_layer(fkv_kvpool* pool, uint32_t slot, uint64_t layer, const float* k,
+                                uint64_t k_len, const float* v, uint64_t v_len) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  const fkv_kvpool_config& c = pool->cfg;
+  if (slot >= c.max_slots) return fail(FKV_ERR_CACHE, "unknown slot");
+  if (pool->free_[slot]) return fail(FKV_ERR_CACHE, "append on free slot");
+  if (layer >= c.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
+  const uint64_t expected = c.n_kv_heads * c.head_dim;
+  if (k_len != expected || v_len != expected) return fail(FKV_ERR_CACHE, "kv vector length mismatch");
+  const uint64_t pos = pool->seq_len[slot];
+  if (pos >= c.max_seq_len) return fail(FKV_ERR_CACHE, "sequence length exceeds max");
+  if (pool->layers_appended[slot] != layer) return fail(FKV_ERR_CACHE, "layers must append in order");
+  if (!k || !v) return fail(FKV_ERR_INVALID, "null argument");
+  DeviceGuard dg(pool->paged->cfg.device);
+  const int64_t s = (int64_t)((uint64_t)slot * c.max_seq_len + pos);
+  FKV_HIP(hipMemcpyAsync(pool->stage, k, expected * 4, hipMemcpyHostToDevice, pool->stream), "append");
+  FKV_HIP(hipMemcpyAsync(pool->stage + expected, v, expected * 4, hipMemcpyHostToDevice, pool->stream),
+          "append");
+  FKV_HIP(hipMemcpyAsync(pool->slot_dev, &s, sizeof s, hipMemcpyHostToDevice, pool->stream), "append");
+  FKV_HIP(fkv::launch_append(pool->paged->geom, (uint32_t)layer, pool->stage, pool->stage + expected,
+                             pool->slot_dev, 1, pool->stream),
+          "append");
+  FKV_HIP(hipStreamSynchronize(pool->stream), "append");
+  pool->layers_appended[slot] += 1;
+  return ok();
+}
+
+// commit_token, pool.rs:155-172.
+int32_t fkv_kvpool_commit_token(fkv_kvpool* pool, uint32_t slot) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (slot >= pool->cfg.max_slots) return fail(FKV_ERR_CACHE, "unknown slot");
+  if (pool->free_[slot]) return fail(FKV_ERR_CACHE, "commit on free slot");
+  if (pool->layers_appended[slot] != pool->cfg.n_layers)
+    return fail(FKV_ERR_CACHE, "not every layer appended");
+  const uint64_t next = pool->seq_len[slot] + 1;
+  if (next > pool->cfg.max_seq_len) return fail(FKV_ERR_CACHE, "sequence length exceeds max");
+  pool->seq_len[slot] = next;
+  pool->layers_appended[slot] = 0;
+  return ok();
+}
+
+// k / v, pool.rs:174-204.
+static int32_t kvpool_read(const fkv_kvpool* pool, uint32_t slot, uint64_t layer, uint64_t pos,
+                           float* out, uint64_t out_len, bool want_v) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  const fkv_kvpool_config& c = pool->cfg;
+  if (slot >= c.max_slots) return fail(FKV_ERR_CACHE, "unknown slot");
+  if (pool->free_[slot]) return fail(FKV_ERR_CACHE, "read on free slot");
+  if (pos >= pool->seq_len[slot]) return fail(FKV_ERR_CACHE, "position not yet committed");
+  if (layer >= c.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
+  const uint64_t n = c.n_kv_heads * c.head_dim;
+  if (out_len != n) return fail(FKV_ERR_INVALID, "output length mismatch");
+  if (!out) return fail(FKV_ERR_INVALID, "null argument");
+  DeviceGuard dg(pool->paged->cfg.device);
+  const int64_t s = (int64_t)((uint64_t)slot * c.max_seq_len + pos);
+  FKV_HIP(hipMemcpyAsync(pool->slot_dev, &s, sizeof s, hipMemcpyHostToDevice, pool->stream), "read");
+  FKV_HIP(fkv::launch_gather_slots(pool->paged->geom, (uint32_t)layer, pool->slot_dev, 1,
+                                   FKV_GATHER_F32, pool->stage, pool->stage + n, pool->stream),
+          "read");
+  FKV_HIP(hipMemcpyAsync(out, pool->stage + (want_v ? n : 0), n * 4, hipMemcpyDeviceToHost,
+                         pool->stream),
+          "read");
+  FKV_HIP(hipStreamSynchronize(pool->stream), "read");
+  return ok();
+}
+
+int32_t fkv_kvpool_k(const fkv_kvpool* pool, uint32_t slot, uint64_t layer, uint64_t pos,
+                     float* out, uint64_t out_len) {
+  return kvpool_read(pool, slot, layer, pos, out, out_len, false);
+}
+
+int32_t fkv_kvpool_v(const fkv_kvpool* pool, uint32_t slot, uint64_t layer, uint64_t pos,
+                     float* out, uint64_t out_len) {
+  return kvpool_read(pool, slot, layer, pos, out, out_len, true);
+}
+
+// abandon_partial, pool.rs:207-216.
+int32_t fkv_kvpool_abandon_partial(fkv_kvpool* pool, uint32_t slot) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (slot >= pool->cfg.max_slots || pool->free_[slot])
+    return fail(FKV_ERR_CACHE, "abandon on free slot");
+  pool->layers_appended[slot] = 0;
+  return ok();
+}
+
+// uncommit_token, pool.rs:218-231.
+int32_t fkv_kvpool_uncommit_token(fkv_kvpool* pool, uint32_t slot) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  if (slot >= pool->cfg.max_slots || pool->free_[slot])
+    return fail(FKV_ERR_CACHE, "uncommit on free slot");
+  if (pool->seq_len[slot] == 0) return fail(FKV_ERR_CACHE, "nothing to uncommit");
+  pool->seq_len[slot] -= 1;
+  pool->layers_appended[slot] = 0;
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,75 @@
+// Internal interface between the C ABI (fkv_api.cpp) and the HIP kernels
+// (fkv_kernels.hip). Not installed; the public interface is include/ferrum_kv.h.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+#include <stdint.h>
+
+namespace fkv {
+
+// Geometry of one paged pool, passed by value to every kernel.
+// pool[block][layer][kv][head][tile]; tile = [B][D] elements (F32/F16) or
+// [B*D int8][B*D/32 f16 scales] (Q8_0), padded to a multiple of 16 bytes.
+struct Geom {
+  uint8_t* base;
+  uint64_t tile_bytes;
+  uint64_t block_bytes;
+  uint64_t num_blocks;
+  uint32_t n_layers;
+  uint32_t n_kv_heads;
+  uint32_t head_dim;
+  uint32_t block_size;
+  int32_t dtype;     // 0 f32, 1 f16, 8 q8_0
+  int32_t rounding;  // 0 nearest-even, 1 ties away
+  uint32_t* fault;   // device word, FKV_FAULT_* bits
+};
+
+constexpr int kDtypeF32 = 0;
+constexpr int kDtypeF16 = 1;
+constexpr int kDtypeQ8 = 8;
+
+constexpr uint32_t kFaultSlot = 1u;
+constexpr uint32_t kFaultBlock = 2u;
+constexpr uint32_t kFaultCtx = 4u;
+
+// Decode attention partitioning: 4 waves per workgroup, each wave owns 4 blocks
+// of 16 tokens, so one workgroup covers a 256-token partition of one
+// (sequence, kv head).
+constexpr int kAttnBlock = 16;
+constexpr int kAttnWaves = 4;
+constexpr int kAttnBlocksPerWave = 4;
+constexpr int kAttnPartTokens = kAttnBlock * kAttnWaves * kAttnBlocksPerWave;  // 256
+
+inline uint64_t tile_bytes_for(int dtype, uint32_t block_size, uint32_t head_dim) {
+  uint64_t e = (uint64_t)block_size * head_dim;
+  uint64_t raw = dtype == kDtypeF32 ? e * 4 : dtype == kDtypeF16 ? e * 2 : e + (e / 32) * 2;
+  return (raw + 15) / 16 * 16;
+}
+
+// Launchers (return the hipError_t of the launch).
+hipError_t launch_append(const Geom& g, uint32_t layer, const float* k, const float* v,
+                         const int64_t* slots, uint32_t n_tokens, hipStream_t s);
+hipError_t launch_gather_slots(const Geom& g, uint32_t layer, const int64_t* slots,
+                               uint32_t n_tokens, int format, void* out_k, void* out_v,
+                               hipStream_t s);
+hipError_t launch_gather_tables(const Geom& g, uint32_t layer, const int32_t* tables,
+                                uint32_t max_blocks, const int32_t* ctx_lens,
+                                const int64_t* out_offsets, uint32_t n_seqs,
+                                uint32_t max_ctx_len, int format, void* out_k, void* out_v,
+                                hipStream_t s);
+hipError_t launch_copy_blocks(const Geom& g, const int64_t* pairs, uint32_t n_pairs,
+                              hipStream_t s);
+hipError_t launch_fill(void* dst, uint8_t byte, uint64_t bytes, hipStream_t s);
+hipError_t launch_device_copy(void* dst, const void* src, uint64_t bytes, hipStream_t s);
+
+// Returns hipErrorInvalidValue when no kernel is instantiated for the shape.
+bool attention_supported(int dtype, uint32_t head_dim, uint32_t group);
+hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
+                                   const float* q, float* out, const int32_t* tables,
+                                   uint32_t max_blocks, const int32_t* ctx_lens,
+                                   uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                                   void* workspace, hipStream_t s);
+uint64_t attention_workspace_bytes(uint32_t n_heads, uint32_t head_dim, uint32_t n_seqs,
+                                   uint32_t max_ctx_len);
+
+}  // namespace fkv

@@ -1,0 +1,254 @@
+/*
+ * ferrum_kv.h — C ABI of the MI355X (gfx950) paged KV-cache hot path.
+ *
+ * Two surfaces share one library (libferrum_kv.so):
+ *
+ *  1. The revision-1 compat surface (fkv_kvpool_*). It mirrors Ferrum's
+ *     `trait KvPool` (/root/reference/crates/core-types/src/kv.rs:21-46) and the
+ *     inherent methods of `PreallocatedKvPool`
+ *     (/root/reference/crates/kvcache/src/pool.rs:20-231) one entry point per
+ *     method, with the same checks in the same order and the same message
+ *     strings. Storage is device memory; K/V cross the boundary as host f32
+ *     arrays and reads copy out instead of borrowing.
+ *
+ *  2. The paged surface (fkv_paged_*, fkv_block_*, fkv_append, fkv_gather_*,
+ *     fkv_copy_blocks, fkv_swap_*, fkv_decode_attention*). Ferrum revision 1
+ *     has no paged pool (its pool is one dense slot per sequence, pool.rs:1-18),
+ *     so this is a new interface placed beside the frozen one, not new methods
+ *     on it (core-types/src/lib.rs:3-6, :44-45). Every device operation is
+ *     asynchronous on the stream it is given and takes device pointers.
+ *
+ * Errors: every entry point returns an fkv_status. A non-zero status leaves a
+ * thread-local message readable with fkv_last_error(), formatted exactly as
+ * Ferrum's `FerrumError` Display (core-types/src/error.rs:21-46):
+ *   FKV_ERR_CACHE       -> "cache: <msg>"      (FerrumError::Cache)
+ *   FKV_ERR_UNAVAILABLE -> "<msg>"             (FerrumError::Unavailable, HTTP 503)
+ *   FKV_ERR_KERNEL      -> "kernel: <msg>"     (FerrumError::Kernel)
+ *   FKV_ERR_INVALID     -> "<msg>"             (FerrumError::InvalidRequest)
+ *   FKV_ERR_INTERNAL    -> "<msg>"             (FerrumError::Internal; HIP failures)
+ *
+ * Threading: a pool handle is single-writer, like `&mut self` in Ferrum.
+ * Concurrent calls on one handle must be serialised by the caller.
+ *
+ * HBM layout of a paged pool (one device allocation):
+ *   pool[block][layer][kv (0=K,1=V)][kv_head][tile]
+ *   tile (F32/F16): [block_size tokens][head_dim] elements
+ *   tile (Q8_0)   : [block_size*head_dim int8 quants][block_size*head_dim/32 f16 scales]
+ * A block therefore holds every layer of block_size consecutive tokens, and the
+ * (block, layer, kv, head) tile is contiguous (4 KiB for f16, D=128, B=16).
+ * Slot = block * block_size + offset_in_block (the vLLM slot-mapping convention).
+ */
+#ifndef FERRUM_KV_H
+#define FERRUM_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FKV_ABI_VERSION 1
+
+/* Status codes; one per FerrumError variant the path can return. */
+#define FKV_OK 0
+#define FKV_ERR_CACHE 1
+#define FKV_ERR_UNAVAILABLE 2
+#define FKV_ERR_KERNEL 3
+#define FKV_ERR_INVALID 4
+#define FKV_ERR_INTERNAL 5
+
+/* KV storage dtypes. Values are the ggml type ids of core-types/src/dtype.rs:27-33. */
+#define FKV_DTYPE_F32 0
+#define FKV_DTYPE_F16 1
+#define FKV_DTYPE_Q8_0 8
+
+/* f32 -> binary16 rounding used for F16 storage and for Q8_0 block scales.
+ * NEAREST_EVEN is IEEE 754 roundTiesToEven (the default).
+ * HALF_AWAY reproduces Ferrum's only encoder, `f32_to_f16_bits`
+ * (crates/kernels/src/q8_dot.rs:111-139), which rounds ties away from zero. */
+#define FKV_ROUND_NEAREST_EVEN 0
+#define FKV_ROUND_HALF_AWAY 1
+
+/* Output formats of the gather entry points. */
+#define FKV_GATHER_F32 0 /* decoded to f32, like KvPool::k/v (kv.rs:43-45) */
+#define FKV_GATHER_RAW 1 /* storage bytes; Q8_0 as Ferrum's 34-byte blocks (dtype.rs:19-21) */
+
+/* Bits reported by fkv_paged_take_fault_flags(): device-side input faults that
+ * the kernels skipped instead of touching memory out of bounds. */
+#define FKV_FAULT_SLOT_RANGE 1u   /* append/gather slot >= num_blocks*block_size */
+#define FKV_FAULT_BLOCK_RANGE 2u  /* block table / copy pair id outside [0, num_blocks) */
+#define FKV_FAULT_CTX_RANGE 4u    /* ctx_len > max_blocks_per_seq * block_size or < 0 */
+
+/* Version of this ABI; equals FKV_ABI_VERSION of the header the library was built with. */
+int32_t fkv_abi_version(void);
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* fkv_last_error(void);
+
+/* Number of visible HIP devices (0 when no GPU); never fails. */
+int32_t fkv_device_count(void);
+
+/* ------------------------------------------------------------------------- */
+/* Revision-1 compat surface: Ferrum's KvPool over device storage.            */
+/* ------------------------------------------------------------------------- */
+
+/* Mirrors `KvPoolConfig` (core-types/src/kv.rs:12-19). */
+typedef struct fkv_kvpool_config {
+  uint64_t n_layers;
+  uint64_t n_kv_heads;
+  uint64_t head_dim;
+  uint64_t max_seq_len;
+  uint64_t max_slots;
+} fkv_kvpool_config;
+
+typedef struct fkv_kvpool fkv_kvpool;
+
+/* PreallocatedKvPool::new (pool.rs:21-46): "kv pool dimension is zero",
+ * "kv pool size overflow". Storage is max_slots*n_layers*max_seq_len*n_kv_heads*
+ * head_dim*2 f32 on `device`, allocated once. */
+int32_t fkv_kvpool_new(const fkv_kvpool_config* config, int32_t device, fkv_kvpool** out);
+int32_t fkv_kvpool_destroy(fkv_kvpool* pool);
+/* KvPool::config (kv.rs:22). */
+int32_t fkv_kvpool_get_config(const fkv_kvpool* pool, fkv_kvpool_config* out);
+/* f32 elements of device storage (pool.rs:293-307 checks this never grows). */
+int32_t fkv_kvpool_storage_len(const fkv_kvpool* pool, uint64_t* out);
+/* KvPool::alloc (pool.rs:83-101): first free slot, zero-filled; full pool is
+ * FKV_ERR_UNAVAILABLE "no free kv slots". */
+int32_t fkv_kvpool_alloc(fkv_kvpool* pool, uint32_t* slot_out);
+/* KvPool::free (pool.rs:103-112): "free of unallocated slot". */
+int32_t fkv_kvpool_free(fkv_kvpool* pool, uint32_t slot);
+/* KvPool::seq_len (pool.rs:114-120): "unknown slot". */
+int32_t fkv_kvpool_seq_len(const fkv_kvpool* pool, uint32_t slot, uint64_t* out);
+/* KvPool::append_layer (pool.rs:122-153). k, v: host f32 [n_kv_heads*head_dim]. */
+int32_t fkv_kvpool_append_layer(fkv_kvpool* pool, uint32_t slot, uint64_t layer,
+                                const float* k, uint64_t k_len, const float* v,
+                                uint64_t v_len);
+/* KvPool::commit_token (pool.rs:155-172). */
+int32_t fkv_kvpool_commit_token(fkv_kvpool* pool, uint32_t slot);
+/* KvPool::k / KvPool::v (pool.rs:174-204); copies n_kv_heads*head_dim f32 to host out. */
+int32_t fkv_kvpool_k(const fkv_kvpool* pool, uint32_t slot, uint64_t layer, uint64_t pos,
+                     float* out, uint64_t out_len);
+int32_t fkv_kvpool_v(const fkv_kvpool* pool, uint32_t slot, uint64_t layer, uint64_t pos,
+                     float* out, uint64_t out_len);
+/* PreallocatedKvPool::abandon_partial / uncommit_token (pool.rs:207-231). */
+int32_t fkv_kvpool_abandon_partial(fkv_kvpool* pool, uint32_t slot);
+int32_t fkv_kvpool_uncommit_token(fkv_kvpool* pool, uint32_t slot);
+
+/* ------------------------------------------------------------------------- */
+/* Paged surface.                                                              */
+/* ------------------------------------------------------------------------- */
+
+typedef struct fkv_paged_config {
+  uint32_t n_layers;
+  uint32_t n_kv_heads;
+  uint32_t head_dim;        /* Q8_0 needs a multiple of 32 */
+  uint32_t block_size;      /* tokens per block; decode attention needs 16 */
+  uint64_t num_blocks;      /* device blocks */
+  uint64_t num_host_blocks; /* pinned host blocks for swap (0 = none) */
+  int32_t kv_dtype;         /* FKV_DTYPE_* */
+  int32_t f16_rounding;     /* FKV_ROUND_* */
+  int32_t device;           /* HIP device ordinal */
+  int32_t reserved;
+} fkv_paged_config;
+
+typedef struct fkv_paged_info {
+  uint64_t tile_bytes;   /* one (block, layer, kv, head) tile */
+  uint64_t block_bytes;  /* one block: n_layers*2*n_kv_heads*tile_bytes */
+  uint64_t pool_bytes;   /* num_blocks*block_bytes */
+  uint64_t free_blocks;  /* blocks with refcount 0 */
+  void* device_base;     /* start of device storage */
+  void* host_base;       /* start of pinned host swap storage, or NULL */
+} fkv_paged_info;
+
+typedef struct fkv_pool fkv_pool;
+
+/* Create a pool: one hipMalloc of num_blocks*block_bytes (plus hipHostMalloc for
+ * swap). Zero dims: FKV_ERR_CACHE "kv pool dimension is zero" (pool.rs:28). */
+int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out);
+int32_t fkv_paged_destroy(fkv_pool* pool);
+int32_t fkv_paged_get_info(const fkv_pool* pool, fkv_paged_info* out);
+/* Reads and clears the FKV_FAULT_* bits the kernels raised (synchronises the device). */
+int32_t fkv_paged_take_fault_flags(fkv_pool* pool, uint32_t* flags_out);
+/* Fill every byte of device storage with `byte` (async on stream). */
+int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream);
+/* Synchronous raw copies between device storage and host memory (byte offsets
+ * into the pool). Used to persist or inspect the pool image. */
+int32_t fkv_paged_read(fkv_pool* pool, uint64_t offset, uint64_t bytes, void* host_dst);
+int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const void* host_src);
+
+/* Host-side block allocator (free list with refcounts). Replaces the slot scan
+ * of pool.rs:83-101; exhaustion is FKV_ERR_UNAVAILABLE "no free kv blocks", the
+ * analogue of "no free kv slots" that the scheduler stops admission on
+ * (scheduler/src/batcher.rs:110-113). All-or-nothing. */
+int32_t fkv_block_alloc(fkv_pool* pool, uint32_t n, int32_t* ids_out);
+/* Drop one reference per id; a block returns to the free list at refcount 0.
+ * Unallocated id: FKV_ERR_CACHE "free of unallocated block". */
+int32_t fkv_block_free(fkv_pool* pool, uint32_t n, const int32_t* ids);
+/* Add one reference per id (copy-on-write sharing after a fork). */
+int32_t fkv_block_ref(fkv_pool* pool, uint32_t n, const int32_t* ids);
+int32_t fkv_block_refcount(const fkv_pool* pool, int32_t id, uint32_t* out);
+
+/* Append: the paged form of KvPool::append_layer (pool.rs:122-153).
+ * k, v: device f32 [n_tokens][n_kv_heads][head_dim] (post-RoPE K, kv.rs:30-31).
+ * slot_mapping: device int64 [n_tokens]; slot < 0 skips the token (padding).
+ * F16 storage rounds with the pool's f16_rounding; Q8_0 quantises each 32-value
+ * run like Q8Activation::quantize_into (q8_dot.rs:35-61). */
+int32_t fkv_append(fkv_pool* pool, uint32_t layer, const float* k, const float* v,
+                   const int64_t* slot_mapping, uint32_t n_tokens, void* stream);
+
+/* Gather by slot: the inverse of fkv_append, the paged form of KvPool::k/v
+ * (pool.rs:174-204). out_k/out_v: device [n_tokens][n_kv_heads][head_dim] in
+ * `format`; a slot < 0 leaves its output row untouched. */
+int32_t fkv_gather_slots(fkv_pool* pool, uint32_t layer, const int64_t* slot_mapping,
+                         uint32_t n_tokens, int32_t format, void* out_k, void* out_v,
+                         void* stream);
+
+/* Gather by block table: sequence s's positions 0..ctx_lens[s]-1 go to rows
+ * out_offsets[s] .. out_offsets[s]+ctx_lens[s]-1 of out_k/out_v (device).
+ * block_tables: device int32 [n_seqs][max_blocks_per_seq]. */
+int32_t fkv_gather_tables(fkv_pool* pool, uint32_t layer, const int32_t* block_tables,
+                          uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                          const int64_t* out_offsets, uint32_t n_seqs, uint32_t max_ctx_len,
+                          int32_t format, void* out_k, void* out_v, void* stream);
+
+/* Copy whole blocks (every layer, K and V): pairs is device int64 [n_pairs][2] of
+ * (src, dst). Used for copy-on-write after a fork and for compaction. dst blocks
+ * must be distinct and must not be sources in the same call. */
+int32_t fkv_copy_blocks(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void* stream);
+
+/* Swap whole blocks between HBM and the pool's pinned host storage.
+ * pairs is HOST int64 [n_pairs][2]: swap_out (device_block, host_block),
+ * swap_in (host_block, device_block). Asynchronous on stream. */
+int32_t fkv_swap_out(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void* stream);
+int32_t fkv_swap_in(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void* stream);
+
+/* Paged decode attention: the attention loop of Llama::forward_one_token
+ * (crates/model/src/llama.rs:220-247) over KV read through block tables.
+ * For query head h of sequence s, with g = n_heads / n_kv_heads:
+ *   score[p] = dot(q[s][h], K[p][h / g]) * scale, p < ctx_lens[s]
+ *   out[s][h] = softmax(score) . V[.][h / g]
+ * A non-finite maximum score gives zeros (kernels/src/scalar.rs:125-130).
+ * q, out: device f32 [n_seqs][n_heads][head_dim]. block_tables: device int32
+ * [n_seqs][max_blocks_per_seq]; ctx_lens: device int32 [n_seqs], each
+ * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, g in {1,2,4,8,16}.
+ * workspace: device scratch of fkv_decode_attention_workspace_size() bytes
+ * (split-context partials); it may be NULL when that size is 0. */
+int32_t fkv_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                            uint32_t n_seqs, uint32_t max_ctx_len,
+                                            uint64_t* bytes_out);
+int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                             const float* q, float* out, const int32_t* block_tables,
+                             uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                             uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                             void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* Device-to-device byte copy with the same 16-byte vector kernel style as the
+ * pool kernels; used to calibrate HBM counters and to measure copy bandwidth. */
+int32_t fkv_device_copy(void* dst, const void* src, uint64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FERRUM_KV_H */

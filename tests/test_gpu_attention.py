@@ -1,0 +1,148 @@
+"""GPU parity: paged decode attention against the CPU oracle (llama.rs:220-247).
+
+Bar: |got - want| <= 2e-3 + 1e-2 * |want| elementwise,
+against the oracle's restatement of the reference loop and against an f64 brute
+force; bit-identical outputs when only the physical block placement changes;
+the non-finite-max rule of scalar.rs:125-130.
+"""
+import numpy as np
+import pytest
+
+from tests.helpers import assert_close, attention_f64, make_pools, slots_for, to_dev
+
+pytestmark = pytest.mark.gpu
+
+CTXS = [1, 15, 16, 17, 255, 256, 257, 700, 1500]
+
+
+def _build(dtype, d, hkv, ctxs, seed=0, perm_seed=None, layers=2, extra_blocks=8):
+    """Pool with every sequence's K/V appended through a scattered block table."""
+    rng = np.random.default_rng(seed)
+    nb = [(c + 15) // 16 for c in ctxs]
+    nblk = sum(nb) + extra_blocks
+    pool, layout = make_pools(layers, hkv, d, nblk, dtype=dtype)
+    pool.fill(0)
+    prng = np.random.default_rng(seed if perm_seed is None else perm_seed)
+    perm = prng.permutation(nblk).astype(np.int32)
+    max_blocks = max(1, max(nb))
+    tab = np.zeros((len(ctxs), max_blocks), np.int32)
+    off = 0
+    for i, n in enumerate(nb):
+        tab[i, :n] = perm[off: off + n]
+        off += n
+    total = sum(ctxs)
+    for layer in range(layers):
+        k = rng.standard_normal((total, hkv, d), dtype=np.float32)
+        v = rng.standard_normal((total, hkv, d), dtype=np.float32)
+        slots = np.concatenate([slots_for(tab[i], c) for i, c in enumerate(ctxs)])
+        pool.append(layer, to_dev(k), to_dev(v), to_dev(slots))
+    return pool, layout, tab
+
+
+def _run(pool, layer, q, tab, ctxs):
+    import torch
+    out = torch.full(q.shape, 123.0, dtype=torch.float32, device="cuda")
+    ctx = np.array(ctxs, np.int32)
+    pool.decode_attention(layer, to_dev(q), out, to_dev(tab), to_dev(ctx), int(ctx.max()))
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+SHAPES = [(1, 128, 4), (1, 128, 8), (1, 64, 8), (1, 128, 1), (1, 64, 2), (1, 128, 16),
+          (0, 128, 4), (0, 64, 8), (8, 128, 4), (8, 128, 8), (8, 64, 1)]
+
+
+@pytest.mark.parametrize("dtype,d,g", SHAPES)
+def test_attention_matches_oracle(dtype, d, g):
+    import ferrum_amd as fa
+    from oracle import ref
+    hkv = 2
+    pool, layout, tab = _build(dtype, d, hkv, CTXS, seed=d + g)
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((len(CTXS), hkv * g, d), dtype=np.float32)
+    got = _run(pool, 1, q, tab, CTXS)
+    assert pool.take_fault_flags() == 0
+    image = pool.read()
+    scale = fa.default_scale(d)
+    want = ref.attention(layout, image, 1, q, tab, np.array(CTXS), scale)
+    err = assert_close(got, want)
+    # independent f64 brute force on decoded rows for a few (seq, head)
+    for s in (0, 4, len(CTXS) - 1):
+        c = CTXS[s]
+        slots = slots_for(tab[s], c)
+        kr, vr = ref.gather_slots(layout, image, 1, slots, 0)
+        for h in (0, hkv * g - 1):
+            exp = attention_f64(q[s, h], kr[:, h // g], vr[:, h // g], scale)
+            assert_close(got[s, h], exp, what="f64 brute force")
+    print(f"max abs err vs oracle {err:.2e}")
+
+
+def test_attention_long_context_uses_combine():
+    import ferrum_amd as fa
+    from oracle import ref
+    ctxs = [20000, 3, 4097]
+    pool, layout, tab = _build(1, 128, 8, ctxs, seed=11, layers=1)
+    q = np.random.default_rng(5).standard_normal((3, 32, 128), dtype=np.float32)
+    got = _run(pool, 0, q, tab, ctxs)
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array(ctxs), fa.default_scale(128))
+    assert_close(got, want)
+
+
+def test_attention_is_invariant_to_block_placement():
+    q = np.random.default_rng(9).standard_normal((len(CTXS), 8, 128), dtype=np.float32)
+    outs = []
+    for perm_seed in (1, 2):
+        pool, _, tab = _build(1, 128, 2, CTXS, seed=3, perm_seed=perm_seed)
+        outs.append(_run(pool, 1, q, tab, CTXS))
+        pool.close()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+def test_attention_zero_context_gives_zeros():
+    pool, _, tab = _build(1, 64, 2, [5, 16], seed=4)
+    q = np.ones((2, 4, 64), np.float32)
+    import torch
+    out = torch.full(q.shape, 9.0, dtype=torch.float32, device="cuda")
+    ctx = np.array([0, 16], np.int32)
+    pool.decode_attention(0, to_dev(q), out, to_dev(tab), to_dev(ctx), 16)
+    o = out.cpu().numpy()
+    assert np.all(o[0] == 0.0)
+    assert np.all(np.isfinite(o[1])) and np.any(o[1] != 0.0)
+
+
+@pytest.mark.parametrize("ctx", [40, 600])
+def test_attention_non_finite_scores(ctx):
+    """One K row is (+inf, 0, ..., 0). Head 0 (q0 > 0) scores it +inf: a non-finite
+    max gives zeros (scalar.rs:127-130). Head 1 (q0 < 0) scores it -inf: the token
+    only drops out. Head 2 (q0 == 0) scores it 0*inf = NaN with a finite max: the
+    output is NaN. A second pool where every score of a head is -inf gives zeros."""
+    import ferrum_amd as fa
+    from oracle import ref
+    d, hkv, g = 64, 1, 4
+    nb = (ctx + 15) // 16
+    pool, layout = make_pools(1, hkv, d, nb + 2, dtype=0)
+    pool.fill(0)
+    rng = np.random.default_rng(0)
+    k = rng.standard_normal((ctx, hkv, d), dtype=np.float32)
+    v = rng.standard_normal((ctx, hkv, d), dtype=np.float32)
+    k[ctx // 3, 0, :] = 0.0
+    k[ctx // 3, 0, 0] = np.inf
+    tab = np.arange(nb, dtype=np.int32)[None, :]
+    slots = slots_for(tab[0], ctx)
+    pool.append(0, to_dev(k), to_dev(v), to_dev(slots))
+    q = rng.standard_normal((1, g, d), dtype=np.float32)
+    q[0, 0, 0], q[0, 1, 0], q[0, 2, 0], q[0, 3, 0] = 1.0, -1.0, 0.0, 2.0
+    got = _run(pool, 0, q, tab, [ctx])
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array([ctx]), fa.default_scale(d))
+    assert np.all(want[0, 0] == 0) and np.all(want[0, 3] == 0)
+    assert np.all(np.isfinite(want[0, 1])) and np.all(np.isnan(want[0, 2]))
+    assert_close(got, want)
+
+    # every score -inf
+    k2 = np.zeros((ctx, hkv, d), np.float32)
+    k2[:, 0, 0] = np.inf
+    pool.append(0, to_dev(k2), to_dev(v), to_dev(slots))
+    q2 = rng.standard_normal((1, g, d), dtype=np.float32)
+    q2[0, :, 0] = -1.0
+    got2 = _run(pool, 0, q2, tab, [ctx])
+    assert np.all(got2 == 0.0)
