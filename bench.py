@@ -134,7 +134,7 @@ def main():
     ctx_step_d = torch.from_numpy(ctx_step).to(dev)
     max_ctx = int(ctx_step.max())
     ws_bytes = pool.attention_workspace_bytes(hq, n_seqs, max_ctx)
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    ws = torch.zeros(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
     scale = fa.default_scale(d)
 
     h = ctypes.c_void_p(pool.handle)

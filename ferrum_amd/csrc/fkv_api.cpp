@@ -400,7 +400,7 @@ static int32_t check_attention(const fkv_pool* pool, uint32_t n_heads, uint32_t 
       !fkv::attention_supported(c.kv_dtype, c.head_dim, n_heads / c.n_kv_heads))
     return fail(FKV_ERR_KERNEL, "unsupported attention shape");
   uint64_t parts = ((uint64_t)max_ctx_len + fkv::kAttnPartTokens - 1) / fkv::kAttnPartTokens;
-  if (parts > 65535) return fail(FKV_ERR_KERNEL, "context too long");
+  if (parts > 65535 || max_ctx_len > (1u << 30)) return fail(FKV_ERR_KERNEL, "context too long");
   return FKV_OK;
 }
 
@@ -410,7 +410,7 @@ int32_t fkv_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_hea
   if (!pool || !bytes_out) return fail(FKV_ERR_INVALID, "null argument");
   int32_t st = check_attention(pool, n_heads, max_ctx_len);
   if (st) return st;
-  *bytes_out = fkv::attention_workspace_bytes(n_heads, pool->cfg.head_dim, n_seqs, max_ctx_len);
+  *bytes_out = fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
   return ok();
 }
 
@@ -431,7 +431,7 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, c
   if ((uint64_t)max_ctx_len > (uint64_t)max_blocks_per_seq * pool->cfg.block_size)
     return fail(FKV_ERR_INVALID, "max_ctx_len exceeds the block table");
   const uint64_t need =
-      fkv::attention_workspace_bytes(n_heads, pool->cfg.head_dim, n_seqs, max_ctx_len);
+      fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
   if (workspace_bytes < need || (need && !workspace))
     return fail(FKV_ERR_INVALID, "attention workspace too small");
   DeviceGuard dg(pool->cfg.device);

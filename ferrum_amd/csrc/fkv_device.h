@@ -1,0 +1,103 @@
+// Device-side helpers shared by the HIP kernels of libferrum_kv.so (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fkv_internal.h"
+
+namespace fkv {
+namespace dev {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ uint8_t* tile_ptr(const Geom& g, uint64_t block, uint32_t layer,
+                                             uint32_t kv, uint32_t head) {
+  return g.base + block * g.block_bytes +
+         ((uint64_t)(layer * 2u + kv) * g.n_kv_heads + head) * g.tile_bytes;
+}
+
+__device__ __forceinline__ void raise_fault(uint32_t* f, uint32_t bit) {
+  atomicOr(f, bit);
+}
+
+// ---------------------------------------------------------------------------
+// binary16 <-> binary32
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// f32 -> binary16 bits. rounding 0: v_cvt_f16_f32 (IEEE roundTiesToEven).
+// rounding 1: ties away from zero, as Ferrum's f32_to_f16_bits
+// (crates/kernels/src/q8_dot.rs:111-139): the round-toward-zero neighbour from
+// v_cvt_pkrtz_f16_f32 and the next binary16 up are compared by distance; both
+// differences are exact near a tie (Sterbenz), which is where the choice matters.
+// NaN keeps its top 10 payload bits and stays a NaN (q8_dot.rs:118-121).
+__device__ __forceinline__ uint32_t encode_f16(float x, int rounding) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 16) & 0x8000u;
+  uint32_t ax = u & 0x7fffffffu;
+  if (ax > 0x7f800000u) {
+    uint32_t hf = (ax & 0x7fffffu) >> 13;
+    return sign | 0x7c00u | hf | (hf == 0u ? 1u : 0u);
+  }
+  if (rounding == 0) {
+    _Float16 h = (_Float16)x;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
+  }
+  if (ax == 0x7f800000u) return sign | 0x7c00u;
+  float a = __uint_as_float(ax);
+  auto pk = __builtin_amdgcn_cvt_pkrtz(a, 0.0f);
+  uint32_t lo = __builtin_bit_cast(uint32_t, pk) & 0xffffu;
+  float lo_v = f16_bits_to_f32(lo);
+  float hi_v = (lo == 0x7bffu) ? 65536.0f : f16_bits_to_f32(lo + 1u);
+  uint32_t r = (hi_v - a <= a - lo_v) ? lo + 1u : lo;
+  return sign | r;
+}
+
+// ---------------------------------------------------------------------------
+// Wave reductions (DPP inside 16-lane rows, readlane across rows)
+// ---------------------------------------------------------------------------
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xf, 0xf, true));
+}
+
+// Sum over aligned groups of N lanes (N <= 16), result in every lane of the group.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  if constexpr (N >= 2) x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
+  if constexpr (N >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) x += dpp<0x141>(x);  // row_half_mirror
+  if constexpr (N >= 16) x += dpp<0x140>(x); // row_mirror
+  if constexpr (N >= 32) x += __shfl_xor(x, 16);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  x = __builtin_fmaxf(x, dpp<0xB1>(x));
+  x = __builtin_fmaxf(x, dpp<0x4E>(x));
+  x = __builtin_fmaxf(x, dpp<0x141>(x));
+  x = __builtin_fmaxf(x, dpp<0x140>(x));
+  float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return __builtin_fmaxf(__builtin_fmaxf(r0, r1), __builtin_fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+  x = group_sum<16>(x);
+  float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+
+}  // namespace dev
+}  // namespace fkv

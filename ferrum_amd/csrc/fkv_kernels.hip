@@ -12,58 +12,13 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "fkv_device.h"
 #include "fkv_internal.h"
 
 namespace fkv {
 namespace {
 
-constexpr float kLog2e = 1.4426950408889634f;
-
-__device__ __forceinline__ uint8_t* tile_ptr(const Geom& g, uint64_t block, uint32_t layer,
-                                             uint32_t kv, uint32_t head) {
-  return g.base + block * g.block_bytes +
-         ((uint64_t)(layer * 2u + kv) * g.n_kv_heads + head) * g.tile_bytes;
-}
-
-__device__ __forceinline__ void raise_fault(uint32_t* f, uint32_t bit) {
-  atomicOr(f, bit);
-}
-
-// ---------------------------------------------------------------------------
-// binary16 <-> binary32
-// ---------------------------------------------------------------------------
-
-__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
-  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
-}
-
-// f32 -> binary16 bits. rounding 0: v_cvt_f16_f32 (IEEE roundTiesToEven).
-// rounding 1: ties away from zero, as Ferrum's f32_to_f16_bits
-// (crates/kernels/src/q8_dot.rs:111-139): the round-toward-zero neighbour from
-// v_cvt_pkrtz_f16_f32 and the next binary16 up are compared by distance; both
-// differences are exact near a tie (Sterbenz), which is where the choice matters.
-// NaN keeps its top 10 payload bits and stays a NaN (q8_dot.rs:118-121).
-__device__ __forceinline__ uint32_t encode_f16(float x, int rounding) {
-  uint32_t u = __float_as_uint(x);
-  uint32_t sign = (u >> 16) & 0x8000u;
-  uint32_t ax = u & 0x7fffffffu;
-  if (ax > 0x7f800000u) {
-    uint32_t hf = (ax & 0x7fffffu) >> 13;
-    return sign | 0x7c00u | hf | (hf == 0u ? 1u : 0u);
-  }
-  if (rounding == 0) {
-    _Float16 h = (_Float16)x;
-    return (uint32_t)__builtin_bit_cast(uint16_t, h);
-  }
-  if (ax == 0x7f800000u) return sign | 0x7c00u;
-  float a = __uint_as_float(ax);
-  auto pk = __builtin_amdgcn_cvt_pkrtz(a, 0.0f);
-  uint32_t lo = __builtin_bit_cast(uint32_t, pk) & 0xffffu;
-  float lo_v = f16_bits_to_f32(lo);
-  float hi_v = (lo == 0x7bffu) ? 65536.0f : f16_bits_to_f32(lo + 1u);
-  uint32_t r = (hi_v - a <= a - lo_v) ? lo + 1u : lo;
-  return sign | r;
-}
+using namespace dev;
 
 // ---------------------------------------------------------------------------
 // Q8_0 block quantiser (q8_dot.rs:46-59)
@@ -423,462 +378,6 @@ __global__ void copy_tail_kernel(uint8_t* dst, const uint8_t* src, uint64_t from
   if (i < bytes) dst[i] = src[i];
 }
 
-// ---------------------------------------------------------------------------
-// Wave reductions (DPP inside 16-lane rows, readlane across rows)
-// ---------------------------------------------------------------------------
-
-template <int kCtrl>
-__device__ __forceinline__ float dpp(float x) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), kCtrl, 0xf, 0xf, true));
-}
-
-// Sum over aligned groups of N lanes (N <= 16), result in every lane of the group.
-template <int N>
-__device__ __forceinline__ float group_sum(float x) {
-  if constexpr (N >= 2) x += dpp<0xB1>(x);   // quad_perm [1,0,3,2]
-  if constexpr (N >= 4) x += dpp<0x4E>(x);   // quad_perm [2,3,0,1]
-  if constexpr (N >= 8) x += dpp<0x141>(x);  // row_half_mirror
-  if constexpr (N >= 16) x += dpp<0x140>(x); // row_mirror
-  if constexpr (N >= 32) x += __shfl_xor(x, 16);
-  return x;
-}
-
-__device__ __forceinline__ float wave_max(float x) {
-  x = __builtin_fmaxf(x, dpp<0xB1>(x));
-  x = __builtin_fmaxf(x, dpp<0x4E>(x));
-  x = __builtin_fmaxf(x, dpp<0x141>(x));
-  x = __builtin_fmaxf(x, dpp<0x140>(x));
-  float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
-  float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
-  float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
-  float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
-  return __builtin_fmaxf(__builtin_fmaxf(r0, r1), __builtin_fmaxf(r2, r3));
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-  x = group_sum<16>(x);
-  float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
-  float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
-  float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
-  float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
-  return (r0 + r1) + (r2 + r3);
-}
-
-// ---------------------------------------------------------------------------
-// Paged decode attention
-// ---------------------------------------------------------------------------
-//
-// One workgroup (4 waves) = one 256-token partition of one (sequence, kv head);
-// all G = n_heads/n_kv_heads query heads of the group share every K/V tile.
-// Each wave owns 4 consecutive 16-token blocks. A 16-token K or V tile is read
-// as rows: LPR lanes cover one token row with 16-byte loads, RPP rows per load
-// instruction, PASSES instructions per tile, so each load instruction reads
-// 1 KiB of consecutive HBM.
-//   phase 1  scores s[g][t] = (q_g . K_t) * scale  -> LDS
-//   phase 2  per head: max m, e_t = exp(s_t - m), l = sum e_t   (exact per partition)
-//   phase 3  acc[g][d] = sum_t e[g][t] * V_t[d]; rows and waves reduced via LDS
-// With one partition the output is acc / l; otherwise (m, l, acc) go to the
-// workspace and attn_combine_kernel merges partitions (log-sum-exp).
-
-template <int DT>
-struct KvTraits;
-template <>
-struct KvTraits<kDtypeF16> { static constexpr int kBytes = 2; };
-template <>
-struct KvTraits<kDtypeF32> { static constexpr int kBytes = 4; };
-template <>
-struct KvTraits<kDtypeQ8> { static constexpr int kBytes = 1; };
-
-template <int DT, int D>
-struct AttnShape {
-  static constexpr int E = KvTraits<DT>::kBytes;
-  static constexpr int EPL = 16 / E;            // values per lane per 16-byte load
-  static constexpr int LPR = D / EPL;           // lanes per token row
-  static constexpr int RPP = 64 / LPR;          // token rows per load instruction
-  static constexpr int PASSES = kAttnBlock / RPP;
-  static constexpr bool kPrefetchV = PASSES <= 4;
-  static_assert(LPR >= 1 && LPR <= 32 && RPP * LPR == 64 && PASSES * RPP == kAttnBlock, "shape");
-};
-
-// Decode one 16-byte load (EPL values) to f32.
-template <int DT, int EPL>
-__device__ __forceinline__ void decode16(const uint4& w, float (&f)[EPL]) {
-  if constexpr (DT == kDtypeF16) {
-    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      f[2 * i] = f16_bits_to_f32(a[i] & 0xffffu);
-      f[2 * i + 1] = f16_bits_to_f32(a[i] >> 16);
-    }
-  } else if constexpr (DT == kDtypeF32) {
-    f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y);
-    f[2] = __uint_as_float(w.z); f[3] = __uint_as_float(w.w);
-  } else {
-    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-#pragma unroll
-      for (int b = 0; b < 4; b++) f[4 * i + b] = (float)(int8_t)((a[i] >> (8 * b)) & 0xffu);
-    }
-  }
-}
-
-template <int DT, int D, int G>
-__global__ void __launch_bounds__(256) attn_partition_kernel(
-    Geom g, uint32_t layer, uint32_t n_heads, const float* __restrict__ q,
-    float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
-    const int32_t* __restrict__ ctx_lens, uint32_t max_parts, float scale,
-    float* __restrict__ ws_o, float* __restrict__ ws_ml) {
-  using S = AttnShape<DT, D>;
-  constexpr int EPL = S::EPL, LPR = S::LPR, RPP = S::RPP, PASSES = S::PASSES;
-  constexpr int NB = kAttnBlocksPerWave;
-
-  // s_acc (phase 3 output) reuses the bytes of s_score, which is dead after phase 2.
-  constexpr int kScoreFloats = G * kAttnPartTokens;
-  constexpr int kAccFloats = kAttnWaves * G * D;
-  __shared__ float s_union[kScoreFloats > kAccFloats ? kScoreFloats : kAccFloats];
-  __shared__ float s_p[kAttnPartTokens][G];
-  __shared__ float s_m[G];
-  __shared__ float s_l[G];
-  float (*s_score)[kAttnPartTokens] = reinterpret_cast<float (*)[kAttnPartTokens]>(s_union);
-  float (*s_acc)[G][D] = reinterpret_cast<float (*)[G][D]>(s_union);
-
-  const uint32_t sk = blockIdx.x;
-  const uint32_t part = blockIdx.y;
-  const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
-  const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
-  int32_t ctx = ctx_lens[seq];
-  if (ctx < 0 || ctx > cap) {
-    if (part == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
-    ctx = ctx < 0 ? 0 : cap;
-  }
-  const int32_t nparts = ctx > 0 ? (ctx + kAttnPartTokens - 1) / kAttnPartTokens : 1;
-  if ((int32_t)part >= nparts) return;
-
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-  const int r = lane / LPR, c = lane % LPR;
-  const int32_t part_start = (int32_t)part * kAttnPartTokens;
-  const int32_t n_valid = ctx - part_start < kAttnPartTokens ? ctx - part_start : kAttnPartTokens;
-
-  // Query slice of this lane for every head of the group.
-  float qr[G][EPL];
-  {
-    const float* qb = q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G) * D + c * EPL;
-#pragma unroll
-    for (int gg = 0; gg < G; gg++) {
-#pragma unroll
-      for (int i = 0; i < EPL; i += 4) {
-        float4 t = *(const float4*)(qb + (uint64_t)gg * D + i);
-        qr[gg][i] = t.x; qr[gg][i + 1] = t.y; qr[gg][i + 2] = t.z; qr[gg][i + 3] = t.w;
-      }
-    }
-  }
-
-  // Physical blocks of this wave (wave-uniform).
-  const int32_t lblk0 = (int32_t)part * (kAttnWaves * NB) + wave * NB;
-  const int32_t* table = tables + (uint64_t)seq * max_blocks;
-  int32_t phys[NB];
-  bool live[NB], valid_blk[NB];
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    int32_t lb = lblk0 + j;
-    valid_blk[j] = lb * kAttnBlock < ctx;
-    int32_t p = valid_blk[j] ? table[lb] : 0;
-    p = __builtin_amdgcn_readfirstlane(p);
-    bool ok = valid_blk[j] && p >= 0 && (uint64_t)p < g.num_blocks;
-    if (valid_blk[j] && !ok && lane == 0) raise_fault(g.fault, kFaultBlock);
-    live[j] = ok;
-    phys[j] = p;
-  }
-
-  const uint64_t row_bytes = (uint64_t)D * S::E;
-  const uint64_t scale_off = (uint64_t)kAttnBlock * D;  // Q8_0 scales follow the quants
-
-  // Issue K loads for all blocks, then V loads (kept in flight through phase 1-2).
-  uint4 kreg[NB][PASSES];
-  uint32_t ksc[NB][PASSES];
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    if (live[j]) {
-      const uint8_t* kt = tile_ptr(g, (uint64_t)phys[j], layer, 0, kvh);
-#pragma unroll
-      for (int ps = 0; ps < PASSES; ps++) {
-        int row = ps * RPP + r;
-        kreg[j][ps] = *(const uint4*)(kt + row * row_bytes + c * 16);
-        if constexpr (DT == kDtypeQ8)
-          ksc[j][ps] = ((const uint16_t*)(kt + scale_off))[row * (D / 32) + (c * EPL) / 32];
-      }
-    }
-  }
-  uint4 vreg[S::kPrefetchV ? NB : 1][PASSES];
-  uint32_t vsc[S::kPrefetchV ? NB : 1][PASSES];
-  if constexpr (S::kPrefetchV) {
-#pragma unroll
-    for (int j = 0; j < NB; j++) {
-      if (live[j]) {
-        const uint8_t* vt = tile_ptr(g, (uint64_t)phys[j], layer, 1, kvh);
-#pragma unroll
-        for (int ps = 0; ps < PASSES; ps++) {
-          int row = ps * RPP + r;
-          vreg[j][ps] = *(const uint4*)(vt + row * row_bytes + c * 16);
-          if constexpr (DT == kDtypeQ8)
-            vsc[j][ps] = ((const uint16_t*)(vt + scale_off))[row * (D / 32) + (c * EPL) / 32];
-        }
-      }
-    }
-  }
-
-  // Phase 1: scores.
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ps++) {
-      const int32_t tl = (wave * NB + j) * kAttnBlock + ps * RPP + r;  // token within partition
-      float part_dot[G];
-      if (live[j]) {
-        float kf[EPL];
-        decode16<DT, EPL>(kreg[j][ps], kf);
-#pragma unroll
-        for (int gg = 0; gg < G; gg++) {
-          float a = 0.0f;
-#pragma unroll
-          for (int i = 0; i < EPL; i++) a = __builtin_fmaf(qr[gg][i], kf[i], a);
-          if constexpr (DT == kDtypeQ8) a *= f16_bits_to_f32(ksc[j][ps]);
-          part_dot[gg] = group_sum<LPR>(a);
-        }
-      }
-      if (c == 0) {
-#pragma unroll
-        for (int gg = 0; gg < G; gg++)
-          s_score[gg][tl] = (live[j] && tl < n_valid) ? part_dot[gg] * scale : -__builtin_inff();
-      }
-    }
-  }
-  __syncthreads();
-
-  // Phase 2: exact softmax statistics of this partition, one wave per head.
-  for (int gg = wave; gg < G; gg += kAttnWaves) {
-    float m = -__builtin_inff();
-    for (int t = lane; t < kAttnPartTokens; t += 64)
-      if (t < n_valid) m = __builtin_fmaxf(m, s_score[gg][t]);  // NaN is skipped
-    m = wave_max(m);
-    float l = 0.0f;
-    const bool m_neg_inf = (m == -__builtin_inff());
-    for (int t = lane; t < kAttnPartTokens; t += 64) {
-      float e = 0.0f;
-      if (t < n_valid) {
-        float s = s_score[gg][t];
-        // All scores -inf/NaN: weights are 0, but a NaN score must stay NaN.
-        e = m_neg_inf ? (s != s ? s : 0.0f) : __builtin_amdgcn_exp2f((s - m) * kLog2e);
-      }
-      s_p[t][gg] = e;
-      l += e;
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      s_m[gg] = m;
-      s_l[gg] = l;
-    }
-  }
-  __syncthreads();
-
-  // Phase 3: weighted V.
-  float acc[G][EPL];
-#pragma unroll
-  for (int gg = 0; gg < G; gg++)
-#pragma unroll
-    for (int i = 0; i < EPL; i++) acc[gg][i] = 0.0f;
-
-#pragma unroll
-  for (int j = 0; j < NB; j++) {
-    if (!live[j]) continue;
-    uint4 vl[PASSES];
-    uint32_t vs[PASSES];
-    if constexpr (S::kPrefetchV) {
-#pragma unroll
-      for (int ps = 0; ps < PASSES; ps++) {
-        vl[ps] = vreg[j][ps];
-        vs[ps] = vsc[j][ps];
-      }
-    } else {
-      const uint8_t* vt = tile_ptr(g, (uint64_t)phys[j], layer, 1, kvh);
-#pragma unroll
-      for (int ps = 0; ps < PASSES; ps++) {
-        int row = ps * RPP + r;
-        vl[ps] = *(const uint4*)(vt + row * row_bytes + c * 16);
-        if constexpr (DT == kDtypeQ8)
-          vs[ps] = ((const uint16_t*)(vt + scale_off))[row * (D / 32) + (c * EPL) / 32];
-      }
-    }
-#pragma unroll
-    for (int ps = 0; ps < PASSES; ps++) {
-      const int32_t tl = (wave * NB + j) * kAttnBlock + ps * RPP + r;
-      if (tl < n_valid) {
-        float vf[EPL];
-        decode16<DT, EPL>(vl[ps], vf);
-        float pw[G];
-#pragma unroll
-        for (int gg = 0; gg < G; gg++) pw[gg] = s_p[tl][gg];
-        if constexpr (DT == kDtypeQ8) {
-          float sv = f16_bits_to_f32(vs[ps]);
-#pragma unroll
-          for (int gg = 0; gg < G; gg++) pw[gg] *= sv;
-        }
-#pragma unroll
-        for (int gg = 0; gg < G; gg++)
-#pragma unroll
-          for (int i = 0; i < EPL; i++) acc[gg][i] = __builtin_fmaf(pw[gg], vf[i], acc[gg][i]);
-      }
-    }
-  }
-  (void)vsc;
-
-  // Reduce the RPP token rows of the wave (lanes with equal c).
-#pragma unroll
-  for (int gg = 0; gg < G; gg++)
-#pragma unroll
-    for (int i = 0; i < EPL; i++) {
-      float x = acc[gg][i];
-#pragma unroll
-      for (int o = LPR; o < 64; o <<= 1) x += __shfl_xor(x, o);
-      acc[gg][i] = x;
-    }
-  if (r == 0) {
-#pragma unroll
-    for (int gg = 0; gg < G; gg++)
-#pragma unroll
-      for (int i = 0; i < EPL; i++) s_acc[wave][gg][c * EPL + i] = acc[gg][i];
-  }
-  __syncthreads();
-
-  for (int e = threadIdx.x; e < G * D; e += 256) {
-    const int gg = e / D, d = e % D;
-    float o = (s_acc[0][gg][d] + s_acc[1][gg][d]) + (s_acc[2][gg][d] + s_acc[3][gg][d]);
-    const uint64_t head = (uint64_t)seq * n_heads + (uint64_t)kvh * G + gg;
-    if (nparts == 1) {
-      const float m = s_m[gg];
-      out[head * D + d] = __builtin_isfinite(m) ? o * (1.0f / s_l[gg]) : 0.0f;
-    } else {
-      ws_o[(head * max_parts + part) * D + d] = o;
-      if (d == 0) {
-        ws_ml[(head * max_parts + part) * 2] = s_m[gg];
-        ws_ml[(head * max_parts + part) * 2 + 1] = s_l[gg];
-      }
-    }
-  }
-}
-
-// Merge the partitions of one (sequence, query head): M = max_p m_p (NaN
-// skipped); a non-finite M gives zeros (scalar.rs:127-130); otherwise
-// out = sum_p w_p o_p / sum_p w_p l_p with w_p = exp(m_p - M).
-// 256 threads: thread t covers dims 4*(t % (D/4)).. and partitions p = t / (D/4) mod P.
-template <int D>
-__global__ void __launch_bounds__(256) attn_combine_kernel(
-    const int32_t* __restrict__ ctx_lens, uint32_t n_heads, uint32_t max_blocks,
-    uint32_t max_parts, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-    float* __restrict__ out) {
-  constexpr int kLanesPerRow = D / 4;
-  constexpr int kRows = 256 / kLanesPerRow;
-  __shared__ float s_red[kRows][D];
-  __shared__ float s_lred[kRows];
-  __shared__ float s_max[4];
-
-  const uint32_t head = blockIdx.x;  // seq * n_heads + h
-  const uint32_t seq = head / n_heads;
-  const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
-  int32_t ctx = ctx_lens[seq];
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-  const int32_t nparts = ctx > 0 ? (ctx + kAttnPartTokens - 1) / kAttnPartTokens : 1;
-  if (nparts == 1) return;
-
-  const float* ml = ws_ml + (uint64_t)head * max_parts * 2;
-  const float* po = ws_o + (uint64_t)head * max_parts * D;
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-
-  float m = -__builtin_inff();
-  for (int p = threadIdx.x; p < nparts; p += 256) m = __builtin_fmaxf(m, ml[2 * p]);
-  m = wave_max(m);
-  if (lane == 0) s_max[wave] = m;
-  __syncthreads();
-  const float M = __builtin_fmaxf(__builtin_fmaxf(s_max[0], s_max[1]),
-                                  __builtin_fmaxf(s_max[2], s_max[3]));
-  float* o = out + (uint64_t)head * D;
-  if (!__builtin_isfinite(M)) {
-    for (int d = threadIdx.x; d < D; d += 256) o[d] = 0.0f;
-    return;
-  }
-  const int col = threadIdx.x % kLanesPerRow, row = threadIdx.x / kLanesPerRow;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float lsum = 0.0f;
-  for (int p = row; p < nparts; p += kRows) {
-    const float w = __builtin_amdgcn_exp2f((ml[2 * p] - M) * kLog2e);
-    lsum = __builtin_fmaf(w, ml[2 * p + 1], lsum);
-    const float4 v = *(const float4*)(po + (uint64_t)p * D + col * 4);
-    acc.x = __builtin_fmaf(w, v.x, acc.x);
-    acc.y = __builtin_fmaf(w, v.y, acc.y);
-    acc.z = __builtin_fmaf(w, v.z, acc.z);
-    acc.w = __builtin_fmaf(w, v.w, acc.w);
-  }
-  s_red[row][col * 4] = acc.x;
-  s_red[row][col * 4 + 1] = acc.y;
-  s_red[row][col * 4 + 2] = acc.z;
-  s_red[row][col * 4 + 3] = acc.w;
-  if (col == 0) s_lred[row] = lsum;
-  __syncthreads();
-  if (threadIdx.x < D) {
-    float a = 0.0f, l = 0.0f;
-#pragma unroll
-    for (int rr = 0; rr < kRows; rr++) {
-      a += s_red[rr][threadIdx.x];
-      l += s_lred[rr];
-    }
-    o[threadIdx.x] = a * (1.0f / l);
-  }
-}
-
-template <int DT, int D, int G>
-hipError_t launch_attn_t(const Geom& g, uint32_t layer, uint32_t n_heads, const float* q,
-                         float* out, const int32_t* tables, uint32_t max_blocks,
-                         const int32_t* ctx_lens, uint32_t n_seqs, uint32_t max_parts,
-                         float scale, float* ws_o, float* ws_ml, hipStream_t s) {
-  dim3 grid(n_seqs * g.n_kv_heads, max_parts);
-  attn_partition_kernel<DT, D, G><<<grid, 256, 0, s>>>(g, layer, n_heads, q, out, tables,
-                                                       max_blocks, ctx_lens, max_parts, scale,
-                                                       ws_o, ws_ml);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || max_parts <= 1) return e;
-  attn_combine_kernel<D><<<n_seqs * n_heads, 256, 0, s>>>(ctx_lens, n_heads, max_blocks,
-                                                          max_parts, ws_o, ws_ml, out);
-  return hipGetLastError();
-}
-
-template <int DT, int D>
-hipError_t dispatch_group(uint32_t G, const Geom& g, uint32_t layer, uint32_t n_heads,
-                          const float* q, float* out, const int32_t* tables,
-                          uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
-                          uint32_t max_parts, float scale, float* ws_o, float* ws_ml,
-                          hipStream_t s) {
-#define FKV_G(N)                                                                          \
-  case N:                                                                                 \
-    return launch_attn_t<DT, D, N>(g, layer, n_heads, q, out, tables, max_blocks, ctx_lens, \
-                                   n_seqs, max_parts, scale, ws_o, ws_ml, s);
-  switch (G) {
-    FKV_G(1)
-    FKV_G(2)
-    FKV_G(4)
-    FKV_G(8)
-    default:
-      break;
-  }
-  if constexpr (DT != kDtypeQ8) {
-    if (G == 16)
-      return launch_attn_t<DT, D, 16>(g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
-                                      n_seqs, max_parts, scale, ws_o, ws_ml, s);
-  }
-#undef FKV_G
-  return hipErrorInvalidValue;
-}
-
 inline uint32_t grid_for(uint64_t units, uint32_t max_wg = 8192) {
   uint64_t wg = (units + 255) / 256;
   if (wg < 1) wg = 1;
@@ -1010,51 +509,6 @@ hipError_t launch_device_copy(void* dst, const void* src, uint64_t bytes, hipStr
   if (bytes % 16)
     copy_tail_kernel<<<1, 64, 0, s>>>((uint8_t*)dst, (const uint8_t*)src, vecs * 16u, bytes);
   return hipGetLastError();
-}
-
-bool attention_supported(int dtype, uint32_t head_dim, uint32_t group) {
-  if (head_dim != 64 && head_dim != 128) return false;
-  if (dtype != kDtypeF16 && dtype != kDtypeF32 && dtype != kDtypeQ8) return false;
-  if (group == 1 || group == 2 || group == 4 || group == 8) return true;
-  return group == 16 && dtype != kDtypeQ8;
-}
-
-uint64_t attention_workspace_bytes(uint32_t n_heads, uint32_t head_dim, uint32_t n_seqs,
-                                   uint32_t max_ctx_len) {
-  uint64_t parts = max_ctx_len ? (max_ctx_len + kAttnPartTokens - 1) / kAttnPartTokens : 1;
-  if (parts <= 1) return 0;
-  return (uint64_t)n_seqs * n_heads * parts * ((uint64_t)head_dim + 2u) * 4u;
-}
-
-hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
-                                   const float* q, float* out, const int32_t* tables,
-                                   uint32_t max_blocks, const int32_t* ctx_lens,
-                                   uint32_t n_seqs, uint32_t max_ctx_len, float scale,
-                                   void* workspace, hipStream_t s) {
-  if (n_seqs == 0) return hipSuccess;
-  const uint32_t G = n_heads / g.n_kv_heads;
-  const uint32_t max_parts =
-      max_ctx_len ? (max_ctx_len + kAttnPartTokens - 1) / kAttnPartTokens : 1;
-  float* ws_o = (float*)workspace;
-  float* ws_ml = ws_o ? ws_o + (uint64_t)n_seqs * n_heads * max_parts * g.head_dim : nullptr;
-  if (g.head_dim == 128) {
-    if (g.dtype == kDtypeF16)
-      return dispatch_group<kDtypeF16, 128>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                            ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
-    if (g.dtype == kDtypeF32)
-      return dispatch_group<kDtypeF32, 128>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                            ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
-    return dispatch_group<kDtypeQ8, 128>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                         ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
-  }
-  if (g.dtype == kDtypeF16)
-    return dispatch_group<kDtypeF16, 64>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                         ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
-  if (g.dtype == kDtypeF32)
-    return dispatch_group<kDtypeF32, 64>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                         ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
-  return dispatch_group<kDtypeQ8, 64>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                      ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
 }
 
 }  // namespace fkv

@@ -308,7 +308,8 @@ class PagedKvPool:
         ws_ptr, ws_bytes = 0, 0
         if need:
             if workspace is None:
-                workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+                # zero-filled: the first bytes are split counters that must start at 0
+                workspace = torch.zeros(need, dtype=torch.uint8, device=q.device)
             ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
         check(self._lib.fkv_decode_attention(
             self._h, layer, n_heads, _dev(q, torch.float32, "q"), _dev(out, torch.float32, "out"),

@@ -233,7 +233,10 @@ int32_t fkv_swap_in(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void
  * [n_seqs][max_blocks_per_seq]; ctx_lens: device int32 [n_seqs], each
  * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, g in {1,2,4,8,16}.
  * workspace: device scratch of fkv_decode_attention_workspace_size() bytes
- * (split-context partials); it may be NULL when that size is 0. */
+ * (split-context partials and per-(sequence, kv head) merge counters); it may
+ * be NULL when that size is 0. It must be zero-filled once before its first
+ * use; every call leaves it ready for the next. Calls that share one workspace
+ * must not overlap (same stream, or ordered by events). */
 int32_t fkv_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
                                             uint32_t n_seqs, uint32_t max_ctx_len,
                                             uint64_t* bytes_out);
