@@ -55,6 +55,19 @@ def append_bytes(n_tokens, hkv, d, elem_bytes):
     return int(n_tokens * (2 * hkv * d * 4 + 2 * hkv * d * elem_bytes + 8))
 
 
+def read_traffic(path):
+    """HBM bytes per attention call from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (the line `hbm_bytes_per_launch: N`), or None when it is absent."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("hbm_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -199,11 +212,7 @@ def main():
     copy_gbs = 2 * nbytes * 5 / (c0.elapsed_time(c1) * 1e-3) / 1e9
     del a, b
 
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "decode_attention_llama3_8b_c2_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = read_traffic(os.path.join(ROOT, "profiles", "decode_attention_llama3_8b_c2_hbm_traffic.md"))
 
     result = {
         "metric": "paged decode-attn HBM GB/s (% of peak) + KV append tokens/s, 1xMI355X",
@@ -238,7 +247,7 @@ def main():
         "device_copy_gbs": round(copy_gbs, 1),
         "roofline": {
             "bound": "hbm",
-            "kernel": "fkv decode attention (attn_partition_kernel + attn_combine_kernel)",
+            "kernel": "fkv_decode_attention (attn_split_kernel + attn_combine_kernel)",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -162,7 +162,7 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 #pragma unroll
       for (int ps = 0; ps < PASSES; ps++) {
         int row = ps * RPP + r;
-        kreg[j][ps] = *(const uint4*)(kt + row * row_bytes + c * 16);
+        kreg[j][ps] = load_stream16(kt + row * row_bytes + c * 16);
         if constexpr (DT == kDtypeQ8)
           ksc[j][ps] = ((const uint16_t*)(kt + scale_off))[row * (D / 32) + (c * EPL) / 32];
       }
@@ -178,7 +178,7 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 #pragma unroll
         for (int ps = 0; ps < PASSES; ps++) {
           int row = ps * RPP + r;
-          vreg[j][ps] = *(const uint4*)(vt + row * row_bytes + c * 16);
+          vreg[j][ps] = load_stream16(vt + row * row_bytes + c * 16);
           if constexpr (DT == kDtypeQ8)
             vsc[j][ps] = ((const uint16_t*)(vt + scale_off))[row * (D / 32) + (c * EPL) / 32];
         }
@@ -263,7 +263,7 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 #pragma unroll
       for (int ps = 0; ps < PASSES; ps++) {
         int row = ps * RPP + r;
-        vl[ps] = *(const uint4*)(vt + row * row_bytes + c * 16);
+        vl[ps] = load_stream16(vt + row * row_bytes + c * 16);
         if constexpr (DT == kDtypeQ8)
           vs[ps] = ((const uint16_t*)(vt + scale_off))[row * (D / 32) + (c * EPL) / 32];
       }
@@ -539,7 +539,7 @@ __global__ void __launch_bounds__(256) attn_split_kernel(
 #pragma unroll
       for (int ps = 0; ps < PASSES; ps++) {
         const int row = ps * RPP + r;
-        reg[j][ps] = *(const uint4*)(t + row * row_bytes + c * 16);
+        reg[j][ps] = load_stream16(t + row * row_bytes + c * 16);
         if constexpr (DT == kDtypeQ8)
           sc[j][ps] = ((const uint16_t*)(t + scale_off))[row * (D / 32) + (c * EPL) / 32];
       }

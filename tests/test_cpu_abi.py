@@ -1,0 +1,86 @@
+"""CPU: libferrum_kv.so loads and exports every entry point include/ferrum_kv.h
+declares; argument validation that happens before any device work returns the
+reference's error variants and strings (no kernel is launched here)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import ferrum_amd as fa
+from ferrum_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    names = []
+    for h in sorted(os.listdir(os.path.join(ROOT, "include"))):
+        if h.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", h)).read()
+            text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+            names += re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(fkv_\w+)\s*\(", text, flags=re.M)
+    return sorted(set(names))
+
+
+def test_every_declared_entry_point_is_exported_and_bound():
+    names = header_functions()
+    assert len(names) >= 30
+    lib = _lib.load()
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature"
+    assert sorted(_lib.SIGNATURES) == names
+
+
+def test_abi_version_and_device_count():
+    lib = _lib.load()
+    assert lib.fkv_abi_version() == 1
+    assert lib.fkv_device_count() >= 0
+
+
+def _create(**kw):
+    base = dict(n_layers=2, n_kv_heads=2, head_dim=64, num_blocks=4)
+    base.update(kw)
+    return fa.PagedKvPool(fa.PagedConfig(**base))
+
+
+@pytest.mark.parametrize("field", ["n_layers", "n_kv_heads", "head_dim", "num_blocks", "block_size"])
+def test_zero_dimension_is_cache_error(field):
+    # pool.rs:28 "kv pool dimension is zero", checked before any allocation
+    with pytest.raises(fa.CacheError, match="^cache: kv pool dimension is zero$"):
+        _create(**{field: 0})
+
+
+def test_config_validation_messages():
+    with pytest.raises(fa.KernelError, match="^kernel: q8_0 k is not a multiple of 32$"):
+        _create(kv_dtype=fa.DTYPE_Q8_0, head_dim=48)
+    with pytest.raises(fa.KernelError, match="^kernel: unsupported dtype$"):
+        _create(kv_dtype=3)
+    with pytest.raises(fa.InvalidRequest, match="unknown f16 rounding mode"):
+        _create(f16_rounding=7)
+    with pytest.raises(fa.CacheError, match="^cache: kv pool size overflow$"):
+        _create(num_blocks=1 << 40)
+    with pytest.raises(fa.CacheError, match="^cache: kv pool dimension is zero$"):
+        fa.PreallocatedKvPool.new(fa.KvPoolConfig(0, 1, 4, 3, 2))
+    with pytest.raises(fa.CacheError, match="^cache: kv pool size overflow$"):
+        fa.PreallocatedKvPool.new(fa.KvPoolConfig(1 << 20, 1 << 20, 1 << 20, 1 << 20, 2))
+
+
+def test_null_arguments_are_invalid_request():
+    lib = _lib.load()
+    assert lib.fkv_paged_create(None, None) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_last_error() == b"null argument"
+    assert lib.fkv_append(None, 0, None, None, None, 0, None) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_device_copy(ctypes.c_void_p(16), ctypes.c_void_p(8), 16, None) == _lib.FKV_ERR_INVALID
+    assert b"16-byte aligned" in lib.fkv_last_error()
+    # a successful no-op call clears the thread's message
+    assert lib.fkv_paged_destroy(None) == 0
+    assert lib.fkv_last_error() == b""
+
+
+def test_error_classes_mirror_ferrum_error():
+    # FerrumError Display (core-types/src/error.rs:21-46) and HTTP mapping (:101)
+    assert fa.Unavailable("no free kv blocks").http_status == 503
+    assert fa.InvalidRequest("x").http_status == 400
+    assert issubclass(fa.CacheError, fa.FerrumError)
