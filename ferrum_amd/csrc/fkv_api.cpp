@@ -410,6 +410,7 @@ int32_t fkv_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_hea
   if (!pool || !bytes_out) return fail(FKV_ERR_INVALID, "null argument");
   int32_t st = check_attention(pool, n_heads, max_ctx_len);
   if (st) return st;
+  DeviceGuard dg(pool->cfg.device);  // the F16 plan depends on the device's CU count
   *bytes_out = fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
   return ok();
 }
@@ -430,11 +431,11 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, c
     return fail(FKV_ERR_INVALID, "too many sequences");
   if ((uint64_t)max_ctx_len > (uint64_t)max_blocks_per_seq * pool->cfg.block_size)
     return fail(FKV_ERR_INVALID, "max_ctx_len exceeds the block table");
+  DeviceGuard dg(pool->cfg.device);
   const uint64_t need =
       fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
   if (workspace_bytes < need || (need && !workspace))
     return fail(FKV_ERR_INVALID, "attention workspace too small");
-  DeviceGuard dg(pool->cfg.device);
   FKV_HIP(fkv::launch_decode_attention(pool->geom, layer, n_heads, q, out, block_tables,
                                        max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale,
                                        workspace, (hipStream_t)stream),

@@ -2,9 +2,16 @@
 // Llama::forward_one_token (crates/model/src/llama.rs:220-247) over K/V read
 // through block tables, with the softmax of crates/kernels/src/scalar.rs:125-141
 // (a non-finite maximum gives zeros).
+//
+// This file holds the VALU kernels and the dispatch:
+//   Q8_0 storage   attn_split_kernel (G <= 8), dequantising inside the dot products
+//   F32 storage    attn_partition_kernel (G in {1, 2, 4, 8, 16})
+//   F16 storage    the MFMA kernels of fkv_attention_mfma.hip
+// and attn_combine_kernel, which merges split partials for all of them.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <type_traits>
 
@@ -41,8 +48,6 @@ using namespace dev;
 template <int DT>
 struct KvTraits;
 template <>
-struct KvTraits<kDtypeF16> { static constexpr int kBytes = 2; };
-template <>
 struct KvTraits<kDtypeF32> { static constexpr int kBytes = 4; };
 template <>
 struct KvTraits<kDtypeQ8> { static constexpr int kBytes = 1; };
@@ -61,14 +66,7 @@ struct AttnShape {
 // Decode one 16-byte load (EPL values) to f32.
 template <int DT, int EPL>
 __device__ __forceinline__ void decode16(const uint4& w, float (&f)[EPL]) {
-  if constexpr (DT == kDtypeF16) {
-    const uint32_t a[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      f[2 * i] = f16_bits_to_f32(a[i] & 0xffffu);
-      f[2 * i + 1] = f16_bits_to_f32(a[i] >> 16);
-    }
-  } else if constexpr (DT == kDtypeF32) {
+  if constexpr (DT == kDtypeF32) {
     f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y);
     f[2] = __uint_as_float(w.z); f[3] = __uint_as_float(w.w);
   } else {
@@ -395,7 +393,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Split-context streaming kernel (F16 and Q8_0 storage, G <= 8)
+// Split-context streaming kernel (Q8_0 storage, G <= 8)
 // ---------------------------------------------------------------------------
 //
 // Workgroup = 4 waves = one split (split_tokens tokens) of one (sequence, kv
@@ -800,16 +798,35 @@ hipError_t dispatch_group(uint32_t G, const Geom& g, uint32_t layer, uint32_t n_
 
 bool attention_supported(int dtype, uint32_t head_dim, uint32_t group) {
   if (head_dim != 64 && head_dim != 128) return false;
-  if (dtype != kDtypeF16 && dtype != kDtypeF32 && dtype != kDtypeQ8) return false;
+  if (dtype == kDtypeF16) return group >= 1 && group <= 16;
+  if (dtype != kDtypeF32 && dtype != kDtypeQ8) return false;
   if (group == 1 || group == 2 || group == 4 || group == 8) return true;
   return group == 16 && dtype != kDtypeQ8;
+}
+
+hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
+                                    uint32_t n_seqs, uint32_t n_heads, uint32_t max_blocks,
+                                    uint32_t max_splits, uint32_t split_tokens,
+                                    const float* ws_o, const float* ws_ml, float* out,
+                                    hipStream_t s) {
+  if (head_dim == 128)
+    attn_combine_kernel<128><<<n_seqs * n_heads, 256, 0, s>>>(
+        ctx_lens, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
+  else
+    attn_combine_kernel<64><<<n_seqs * n_heads, 256, 0, s>>>(
+        ctx_lens, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
+  return hipGetLastError();
 }
 
 namespace {
 
 // How one decode-attention call is cut up, and where its workspace regions live.
 struct AttnPlan {
-  bool split_path = false;  // attn_split_kernel (else attn_partition + combine)
+  bool stream_path = false; // attn_mfma_stream_kernel (F16) + stream combine
+  uint32_t stream_waves = 0;
+  uint64_t pre_off = 0;
+  bool mfma_path = false;   // attn_mfma_kernel (F16) + combine
+  bool split_path = false;  // attn_split_kernel (Q8_0) + combine; else attn_partition + combine
   uint32_t split_tokens = kAttnPartTokens;
   uint32_t max_splits = 1;
   uint64_t o_off = 0, ml_off = 0, total = 0;
@@ -823,7 +840,7 @@ inline uint64_t align256(uint64_t x) { return (x + 255) / 256 * 256; }
 uint32_t choose_split_tokens(uint32_t max_ctx_len) {
   if (const char* e = getenv("FKV_ATTN_SPLIT_TOKENS")) {
     long v = strtol(e, nullptr, 10);
-    if (v >= 256 && v % 256 == 0 && v <= (1 << 20)) return (uint32_t)v;
+    if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) return (uint32_t)v;
   }
   uint64_t st = ((uint64_t)max_ctx_len / 64 + 255) / 256 * 256;
   if (st < 512) st = 512;
@@ -834,8 +851,24 @@ uint32_t choose_split_tokens(uint32_t max_ctx_len) {
 AttnPlan plan_attention(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_ctx_len) {
   AttnPlan p;
   const uint32_t G = g.n_kv_heads ? n_heads / g.n_kv_heads : 0;
-  p.split_path = (g.dtype == kDtypeF16 || g.dtype == kDtypeQ8) && G >= 1 && G <= 8;
-  p.split_tokens = p.split_path ? choose_split_tokens(max_ctx_len) : kAttnPartTokens;
+  const char* mode = getenv("FKV_ATTN_MODE");
+  // F16: the split kernel by default; FKV_ATTN_MODE=stream selects the persistent one.
+  if (g.dtype == kDtypeF16 && G >= 1 && G <= 16 && stream_attention_supported(n_seqs) && mode &&
+      strcmp(mode, "stream") == 0) {
+    p.stream_waves = stream_attention_waves(g.head_dim, n_seqs);
+    if (p.stream_waves > 0) {
+      p.stream_path = true;
+      const uint64_t slots = (uint64_t)p.stream_waves + (uint64_t)n_seqs * g.n_kv_heads;
+      p.pre_off = 0;
+      p.o_off = align256(((uint64_t)n_seqs + 1) * 4u);
+      p.ml_off = p.o_off + align256(slots * G * g.head_dim * 4u);
+      p.total = p.ml_off + align256(slots * G * 2u * 4u);
+      return p;
+    }
+  }
+  p.mfma_path = g.dtype == kDtypeF16 && G >= 1 && G <= 16;
+  p.split_path = g.dtype == kDtypeQ8 && G >= 1 && G <= 8;
+  p.split_tokens = (p.mfma_path || p.split_path) ? choose_split_tokens(max_ctx_len) : kAttnPartTokens;
   p.max_splits = max_ctx_len ? (max_ctx_len + p.split_tokens - 1) / p.split_tokens : 1;
   if (p.max_splits <= 1) return p;  // single split: no workspace
   const uint64_t items = (uint64_t)n_seqs * n_heads * p.max_splits;
@@ -893,11 +926,21 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
   const uint32_t G = n_heads / g.n_kv_heads;
   const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
   uint8_t* ws = (uint8_t*)workspace;
+  if (p.stream_path)
+    return launch_attention_stream(g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
+                                   n_seqs, scale, p.stream_waves, (uint32_t*)(ws + p.pre_off),
+                                   (float*)(ws + p.o_off), (float*)(ws + p.ml_off), s);
+  if (p.mfma_path) {
+    float* ws_o = ws ? (float*)(ws + p.o_off) : nullptr;
+    float* ws_ml = ws ? (float*)(ws + p.ml_off) : nullptr;
+    hipError_t e = launch_attention_mfma(g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
+                                         n_seqs, p.max_splits, p.split_tokens, scale, ws_o,
+                                         ws_ml, s);
+    if (e != hipSuccess || p.max_splits <= 1) return e;
+    return launch_attention_combine(g.head_dim, ctx_lens, n_seqs, n_heads, max_blocks,
+                                    p.max_splits, p.split_tokens, ws_o, ws_ml, out, s);
+  }
   if (p.split_path) {
-    if (g.dtype == kDtypeF16)
-      return g.head_dim == 128
-                 ? dispatch_split<kDtypeF16, 128>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens, n_seqs, p, scale, ws, s)
-                 : dispatch_split<kDtypeF16, 64>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens, n_seqs, p, scale, ws, s);
     return g.head_dim == 128
                ? dispatch_split<kDtypeQ8, 128>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens, n_seqs, p, scale, ws, s)
                : dispatch_split<kDtypeQ8, 64>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens, n_seqs, p, scale, ws, s);
@@ -905,19 +948,14 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
   const uint32_t max_parts = p.max_splits;
   float* ws_o = ws ? (float*)(ws + p.o_off) : nullptr;
   float* ws_ml = ws ? (float*)(ws + p.ml_off) : nullptr;
+  // F16 never gets here (mfma_path covers every supported group size).
   if (g.head_dim == 128) {
-    if (g.dtype == kDtypeF16)
-      return dispatch_group<kDtypeF16, 128>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                            ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
     if (g.dtype == kDtypeF32)
       return dispatch_group<kDtypeF32, 128>(G, g, layer, n_heads, q, out, tables, max_blocks,
                                             ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
     return dispatch_group<kDtypeQ8, 128>(G, g, layer, n_heads, q, out, tables, max_blocks,
                                          ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
   }
-  if (g.dtype == kDtypeF16)
-    return dispatch_group<kDtypeF16, 64>(G, g, layer, n_heads, q, out, tables, max_blocks,
-                                         ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
   if (g.dtype == kDtypeF32)
     return dispatch_group<kDtypeF32, 64>(G, g, layer, n_heads, q, out, tables, max_blocks,
                                          ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);

@@ -1,0 +1,762 @@
+// Paged decode attention on the matrix cores of gfx950, for F16 KV storage.
+// Same contract as the attention loop of Llama::forward_one_token
+// (crates/model/src/llama.rs:220-247): for each query head h of a sequence,
+// score[p] = dot(q_h, K[p][h / g]) * scale, softmax over the context
+// (crates/kernels/src/scalar.rs:125-141, a non-finite maximum gives zeros), then
+// out_h = sum_p w_p V[p][h / g], with f32 accumulation.
+//
+// Decode attention is a GEMV over HBM, but with a GQA group of G query heads it
+// is G GEMVs over the same K/V bytes. Done on the VALU (v_fma_mix) that work
+// capped the stream at 47% of HBM peak for G = 8; on MFMA it is a few percent
+// of the matrix-core rate, and the VALU only runs the softmax.
+//
+// One wave processes one 16-token block at a time:
+//
+//   QK   S[token][head] = K[16 x D] . Q^T[D x 16] with v_mfma_f32_16x16x32_f16:
+//        A = the K tile (lane l: token l%16, dims c*32 + (l/16)*8 .. +7, one
+//        16-byte load per chunk c from the [D/8][B][8] tile, so each load
+//        instruction reads 1 KiB of consecutive bytes); B = q split into f16 hi +
+//        lo parts (two MFMAs per chunk, ~22 significant bits) after a per-head
+//        power-of-two scaling that keeps q inside the f16 range. Output lane l
+//        holds tokens (l/16)*4 + r of head l%16.
+//   soft lazy online softmax in the log2 domain: each lane keeps a partial sum
+//        for its head; only when a score exceeds the head's reference max by
+//        2^8 (any lane, by ballot) does the wave take the exact running max and
+//        rescale the partial sums and accumulators.
+//   PV   O[head][dim] += P[16 x 16 tokens] . V[16 tokens x 16 dims] with
+//        v_mfma_f32_16x16x16_f16 for each 16-dim column tile: A = P in f16 (lane
+//        l: head l%16, tokens (l/16)*4 .. +3 -- exactly the QK output layout, so
+//        no lane exchange), B = V from the dim-major V tile (lane l: dim
+//        16m + l%16, tokens (l/16)*4 .. +3, one 8-byte load; 512 consecutive
+//        bytes per load instruction).
+//
+// Heads >= G in the 16-wide MFMA are padding: their q is zero and their scores
+// are forced to -inf, so they never trigger a rescale and are never written.
+//
+// Two schedules share that block step:
+//   attn_mfma_kernel  (default) one workgroup per (sequence, KV head, 512-token
+//        split); its 4 waves take every fourth block and merge in LDS; splits
+//        of one sequence are merged by attn_combine_kernel (log-sum-exp).
+//   attn_mfma_stream_kernel  (FKV_ATTN_MODE=stream) persistent: the grid is the
+//        number of workgroups the GPU holds at once; every wave takes an equal
+//        contiguous range of the flattened (sequence, KV head, block) list and
+//        streams it without a break. A (sequence, KV head) inside one wave's
+//        range is written to `out` directly; one cut by a range boundary leaves
+//        partials that attn_stream_combine_kernel merges. Measured on MI355X it
+//        is no faster than the split kernel: equal ranges finish 55-98 us apart
+//        because XCDs stream at different rates.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "fkv_device.h"
+#include "fkv_internal.h"
+
+// Blocks in flight per wave (the load ring depth) of attn_mfma_kernel.
+#ifndef FKV_MFMA_RING
+#define FKV_MFMA_RING 1
+#endif
+
+namespace fkv {
+namespace {
+
+using namespace dev;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kHeads = 16;            // MFMA column count: query heads of one group
+constexpr float kRescaleLog2 = 8.0f;  // rescale when a score passes the reference max by 2^8
+constexpr int B = kAttnBlock;
+
+__device__ __forceinline__ u32x2_t load_stream8(const uint8_t* p) {
+  return __builtin_nontemporal_load((const u32x2_t*)p);
+}
+
+// Per-lane view of one wave's 16 x 16 MFMA tiles.
+struct Lane {
+  int lane;   // 0..63
+  int col;    // K token row / q head / score head / V dim within a 16-column tile
+  int grp;    // MFMA k group (0..3)
+  bool real;  // col < G: this lane's score column is a real query head
+};
+
+// q of one (sequence, KV head) group -> QK B operand: per-head power-of-two
+// scaling (the head's largest |q * scale * log2 e| lands in [2^14, 2^15), far
+// from f16 overflow), then an f16 hi + lo split. hscale undoes the scaling.
+template <int D>
+__device__ __forceinline__ void prep_q(const float* qg, const Lane& ln, float qscale,
+                                       f16x8 (&qh)[D / 32], f16x8 (&ql)[D / 32],
+                                       float& hscale) {
+  constexpr int NC = D / 32;
+  const float* qb = qg + (ln.real ? ln.col : 0) * D + ln.grp * 8;
+  float x[NC][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const float4 a = *(const float4*)(qb + c * 32);
+    const float4 b = *(const float4*)(qb + c * 32 + 4);
+    const float v8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      x[c][e] = ln.real ? v8[e] * qscale : 0.0f;
+      amax = __builtin_fmaxf(amax, __builtin_fabsf(x[c][e]));
+    }
+  }
+  amax = __builtin_fmaxf(amax, __shfl_xor(amax, 16));
+  amax = __builtin_fmaxf(amax, __shfl_xor(amax, 32));
+  int k = 0;
+  if (amax > 0.0f && __builtin_isfinite(amax)) {
+    int ex;
+    (void)__builtin_frexpf(amax, &ex);
+    k = 15 - ex;
+  }
+  const float up = __builtin_ldexpf(1.0f, k);
+  hscale = __builtin_ldexpf(1.0f, -k);
+#pragma unroll
+  for (int c = 0; c < NC; c++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float y = x[c][e] * up;
+      const _Float16 hi = (_Float16)y;
+      qh[c][e] = hi;
+      ql[c][e] = (_Float16)(y - (float)hi);
+    }
+}
+
+// Running softmax state of the lane's head plus the wave's O accumulators
+// (row r of acc[m] is head grp*4 + r, dim 16m + col).
+template <int D>
+struct Accum {
+  float m_ref, l_part;
+  f32x4 acc[D / 16];
+  __device__ __forceinline__ void reset() {
+    m_ref = -__builtin_inff();
+    l_part = 0.0f;
+#pragma unroll
+    for (int m = 0; m < D / 16; m++) acc[m] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  }
+};
+
+// Scores of one block (log2 domain) for this lane's head and tokens
+// t0 + grp*4 + r; tokens at or past `end`, dead blocks and padding heads get -inf.
+template <int D>
+__device__ __forceinline__ void qk_block(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
+                                         const f16x8 (&ql)[D / 32], float hscale,
+                                         const Lane& ln, bool live, int32_t t0, int32_t end,
+                                         float (&s)[4]) {
+  // hi and lo parts in separate chains: a K value of +-inf times a zero lo part
+  // is NaN, where the f32 dot of the reference gives +-inf. A NaN that only the lo
+  // chain has is that case, and the hi chain alone is the right score.
+  f32x4 ah = {0.0f, 0.0f, 0.0f, 0.0f}, al = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < D / 32; c++) {
+    const f16x8 kv = __builtin_bit_cast(f16x8, kr[c]);
+    ah = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qh[c], ah, 0, 0, 0);
+    al = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], al, 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const bool ok = ln.real && live && t0 + ln.grp * 4 + r < end;
+    const float x = (al[r] != al[r] && ah[r] == ah[r]) ? ah[r] : ah[r] + al[r];
+    s[r] = ok ? x * hscale : -__builtin_inff();
+  }
+}
+
+// Lazy online softmax update and P (f16, the PV A operand) of one block.
+template <int D>
+__device__ __forceinline__ f16x4 softmax_block(const float (&s)[4], const Lane& ln,
+                                               Accum<D>& st) {
+  const float lmax = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), __builtin_fmaxf(s[2], s[3]));
+  const bool bad =
+      ln.real && (!(lmax <= st.m_ref + kRescaleLog2) || !__builtin_isfinite(st.m_ref));
+  // Accumulator row r of this lane is head grp*4 + r, whose alpha lives in lane
+  // grp*4 + r. The factors are found only on the rare rescale path, but applied
+  // unconditionally: a multiply inside the branch makes the compiler keep a second
+  // copy of every accumulator register across the loop.
+  float ar[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+    float x = lmax;
+    x = __builtin_fmaxf(x, __shfl_xor(x, 16));
+    x = __builtin_fmaxf(x, __shfl_xor(x, 32));
+    const float mn = __builtin_fmaxf(st.m_ref, x);
+    const float alpha = (mn == -__builtin_inff()) ? 1.0f : __builtin_amdgcn_exp2f(st.m_ref - mn);
+    st.l_part *= alpha;
+    st.m_ref = mn;
+#pragma unroll
+    for (int r = 0; r < 4; r++) ar[r] = __shfl(alpha, ln.grp * 4 + r);
+  }
+#pragma unroll
+  for (int m = 0; m < D / 16; m++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) st.acc[m][r] *= ar[r];
+  const bool dead = (st.m_ref == -__builtin_inff());
+  f16x4 pw;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float sv = s[r];
+    // all scores so far -inf/NaN: weight 0, but a NaN score stays NaN
+    const float e = dead ? (sv != sv ? sv : 0.0f) : __builtin_amdgcn_exp2f(sv - st.m_ref);
+    st.l_part += e;
+    pw[r] = (_Float16)e;
+  }
+  return pw;
+}
+
+// O += P . V for one block. Tokens at or past `end` carry weight 0 but their V
+// bytes may be anything (0 * NaN = NaN), so a partial block zeroes them first.
+template <int D>
+__device__ __forceinline__ void pv_block(u32x2_t (&vr)[D / 16], f16x4 pw, const Lane& ln,
+                                         int32_t t0, int32_t end, Accum<D>& st) {
+  if (t0 + B > end) {
+    const int nv = end - (t0 + ln.grp * 4);  // valid tokens among this lane's 4
+    const uint32_t m0 = nv >= 2 ? 0xffffffffu : (nv == 1 ? 0x0000ffffu : 0u);
+    const uint32_t m1 = nv >= 4 ? 0xffffffffu : (nv == 3 ? 0x0000ffffu : 0u);
+#pragma unroll
+    for (int m = 0; m < D / 16; m++) {
+      vr[m].x &= m0;
+      vr[m].y &= m1;
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < D / 16; m++)
+    st.acc[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(pw, __builtin_bit_cast(f16x4, vr[m]),
+                                                      st.acc[m], 0, 0, 0);
+}
+
+// K tile [D/8][B][8]: lane (col, grp) reads run (c*4 + grp) of token col; one
+// load instruction covers runs c*4 .. c*4+3 of all 16 tokens (1 KiB).
+template <int D>
+__device__ __forceinline__ void load_k(const uint8_t* ktile, const Lane& ln,
+                                       uint4 (&kr)[D / 32]) {
+  const uint8_t* t = ktile + ((uint64_t)ln.grp * B + ln.col) * 16;
+#pragma unroll
+  for (int c = 0; c < D / 32; c++) kr[c] = load_stream16(t + c * 4 * B * 16);
+}
+
+// V tile [D][B]: lane (col, grp) reads tokens grp*4 .. +3 of dim 16m + col.
+template <int D>
+__device__ __forceinline__ void load_v(const uint8_t* vtile, const Lane& ln,
+                                       u32x2_t (&vr)[D / 16]) {
+  const uint8_t* t = vtile + ((uint64_t)ln.col * B + ln.grp * 4) * 2;
+#pragma unroll
+  for (int m = 0; m < D / 16; m++) vr[m] = load_stream8(t + m * 16 * B * 2);
+}
+
+// ---------------------------------------------------------------------------
+// Persistent streaming kernel
+// ---------------------------------------------------------------------------
+
+// Block-count prefix of the sequences (clamped contexts) into s_pre[0..n_seqs]
+// by one 256-thread workgroup.
+__device__ void block_prefix(const int32_t* __restrict__ ctx_lens, uint32_t n_seqs, int32_t cap,
+                             uint32_t* s_pre, uint32_t* s_tmp, uint32_t* fault, bool report) {
+  const uint32_t tid = threadIdx.x;
+  const uint32_t per = (n_seqs + 255u) / 256u;
+  const uint32_t lo = tid * per < n_seqs ? tid * per : n_seqs;
+  const uint32_t hi = lo + per < n_seqs ? lo + per : n_seqs;
+  uint32_t sum = 0;
+  for (uint32_t i = lo; i < hi; i++) {
+    int32_t c = ctx_lens[i];
+    if (c < 0 || c > cap) {
+      if (report) raise_fault(fault, kFaultCtx);
+      c = c < 0 ? 0 : cap;
+    }
+    const uint32_t nb = (uint32_t)(c + B - 1) / B;
+    s_pre[i] = nb;
+    sum += nb;
+  }
+  s_tmp[tid] = sum;
+  __syncthreads();
+  if (tid < 64) {  // exclusive scan of the 256 chunk sums by wave 0
+    uint32_t v[4], t = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      v[k] = t;
+      t += s_tmp[tid * 4 + k];
+    }
+    uint32_t incl = t;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(incl, o);
+      if ((int)tid >= o) incl += y;
+    }
+    const uint32_t excl = incl - t;
+#pragma unroll
+    for (int k = 0; k < 4; k++) s_tmp[tid * 4 + k] = excl + v[k];
+  }
+  __syncthreads();
+  uint32_t run = s_tmp[tid];
+  for (uint32_t i = lo; i < hi; i++) {
+    const uint32_t nb = s_pre[i];
+    s_pre[i] = run;
+    run += nb;
+  }
+  if (tid == 255) s_pre[n_seqs] = run;
+  __syncthreads();
+}
+
+// Waves that share T flattened items: all of the grid's, but never more than T.
+__device__ __forceinline__ uint64_t stream_waves(uint64_t grid_waves, uint64_t T) {
+  return grid_waves < T ? grid_waves : T;
+}
+
+// Wave owning flattened item x: the largest w with floor(w * T / NW) <= x.
+__device__ __forceinline__ uint64_t wave_of(uint64_t x, uint64_t T, uint64_t NW) {
+  return ((x + 1) * NW - 1) / T;
+}
+
+// Three waves per SIMD: 170 VGPRs at most (unconstrained the compiler takes 186
+// at D = 128 and the CU holds only two of these workgroups).
+#ifndef FKV_STREAM_WAVES_PER_EU
+#define FKV_STREAM_WAVES_PER_EU 3
+#endif
+
+template <int D>
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(FKV_STREAM_WAVES_PER_EU, 8))) attn_mfma_stream_kernel(
+    Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
+    float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
+    const int32_t* __restrict__ ctx_lens, uint32_t n_seqs, float scale,
+    uint32_t* __restrict__ ws_pre, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  constexpr int NC = D / 32, NM = D / 16;
+  extern __shared__ uint32_t s_pre[];  // n_seqs + 1 block prefix sums
+  __shared__ uint32_t s_tmp[256];
+
+  const int32_t cap = (int32_t)(max_blocks * B);
+  block_prefix(ctx_lens, n_seqs, cap, s_pre, s_tmp, g.fault, blockIdx.x == 0);
+  if (blockIdx.x == 0)
+    for (uint32_t i = threadIdx.x; i <= n_seqs; i += 256) ws_pre[i] = s_pre[i];
+
+  // Every value read from the prefix table is the same in all lanes; readfirstlane
+  // keeps the cursor arithmetic in scalar registers.
+  auto pre = [&](uint32_t i) { return (uint32_t)__builtin_amdgcn_readfirstlane(s_pre[i]); };
+  const uint64_t hkv = g.n_kv_heads;
+  const uint64_t T = hkv * pre(n_seqs);
+  // At most one wave per item, so every wave that takes part owns at least one.
+  const uint64_t NW = stream_waves((uint64_t)gridDim.x * kAttnWaves, T);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint64_t w = (uint64_t)blockIdx.x * kAttnWaves + wave;
+  if (w >= NW) return;
+  const uint64_t a = w * T / NW, b_end = (w + 1) * T / NW;
+
+  Lane ln;
+  ln.lane = threadIdx.x & 63;
+  ln.col = ln.lane & 15;
+  ln.grp = ln.lane >> 4;
+  ln.real = ln.col < (int)G;
+  const float qscale = scale * kLog2e;
+
+  // Cursor over (sequence, KV head, block), starting at item a.
+  struct Cursor {
+    uint32_t s, kvh, bi, nb;
+    uint64_t seg0;  // flattened index of the segment's first item
+  };
+  Cursor cur;
+  {
+    uint32_t lo = 0, hi = n_seqs;  // largest s with hkv * s_pre[s] <= a: it has blocks
+    while (hi - lo > 1) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (hkv * pre(mid) <= a) lo = mid;
+      else hi = mid;
+    }
+    cur.s = lo;
+    cur.nb = pre(lo + 1) - pre(lo);
+    const uint64_t rel = a - hkv * pre(lo);
+    cur.kvh = (uint32_t)(rel / cur.nb);
+    cur.bi = (uint32_t)(rel % cur.nb);
+    cur.seg0 = hkv * pre(lo) + (uint64_t)cur.kvh * cur.nb;
+  }
+  auto advance = [&](Cursor c) {
+    if (++c.bi == c.nb) {
+      c.bi = 0;
+      c.seg0 += c.nb;
+      if (++c.kvh == hkv) {
+        c.kvh = 0;
+        do {
+          c.s++;
+        } while (pre(c.s + 1) == pre(c.s));  // skip sequences without blocks
+        c.nb = pre(c.s + 1) - pre(c.s);
+      }
+    }
+    return c;
+  };
+  // Physical block of an item; an entry outside the pool raises the fault flag,
+  // reads block 0 instead and is skipped.
+  auto phys = [&](const Cursor& c, bool& ok) {
+    const int32_t p = __builtin_amdgcn_readfirstlane(tables[(uint64_t)c.s * max_blocks + c.bi]);
+    ok = p >= 0 && (uint64_t)p < g.num_blocks;
+    if (!ok && ln.lane == 0) raise_fault(g.fault, kFaultBlock);
+    return ok ? (uint64_t)p : 0;
+  };
+
+  uint4 kr[NC];
+  u32x2_t vr[NM];
+  bool live;
+  {
+    const uint64_t p = phys(cur, live);
+    load_k<D>(tile_ptr(g, p, layer, 0, cur.kvh), ln, kr);
+    load_v<D>(tile_ptr(g, p, layer, 1, cur.kvh), ln, vr);
+  }
+  f16x8 qh[NC], ql[NC];
+  float hscale;
+  Accum<D> st;
+
+  uint64_t i = a;
+  for (;;) {  // one (sequence, KV head) segment per pass; cur is its first item here
+    const uint32_t seq = cur.s, kvh = cur.kvh, nb = cur.nb;
+    const uint64_t seg0 = cur.seg0;
+    const uint64_t stop = seg0 + nb < b_end ? seg0 + nb : b_end;
+    int32_t end = __builtin_amdgcn_readfirstlane(ctx_lens[seq]);
+    end = end < 0 ? 0 : (end > cap ? cap : end);
+    prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G) * D, ln, qscale, qh, ql, hscale);
+    st.reset();
+
+    for (; i < stop; i++) {
+      const bool more = i + 1 < b_end;
+      const int32_t t0 = (int32_t)cur.bi * B;
+      float s[4];
+      qk_block<D>(kr, qh, ql, hscale, ln, live, t0, end, s);
+      const bool cur_live = live;
+      uint64_t np = 0;
+      if (more) {  // next item, possibly the next segment's first
+        cur = advance(cur);
+        np = phys(cur, live);
+        load_k<D>(tile_ptr(g, np, layer, 0, cur.kvh), ln, kr);
+      }
+      const f16x4 pw = softmax_block<D>(s, ln, st);
+      if (cur_live) pv_block<D>(vr, pw, ln, t0, end, st);
+      if (more) load_v<D>(tile_ptr(g, np, layer, 1, cur.kvh), ln, vr);
+    }
+
+    // The wave's last item of this segment.
+    float lsum = st.l_part;
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    const uint64_t head0 = (uint64_t)seq * n_heads + (uint64_t)kvh * G;
+    if (seg0 >= a && seg0 + nb <= b_end) {  // whole segment in this wave: final output
+      // M and L of head grp*4 + r live in lane grp*4 + r
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int h = ln.grp * 4 + r;
+        const float M = __shfl(st.m_ref, h);
+        const float L = __shfl(lsum, h);
+        const float inv = 1.0f / L;
+        if (h < (int)G) {
+#pragma unroll
+          for (int m = 0; m < NM; m++)
+            out[(head0 + h) * D + m * 16 + ln.col] =
+                __builtin_isfinite(M) ? st.acc[m][r] * inv : 0.0f;
+        }
+      }
+    } else {
+      const uint64_t slot = w + (uint64_t)seq * hkv + kvh;
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int h = ln.grp * 4 + r;
+        if (h < (int)G) {
+#pragma unroll
+          for (int m = 0; m < NM; m++)
+            ws_o[(slot * G + h) * D + m * 16 + ln.col] = st.acc[m][r];
+        }
+      }
+      if (ln.lane < (int)G) {
+        ws_ml[(slot * G + ln.lane) * 2] = st.m_ref;  // log2 domain
+        ws_ml[(slot * G + ln.lane) * 2 + 1] = lsum;
+      }
+    }
+    if (i >= b_end) break;
+  }
+}
+
+// Merges the partials of every (sequence, KV head) segment that the stream
+// kernel cut between waves; one workgroup per (segment, query head of the group).
+// Segments held whole by one wave were written by the stream kernel; empty ones
+// (context 0) get zeros. 256 threads: dims 4*(t % (D/4)) .., partial rows t / (D/4).
+template <int D>
+__global__ void __launch_bounds__(256) attn_stream_combine_kernel(
+    uint32_t n_seqs, uint32_t hkv, uint32_t G, uint64_t grid_waves, const uint32_t* __restrict__ ws_pre,
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ out) {
+  constexpr int kLanesPerRow = D / 4;
+  constexpr int kRows = 256 / kLanesPerRow;
+  __shared__ float s_red[kRows][D];
+  __shared__ float s_lred[kRows];
+  __shared__ float s_max[4];
+
+  const uint32_t seg = blockIdx.x / G, h = blockIdx.x % G;
+  const uint32_t s = seg / hkv, kvh = seg % hkv;
+  const uint32_t nb = ws_pre[s + 1] - ws_pre[s];
+  float* o = out + ((uint64_t)s * hkv * G + (uint64_t)kvh * G + h) * D;
+  if (nb == 0) {
+    for (int d = threadIdx.x; d < D; d += 256) o[d] = 0.0f;
+    return;
+  }
+  const uint64_t T = (uint64_t)hkv * ws_pre[n_seqs];
+  const uint64_t NW = stream_waves(grid_waves, T);
+  const uint64_t seg0 = (uint64_t)hkv * ws_pre[s] + (uint64_t)kvh * nb;
+  const uint64_t wf = wave_of(seg0, T, NW), wl = wave_of(seg0 + nb - 1, T, NW);
+  if (wf == wl) return;
+  const uint32_t np = (uint32_t)(wl - wf + 1);
+  const uint64_t slot0 = wf + seg;  // slot of partial p: wf + p + seg
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+
+  float m = -__builtin_inff();
+  for (uint32_t p = threadIdx.x; p < np; p += 256)
+    m = __builtin_fmaxf(m, ws_ml[((slot0 + p) * G + h) * 2]);
+  m = wave_max(m);
+  if (lane == 0) s_max[wave] = m;
+  __syncthreads();
+  const float M = __builtin_fmaxf(__builtin_fmaxf(s_max[0], s_max[1]),
+                                  __builtin_fmaxf(s_max[2], s_max[3]));
+  if (!__builtin_isfinite(M)) {
+    for (int d = threadIdx.x; d < D; d += 256) o[d] = 0.0f;
+    return;
+  }
+  const int col = threadIdx.x % kLanesPerRow, row = threadIdx.x / kLanesPerRow;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  float lsum = 0.0f;
+  for (uint32_t p = row; p < np; p += kRows) {
+    const uint64_t sl = (slot0 + p) * G + h;
+    const float mp = ws_ml[sl * 2];
+    const float wgt = (mp == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mp - M);
+    lsum = __builtin_fmaf(wgt, ws_ml[sl * 2 + 1], lsum);
+    const float4 v = *(const float4*)(ws_o + sl * D + col * 4);
+    acc.x = __builtin_fmaf(wgt, v.x, acc.x);
+    acc.y = __builtin_fmaf(wgt, v.y, acc.y);
+    acc.z = __builtin_fmaf(wgt, v.z, acc.z);
+    acc.w = __builtin_fmaf(wgt, v.w, acc.w);
+  }
+  s_red[row][col * 4] = acc.x;
+  s_red[row][col * 4 + 1] = acc.y;
+  s_red[row][col * 4 + 2] = acc.z;
+  s_red[row][col * 4 + 3] = acc.w;
+  if (col == 0) s_lred[row] = lsum;
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float a = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int rr = 0; rr < kRows; rr++) {
+      a += s_red[rr][threadIdx.x];
+      l += s_lred[rr];
+    }
+    o[threadIdx.x] = a * (1.0f / l);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split kernel (one workgroup per (sequence, KV head, split))
+// ---------------------------------------------------------------------------
+
+template <int D, int NBUF>
+__global__ void __launch_bounds__(256) attn_mfma_kernel(
+    Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
+    float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
+    const int32_t* __restrict__ ctx_lens, uint32_t max_splits, int32_t split_tokens,
+    float scale, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+  constexpr int NC = D / 32, NM = D / 16;
+
+  __shared__ float s_o[kAttnWaves][kHeads * D];
+  __shared__ float s_m[kAttnWaves][kHeads];
+  __shared__ float s_l[kAttnWaves][kHeads];
+
+  const uint32_t sk = blockIdx.x, split = blockIdx.y;
+  const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
+  const int32_t cap = (int32_t)(max_blocks * B);
+  int32_t ctx = ctx_lens[seq];
+  if (ctx < 0 || ctx > cap) {
+    if (split == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
+    ctx = ctx < 0 ? 0 : cap;
+  }
+  const int32_t nsplits = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 1;
+  if ((int32_t)split >= nsplits) return;
+  const int32_t s0 = (int32_t)split * split_tokens;
+  const int32_t s1 = ctx - s0 < split_tokens ? ctx : s0 + split_tokens;
+  const int32_t nblk = s1 > s0 ? (s1 - s0 + B - 1) / B : 0;
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  Lane ln;
+  ln.lane = threadIdx.x & 63;
+  ln.col = ln.lane & 15;
+  ln.grp = ln.lane >> 4;
+  ln.real = ln.col < (int)G;
+
+  f16x8 qh[NC], ql[NC];
+  float hscale;
+  prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G) * D, ln, scale * kLog2e, qh, ql,
+            hscale);
+
+  const int32_t* table = tables + (uint64_t)seq * max_blocks;
+  const int32_t blk0 = s0 / B;
+  Accum<D> st;
+  st.reset();
+
+  // Ring of NBUF block buffers: wave w owns blocks w, w + 4, w + 8, ... of the
+  // split; block t of the wave lives in buffer t % NBUF. Block t + NBUF's K load
+  // is issued as soon as block t's QK has consumed the buffer, and its V load
+  // once block t's P.V has.
+  uint4 kr[NBUF][NC];
+  u32x2_t vr[NBUF][NM];
+  int32_t bid[NBUF];
+  bool blive[NBUF];
+  const int32_t nt = wave < nblk ? (nblk - wave + kAttnWaves - 1) / kAttnWaves : 0;
+
+  // Physical block of the wave's block t (wave-uniform). A block-table entry
+  // outside the pool raises the fault flag, loads block 0 instead and is skipped.
+  auto fetch = [&](int t, int b) {
+    const int32_t p = table[blk0 + wave + kAttnWaves * t];
+    const bool okb = p >= 0 && (uint64_t)p < g.num_blocks;
+    if (!okb && ln.lane == 0) raise_fault(g.fault, kFaultBlock);
+    blive[b] = okb;
+    bid[b] = okb ? p : 0;
+  };
+  auto process = [&](int t, int b) {
+    const bool live = blive[b];
+    const bool refill = t + NBUF < nt;
+    const int32_t t0 = s0 + (wave + kAttnWaves * t) * B;  // first token of the block
+    float s[4];
+    qk_block<D>(kr[b], qh, ql, hscale, ln, live, t0, s1, s);
+    if (refill) {
+      fetch(t + NBUF, b);
+      load_k<D>(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln, kr[b]);
+    }
+    const f16x4 pw = softmax_block<D>(s, ln, st);
+    if (live) pv_block<D>(vr[b], pw, ln, t0, s1, st);
+    if (refill) load_v<D>(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln, vr[b]);
+  };
+
+#pragma unroll
+  for (int b = 0; b < NBUF; b++) {
+    if (b < nt) {
+      fetch(b, b);
+      load_k<D>(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln, kr[b]);
+      load_v<D>(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln, vr[b]);
+    }
+  }
+  for (int t = 0; t < nt; t += NBUF) {
+#pragma unroll
+    for (int b = 0; b < NBUF; b++)
+      if (t + b < nt) process(t + b, b);
+  }
+
+  // ---- per wave: l over the 4 lanes of each head; O rows to LDS.
+  float lsum = st.l_part;
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int h = ln.grp * 4 + r;
+    if (h < (int)G) {
+#pragma unroll
+      for (int m = 0; m < NM; m++) s_o[wave][h * D + m * 16 + ln.col] = st.acc[m][r];
+    }
+  }
+  if (ln.lane < (int)G) {
+    s_m[wave][ln.lane] = st.m_ref;
+    s_l[wave][ln.lane] = lsum;
+  }
+  __syncthreads();
+
+  // ---- merge the 4 waves (m in the log2 domain).
+  const uint64_t head0 = (uint64_t)seq * n_heads + (uint64_t)kvh * G;
+  for (int e = threadIdx.x; e < (int)G * D; e += 256) {
+    const int gg = e / D, d = e % D;
+    float M = -__builtin_inff();
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; w++) M = __builtin_fmaxf(M, s_m[w][gg]);
+    float o = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; w++) {
+      const float mw = s_m[w][gg];
+      const float wt = (mw == -__builtin_inff()) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+      o = __builtin_fmaf(wt, s_o[w][gg * D + d], o);
+      L = __builtin_fmaf(wt, s_l[w][gg], L);
+    }
+    const uint64_t head = head0 + gg;
+    if (nsplits == 1) {
+      out[head * D + d] = __builtin_isfinite(M) ? o * (1.0f / L) : 0.0f;
+    } else {
+      ws_o[(head * max_splits + split) * D + d] = o;
+      if (d == 0) {
+        ws_ml[(head * max_splits + split) * 2] = M * 0.6931471805599453f;  // natural log
+        ws_ml[(head * max_splits + split) * 2 + 1] = L;
+      }
+    }
+  }
+}
+
+// Workgroups of the stream kernel one CU holds at once (0 if it cannot launch).
+template <int D>
+int stream_wgs_per_cu(size_t lds_bytes) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, attn_mfma_stream_kernel<D>, 256,
+                                                   lds_bytes) != hipSuccess)
+    return 0;
+  return n;
+}
+
+}  // namespace
+
+bool stream_attention_supported(uint32_t n_seqs) {
+  return n_seqs >= 1 && n_seqs <= kStreamMaxSeqs;
+}
+
+uint32_t stream_attention_waves(uint32_t head_dim, uint32_t n_seqs) {
+  const size_t lds = ((size_t)n_seqs + 1) * 4;
+  const int per_cu = head_dim == 128 ? stream_wgs_per_cu<128>(lds) : stream_wgs_per_cu<64>(lds);
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return 0;
+  if (per_cu <= 0 || cus <= 0) return 0;
+  return (uint32_t)(per_cu * cus) * kAttnWaves;
+}
+
+hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_heads,
+                                   const float* q, float* out, const int32_t* tables,
+                                   uint32_t max_blocks, const int32_t* ctx_lens,
+                                   uint32_t n_seqs, float scale, uint32_t n_waves,
+                                   uint32_t* ws_pre, float* ws_o, float* ws_ml, hipStream_t s) {
+  const uint32_t G = n_heads / g.n_kv_heads;
+  const uint32_t grid = n_waves / kAttnWaves;
+  const size_t lds = ((size_t)n_seqs + 1) * 4;
+  if (g.head_dim == 128)
+    attn_mfma_stream_kernel<128><<<grid, 256, lds, s>>>(g, layer, n_heads, G, q, out, tables,
+                                                        max_blocks, ctx_lens, n_seqs, scale,
+                                                        ws_pre, ws_o, ws_ml);
+  else
+    attn_mfma_stream_kernel<64><<<grid, 256, lds, s>>>(g, layer, n_heads, G, q, out, tables,
+                                                       max_blocks, ctx_lens, n_seqs, scale,
+                                                       ws_pre, ws_o, ws_ml);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const uint32_t cgrid = n_seqs * g.n_kv_heads * G;
+  if (g.head_dim == 128)
+    attn_stream_combine_kernel<128><<<cgrid, 256, 0, s>>>(n_seqs, g.n_kv_heads, G, n_waves,
+                                                          ws_pre, ws_o, ws_ml, out);
+  else
+    attn_stream_combine_kernel<64><<<cgrid, 256, 0, s>>>(n_seqs, g.n_kv_heads, G, n_waves,
+                                                         ws_pre, ws_o, ws_ml, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads,
+                                 const float* q, float* out, const int32_t* tables,
+                                 uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
+                                 uint32_t max_splits, uint32_t split_tokens, float scale,
+                                 float* ws_o, float* ws_ml, hipStream_t s) {
+  const uint32_t G = n_heads / g.n_kv_heads;
+  dim3 grid(n_seqs * g.n_kv_heads, max_splits);
+  constexpr int NBUF = FKV_MFMA_RING;
+  if (g.head_dim == 128)
+    attn_mfma_kernel<128, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,
+                                                     max_blocks, ctx_lens, max_splits,
+                                                     (int32_t)split_tokens, scale, ws_o, ws_ml);
+  else
+    attn_mfma_kernel<64, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,
+                                                    max_blocks, ctx_lens, max_splits,
+                                                    (int32_t)split_tokens, scale, ws_o, ws_ml);
+  return hipGetLastError();
+}
+
+}  // namespace fkv

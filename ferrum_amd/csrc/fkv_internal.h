@@ -8,8 +8,10 @@
 namespace fkv {
 
 // Geometry of one paged pool, passed by value to every kernel.
-// pool[block][layer][kv][head][tile]; tile = [B][D] elements (F32/F16) or
-// [B*D int8][B*D/32 f16 scales] (Q8_0), padded to a multiple of 16 bytes.
+// pool[block][layer][kv][head][tile]; tile = [B][D] elements (F32), [D/8][B][8]
+// (F16 K: 16-byte runs of 8 dims, token-contiguous per run), [D][B] (F16 V), or
+// [B*D int8][B*D/32 f16 scales] (Q8_0), padded to a multiple of 16 bytes. The
+// F16 orders are the QK and P.V operand orders of the MFMA decode kernel.
 struct Geom {
   uint8_t* base;
   uint64_t tile_bytes;
@@ -42,7 +44,10 @@ constexpr int kAttnPartTokens = kAttnBlock * kAttnWaves * kAttnBlocksPerWave;  /
 
 inline uint64_t tile_bytes_for(int dtype, uint32_t block_size, uint32_t head_dim) {
   uint64_t e = (uint64_t)block_size * head_dim;
-  uint64_t raw = dtype == kDtypeF32 ? e * 4 : dtype == kDtypeF16 ? e * 2 : e + (e / 32) * 2;
+  // F16 K tiles store runs of 8 dims, so head_dim is padded to a multiple of 8.
+  uint64_t raw = dtype == kDtypeF32 ? e * 4
+                 : dtype == kDtypeF16 ? (uint64_t)block_size * ((head_dim + 7) / 8 * 8) * 2
+                                      : e + (e / 32) * 2;
   return (raw + 15) / 16 * 16;
 }
 
@@ -64,6 +69,33 @@ hipError_t launch_device_copy(void* dst, const void* src, uint64_t bytes, hipStr
 
 // Returns hipErrorInvalidValue when no kernel is instantiated for the shape.
 bool attention_supported(int dtype, uint32_t head_dim, uint32_t group);
+// F16 decode attention on the matrix cores (fkv_attention_mfma.hip); head_dim 64
+// or 128, any group size 1..16.
+hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads,
+                                 const float* q, float* out, const int32_t* tables,
+                                 uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
+                                 uint32_t max_splits, uint32_t split_tokens, float scale,
+                                 float* ws_o, float* ws_ml, hipStream_t s);
+// F16 decode attention, persistent schedule (fkv_attention_mfma.hip): n_waves
+// waves share the flattened (sequence, KV head, block) list equally; needs
+// 1 <= n_seqs <= kStreamMaxSeqs (the LDS prefix table). ws_pre holds n_seqs + 1
+// uint32; ws_o / ws_ml hold (n_waves + n_seqs * n_kv_heads) partial slots of G
+// heads x (head_dim | 2) floats.
+constexpr uint32_t kStreamMaxSeqs = 8192;
+bool stream_attention_supported(uint32_t n_seqs);
+// Waves of a full-occupancy stream launch on the current device (0: unavailable).
+uint32_t stream_attention_waves(uint32_t head_dim, uint32_t n_seqs);
+hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_heads,
+                                   const float* q, float* out, const int32_t* tables,
+                                   uint32_t max_blocks, const int32_t* ctx_lens,
+                                   uint32_t n_seqs, float scale, uint32_t n_waves,
+                                   uint32_t* ws_pre, float* ws_o, float* ws_ml, hipStream_t s);
+// Merges split partials (m, l, o) per (sequence, query head) into out.
+hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
+                                    uint32_t n_seqs, uint32_t n_heads, uint32_t max_blocks,
+                                    uint32_t max_splits, uint32_t split_tokens,
+                                    const float* ws_o, const float* ws_ml, float* out,
+                                    hipStream_t s);
 hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
                                    const float* q, float* out, const int32_t* tables,
                                    uint32_t max_blocks, const int32_t* ctx_lens,

@@ -56,14 +56,13 @@ __device__ __forceinline__ uint32_t q8_quantize(const float (&x)[32], int roundi
 // Append (paged KvPool::append_layer)
 // ---------------------------------------------------------------------------
 
-// F32/F16 storage, head_dim % 8 == 0, 16-byte aligned k/v: one thread moves 8
-// values of one (token, kv, head) row (32 B f32 in, 16 B f16 or 32 B f32 out).
-template <int DT>
-__global__ void __launch_bounds__(256) append_vec8_kernel(Geom g, uint32_t layer,
-                                                          const float* __restrict__ k,
-                                                          const float* __restrict__ v,
-                                                          const int64_t* __restrict__ slots,
-                                                          uint32_t n_tokens) {
+// F32 storage, head_dim % 8 == 0, 16-byte aligned k/v: one thread moves 8
+// values of one (token, kv, head) row (32 B in, 32 B out).
+__global__ void __launch_bounds__(256) append_f32_kernel(Geom g, uint32_t layer,
+                                                         const float* __restrict__ k,
+                                                         const float* __restrict__ v,
+                                                         const int64_t* __restrict__ slots,
+                                                         uint32_t n_tokens) {
   const uint32_t cpr = g.head_dim / 8;
   const uint32_t cph = g.n_kv_heads * cpr;
   const uint64_t total = (uint64_t)n_tokens * 2u * cph;
@@ -80,24 +79,71 @@ __global__ void __launch_bounds__(256) append_vec8_kernel(Geom g, uint32_t layer
       continue;
     }
     const float* src = (kv ? v : k) + ((uint64_t)token * g.n_kv_heads + h) * g.head_dim + c * 8u;
-    float4 a = *(const float4*)src;
-    float4 b = *(const float4*)(src + 4);
-    uint64_t blk = (uint64_t)slot / g.block_size;
-    uint32_t off = (uint32_t)((uint64_t)slot % g.block_size);
-    uint8_t* tile = tile_ptr(g, blk, layer, kv, h);
-    if constexpr (DT == kDtypeF16) {
-      uint4 o;
-      o.x = encode_f16(a.x, g.rounding) | (encode_f16(a.y, g.rounding) << 16);
-      o.y = encode_f16(a.z, g.rounding) | (encode_f16(a.w, g.rounding) << 16);
-      o.z = encode_f16(b.x, g.rounding) | (encode_f16(b.y, g.rounding) << 16);
-      o.w = encode_f16(b.z, g.rounding) | (encode_f16(b.w, g.rounding) << 16);
-      *(uint4*)(tile + ((uint64_t)off * g.head_dim + c * 8u) * 2u) = o;
-    } else {
-      float4* dst = (float4*)(tile + ((uint64_t)off * g.head_dim + c * 8u) * 4u);
-      dst[0] = a;
-      dst[1] = b;
-    }
+    uint8_t* tile = tile_ptr(g, (uint64_t)slot / g.block_size, layer, kv, h);
+    float4* dst = (float4*)(tile + (((uint64_t)slot % g.block_size) * g.head_dim + c * 8u) * 4u);
+    dst[0] = *(const float4*)src;
+    dst[1] = *(const float4*)(src + 4);
   }
+}
+
+// F16 storage, head_dim % 16 == 0, 16-byte aligned k/v. Workgroups [0, k_groups)
+// write K: one thread per 8 dims of a (token, head) row, one 16-byte store into
+// run c of the [D/8][B][8] tile. The rest write V into the [D][B] tile: one wave
+// per (16 input tokens, head, 16 dims), lane (t, g) holding dims 4g..4g+3 of
+// token t, so each 2-byte store instruction fills whole 32-byte dim rows when
+// the 16 tokens sit at consecutive offsets of one block (prefill), and is still
+// exact for any other slot mapping.
+__global__ void __launch_bounds__(256) append_f16_kernel(Geom g, uint32_t layer,
+                                                         const float* __restrict__ k,
+                                                         const float* __restrict__ v,
+                                                         const int64_t* __restrict__ slots,
+                                                         uint32_t n_tokens, uint32_t k_groups) {
+  const uint32_t D = g.head_dim, Bs = g.block_size;
+  const uint64_t cap = g.num_blocks * Bs;
+  if (blockIdx.x < k_groups) {
+    const uint32_t cpr = D / 8, cph = g.n_kv_heads * cpr;
+    const uint64_t u = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+    if (u >= (uint64_t)n_tokens * cph) return;
+    const uint32_t token = (uint32_t)(u / cph), r2 = (uint32_t)(u % cph);
+    const uint32_t h = r2 / cpr, c = r2 % cpr;
+    const int64_t slot = slots[token];
+    if (slot < 0) return;
+    if ((uint64_t)slot >= cap) {
+      if (r2 == 0) raise_fault(g.fault, kFaultSlot);
+      return;
+    }
+    const float* src = k + ((uint64_t)token * g.n_kv_heads + h) * D + c * 8u;
+    const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
+    uint8_t* tile = tile_ptr(g, (uint64_t)slot / Bs, layer, 0, h);
+    *(uint4*)(tile + ((uint64_t)c * Bs + (uint64_t)slot % Bs) * 16u) =
+        make_uint4(encode_f16(a.x, g.rounding) | (encode_f16(a.y, g.rounding) << 16),
+                   encode_f16(a.z, g.rounding) | (encode_f16(a.w, g.rounding) << 16),
+                   encode_f16(b.x, g.rounding) | (encode_f16(b.y, g.rounding) << 16),
+                   encode_f16(b.z, g.rounding) | (encode_f16(b.w, g.rounding) << 16));
+    return;
+  }
+  const uint32_t dgs = D / 16;  // 16-dim groups per head
+  const uint64_t wv = ((uint64_t)(blockIdx.x - k_groups) * 256u + threadIdx.x) / 64u;
+  const uint32_t lane = threadIdx.x % 64u, t = lane % 16u, grp = lane / 16u;
+  const uint64_t tb = wv / ((uint64_t)g.n_kv_heads * dgs);
+  const uint32_t rem = (uint32_t)(wv % ((uint64_t)g.n_kv_heads * dgs));
+  const uint32_t h = rem / dgs, dg = rem % dgs;
+  const uint64_t token = tb * 16u + t;
+  if (token >= n_tokens) return;
+  const int64_t slot = slots[token];
+  if (slot < 0) return;
+  if ((uint64_t)slot >= cap) {
+    if (rem == 0 && grp == 0) raise_fault(g.fault, kFaultSlot);
+    return;
+  }
+  const uint32_t d0 = dg * 16u + grp * 4u;
+  const float4 x = *(const float4*)(v + (token * g.n_kv_heads + h) * D + d0);
+  uint16_t* vt = (uint16_t*)tile_ptr(g, (uint64_t)slot / Bs, layer, 1, h) + (uint64_t)d0 * Bs +
+                 (uint64_t)slot % Bs;
+  vt[0] = (uint16_t)encode_f16(x.x, g.rounding);
+  vt[Bs] = (uint16_t)encode_f16(x.y, g.rounding);
+  vt[2 * Bs] = (uint16_t)encode_f16(x.z, g.rounding);
+  vt[3 * Bs] = (uint16_t)encode_f16(x.w, g.rounding);
 }
 
 // Any head_dim, F32/F16 storage: one element per thread.
@@ -123,11 +169,13 @@ __global__ void __launch_bounds__(256) append_scalar_kernel(Geom g, uint32_t lay
     }
     float x = (kv ? v : k)[(uint64_t)token * per_kv + e];
     uint8_t* tile = tile_ptr(g, (uint64_t)slot / g.block_size, layer, kv, h);
-    uint64_t idx = ((uint64_t)slot % g.block_size) * D + d;
+    const uint64_t off = (uint64_t)slot % g.block_size;
     if (g.dtype == kDtypeF16)
-      ((uint16_t*)tile)[idx] = (uint16_t)encode_f16(x, g.rounding);
+      ((uint16_t*)tile)[kv ? (uint64_t)d * g.block_size + off
+                           : ((uint64_t)(d / 8) * g.block_size + off) * 8 + d % 8] =
+          (uint16_t)encode_f16(x, g.rounding);
     else
-      ((float*)tile)[idx] = x;
+      ((float*)tile)[off * D + d] = x;
   }
 }
 
@@ -204,8 +252,20 @@ __device__ __forceinline__ void gather_chunk(const Geom& g, uint32_t layer, uint
     }
     return;
   }
-  if (g.dtype == kDtypeF16) {
-    const uint16_t* src = (const uint16_t*)tile + (uint64_t)off * D + c * 8u;
+  if (g.dtype == kDtypeF16 && kv == 1) {  // V tile [D][B]: dims are rows
+    const uint16_t* src = (const uint16_t*)tile + (uint64_t)c * 8u * g.block_size + off;
+    const uint32_t B = g.block_size;
+    if (format == 0) {
+      float* o = (float*)dst_row + c * 8u;
+      for (int j = 0; j < 8; j++) o[j] = f16_bits_to_f32(src[j * B]);
+    } else {
+      uint16_t* o = (uint16_t*)dst_row + c * 8u;
+      for (int j = 0; j < 8; j++) o[j] = src[j * B];
+    }
+    return;
+  }
+  if (g.dtype == kDtypeF16) {  // K tile [D/8][B][8]: run c of token off
+    const uint16_t* src = (const uint16_t*)tile + ((uint64_t)c * g.block_size + off) * 8u;
     if (format == 0) {
       float* o = (float*)dst_row + c * 8u;
       if (aligned) {
@@ -400,12 +460,17 @@ hipError_t launch_append(const Geom& g, uint32_t layer, const float* k, const fl
       append_q8_kernel<true><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
     else
       append_q8_kernel<false><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
-  } else if (g.head_dim % 8 == 0 && aligned) {
+  } else if (g.dtype == kDtypeF16 && g.head_dim % 16 == 0 && aligned) {
+    const uint64_t k_threads = (uint64_t)n_tokens * g.n_kv_heads * (g.head_dim / 8u);
+    const uint64_t v_waves =
+        ((uint64_t)n_tokens + 15u) / 16u * g.n_kv_heads * (g.head_dim / 16u);
+    const uint64_t k_groups = (k_threads + 255u) / 256u, v_groups = (v_waves + 3u) / 4u;
+    if (k_groups + v_groups > 0x7fffffffull) return hipErrorInvalidValue;
+    append_f16_kernel<<<(uint32_t)(k_groups + v_groups), 256, 0, s>>>(g, layer, k, v, slots,
+                                                                      n_tokens, (uint32_t)k_groups);
+  } else if (g.dtype == kDtypeF32 && g.head_dim % 8 == 0 && aligned) {
     uint64_t units = (uint64_t)n_tokens * 2u * g.n_kv_heads * (g.head_dim / 8u);
-    if (g.dtype == kDtypeF16)
-      append_vec8_kernel<kDtypeF16><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
-    else
-      append_vec8_kernel<kDtypeF32><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
+    append_f32_kernel<<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
   } else {
     uint64_t units = (uint64_t)n_tokens * 2u * g.n_kv_heads * g.head_dim;
     append_scalar_kernel<<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
@@ -435,11 +500,13 @@ __global__ void __launch_bounds__(256) gather_slots_scalar_kernel(Geom g, uint32
       continue;
     }
     const uint8_t* tile = tile_ptr(g, (uint64_t)slot / g.block_size, layer, kv, h);
-    uint64_t idx = ((uint64_t)slot % g.block_size) * D + d;
+    const uint64_t off = (uint64_t)slot % g.block_size;
+    uint64_t idx = off * D + d;
     uint8_t* o = kv ? out_v : out_k;
     uint64_t oi = (uint64_t)token * per_kv + e;
     if (g.dtype == kDtypeF16) {
-      uint16_t bits = ((const uint16_t*)tile)[idx];
+      uint16_t bits = ((const uint16_t*)tile)[kv ? (uint64_t)d * g.block_size + off
+                                                 : ((uint64_t)(d / 8) * g.block_size + off) * 8 + d % 8];
       if (format == 0) ((float*)o)[oi] = f16_bits_to_f32(bits);
       else ((uint16_t*)o)[oi] = bits;
     } else {

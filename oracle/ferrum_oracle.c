@@ -21,6 +21,8 @@
 
 /* ------------------------------------------------------------------------- */
 /* Layout (include/ferrum_kv.h): pool[block][layer][kv][head][tile].          */
+/* F32 tiles are token-major [B][D]. F16 K tiles are [D/8][B][8] and F16 V     */
+/* tiles are [D][B]: the operand orders of the MFMA decode kernel.             */
 /* ------------------------------------------------------------------------- */
 
 /* Tiles are padded to a multiple of 16 bytes so every tile starts 16-byte aligned. */
@@ -28,7 +30,7 @@ uint64_t fo_tile_bytes(const fo_layout* l) {
   uint64_t elems = (uint64_t)l->block_size * l->head_dim, raw;
   switch (l->dtype) {
     case 0: raw = elems * 4; break;
-    case 1: raw = elems * 2; break;
+    case 1: raw = (uint64_t)l->block_size * ((l->head_dim + 7) / 8 * 8) * 2; break;  /* K runs of 8 */
     case 8: raw = elems + (elems / 32) * 2; break;
     default: return 0;
   }
@@ -216,14 +218,21 @@ void fo_softmax(float* x, uint64_t n) {
 /* Paged pool image operations                                                 */
 /* ------------------------------------------------------------------------- */
 
-/* Encode one row of D values into token `off` of a tile. */
-static void encode_row(const fo_layout* l, uint8_t* tile, uint32_t off, const float* src) {
+/* Element index of (token off, dim d) inside an F16 tile of kind kv:
+ * K [D/8][B][8] (16-byte runs of 8 dims, token-contiguous per run), V [D][B]. */
+static uint64_t f16_index(const fo_layout* l, int kv, uint32_t off, uint32_t d) {
+  if (kv) return (uint64_t)d * l->block_size + off;
+  return ((uint64_t)(d / 8) * l->block_size + off) * 8 + d % 8;
+}
+
+/* Encode one row of D values into token `off` of a tile of kind kv (0 K, 1 V). */
+static void encode_row(const fo_layout* l, int kv, uint8_t* tile, uint32_t off, const float* src) {
   uint32_t D = l->head_dim;
   if (l->dtype == 0) {
     memcpy(tile + (uint64_t)off * D * 4, src, (size_t)D * 4);
   } else if (l->dtype == 1) {
-    uint16_t* dst = (uint16_t*)(tile + (uint64_t)off * D * 2);
-    for (uint32_t d = 0; d < D; d++) dst[d] = fo_f32_to_f16(src[d], l->rounding);
+    uint16_t* dst = (uint16_t*)tile;
+    for (uint32_t d = 0; d < D; d++) dst[f16_index(l, kv, off, d)] = fo_f32_to_f16(src[d], l->rounding);
   } else {
     uint8_t* qs = tile + (uint64_t)off * D;
     uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
@@ -238,14 +247,14 @@ static void encode_row(const fo_layout* l, uint8_t* tile, uint32_t off, const fl
   }
 }
 
-/* Decode token `off` of a tile to f32 (dtype.rs:135-154 / scalar.rs:261-279). */
-static void decode_row(const fo_layout* l, const uint8_t* tile, uint32_t off, float* dst) {
+/* Decode token `off` of a tile of kind kv to f32 (dtype.rs:135-154 / scalar.rs:261-279). */
+static void decode_row(const fo_layout* l, int kv, const uint8_t* tile, uint32_t off, float* dst) {
   uint32_t D = l->head_dim;
   if (l->dtype == 0) {
     memcpy(dst, tile + (uint64_t)off * D * 4, (size_t)D * 4);
   } else if (l->dtype == 1) {
-    const uint16_t* src = (const uint16_t*)(tile + (uint64_t)off * D * 2);
-    for (uint32_t d = 0; d < D; d++) dst[d] = fo_f16_to_f32(src[d]);
+    const uint16_t* src = (const uint16_t*)tile;
+    for (uint32_t d = 0; d < D; d++) dst[d] = fo_f16_to_f32(src[f16_index(l, kv, off, d)]);
   } else {
     const uint8_t* qs = tile + (uint64_t)off * D;
     const uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
@@ -256,13 +265,15 @@ static void decode_row(const fo_layout* l, const uint8_t* tile, uint32_t off, fl
   }
 }
 
-/* Raw storage bytes of one row; Q8_0 is re-packed into Ferrum's 34-byte blocks. */
-static void raw_row(const fo_layout* l, const uint8_t* tile, uint32_t off, uint8_t* dst) {
+/* Raw storage values of one token row (binary16 bits in dim order for F16); Q8_0 is
+ * re-packed into Ferrum's 34-byte blocks. */
+static void raw_row(const fo_layout* l, int kv, const uint8_t* tile, uint32_t off, uint8_t* dst) {
   uint32_t D = l->head_dim;
   if (l->dtype == 0) {
     memcpy(dst, tile + (uint64_t)off * D * 4, (size_t)D * 4);
   } else if (l->dtype == 1) {
-    memcpy(dst, tile + (uint64_t)off * D * 2, (size_t)D * 2);
+    const uint16_t* src = (const uint16_t*)tile;
+    for (uint32_t d = 0; d < D; d++) ((uint16_t*)dst)[d] = src[f16_index(l, kv, off, d)];
   } else {
     const uint8_t* qs = tile + (uint64_t)off * D;
     const uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
@@ -294,8 +305,8 @@ uint64_t fo_append(const fo_layout* l, uint8_t* pool, uint32_t layer, const floa
     uint64_t blk = (uint64_t)s / l->block_size;
     uint32_t off = (uint32_t)((uint64_t)s % l->block_size);
     for (uint32_t h = 0; h < l->n_kv_heads; h++) {
-      encode_row(l, pool + tile_offset(l, blk, layer, 0, h), off, k + i * row + h * l->head_dim);
-      encode_row(l, pool + tile_offset(l, blk, layer, 1, h), off, v + i * row + h * l->head_dim);
+      encode_row(l, 0, pool + tile_offset(l, blk, layer, 0, h), off, k + i * row + h * l->head_dim);
+      encode_row(l, 1, pool + tile_offset(l, blk, layer, 1, h), off, v + i * row + h * l->head_dim);
     }
   }
   return skipped;
@@ -307,11 +318,11 @@ static void gather_one(const fo_layout* l, const uint8_t* pool, uint32_t layer, 
     const uint8_t* tk = pool + tile_offset(l, blk, layer, 0, h);
     const uint8_t* tv = pool + tile_offset(l, blk, layer, 1, h);
     if (format == 0) {
-      decode_row(l, tk, off, (float*)ok + (uint64_t)h * l->head_dim);
-      decode_row(l, tv, off, (float*)ov + (uint64_t)h * l->head_dim);
+      decode_row(l, 0, tk, off, (float*)ok + (uint64_t)h * l->head_dim);
+      decode_row(l, 1, tv, off, (float*)ov + (uint64_t)h * l->head_dim);
     } else {
-      raw_row(l, tk, off, ok + h * raw_row_bytes(l));
-      raw_row(l, tv, off, ov + h * raw_row_bytes(l));
+      raw_row(l, 0, tk, off, ok + h * raw_row_bytes(l));
+      raw_row(l, 1, tv, off, ov + h * raw_row_bytes(l));
     }
   }
 }
@@ -379,14 +390,14 @@ static void attention_one(const fo_layout* l, const uint8_t* pool, uint32_t laye
     if (ctx <= 0) continue; /* empty: softmax_max is -inf, non-finite -> zeros */
     for (int32_t p = 0; p < ctx; p++) {
       int32_t blk = table[(uint32_t)p / l->block_size];
-      decode_row(l, pool + tile_offset(l, (uint64_t)blk, layer, 0, kvh),
+      decode_row(l, 0, pool + tile_offset(l, (uint64_t)blk, layer, 0, kvh),
                  (uint32_t)p % l->block_size, row);
       scores[p] = fo_dot(qh, row, D) * scale;
     }
     fo_softmax(scores, (uint64_t)ctx);
     for (int32_t p = 0; p < ctx; p++) {
       int32_t blk = table[(uint32_t)p / l->block_size];
-      decode_row(l, pool + tile_offset(l, (uint64_t)blk, layer, 1, kvh),
+      decode_row(l, 1, pool + tile_offset(l, (uint64_t)blk, layer, 1, kvh),
                  (uint32_t)p % l->block_size, row);
       float w = scores[p];
       for (uint32_t d = 0; d < D; d++) oh[d] += w * row[d];
@@ -521,13 +532,14 @@ AVX2_FN void fo_avx2_softmax(float* x, uint64_t n) {
 
 /* Row decode with the x86 conversions the AVX2 backend would use: F16C for
  * binary16 (exact), and avx2.rs:660-694's i8 -> f32 * scale for Q8_0. */
-AVX2_FN static void decode_row_avx2(const fo_layout* l, const uint8_t* tile, uint32_t off,
+AVX2_FN static void decode_row_avx2(const fo_layout* l, int kv, const uint8_t* tile, uint32_t off,
                                     float* dst) {
   uint32_t D = l->head_dim;
-  if (l->dtype == 1 && D % 8 == 0) {
-    const uint16_t* src = (const uint16_t*)(tile + (uint64_t)off * D * 2);
+  if (l->dtype == 1 && D % 8 == 0 && kv == 0) {
+    const uint16_t* src = (const uint16_t*)tile + (uint64_t)off * 8;  /* K [D/8][B][8] */
     for (uint32_t d = 0; d < D; d += 8)
-      _mm256_storeu_ps(dst + d, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(src + d))));
+      _mm256_storeu_ps(dst + d, _mm256_cvtph_ps(_mm_loadu_si128(
+                                    (const __m128i*)(src + (uint64_t)(d / 8) * l->block_size * 8))));
   } else if (l->dtype == 8) {
     const uint8_t* qs = tile + (uint64_t)off * D;
     const uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
@@ -545,7 +557,7 @@ AVX2_FN static void decode_row_avx2(const fo_layout* l, const uint8_t* tile, uin
       }
     }
   } else {
-    decode_row(l, tile, off, dst);
+    decode_row(l, kv, tile, off, dst);
   }
 }
 
@@ -580,14 +592,14 @@ AVX2_FN void fo_avx2_attention(const fo_layout* l, const uint8_t* pool, uint32_t
       if (ctx <= 0) continue;
       for (int32_t p = 0; p < ctx; p++) {
         int32_t blk = table[(uint32_t)p / l->block_size];
-        decode_row_avx2(l, pool + tile_offset(l, (uint64_t)blk, layer, 0, kvh),
+        decode_row_avx2(l, 0, pool + tile_offset(l, (uint64_t)blk, layer, 0, kvh),
                         (uint32_t)p % l->block_size, row);
         scores[p] = fo_avx2_dot(qh, row, D) * scale;
       }
       fo_avx2_softmax(scores, (uint64_t)ctx);
       for (int32_t p = 0; p < ctx; p++) {
         int32_t blk = table[(uint32_t)p / l->block_size];
-        decode_row_avx2(l, pool + tile_offset(l, (uint64_t)blk, layer, 1, kvh),
+        decode_row_avx2(l, 1, pool + tile_offset(l, (uint64_t)blk, layer, 1, kvh),
                         (uint32_t)p % l->block_size, row);
         __m256 w = _mm256_set1_ps(scores[p]);
         uint32_t d = 0;

@@ -49,11 +49,25 @@ def _run(pool, layer, q, tab, ctxs):
 
 
 SHAPES = [(1, 128, 4), (1, 128, 8), (1, 64, 8), (1, 128, 1), (1, 64, 2), (1, 128, 16),
+          (1, 128, 3), (1, 64, 5), (1, 64, 16), (1, 128, 12),
           (0, 128, 4), (0, 64, 8), (8, 128, 4), (8, 128, 8), (8, 64, 1)]
 
 
+@pytest.fixture(params=["split", "stream"])
+def f16_schedule(request, monkeypatch):
+    """F16 runs on the MFMA split kernel by default; FKV_ATTN_MODE=stream selects
+    the persistent schedule. Both must meet the same bar."""
+    if request.param == "stream":
+        monkeypatch.setenv("FKV_ATTN_MODE", "stream")
+    else:
+        monkeypatch.delenv("FKV_ATTN_MODE", raising=False)
+    return request.param
+
+
 @pytest.mark.parametrize("dtype,d,g", SHAPES)
-def test_attention_matches_oracle(dtype, d, g):
+def test_attention_matches_oracle(dtype, d, g, f16_schedule):
+    if dtype != 1 and f16_schedule == "stream":
+        pytest.skip("the schedule switch only applies to F16 storage")
     import ferrum_amd as fa
     from oracle import ref
     hkv = 2
@@ -77,7 +91,7 @@ def test_attention_matches_oracle(dtype, d, g):
     print(f"max abs err vs oracle {err:.2e}")
 
 
-def test_attention_long_context_uses_combine():
+def test_attention_long_context_uses_combine(f16_schedule):
     import ferrum_amd as fa
     from oracle import ref
     ctxs = [20000, 3, 4097]
@@ -110,8 +124,9 @@ def test_attention_zero_context_gives_zeros():
     assert np.all(np.isfinite(o[1])) and np.any(o[1] != 0.0)
 
 
+@pytest.mark.parametrize("dtype", [0, 1])
 @pytest.mark.parametrize("ctx", [40, 600])
-def test_attention_non_finite_scores(ctx):
+def test_attention_non_finite_scores(ctx, dtype):
     """One K row is (+inf, 0, ..., 0). Head 0 (q0 > 0) scores it +inf: a non-finite
     max gives zeros (scalar.rs:127-130). Head 1 (q0 < 0) scores it -inf: the token
     only drops out. Head 2 (q0 == 0) scores it 0*inf = NaN with a finite max: the
@@ -120,7 +135,7 @@ def test_attention_non_finite_scores(ctx):
     from oracle import ref
     d, hkv, g = 64, 1, 4
     nb = (ctx + 15) // 16
-    pool, layout = make_pools(1, hkv, d, nb + 2, dtype=0)
+    pool, layout = make_pools(1, hkv, d, nb + 2, dtype=dtype)
     pool.fill(0)
     rng = np.random.default_rng(0)
     k = rng.standard_normal((ctx, hkv, d), dtype=np.float32)
