@@ -82,15 +82,17 @@ struct Lane {
   bool real;  // col < G: this lane's score column is a real query head
 };
 
-// q of one (sequence, KV head) group -> QK B operand: per-head power-of-two
-// scaling (the head's largest |q * scale * log2 e| lands in [2^14, 2^15), far
-// from f16 overflow), then an f16 hi + lo split. hscale undoes the scaling.
+// q rows -> QK B operand. Lane (col, grp) reads dims c*32 + grp*8 .. +7 of the
+// query row of column col (qrow: any readable row for padding columns). Each row
+// gets a power-of-two scaling (its largest |q * scale * log2 e| lands in
+// [2^14, 2^15), far from f16 overflow), then an f16 hi + lo split; hscale undoes
+// the scaling.
 template <int D>
-__device__ __forceinline__ void prep_q(const float* qg, const Lane& ln, float qscale,
+__device__ __forceinline__ void prep_q(const float* qrow, const Lane& ln, float qscale,
                                        f16x8 (&qh)[D / 32], f16x8 (&ql)[D / 32],
                                        float& hscale) {
   constexpr int NC = D / 32;
-  const float* qb = qg + (ln.real ? ln.col : 0) * D + ln.grp * 8;
+  const float* qb = qrow + ln.grp * 8;
   float x[NC][8];
   float amax = 0.0f;
 #pragma unroll
@@ -410,7 +412,8 @@ __attribute__((amdgpu_waves_per_eu(FKV_STREAM_WAVES_PER_EU, 8))) attn_mfma_strea
     const uint64_t stop = seg0 + nb < b_end ? seg0 + nb : b_end;
     int32_t end = __builtin_amdgcn_readfirstlane(ctx_lens[seq]);
     end = end < 0 ? 0 : (end > cap ? cap : end);
-    prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G) * D, ln, qscale, qh, ql, hscale);
+    prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D, ln,
+            qscale, qh, ql, hscale);
     st.reset();
 
     for (; i < stop; i++) {
@@ -583,8 +586,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(
 
   f16x8 qh[NC], ql[NC];
   float hscale;
-  prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G) * D, ln, scale * kLog2e, qh, ql,
-            hscale);
+  prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D, ln,
+            scale * kLog2e, qh, ql, hscale);
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
   const int32_t blk0 = s0 / B;
@@ -685,6 +688,114 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Chunked-prefill attention
+// ---------------------------------------------------------------------------
+//
+// The reference prefills token by token (crates/model/src/llama.rs:363-378), each
+// token running the attention loop of :220-247 over positions 0 ..= its own.
+// Here the chunk's K/V are already in the pool, and the 16 MFMA columns carry
+// query rows instead of heads: column c of a tile is (token c / G, head c % G)
+// for 16 / G consecutive query tokens, each with its own causal end. QK, the
+// softmax reductions (over the 4 lanes of a column) and PV are the decode step
+// unchanged. One wave per tile; 4 tiles per workgroup, no LDS.
+template <int D>
+__global__ void __launch_bounds__(256) attn_prefill_kernel(
+    Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
+    float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
+    const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ q_lens,
+    const int64_t* __restrict__ q_offsets, float scale) {
+  constexpr int NC = D / 32, NM = D / 16;
+  const uint32_t sk = blockIdx.x;
+  const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int32_t tile = (int32_t)blockIdx.y * kAttnWaves + wave;
+  const int32_t T = 16 / (int32_t)G;  // query tokens per tile
+  const int32_t cap = (int32_t)(max_blocks * B);
+  int32_t ctx = ctx_lens[seq];
+  int32_t ql = q_lens[seq];
+  if (ctx < 0 || ctx > cap || ql < 0 || ql > (ctx < 0 ? 0 : (ctx > cap ? cap : ctx))) {
+    if (blockIdx.y == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
+    ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+    ql = ql < 0 ? 0 : (ql > ctx ? ctx : ql);
+  }
+  if (tile * T >= ql) return;
+  const int32_t p0 = ctx - ql;  // position of query 0
+
+  Lane ln;
+  ln.lane = threadIdx.x & 63;
+  ln.col = ln.lane & 15;
+  ln.grp = ln.lane >> 4;
+  const int32_t jcol = tile * T + ln.col / (int32_t)G;  // query token of this column
+  ln.real = ln.col < T * (int32_t)G && jcol < ql;
+  const int32_t end_col = p0 + jcol + 1;                // causal end of the column
+  const int32_t jlast = tile * T + T - 1 < ql - 1 ? tile * T + T - 1 : ql - 1;
+  const int32_t end_max = p0 + jlast + 1;              // furthest end in the tile
+  const int32_t nblk = (end_max + B - 1) / B;
+  const int64_t qrow0 = q_offsets[seq];
+  auto row_of = [&](int32_t colv) {  // q/out row of column colv (clamped for padding)
+    const int32_t j = tile * T + colv / (int32_t)G;
+    const int32_t jj = j < ql ? j : ql - 1;
+    return ((uint64_t)(qrow0 + jj) * n_heads + (uint64_t)kvh * G + (uint64_t)(colv % (int32_t)G)) * D;
+  };
+
+  const int32_t* table = tables + (uint64_t)seq * max_blocks;
+  auto phys = [&](int32_t j, bool& ok) {
+    const int32_t p = __builtin_amdgcn_readfirstlane(table[j]);
+    ok = p >= 0 && (uint64_t)p < g.num_blocks;
+    if (!ok && ln.lane == 0) raise_fault(g.fault, kFaultBlock);
+    return ok ? (uint64_t)p : 0;
+  };
+
+  uint4 kr[NC];
+  u32x2_t vr[NM];
+  bool live = false;
+  {
+    const uint64_t p = phys(0, live);
+    load_k<D>(tile_ptr(g, p, layer, 0, kvh), ln, kr);
+    load_v<D>(tile_ptr(g, p, layer, 1, kvh), ln, vr);
+  }
+  f16x8 qh[NC], qlo[NC];
+  float hscale;
+  prep_q<D>(q + row_of(ln.real ? ln.col : 0), ln, scale * kLog2e, qh, qlo, hscale);
+  Accum<D> st;
+  st.reset();
+
+  for (int32_t j = 0; j < nblk; j++) {
+    const bool more = j + 1 < nblk;
+    const int32_t t0 = j * B;
+    float s[4];
+    qk_block<D>(kr, qh, qlo, hscale, ln, live, t0, end_col, s);
+    const bool cur_live = live;
+    uint64_t np = 0;
+    if (more) {
+      np = phys(j + 1, live);
+      load_k<D>(tile_ptr(g, np, layer, 0, kvh), ln, kr);
+    }
+    const f16x4 pw = softmax_block<D>(s, ln, st);
+    if (cur_live) pv_block<D>(vr, pw, ln, t0, end_max, st);
+    if (more) load_v<D>(tile_ptr(g, np, layer, 1, kvh), ln, vr);
+  }
+
+  float lsum = st.l_part;
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  // accumulator row r of this lane is column grp*4 + r; its M and L live in lane grp*4 + r
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int c = ln.grp * 4 + r;
+    const float M = __shfl(st.m_ref, c);
+    const float inv = 1.0f / __shfl(lsum, c);
+    const int32_t jc = tile * T + c / (int32_t)G;
+    if (c < T * (int32_t)G && jc < ql) {
+      float* o = out + row_of(c);
+#pragma unroll
+      for (int m = 0; m < NM; m++)
+        o[m * 16 + ln.col] = __builtin_isfinite(M) ? st.acc[m][r] * inv : 0.0f;
+    }
+  }
+}
+
 // Workgroups of the stream kernel one CU holds at once (0 if it cannot launch).
 template <int D>
 int stream_wgs_per_cu(size_t lds_bytes) {
@@ -737,6 +848,25 @@ hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_hea
   else
     attn_stream_combine_kernel<64><<<cgrid, 256, 0, s>>>(n_seqs, g.n_kv_heads, G, n_waves,
                                                          ws_pre, ws_o, ws_ml, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
+                                    const float* q, float* out, const int32_t* tables,
+                                    uint32_t max_blocks, const int32_t* ctx_lens,
+                                    const int32_t* q_lens, const int64_t* q_offsets,
+                                    uint32_t n_seqs, uint32_t max_q_len, float scale,
+                                    hipStream_t s) {
+  const uint32_t G = n_heads / g.n_kv_heads;
+  const uint32_t T = 16 / G;
+  const uint32_t tiles = (max_q_len + T - 1) / T;
+  dim3 grid(n_seqs * g.n_kv_heads, (tiles + kAttnWaves - 1) / kAttnWaves);
+  if (g.head_dim == 128)
+    attn_prefill_kernel<128><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
+                                                  ctx_lens, q_lens, q_offsets, scale);
+  else
+    attn_prefill_kernel<64><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
+                                                 ctx_lens, q_lens, q_offsets, scale);
   return hipGetLastError();
 }
 

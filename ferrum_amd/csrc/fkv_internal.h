@@ -90,6 +90,15 @@ hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_hea
                                    uint32_t max_blocks, const int32_t* ctx_lens,
                                    uint32_t n_seqs, float scale, uint32_t n_waves,
                                    uint32_t* ws_pre, float* ws_o, float* ws_ml, hipStream_t s);
+// F16 chunked-prefill attention (fkv_attention_mfma.hip): query i of sequence s
+// is at position ctx_lens[s] - q_lens[s] + i and attends causally; q/out rows of
+// sequence s start at q_offsets[s]. Needs G <= 16.
+hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
+                                    const float* q, float* out, const int32_t* tables,
+                                    uint32_t max_blocks, const int32_t* ctx_lens,
+                                    const int32_t* q_lens, const int64_t* q_offsets,
+                                    uint32_t n_seqs, uint32_t max_q_len, float scale,
+                                    hipStream_t s);
 // Merges split partials (m, l, o) per (sequence, query head) into out.
 hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
                                     uint32_t n_seqs, uint32_t n_heads, uint32_t max_blocks,

@@ -32,11 +32,17 @@
  *
  * HBM layout of a paged pool (one device allocation):
  *   pool[block][layer][kv (0=K,1=V)][kv_head][tile]
- *   tile (F32/F16): [block_size tokens][head_dim] elements
- *   tile (Q8_0)   : [block_size*head_dim int8 quants][block_size*head_dim/32 f16 scales]
- * A block therefore holds every layer of block_size consecutive tokens, and the
- * (block, layer, kv, head) tile is contiguous (4 KiB for f16, D=128, B=16).
- * Slot = block * block_size + offset_in_block (the vLLM slot-mapping convention).
+ *   tile (F32)   : [block_size tokens][head_dim] elements
+ *   tile (F16 K) : [head_dim/8][block_size][8]: 16-byte runs of 8 dims, token-
+ *                  contiguous per run (head_dim padded to a multiple of 8)
+ *   tile (F16 V) : [head_dim][block_size]: dim-major
+ *   tile (Q8_0)  : [block_size*head_dim int8 quants][block_size*head_dim/32 f16 scales]
+ * The F16 orders are the operand orders of the MFMA attention kernels: one load
+ * instruction reads 1 KiB of K or 512 B of V of consecutive bytes. A block holds
+ * every layer of block_size consecutive tokens, and the (block, layer, kv, head)
+ * tile is contiguous (4 KiB for f16, D=128, B=16). Slot = block * block_size +
+ * offset_in_block (the vLLM slot-mapping convention). The gather entry points
+ * return token rows whatever the tile order.
  */
 #ifndef FERRUM_KV_H
 #define FERRUM_KV_H
@@ -231,12 +237,14 @@ int32_t fkv_swap_in(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void
  * A non-finite maximum score gives zeros (kernels/src/scalar.rs:125-130).
  * q, out: device f32 [n_seqs][n_heads][head_dim]. block_tables: device int32
  * [n_seqs][max_blocks_per_seq]; ctx_lens: device int32 [n_seqs], each
- * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, g in {1,2,4,8,16}.
+ * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, and g <= 16 (F16,
+ * matrix cores), g in {1,2,4,8,16} (F32) or g in {1,2,4,8} (Q8_0).
  * workspace: device scratch of fkv_decode_attention_workspace_size() bytes
- * (split-context partials and per-(sequence, kv head) merge counters); it may
- * be NULL when that size is 0. It must be zero-filled once before its first
- * use; every call leaves it ready for the next. Calls that share one workspace
- * must not overlap (same stream, or ordered by events). */
+ * holding the split partials (running max, sum and unnormalised output per
+ * query head and context split) that the merge pass reads; it may be NULL when
+ * that size is 0 (every sequence fits one split) and needs no initialisation.
+ * Calls that share one workspace must not overlap (same stream, or ordered by
+ * events). */
 int32_t fkv_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
                                             uint32_t n_seqs, uint32_t max_ctx_len,
                                             uint64_t* bytes_out);
@@ -245,6 +253,25 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
                              uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
                              uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                              void* workspace, uint64_t workspace_bytes, void* stream);
+
+/* Chunked-prefill attention over F16 storage: the reference's token-by-token
+ * prefill (crates/model/src/llama.rs:363-378, each token running the attention
+ * loop of :220-247 over positions 0 ..= its own) for a chunk whose K/V are
+ * already appended. Sequence s has q_lens[s] new tokens at the end of its
+ * ctx_lens[s]-token context: query i sits at position ctx_lens[s] - q_lens[s] + i
+ * and attends to positions 0 ..= that position. q, out: device f32
+ * [rows][n_heads][head_dim]; sequence s's queries are rows q_offsets[s] ..
+ * q_offsets[s] + q_lens[s] - 1 (q_offsets: device int64). q_lens[s] = 1 is
+ * decode. Needs f16 KV, block_size 16, head_dim 64 or 128, g <= 16. K/V values
+ * of tokens that some queries of a 16-column tile must not see still enter the
+ * matrix product with weight 0, so a NaN/Inf V value inside the chunk reaches
+ * earlier queries of its tile. No workspace. */
+int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,
+                              float* out, const int32_t* block_tables,
+                              uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                              const int32_t* q_lens, const int64_t* q_offsets, uint32_t n_seqs,
+                              uint32_t max_q_len, uint32_t max_ctx_len, float scale,
+                              void* stream);
 
 /* Device-to-device byte copy with the same 16-byte vector kernel style as the
  * pool kernels; used to calibrate HBM counters and to measure copy bandwidth. */

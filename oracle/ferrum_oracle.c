@@ -421,6 +421,33 @@ void fo_attention(const fo_layout* l, const uint8_t* pool, uint32_t layer, uint3
   free(row);
 }
 
+/* Prefill, Llama::forward llama.rs:363-378: tokens run one at a time, and the
+ * token at position p attends to positions 0 ..= p (:220-247 with pos = p). The
+ * chunk of sequence s is its last q_lens[s] positions, already in the pool; its
+ * queries are rows q_offsets[s] .. of q and out. */
+void fo_prefill_attention(const fo_layout* l, const uint8_t* pool, uint32_t layer,
+                          uint32_t n_heads, const float* q, float* out,
+                          const int32_t* block_tables, uint32_t max_blocks,
+                          const int32_t* ctx_lens, const int32_t* q_lens,
+                          const int64_t* q_offsets, uint32_t n_seqs, float scale) {
+  int32_t maxctx = 1;
+  for (uint32_t s = 0; s < n_seqs; s++)
+    if (ctx_lens[s] > maxctx) maxctx = ctx_lens[s];
+  float* scores = (float*)malloc((size_t)maxctx * 4);
+  float* row = (float*)malloc((size_t)l->head_dim * 4);
+  uint64_t qs = (uint64_t)n_heads * l->head_dim;
+  for (uint32_t s = 0; s < n_seqs; s++) {
+    int32_t p0 = ctx_lens[s] - q_lens[s];
+    for (int32_t i = 0; i < q_lens[s]; i++) {
+      uint64_t r = (uint64_t)q_offsets[s] + (uint64_t)i;
+      attention_one(l, pool, layer, n_heads, q + r * qs, out + r * qs,
+                    block_tables + (uint64_t)s * max_blocks, p0 + i + 1, scale, scores, row);
+    }
+  }
+  free(scores);
+  free(row);
+}
+
 /* ------------------------------------------------------------------------- */
 /* AVX2 restatement (timed CPU baseline)                                       */
 /* ------------------------------------------------------------------------- */

@@ -24,6 +24,8 @@
  *   fo_dot, fo_softmax     KATs tests.rs:178-195, kernels_contract.rs:437-467
  *   fo_attention           numpy f64 brute force + closed forms (ctx=1, equal keys,
  *                          dominant key, non-finite max)
+ *   fo_prefill_attention   equals fo_attention run once per query position (the
+ *                          definition) and an f64 causal brute force
  *   fo_dense_*             the pool.rs:233-308 unit tests
  *   fo_avx2_*              bit-identity of dot to fo_dot (tests.rs:616-621);
  *                          attention within tolerance of fo_attention
@@ -79,6 +81,14 @@ void fo_copy_blocks(const fo_layout* l, uint8_t* pool, const int64_t* pairs, uin
 void fo_attention(const fo_layout* l, const uint8_t* pool, uint32_t layer, uint32_t n_heads,
                   const float* q, float* out, const int32_t* block_tables, uint32_t max_blocks,
                   const int32_t* ctx_lens, uint32_t n_seqs, float scale);
+
+/* Prefill: query i of sequence s at position ctx_lens[s] - q_lens[s] + i attends
+ * to positions 0 ..= that position (crates/model/src/llama.rs:363-378). */
+void fo_prefill_attention(const fo_layout* l, const uint8_t* pool, uint32_t layer,
+                          uint32_t n_heads, const float* q, float* out,
+                          const int32_t* block_tables, uint32_t max_blocks,
+                          const int32_t* ctx_lens, const int32_t* q_lens,
+                          const int64_t* q_offsets, uint32_t n_seqs, float scale);
 
 /* AVX2 restatement used as the timed CPU baseline (crates/kernels/src/avx2.rs). */
 int32_t fo_avx2_available(void);

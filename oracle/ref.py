@@ -43,6 +43,8 @@ _SIGS = {
     "fo_copy_blocks": (None, [c_void_p, c_void_p, c_void_p, u64]),
     "fo_attention": (None, [c_void_p, c_void_p, u32, u32, c_void_p, c_void_p, c_void_p, u32,
                             c_void_p, u32, ctypes.c_float]),
+    "fo_prefill_attention": (None, [c_void_p, c_void_p, u32, u32, c_void_p, c_void_p, c_void_p,
+                                    u32, c_void_p, c_void_p, c_void_p, u32, ctypes.c_float]),
     "fo_avx2_available": (i32, []),
     "fo_avx2_dot": (ctypes.c_float, [c_void_p, c_void_p, u64]),
     "fo_avx2_softmax": (None, [c_void_p, u64]),
@@ -250,6 +252,21 @@ def attention(layout: Layout, pool: np.ndarray, layer: int, q, tables, ctx_lens,
     out = np.zeros_like(q)
     lib().fo_attention(ctypes.byref(layout.c()), _p(pool), layer, q.shape[1], _p(q), _p(out),
                        _p(t), t.shape[1], _p(c), c.size, scale)
+    return out
+
+
+def prefill_attention(layout: Layout, pool: np.ndarray, layer: int, q, tables, ctx_lens, q_lens,
+                      q_offsets, scale: float) -> np.ndarray:
+    """q: [rows, n_heads, head_dim]; sequence s's q_lens[s] queries are rows q_offsets[s]..
+    at the end of its ctx_lens[s]-token context, attending causally."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    t = np.ascontiguousarray(tables, dtype=np.int32)
+    c = np.ascontiguousarray(ctx_lens, dtype=np.int32)
+    ql = np.ascontiguousarray(q_lens, dtype=np.int32)
+    qo = np.ascontiguousarray(q_offsets, dtype=np.int64)
+    out = np.zeros_like(q)
+    lib().fo_prefill_attention(ctypes.byref(layout.c()), _p(pool), layer, q.shape[1], _p(q),
+                               _p(out), _p(t), t.shape[1], _p(c), _p(ql), _p(qo), c.size, scale)
     return out
 
 

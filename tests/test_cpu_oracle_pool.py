@@ -272,3 +272,29 @@ def test_avx2_attention_within_tolerance_of_oracle():
     b4 = ref.avx2_attention(lay, pool, 0, q, tab, c, 0.088388346, 4)
     assert np.array_equal(b1, b4)
     assert np.allclose(a, b1, rtol=1e-5, atol=1e-6)
+
+
+def test_prefill_is_decode_at_every_position_and_causal_brute_force():
+    """Prefill of a chunk (llama.rs:363-378) == the decode loop at each of its positions,
+    and == an f64 causal softmax(qK^T)V."""
+    ctxs, qls = [40, 300, 17], [40, 33, 5]
+    d, hkv, g = 64, 2, 4
+    lay, pool, tab = _pool_with(1, d, hkv, ctxs, seed=12)
+    rows = sum(qls)
+    offs = np.concatenate([[0], np.cumsum(qls)[:-1]]).astype(np.int64)
+    q = np.random.default_rng(4).standard_normal((rows, hkv * g, d)).astype(np.float32)
+    scale = 0.125
+    got = ref.prefill_attention(lay, pool, 0, q, tab, np.array(ctxs, np.int32),
+                                np.array(qls, np.int32), offs, scale)
+    for s, (c, n) in enumerate(zip(ctxs, qls)):
+        kr, vr = ref.gather_slots(lay, pool, 0, slots_for(tab[s], c), 0)
+        for i in range(n):
+            r = offs[s] + i
+            pos_ctx = c - n + i + 1
+            dec = ref.attention(lay, pool, 0, q[r:r + 1], tab[s:s + 1],
+                                np.array([pos_ctx], np.int32), scale)
+            assert np.array_equal(got[r], dec[0])
+            if i in (0, n - 1):
+                for h in (0, hkv * g - 1):
+                    want = attention_f64(q[r, h], kr[:pos_ctx, h // g], vr[:pos_ctx, h // g], scale)
+                    assert np.allclose(got[r, h], want, rtol=1e-5, atol=1e-6)
