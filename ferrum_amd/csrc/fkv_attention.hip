@@ -327,69 +327,96 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 // Merge the partitions of one (sequence, query head): M = max_p m_p (NaN
 // skipped); a non-finite M gives zeros (scalar.rs:127-130); otherwise
 // out = sum_p w_p o_p / sum_p w_p l_p with w_p = exp(m_p - M).
-// 256 threads: thread t covers dims 4*(t % (D/4)).. and partitions p = t / (D/4) mod P.
+// One wave per (sequence, query head), four per workgroup, no LDS: lane p holds
+// partition p's (m, l) (64 partitions per pass), every lane holds D/64 dims, and
+// the partial-output loads of a pass are issued before its maximum is known.
 template <int D>
 __global__ void __launch_bounds__(256) attn_combine_kernel(
-    const int32_t* __restrict__ ctx_lens, uint32_t n_heads, uint32_t max_blocks,
-    uint32_t max_parts, int32_t part_tokens, const float* __restrict__ ws_o,
-    const float* __restrict__ ws_ml, float* __restrict__ out) {
-  constexpr int kLanesPerRow = D / 4;
-  constexpr int kRows = 256 / kLanesPerRow;
-  __shared__ float s_red[kRows][D];
-  __shared__ float s_lred[kRows];
-  __shared__ float s_max[4];
-
-  const uint32_t head = blockIdx.x;  // seq * n_heads + h
+    const int32_t* __restrict__ ctx_lens, uint32_t n_seq_heads, uint32_t n_heads,
+    uint32_t max_blocks, uint32_t max_parts, int32_t part_tokens,
+    const float* __restrict__ ws_o, const float* __restrict__ ws_ml, float* __restrict__ out) {
+  constexpr int DPL = D / 64;  // dims per lane
+  constexpr int kChunk = 16;   // partial outputs held in registers per step
+  const uint32_t head = blockIdx.x * 4 + (threadIdx.x >> 6);  // seq * n_heads + h
+  if (head >= n_seq_heads) return;
+  const int lane = threadIdx.x & 63;
   const uint32_t seq = head / n_heads;
+  const float* ml = ws_ml + (uint64_t)head * max_parts * 2;
+  const float* po = ws_o + (uint64_t)head * max_parts * D + lane * DPL;
+  // The context length, the first 64 partitions' (m, l) and the first kChunk
+  // partial outputs are loaded together: slots past the head's partition count
+  // hold stale bytes and are masked once the count is known (the workspace has
+  // max_parts slots per head, so every load is in bounds).
+  const int32_t raw_ctx = ctx_lens[seq];
+  const int32_t n0 = (int32_t)max_parts < 64 ? (int32_t)max_parts : 64;
+  float mp = lane < n0 ? ml[2 * lane] : -__builtin_inff();
+  float lp = lane < n0 ? ml[2 * lane + 1] : 0.0f;
+  float v0[kChunk][DPL];
+#pragma unroll
+  for (int j = 0; j < kChunk; j++)
+#pragma unroll
+    for (int i = 0; i < DPL; i++) v0[j][i] = j < (int)max_parts ? po[(uint64_t)j * D + i] : 0.0f;
+
   const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
-  int32_t ctx = ctx_lens[seq];
-  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int32_t ctx = raw_ctx < 0 ? 0 : (raw_ctx > cap ? cap : raw_ctx);
   const int32_t nparts = ctx > 0 ? (ctx + part_tokens - 1) / part_tokens : 1;
   if (nparts == 1) return;
+  if (lane >= nparts) {
+    mp = -__builtin_inff();
+    lp = 0.0f;
+  }
 
-  const float* ml = ws_ml + (uint64_t)head * max_parts * 2;
-  const float* po = ws_o + (uint64_t)head * max_parts * D;
-  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
-
-  float m = -__builtin_inff();
-  for (int p = threadIdx.x; p < nparts; p += 256) m = __builtin_fmaxf(m, ml[2 * p]);
-  m = wave_max(m);
-  if (lane == 0) s_max[wave] = m;
-  __syncthreads();
-  const float M = __builtin_fmaxf(__builtin_fmaxf(s_max[0], s_max[1]),
-                                  __builtin_fmaxf(s_max[2], s_max[3]));
-  float* o = out + (uint64_t)head * D;
+  // The global maximum (partitions past the first 64 need more loads).
+  float M = mp;
+  for (int32_t p0 = 64; p0 < nparts; p0 += 64)
+    if (p0 + lane < nparts) M = __builtin_fmaxf(M, ml[2 * (p0 + lane)]);
+  M = wave_max(M);
+  float* o = out + (uint64_t)head * D + lane * DPL;
   if (!__builtin_isfinite(M)) {
-    for (int d = threadIdx.x; d < D; d += 256) o[d] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < DPL; i++) o[i] = 0.0f;
     return;
   }
-  const int col = threadIdx.x % kLanesPerRow, row = threadIdx.x / kLanesPerRow;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  float lsum = 0.0f;
-  for (int p = row; p < nparts; p += kRows) {
-    const float w = __builtin_amdgcn_exp2f((ml[2 * p] - M) * kLog2e);
-    lsum = __builtin_fmaf(w, ml[2 * p + 1], lsum);
-    const float4 v = *(const float4*)(po + (uint64_t)p * D + col * 4);
-    acc.x = __builtin_fmaf(w, v.x, acc.x);
-    acc.y = __builtin_fmaf(w, v.y, acc.y);
-    acc.z = __builtin_fmaf(w, v.z, acc.z);
-    acc.w = __builtin_fmaf(w, v.w, acc.w);
-  }
-  s_red[row][col * 4] = acc.x;
-  s_red[row][col * 4 + 1] = acc.y;
-  s_red[row][col * 4 + 2] = acc.z;
-  s_red[row][col * 4 + 3] = acc.w;
-  if (col == 0) s_lred[row] = lsum;
-  __syncthreads();
-  if (threadIdx.x < D) {
-    float a = 0.0f, l = 0.0f;
+  float acc[DPL];
 #pragma unroll
-    for (int rr = 0; rr < kRows; rr++) {
-      a += s_red[rr][threadIdx.x];
-      l += s_lred[rr];
+  for (int i = 0; i < DPL; i++) acc[i] = 0.0f;
+  float lsum = 0.0f;
+  for (int32_t p0 = 0; p0 < nparts; p0 += 64) {
+    if (p0 > 0) {
+      const bool mine = p0 + lane < nparts;
+      mp = mine ? ml[2 * (p0 + lane)] : -__builtin_inff();
+      lp = mine ? ml[2 * (p0 + lane) + 1] : 0.0f;
     }
-    o[threadIdx.x] = a * (1.0f / l);
+    const float wp = __builtin_amdgcn_exp2f((mp - M) * kLog2e);
+    const int32_t n = nparts - p0 < 64 ? nparts - p0 : 64;
+    for (int32_t c0 = 0; c0 < n; c0 += kChunk) {
+      float v[kChunk][DPL];
+      if (p0 == 0 && c0 == 0) {
+#pragma unroll
+        for (int j = 0; j < kChunk; j++)
+#pragma unroll
+          for (int i = 0; i < DPL; i++) v[j][i] = v0[j][i];
+      } else {
+#pragma unroll
+        for (int j = 0; j < kChunk; j++)
+#pragma unroll
+          for (int i = 0; i < DPL; i++)
+            v[j][i] = c0 + j < n ? po[(uint64_t)(p0 + c0 + j) * D + i] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < kChunk; j++) {
+        if (c0 + j < n) {
+          const float w = __shfl(wp, c0 + j);
+          lsum = __builtin_fmaf(w, __shfl(lp, c0 + j), lsum);
+#pragma unroll
+          for (int i = 0; i < DPL; i++) acc[i] = __builtin_fmaf(w, v[j][i], acc[i]);
+        }
+      }
+    }
   }
+  const float inv = 1.0f / lsum;
+#pragma unroll
+  for (int i = 0; i < DPL; i++) o[i] = acc[i] * inv;
 }
 
 // ---------------------------------------------------------------------------
@@ -762,9 +789,8 @@ hipError_t launch_attn_t(const Geom& g, uint32_t layer, uint32_t n_heads, const 
                                                        ws_o, ws_ml);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || max_parts <= 1) return e;
-  attn_combine_kernel<D><<<n_seqs * n_heads, 256, 0, s>>>(
-      ctx_lens, n_heads, max_blocks, max_parts, kAttnPartTokens, ws_o, ws_ml, out);
-  return hipGetLastError();
+  return launch_attention_combine(D, ctx_lens, n_seqs, n_heads, max_blocks, max_parts,
+                                  kAttnPartTokens, ws_o, ws_ml, out, s);
 }
 
 template <int DT, int D>
@@ -809,12 +835,13 @@ hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
                                     uint32_t max_splits, uint32_t split_tokens,
                                     const float* ws_o, const float* ws_ml, float* out,
                                     hipStream_t s) {
+  const uint32_t nh = n_seqs * n_heads, grid = (nh + 3) / 4;
   if (head_dim == 128)
-    attn_combine_kernel<128><<<n_seqs * n_heads, 256, 0, s>>>(
-        ctx_lens, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
+    attn_combine_kernel<128><<<grid, 256, 0, s>>>(
+        ctx_lens, nh, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
   else
-    attn_combine_kernel<64><<<n_seqs * n_heads, 256, 0, s>>>(
-        ctx_lens, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
+    attn_combine_kernel<64><<<grid, 256, 0, s>>>(
+        ctx_lens, nh, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
   return hipGetLastError();
 }
 
@@ -891,9 +918,8 @@ hipError_t launch_split_t(const Geom& g, uint32_t layer, uint32_t n_heads, const
       (int32_t)p.split_tokens, scale, ws_o, ws_ml);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.max_splits <= 1) return e;
-  attn_combine_kernel<D><<<n_seqs * n_heads, 256, 0, s>>>(
-      ctx_lens, n_heads, max_blocks, p.max_splits, (int32_t)p.split_tokens, ws_o, ws_ml, out);
-  return hipGetLastError();
+  return launch_attention_combine(D, ctx_lens, n_seqs, n_heads, max_blocks, p.max_splits,
+                                  p.split_tokens, ws_o, ws_ml, out, s);
 }
 
 template <int DT, int D>

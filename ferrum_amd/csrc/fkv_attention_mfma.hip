@@ -551,8 +551,14 @@ __global__ void __launch_bounds__(256) attn_stream_combine_kernel(
 // Split kernel (one workgroup per (sequence, KV head, split))
 // ---------------------------------------------------------------------------
 
+// Waves per SIMD the split kernel is compiled for (the VGPR budget: 4 -> 128).
+#ifndef FKV_MFMA_WAVES_PER_EU
+#define FKV_MFMA_WAVES_PER_EU 3
+#endif
+
 template <int D, int NBUF>
-__global__ void __launch_bounds__(256) attn_mfma_kernel(
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
     const int32_t* __restrict__ ctx_lens, uint32_t max_splits, int32_t split_tokens,
@@ -563,16 +569,17 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(
   __shared__ float s_m[kAttnWaves][kHeads];
   __shared__ float s_l[kAttnWaves][kHeads];
 
-  const uint32_t sk = blockIdx.x, split = blockIdx.y;
+  const uint32_t sk = blockIdx.x;
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int32_t cap = (int32_t)(max_blocks * B);
   int32_t ctx = ctx_lens[seq];
   if (ctx < 0 || ctx > cap) {
-    if (split == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
+    if (blockIdx.y == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
     ctx = ctx < 0 ? 0 : cap;
   }
   const int32_t nsplits = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 1;
-  if ((int32_t)split >= nsplits) return;
+  const int32_t split = (int32_t)blockIdx.y;
+  if (split >= nsplits) return;
   const int32_t s0 = (int32_t)split * split_tokens;
   const int32_t s1 = ctx - s0 < split_tokens ? ctx : s0 + split_tokens;
   const int32_t nblk = s1 > s0 ? (s1 - s0 + B - 1) / B : 0;
@@ -583,11 +590,6 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(
   ln.col = ln.lane & 15;
   ln.grp = ln.lane >> 4;
   ln.real = ln.col < (int)G;
-
-  f16x8 qh[NC], ql[NC];
-  float hscale;
-  prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D, ln,
-            scale * kLog2e, qh, ql, hscale);
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
   const int32_t blk0 = s0 / B;
@@ -602,12 +604,24 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(
   u32x2_t vr[NBUF][NM];
   int32_t bid[NBUF];
   bool blive[NBUF];
+  f16x8 qh[NC], ql[NC];
+  float hscale;
   const int32_t nt = wave < nblk ? (nblk - wave + kAttnWaves - 1) / kAttnWaves : 0;
 
+  // The wave's block-table entries, 64 at a time: lane j holds the entry of the
+  // wave's block (t & ~63) + j. A block's physical id then comes from a register
+  // (readlane) instead of a load that its K/V loads would have to wait for.
+  int32_t tabv = 0;
+  auto load_tab = [&](int tb) {
+    const int j = tb + ln.lane;
+    tabv = j < nt ? table[blk0 + wave + kAttnWaves * j] : 0;
+  };
+  load_tab(0);
   // Physical block of the wave's block t (wave-uniform). A block-table entry
   // outside the pool raises the fault flag, loads block 0 instead and is skipped.
   auto fetch = [&](int t, int b) {
-    const int32_t p = table[blk0 + wave + kAttnWaves * t];
+    if (t > 0 && (t & 63) == 0) load_tab(t);
+    const int32_t p = __builtin_amdgcn_readlane(tabv, t & 63);
     const bool okb = p >= 0 && (uint64_t)p < g.num_blocks;
     if (!okb && ln.lane == 0) raise_fault(g.fault, kFaultBlock);
     blive[b] = okb;
@@ -636,6 +650,9 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(
       load_v<D>(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln, vr[b]);
     }
   }
+  // q is read after the first K/V loads are issued, so its latency overlaps theirs.
+  prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D, ln,
+            scale * kLog2e, qh, ql, hscale);
   for (int t = 0; t < nt; t += NBUF) {
 #pragma unroll
     for (int b = 0; b < NBUF; b++)

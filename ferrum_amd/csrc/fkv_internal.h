@@ -110,9 +110,8 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
                                    uint32_t max_blocks, const int32_t* ctx_lens,
                                    uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                                    void* workspace, hipStream_t s);
-// Device scratch one call needs (0 when every sequence fits one split). Its
-// first bytes hold per-(sequence, kv head) counters that must be zero before
-// the first call; every call leaves them zero.
+// Device scratch one call needs (0 when every sequence fits one split): the
+// split partials, which need no initialisation.
 uint64_t attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
                                    uint32_t max_ctx_len);
 
