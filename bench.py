@@ -3,23 +3,29 @@
 
 Default workload ("Llama-3-8B-shaped decode step"):
 64 sequences, 32 layers, 32 query / 8 KV heads (GQA 4), head_dim 128, f16 KV,
-block 16, context lengths uniform in [128, 4096] (seed 0), block tables
-scattered over the pool by a seeded permutation. One step = for every layer,
-append 1 token per sequence through the slot mapping, then paged decode
-attention over the grown context. Q/K/V ~ N(0,1) (synthetic; no checkpoint).
+block 16, context lengths uniform in [128, 4096] (seed 0), block tables scattered
+over the pool by a seeded permutation. One step = for every layer, one
+fkv_append_decode_attention call: append the new token of every sequence through
+its block table, then paged decode attention over the grown context (the per-layer
+KV work of Llama::forward_one_token, crates/model/src/llama.rs:218-247). Q/K/V ~
+N(0,1), synthetic (no checkpoint).
 
-Printed JSON line: value = decode-attention algorithmic HBM bytes per step /
-wall time per step (whole step, appends included). roofline.achieved uses the
-attention launches alone, timed with HIP events on the launch stream.
-cpu_baseline times the oracle's AVX2 restatement of the reference loop on this
-host, on one full layer of the same pool (a bounded sample).
+--workload picks another BASELINE config (c1 TinyLlama prefill + 64 decode steps,
+c3 continuous batching with chunked prefill in a fragmented 60%-of-HBM pool, c4
+Q8_0 KV, c5 70B long context plus copy_blocks and swap); each prints its own line.
+
+Printed JSON line: value = algorithmic HBM bytes of the step's calls (attention +
+append) / wall time per step, timed over K steps bracketed by synchronisation.
+roofline.achieved = the same bytes per call / the average call duration from HIP
+events on the launch stream around the timed region (every launch in it belongs
+to the measured call). cpu_baseline times the oracle's AVX2 restatement of the
+reference loop on host cores, on a bounded sample of the same pool.
 """
 from __future__ import annotations
 
 import argparse
 import ctypes
 import json
-import math
 import os
 import sys
 import time
@@ -30,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
+METRIC = "paged decode-attn HBM GB/s (% of peak) + KV append tokens/s, 1xMI355X"
 
 
 def parse():
@@ -38,26 +45,123 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
     return ap.parse_args()
 
 
-def attn_bytes(ctx, hq, hkv, d, elem_bytes):
-    """Algorithmic HBM bytes of decode attention for one (sequence, layer):
-    K+V once per KV head (GQA shares tiles), q and out in f32, block table, ctx_len."""
+# ---------------------------------------------------------------------------
+# Algorithmic bytes
+# ---------------------------------------------------------------------------
+
+def elem_bytes(dtype):
+    """Stored bytes per K/V value: f16 2, f32 4, Q8_0 34/32 (32 int8 + one f16 scale)."""
+    return {0: 4.0, 1: 2.0, 8: 34.0 / 32.0}[dtype]
+
+
+def attn_bytes(ctx, hq, hkv, d, e):
+    """Decode attention for one (sequence, layer): K+V once per KV head (GQA shares
+    tiles), q and out in f32, the block-table entries, ctx_len."""
     ctx = np.asarray(ctx, dtype=np.int64)
-    return int((ctx * hkv * d * 2 * elem_bytes + hq * d * 4 * 2 + ((ctx + 15) // 16) * 4 + 4).sum())
+    return float((ctx * hkv * d * 2 * e + hq * d * 4 * 2 + ((ctx + 15) // 16) * 4 + 4).sum())
 
 
-def append_bytes(n_tokens, hkv, d, elem_bytes):
-    """Per token per layer: f32 K/V read, stored K/V written, 8-byte slot."""
-    return int(n_tokens * (2 * hkv * d * 4 + 2 * hkv * d * elem_bytes + 8))
+def append_bytes(n_tokens, hkv, d, e, slot_bytes=8):
+    """Per token per layer: f32 K/V read, stored K/V written, the slot (8 bytes
+    for a slot mapping; 0 when the slot comes from the block table already counted)."""
+    return float(n_tokens * (2 * hkv * d * 4 + 2 * hkv * d * e + slot_bytes))
+
+
+# ---------------------------------------------------------------------------
+# Setup helpers
+# ---------------------------------------------------------------------------
+
+def make_tables(pool, nblk_seq, rng, fragment_cycles=0):
+    """Block tables from the pool's allocator. With fragment_cycles, the free list is
+    first churned by seeded alloc/free cycles of 1..64 blocks, so tables come out
+    scattered the way a long-running server leaves them; otherwise the allocated ids
+    are permuted."""
+    if fragment_cycles:
+        held = []
+        for _ in range(fragment_cycles):
+            if held and (rng.random() < 0.5 or pool.free_block_count() < 64):
+                pool.free_blocks(held.pop(int(rng.integers(len(held)))))
+            else:
+                held.append(pool.alloc_blocks(int(rng.integers(1, 65))))
+        for h in held:
+            pool.free_blocks(h)
+        ids = pool.alloc_blocks(int(nblk_seq.sum()))
+    else:
+        ids = pool.alloc_blocks(int(nblk_seq.sum()))
+        ids = ids[rng.permutation(ids.size)]
+    tables = np.zeros((len(nblk_seq), max(1, int(nblk_seq.max()))), np.int32)
+    off = 0
+    for s, n in enumerate(nblk_seq):
+        tables[s, :n] = ids[off: off + n]
+        off += n
+    return tables
+
+
+def slots_of(tables, seqs, pos, bs=16):
+    return tables[seqs, pos // bs].astype(np.int64) * bs + pos % bs
+
+
+def fill_context(torch, pool, layers, tables, ctx, hkv, d, gen, dev, outlier_frac=0.0,
+                 chunk=1 << 18, timer=None):
+    """Append N(0,1) K/V (optionally with a fraction of +-20 outliers) for positions
+    0 .. ctx[s]-1 of every sequence into every layer, in chunks of tokens."""
+    ctx = np.asarray(ctx, np.int64)
+    seq_of = np.repeat(np.arange(ctx.size), ctx)
+    pos = np.concatenate([np.arange(c) for c in ctx]) if ctx.sum() else np.zeros(0, np.int64)
+    slots_all = torch.from_numpy(slots_of(tables, seq_of, pos)).to(dev)
+    n = slots_all.numel()
+    times = []
+    for layer in layers:
+        for a in range(0, n, chunk):
+            b = min(n, a + chunk)
+            k = torch.randn((b - a, hkv, d), generator=gen, device=dev)
+            v = torch.randn((b - a, hkv, d), generator=gen, device=dev)
+            if outlier_frac:
+                for x in (k, v):
+                    m = torch.rand(x.shape, generator=gen, device=dev) < outlier_frac
+                    sgn = torch.where(torch.rand(x.shape, generator=gen, device=dev) < 0.5, -20.0, 20.0)
+                    x[m] = sgn[m]
+            e0 = e1 = None
+            if timer is not None and a == 0 and b == n:
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+            pool.append(layer, k, v, slots_all[a:b])
+            if e0 is not None:
+                e1.record()
+                times.append((e0, e1))
+            del k, v
+    torch.cuda.synchronize()
+    if timer is not None and times:
+        timer.extend(a.elapsed_time(b) for a, b in times)
+    return n
+
+
+def calibrate_copy(torch, fa, dev, nbytes=4 << 30):
+    """Plain 16-byte device copy (reported alongside; not the peak)."""
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    fa.device_copy(b, a, nbytes)
+    torch.cuda.synchronize()
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    for _ in range(5):
+        fa.device_copy(b, a, nbytes)
+    c1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * 5 / (c0.elapsed_time(c1) * 1e-3) / 1e9
+    del a, b
+    return gbs
 
 
 def read_traffic(path):
-    """HBM bytes per attention call from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary (the line `hbm_bytes_per_launch: N`), or None when it is absent."""
+    """HBM bytes per call from a committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary
+    (the line `hbm_bytes_per_launch: N`), or None when it is absent."""
     try:
         with open(path) as f:
             for line in f:
@@ -66,6 +170,463 @@ def read_traffic(path):
     except OSError:
         pass
     return None
+
+
+# ---------------------------------------------------------------------------
+# Decode steps
+# ---------------------------------------------------------------------------
+
+class DecodeLoop:
+    """Per-layer fused decode calls over K timed steps (plus W warm-up steps).
+    ctx_step[t] holds every sequence's context after step t's append."""
+
+    def __init__(self, torch, fa, lib, pool, L, n_seqs, hq, hkv, d, tables, ctx0, n_steps, gen,
+                 dev, seqs=None):
+        self.torch, self.fa, self.lib, self.pool, self.L = torch, fa, lib, pool, L
+        self.n_seqs, self.hq, self.hkv, self.d = n_seqs, hq, hkv, d
+        self.q = torch.randn((L, n_seqs, hq, d), generator=gen, device=dev)
+        self.out = torch.empty((L, n_seqs, hq, d), device=dev)
+        self.knew = torch.randn((L, n_seqs, hkv, d), generator=gen, device=dev)
+        self.vnew = torch.randn((L, n_seqs, hkv, d), generator=gen, device=dev)
+        self.ctx_step = np.stack([ctx0 + t + 1 for t in range(n_steps)]).astype(np.int32)
+        self.ctx_step_d = torch.from_numpy(self.ctx_step).to(dev)
+        self.tables = tables
+        self.tables_d = torch.from_numpy(tables).to(dev)
+        self.max_blocks = tables.shape[1]
+        self.max_ctx = int(self.ctx_step.max())
+        n = ctypes.c_uint64()
+        fa.errors.check(lib.fkv_append_decode_attention_workspace_size(
+            ctypes.c_void_p(pool.handle), hq, n_seqs, self.max_ctx, ctypes.byref(n)))
+        self.ws_bytes = n.value
+        self.ws = torch.zeros(max(self.ws_bytes, 16), dtype=torch.uint8, device=dev)
+        self.scale = fa.default_scale(d)
+        self.h = ctypes.c_void_p(pool.handle)
+        self.ptrs = [(self.q[l].data_ptr(), self.out[l].data_ptr(), self.knew[l].data_ptr(),
+                      self.vnew[l].data_ptr()) for l in range(L)]
+
+    def step(self, t, sp):
+        cl = self.ctx_step_d[t].data_ptr()
+        tp = self.tables_d.data_ptr()
+        for l in range(self.L):
+            qp, op, kp, vp = self.ptrs[l]
+            rc = self.lib.fkv_append_decode_attention(
+                self.h, l, self.hq, kp, vp, qp, op, tp, self.max_blocks, cl, self.n_seqs,
+                self.max_ctx, self.scale, self.ws.data_ptr(), self.ws_bytes, sp)
+            if rc:
+                self.fa.errors.check(rc)
+
+    def run(self, W, K):
+        torch = self.torch
+        stream = torch.cuda.current_stream()
+        sp = stream.cuda_stream
+        for t in range(W):
+            self.step(t, sp)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for i in range(K):
+            self.step(W + i, sp)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        assert self.pool.take_fault_flags() == 0
+        return wall, e0.elapsed_time(e1)
+
+
+def decode_result(args, dl, W, K, wall, region_ms, e, workload, extra_cfg, kernel_name, traffic):
+    L, hq, hkv, d = dl.L, dl.hq, dl.hkv, dl.d
+    per_step = [attn_bytes(dl.ctx_step[W + i], hq, hkv, d, e) * L for i in range(K)]
+    app_step = append_bytes(dl.n_seqs, hkv, d, e, slot_bytes=0) * L
+    total = float(sum(per_step)) + app_step * K
+    value = total / wall / 1e9
+    call_bytes = total / (K * L)
+    call_ms = region_ms / (K * L)
+    achieved = call_bytes / (call_ms * 1e-3) / 1e9
+    return {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": {0: "f32", 1: "f16", 8: "q8_0"}[dl.pool.config.kv_dtype],
+        "data": "synthetic N(0,1) Q/K/V, seeded; scattered block tables",
+        "config": dict({"workload": workload, "n_seqs": dl.n_seqs, "n_layers": L,
+                        "n_heads": hq, "n_kv_heads": hkv, "head_dim": d, "block_size": 16,
+                        "accumulate": "f32", "mean_ctx": float(dl.ctx_step[W:W + K].mean()),
+                        "parallelism": "single GPU"}, **extra_cfg),
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "append_tokens_per_s": round(dl.n_seqs * K / wall, 1),
+        "append_token_layers_per_s": round(dl.n_seqs * K * L / wall, 1),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": kernel_name,
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "bytes_per_launch": int(call_bytes),
+            "ms_per_launch": round(call_ms, 5),
+        },
+        "cpu_baseline": None,
+    }
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline
+# ---------------------------------------------------------------------------
+
+def cpu_baseline(args, pool, tables, ctx, q_layer, out_layer, layer, hq, hkv, d, dtype,
+                 seqs=None):
+    """The oracle's AVX2 restatement of the reference attention loop (llama.rs:220-247:
+    per query head, no GQA reuse) on one layer of the same pool, copied to the host,
+    at 1 thread and at `threads` threads; `seqs` bounds the sample. Also counts GPU
+    outputs outside the attention tolerance on that sample."""
+    from oracle import ref
+    import ferrum_amd as fa
+
+    if not ref.avx2_available():
+        return None
+    bs = 16
+    seqs = np.arange(tables.shape[0]) if seqs is None else np.asarray(seqs)
+    ctx = np.asarray(ctx, np.int64)[seqs]
+    nb = (ctx + bs - 1) // bs
+    used = [int(b) for s, n in zip(seqs, nb) for b in tables[s, :n]]
+    remap = {b: i for i, b in enumerate(used)}
+    lay = ref.Layout(1, hkv, d, bs, len(used), dtype=dtype)
+    region = lay.block_bytes
+    image = np.empty(lay.pool_bytes, np.uint8)
+    for b, i in remap.items():
+        image[i * region:(i + 1) * region] = pool.read(b * pool.block_bytes + layer * region, region)
+    tab = np.zeros((len(seqs), max(1, int(nb.max()))), np.int32)
+    for j, (s, n) in enumerate(zip(seqs, nb)):
+        tab[j, :n] = [remap[int(b)] for b in tables[s, :n]]
+    qh = np.ascontiguousarray(q_layer[seqs])
+    gpu_out = out_layer[seqs]
+    scale = fa.default_scale(d)
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    e = elem_bytes(dtype)
+    nbytes = attn_bytes(ctx, hq, hkv, d, e)
+    t0 = time.perf_counter()
+    o1 = ref.avx2_attention(lay, image, 0, qh, tab, ctx.astype(np.int32), scale, 1)
+    t1 = time.perf_counter() - t0
+    reps = 3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        on = ref.avx2_attention(lay, image, 0, qh, tab, ctx.astype(np.int32), scale, threads)
+    tn = (time.perf_counter() - t0) / reps
+    assert np.array_equal(o1, on)
+    err = np.abs(gpu_out.astype(np.float64) - o1)
+    bad = int((err > 2e-3 + 1e-2 * np.abs(o1)).sum())
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / tn / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"layer {layer}, {len(seqs)} seqs ({int(ctx.sum())} tokens, "
+                   f"{nbytes / 1e6:.1f} MB algorithmic): AVX2 restatement of llama.rs:220-247 "
+                   f"(per query head, no GQA reuse); {reps} reps at {threads} threads"),
+        "value_1thread": round(nbytes / t1 / 1e9, 3),
+        "seconds_1thread": round(t1, 3),
+        "seconds_threads": round(tn, 3),
+        "cpu_model": model,
+        "host_cpus": os.cpu_count(),
+        "gpu_vs_cpu_out_of_tolerance": bad,
+        "gpu_vs_cpu_max_abs_err": float(np.nanmax(err)) if err.size else 0.0,
+    }
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+
+def decode_workload(args, torch, fa, lib, dev, *, name, L, n_seqs, hq, hkv, d, dtype, ctx0,
+                    num_blocks, fragment_cycles=0, outlier_frac=0.0, extra_cfg=None,
+                    cpu_seqs=None, num_host_blocks=0):
+    """Common decode leg: pool, tables, context fill (bulk append measured), K timed
+    fused steps. Returns (result dict, pool, DecodeLoop) for workload-specific extras."""
+    K, W = args.steps, args.warmup
+    rng = np.random.default_rng(args.seed)
+    nblk_seq = (ctx0 + W + K + 15) // 16
+    pool = fa.PagedKvPool(fa.PagedConfig(n_layers=L, n_kv_heads=hkv, head_dim=d,
+                                         num_blocks=num_blocks, block_size=16, kv_dtype=dtype,
+                                         num_host_blocks=num_host_blocks))
+    tables = make_tables(pool, nblk_seq, rng, fragment_cycles)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    fill_ms = []
+    n_fill = fill_context(torch, pool, range(L), tables, ctx0, hkv, d, gen, dev,
+                          outlier_frac=outlier_frac, timer=fill_ms)
+    dl = DecodeLoop(torch, fa, lib, pool, L, n_seqs, hq, hkv, d, tables, ctx0, W + K, gen, dev)
+    wall, region_ms = dl.run(W, K)
+    e = elem_bytes(dtype)
+    kname = ("fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)" if dtype == 1
+             else "fkv_append_decode_attention (tail slots + append + attn_split_kernel + combine)")
+    res = decode_result(args, dl, W, K, wall, region_ms, e, name, dict(extra_cfg or {}), kname,
+                        None)
+    if fill_ms:
+        ms = float(np.median(fill_ms))
+        res["bulk_append"] = {
+            "tokens_per_launch": int(n_fill), "ms_per_launch": round(ms, 4),
+            "token_layers_per_s": round(n_fill / (ms * 1e-3), 1),
+            "gbs": round(append_bytes(n_fill, hkv, d, e) / (ms * 1e-3) / 1e9, 2)}
+    if not args.no_cpu:
+        t_last = W + K - 1
+        res["cpu_baseline"] = cpu_baseline(args, pool, tables, dl.ctx_step[t_last],
+                                           dl.q[L - 1].cpu().numpy(), dl.out[L - 1].cpu().numpy(),
+                                           L - 1, hq, hkv, d, dtype, seqs=cpu_seqs)
+    return res, pool, dl
+
+
+def run_c2(args, torch, fa, lib, dev):
+    rng = np.random.default_rng(args.seed)
+    n_seqs = 64
+    ctx0 = rng.integers(128, 4097, n_seqs).astype(np.int64)
+    nb = int(((ctx0 + args.warmup + args.steps + 15) // 16).sum()) + 64
+    res, pool, dl = decode_workload(
+        args, torch, fa, lib, dev, name="llama3-8b decode step (BASELINE configs[1])", L=32,
+        n_seqs=n_seqs, hq=32, hkv=8, d=128, dtype=1, ctx0=ctx0, num_blocks=nb,
+        extra_cfg={"kv_dtype": "f16", "ctx": f"uniform[128,4096] seed {args.seed}"})
+    res["roofline"]["traffic"] = read_traffic(
+        os.path.join(ROOT, "profiles", "decode_attention_llama3_8b_c2_hbm_traffic.md"))
+    res["device_copy_gbs"] = round(calibrate_copy(torch, fa, dev), 1)
+    return res
+
+
+def run_c4(args, torch, fa, lib, dev):
+    n_seqs, ctx = 128, 8192
+    ctx0 = np.full(n_seqs, ctx - args.warmup - args.steps, np.int64)
+    nb = int(((ctx0 + args.warmup + args.steps + 15) // 16).sum()) + 64
+    res, pool, dl = decode_workload(
+        args, torch, fa, lib, dev, name="llama3-8b q8_0 kv, 128 x 8192 (BASELINE configs[3])",
+        L=32, n_seqs=n_seqs, hq=32, hkv=8, d=128, dtype=8, ctx0=ctx0, num_blocks=nb,
+        outlier_frac=0.01, extra_cfg={"kv_dtype": "q8_0", "outliers": "1% at +-20"},
+        cpu_seqs=np.arange(8))
+    return res
+
+
+def run_c5(args, torch, fa, lib, dev):
+    """131,072-token decode on 70B-shaped KV, then copy_blocks of 20,000 (src, dst)
+    pairs (CoW fork) and a swap of 20% of the context's blocks out and back in."""
+    ctx = 131072
+    K, W = args.steps, args.warmup
+    ctx0 = np.array([ctx - W - K], np.int64)
+    ctx_blocks = (ctx + 15) // 16
+    n_pairs = 20000
+    n_swap = ctx_blocks // 5
+    nb = ctx_blocks + n_pairs + 64
+    res, pool, dl = decode_workload(
+        args, torch, fa, lib, dev, name="llama3-70b long context 1 x 131072 (BASELINE configs[4])",
+        L=80, n_seqs=1, hq=64, hkv=8, d=128, dtype=1, ctx0=ctx0, num_blocks=nb,
+        extra_cfg={"kv_dtype": "f16", "ctx": ctx}, cpu_seqs=None, num_host_blocks=n_swap)
+    # copy_blocks: sources among the context's blocks, destinations distinct free blocks
+    rng = np.random.default_rng(args.seed + 1)
+    used = dl.tables[0, :ctx_blocks]
+    dst = pool.alloc_blocks(n_pairs)
+    src = used[rng.integers(0, ctx_blocks, n_pairs)]
+    pairs = np.stack([src, dst], 1).astype(np.int64)
+    pairs_d = torch.from_numpy(pairs).to(dev)
+    pool.copy_blocks(pairs_d)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    reps = 3
+    for _ in range(reps):
+        pool.copy_blocks(pairs_d)
+    e1.record()
+    torch.cuda.synchronize()
+    cms = e0.elapsed_time(e1) / reps
+    cbytes = 2.0 * n_pairs * pool.block_bytes
+    for j in rng.integers(0, n_pairs, 4):  # spot check: dst bytes == src bytes
+        a = pool.read(int(src[j]) * pool.block_bytes, pool.block_bytes)
+        b = pool.read(int(dst[j]) * pool.block_bytes, pool.block_bytes)
+        assert np.array_equal(a, b), "copy_blocks mismatch"
+    res["copy_blocks"] = {"pairs": n_pairs, "bytes_per_block": pool.block_bytes,
+                          "ms": round(cms, 3), "gbs": round(cbytes / (cms * 1e-3) / 1e9, 1),
+                          "pct_of_hbm_peak": round(100 * cbytes / (cms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)}
+    pool.free_blocks(dst)
+    res["swap"] = swap_leg(torch, fa, pool, used, n_swap, rng)
+    return res
+
+
+def swap_leg(torch, fa, pool, used, n_swap, rng):
+    """Swap n_swap of the context's blocks out to a second pool's pinned host
+    storage and back; byte-identical round trip checked on a sample."""
+    sel = np.sort(rng.choice(used, n_swap, replace=False)).astype(np.int64)
+    host_pool = pool  # pinned host storage belongs to the pool that swaps
+    pairs_out = np.stack([sel, np.arange(n_swap)], 1)
+    pairs_in = np.stack([np.arange(n_swap), sel], 1)
+    check = sel[rng.integers(0, n_swap, 4)]
+    before = [pool.read(int(b) * pool.block_bytes, pool.block_bytes) for b in check]
+    s = torch.cuda.current_stream()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0.record(s)
+    host_pool.swap_out(pairs_out)
+    e1.record(s)
+    pool.fill(0xA5)  # clobber device copies (the whole pool) before swapping back
+    s2 = torch.cuda.Event(enable_timing=True)
+    s2.record(s)
+    host_pool.swap_in(pairs_in)
+    e2.record(s)
+    torch.cuda.synchronize()
+    out_ms, in_ms = e0.elapsed_time(e1), s2.elapsed_time(e2)
+    after = [pool.read(int(b) * pool.block_bytes, pool.block_bytes) for b in check]
+    assert all(np.array_equal(a, b) for a, b in zip(before, after)), "swap round trip mismatch"
+    nbytes = float(n_swap * pool.block_bytes)
+    return {"blocks": int(n_swap), "bytes": int(nbytes), "out_ms": round(out_ms, 2),
+            "in_ms": round(in_ms, 2), "out_gbs": round(nbytes / (out_ms * 1e-3) / 1e9, 2),
+            "in_gbs": round(nbytes / (in_ms * 1e-3) / 1e9, 2), "bound": "host link (PCIe)"}
+
+
+def run_c3(args, torch, fa, lib, dev):
+    """Continuous batching: 256 decode sequences with log-normal contexts (median
+    2048, sigma 1.0, cap 32768) and 4 chunked-prefill sequences appending 512 tokens
+    each, in one pool sized to ~60% of 288 GB and fragmented by 10,000 seeded
+    alloc/free cycles. Step per layer: fused decode call for the 256 sequences, the
+    prefill chunk's append, then chunked-prefill attention for the 4 sequences."""
+    K, W = args.steps, args.warmup
+    rng = np.random.default_rng(args.seed)
+    L, hq, hkv, d = 32, 32, 8, 128
+    n_dec, n_pre, chunk = 256, 4, 512
+    ctx_dec = np.minimum(np.round(np.exp(rng.normal(np.log(2048), 1.0, n_dec))), 32768 - W - K)
+    ctx_dec = np.maximum(ctx_dec, 1).astype(np.int64)
+    pre_prior = np.array([0, 512, 1024, 1536], np.int64)  # chunked prefill in progress
+    block_bytes = L * 2 * hkv * 16 * d * 2
+    num_blocks = int(0.6 * 288e9 // block_bytes)
+    pool = fa.PagedKvPool(fa.PagedConfig(n_layers=L, n_kv_heads=hkv, head_dim=d,
+                                         num_blocks=num_blocks, block_size=16, kv_dtype=1))
+    nblk = np.concatenate([(ctx_dec + W + K + 15) // 16, (pre_prior + chunk * (W + K) + 15) // 16])
+    tables = make_tables(pool, nblk, rng, fragment_cycles=10000)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    fill_context(torch, pool, range(L), tables, np.concatenate([ctx_dec, pre_prior]), hkv, d,
+                 gen, dev)
+    dl = DecodeLoop(torch, fa, lib, pool, L, n_dec, hq, hkv, d, tables[:n_dec], ctx_dec, W + K,
+                    gen, dev)
+    # prefill inputs: chunk t of sequence p covers positions prior + t*chunk .. +chunk-1
+    tab_pre = torch.from_numpy(np.ascontiguousarray(tables[n_dec:])).to(dev)
+    kp = torch.randn((L, n_pre * chunk, hkv, d), generator=gen, device=dev)
+    vp = torch.randn((L, n_pre * chunk, hkv, d), generator=gen, device=dev)
+    qp = torch.randn((L, n_pre * chunk, hq, d), generator=gen, device=dev)
+    op = torch.empty_like(qp)
+    pre_slots, pre_ctx = [], []
+    for t in range(W + K):
+        start = pre_prior + t * chunk
+        seqs = np.repeat(np.arange(n_pre), chunk)
+        pos = np.concatenate([np.arange(s, s + chunk) for s in start])
+        pre_slots.append(torch.from_numpy(slots_of(tables[n_dec:], seqs, pos)).to(dev))
+        pre_ctx.append(torch.from_numpy((start + chunk).astype(np.int32)).to(dev))
+    q_lens = torch.full((n_pre,), chunk, dtype=torch.int32, device=dev)
+    q_offs = torch.arange(0, n_pre * chunk, chunk, dtype=torch.int64, device=dev)
+    max_pre_ctx = int(pre_prior.max() + chunk * (W + K))
+    h = ctypes.c_void_p(pool.handle)
+    scale = fa.default_scale(d)
+
+    def step(t, sp):
+        cl = dl.ctx_step_d[t].data_ptr()
+        for l in range(L):
+            q_, o_, k_, v_ = dl.ptrs[l]
+            fa.errors.check(lib.fkv_append_decode_attention(
+                h, l, hq, k_, v_, q_, o_, dl.tables_d.data_ptr(), dl.max_blocks, cl, n_dec,
+                dl.max_ctx, scale, dl.ws.data_ptr(), dl.ws_bytes, sp))
+            fa.errors.check(lib.fkv_append(h, l, kp[l].data_ptr(), vp[l].data_ptr(),
+                                           pre_slots[t].data_ptr(), n_pre * chunk, sp))
+            fa.errors.check(lib.fkv_prefill_attention(
+                h, l, hq, qp[l].data_ptr(), op[l].data_ptr(), tab_pre.data_ptr(),
+                tab_pre.shape[1], pre_ctx[t].data_ptr(), q_lens.data_ptr(), q_offs.data_ptr(),
+                n_pre, chunk, max_pre_ctx, scale, sp))
+
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    for t in range(W):
+        step(t, sp)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(K):
+        step(W + i, sp)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    assert pool.take_fault_flags() == 0
+    # decode-only rate from a separate region of back-to-back fused decode calls
+    dw, dms = dl.run(0, K)
+    e = 2.0
+    dec_bytes = [attn_bytes(dl.ctx_step[W + i], hq, hkv, d, e) * L for i in range(K)]
+    pre_attn = sum(attn_bytes_prefill(pre_prior + (W + i) * chunk + chunk, chunk, hq, hkv, d)
+                   for i in range(K)) * L
+    app = (append_bytes(n_dec, hkv, d, e, 0) + append_bytes(n_pre * chunk, hkv, d, e)) * L * K
+    total = float(sum(dec_bytes)) + pre_attn + app
+    res = decode_result(args, dl, 0, K, dw, dms, e, "llama3-8b continuous batching "
+                        "(BASELINE configs[2])",
+                        {"kv_dtype": "f16", "ctx": "log-normal median 2048 sigma 1.0 cap 32768",
+                         "prefill": f"{n_pre} x {chunk}-token chunks",
+                         "pool_blocks": num_blocks, "pool_gb": round(pool.pool_bytes / 1e9, 1),
+                         "fragmented_by": "10000 seeded alloc/free cycles"},
+                        "fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)",
+                        None)
+    # the headline value of this leg is the whole mixed step
+    res["value"] = round(total / wall / 1e9, 2)
+    res["ms_per_step"] = round(wall * 1e3 / K, 4)
+    res["pct_of_hbm_peak"] = round(100 * res["value"] / HBM_PEAK_GBS, 2)
+    res["decode_only_ms_per_step"] = round(dw * 1e3 / K, 4)
+    res["append_tokens_per_s"] = round((n_dec + n_pre * chunk) * K / wall, 1)
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(args, pool, dl.tables, dl.ctx_step[K - 1],
+                                           dl.q[L - 1].cpu().numpy(), dl.out[L - 1].cpu().numpy(),
+                                           L - 1, hq, hkv, d, 1, seqs=np.arange(16))
+    return res
+
+
+def attn_bytes_prefill(ctx_end, q_len, hq, hkv, d):
+    """Chunked prefill of q_len queries ending at ctx_end per sequence: K/V of the
+    whole context once per KV head, q and out in f32."""
+    ctx_end = np.asarray(ctx_end, np.int64)
+    return float((ctx_end * hkv * d * 2 * 2 + q_len * hq * d * 8 + ((ctx_end + 15) // 16) * 4).sum())
+
+
+def run_c1(args, torch, fa, lib, dev):
+    """TinyLlama-shaped: 1 sequence, 22 layers, 32/4 heads, D = 64, 256-block pool with
+    the table a seeded permutation; a 512-token prefill append, then 64 decode steps."""
+    rng = np.random.default_rng(args.seed)
+    L, hq, hkv, d = 22, 32, 4, 64
+    pool = fa.PagedKvPool(fa.PagedConfig(n_layers=L, n_kv_heads=hkv, head_dim=d, num_blocks=256,
+                                         block_size=16, kv_dtype=1))
+    perm = rng.permutation(256).astype(np.int32)
+    tables = perm[None, : (512 + 64 + 15) // 16].copy()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    fill_ms = []
+    fill_context(torch, pool, range(L), tables, np.array([512]), hkv, d, gen, dev, timer=fill_ms)
+    K = 64
+    dl = DecodeLoop(torch, fa, lib, pool, L, 1, hq, hkv, d, tables, np.array([512]), K, gen, dev)
+    wall, region_ms = dl.run(0, K)
+    res = decode_result(args, dl, 0, K, wall, region_ms, 2.0, "tinyllama prefill 512 + 64 "
+                        "decode steps (BASELINE configs[0])", {"kv_dtype": "f16"},
+                        "fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)",
+                        None)
+    res["bulk_append"] = {"tokens_per_launch": 512, "ms_per_launch": round(float(np.median(fill_ms)), 4)}
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(args, pool, tables, dl.ctx_step[K - 1],
+                                           dl.q[L - 1].cpu().numpy(), dl.out[L - 1].cpu().numpy(),
+                                           L - 1, hq, hkv, d, 1)
+    return res
 
 
 def main():
@@ -83,252 +644,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     lib = _lib.load()
-
-    n_seqs, L, hq, hkv, d, bs = 64, 32, 32, 8, 128, 16
-    K, W = args.steps, args.warmup
-    rng = np.random.default_rng(args.seed)
-    ctx0 = rng.integers(128, 4097, n_seqs).astype(np.int64)
-    max_ctx_final = ctx0 + W + K
-    nblk_seq = (max_ctx_final + bs - 1) // bs
-    num_blocks = int(nblk_seq.sum()) + 64
-
-    pool = fa.PagedKvPool(fa.PagedConfig(n_layers=L, n_kv_heads=hkv, head_dim=d,
-                                         num_blocks=num_blocks, block_size=bs,
-                                         kv_dtype=fa.DTYPE_F16))
-    ids = pool.alloc_blocks(int(nblk_seq.sum()))
-    ids = ids[rng.permutation(ids.size)]  # scatter every table over the pool
-    max_blocks = int(nblk_seq.max())
-    tables = np.zeros((n_seqs, max_blocks), np.int32)
-    off = 0
-    for s in range(n_seqs):
-        tables[s, : nblk_seq[s]] = ids[off: off + nblk_seq[s]]
-        off += nblk_seq[s]
-    tables_d = torch.from_numpy(tables).to(dev)
-
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-
-    # Initial context: bulk append of every sequence's prefix into every layer
-    # (also the bulk-append throughput measurement).
-    pos = np.concatenate([np.arange(c) for c in ctx0])
-    seq_of = np.repeat(np.arange(n_seqs), ctx0)
-    slots_fill = tables[seq_of, pos // bs].astype(np.int64) * bs + pos % bs
-    slots_fill_d = torch.from_numpy(slots_fill).to(dev)
-    n_fill = slots_fill.size
-    gen = torch.Generator(device=dev)
-    gen.manual_seed(args.seed)
-    ev_fill = []
-    for layer in range(L):
-        kf = torch.randn((n_fill, hkv, d), generator=gen, device=dev)
-        vf = torch.randn((n_fill, hkv, d), generator=gen, device=dev)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        pool.append(layer, kf, vf, slots_fill_d)
-        e1.record(stream)
-        ev_fill.append((e0, e1))
-        del kf, vf
-    torch.cuda.synchronize()
-    fill_ms = [a.elapsed_time(b) for a, b in ev_fill]
-    bulk_append_ms = float(np.median(fill_ms[1:])) if len(fill_ms) > 1 else fill_ms[0]
-
-    # Per-step inputs, resident in HBM before timing.
-    n_steps = W + K
-    q = torch.randn((L, n_seqs, hq, d), generator=gen, device=dev)
-    out = torch.empty((L, n_seqs, hq, d), device=dev)
-    knew = torch.randn((L, n_seqs, hkv, d), generator=gen, device=dev)
-    vnew = torch.randn((L, n_seqs, hkv, d), generator=gen, device=dev)
-    slots_step = np.zeros((n_steps, n_seqs), np.int64)
-    ctx_step = np.zeros((n_steps, n_seqs), np.int32)
-    for t in range(n_steps):
-        p = ctx0 + t
-        slots_step[t] = tables[np.arange(n_seqs), p // bs].astype(np.int64) * bs + p % bs
-        ctx_step[t] = p + 1
-    slots_step_d = torch.from_numpy(slots_step).to(dev)
-    ctx_step_d = torch.from_numpy(ctx_step).to(dev)
-    max_ctx = int(ctx_step.max())
-    ws_bytes = pool.attention_workspace_bytes(hq, n_seqs, max_ctx)
-    ws = torch.zeros(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    scale = fa.default_scale(d)
-
-    h = ctypes.c_void_p(pool.handle)
-    qp = [q[l].data_ptr() for l in range(L)]
-    op = [out[l].data_ptr() for l in range(L)]
-    kp = [knew[l].data_ptr() for l in range(L)]
-    vp = [vnew[l].data_ptr() for l in range(L)]
-    tp = tables_d.data_ptr()
-
-    def step(t, events=None):
-        sl = slots_step_d[t].data_ptr()
-        cl = ctx_step_d[t].data_ptr()
-        for l in range(L):
-            rc = lib.fkv_append(h, l, kp[l], vp[l], sl, n_seqs, sp)
-            if rc:
-                fa.errors.check(rc)
-            if events is not None:
-                events[l][0].record(stream)
-            rc = lib.fkv_decode_attention(h, l, hq, qp[l], op[l], tp, max_blocks, cl, n_seqs,
-                                          max_ctx, scale, ws.data_ptr(), ws_bytes, sp)
-            if events is not None:
-                events[l][1].record(stream)
-            if rc:
-                fa.errors.check(rc)
-
-    for t in range(W):
-        step(t)
-    torch.cuda.synchronize()
-
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(L)] for _ in range(K)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(K):
-        step(W + i, ev[i])
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    assert pool.take_fault_flags() == 0
-
-    attn_ms = np.array([[a.elapsed_time(b) for a, b in ev[i]] for i in range(K)])
-    per_step_attn_bytes = [attn_bytes(ctx_step[W + i], hq, hkv, d, 2) * L for i in range(K)]
-    total_attn_bytes = float(sum(per_step_attn_bytes))
-    ms_per_step = wall * 1e3 / K
-    value = total_attn_bytes / wall / 1e9
-    launch_bytes = total_attn_bytes / (K * L)
-    launch_ms = float(attn_ms.mean())
-    achieved = launch_bytes / (launch_ms * 1e-3) / 1e9
-    append_tok_s = n_seqs * K / wall  # tokens appended into all L layers per second
-
-    # Calibration: plain device copy of 4 GiB (reported alongside; not the peak).
-    nbytes = 4 << 30
-    a = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-    b = torch.empty_like(a)
-    fa.device_copy(b, a, nbytes)
-    torch.cuda.synchronize()
-    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    c0.record(stream)
-    for _ in range(5):
-        fa.device_copy(b, a, nbytes)
-    c1.record(stream)
-    torch.cuda.synchronize()
-    copy_gbs = 2 * nbytes * 5 / (c0.elapsed_time(c1) * 1e-3) / 1e9
-    del a, b
-
-    traffic = read_traffic(os.path.join(ROOT, "profiles", "decode_attention_llama3_8b_c2_hbm_traffic.md"))
-
-    result = {
-        "metric": "paged decode-attn HBM GB/s (% of peak) + KV append tokens/s, 1xMI355X",
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": K,
-        "warmup": W,
-        "ms_per_step": round(ms_per_step, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f16",
-        "data": "synthetic N(0,1) Q/K/V, seeded; random-permutation block tables",
-        "config": {
-            "workload": "llama3-8b decode step (BASELINE configs[1])",
-            "n_seqs": n_seqs, "n_layers": L, "n_heads": hq, "n_kv_heads": hkv,
-            "head_dim": d, "block_size": bs, "kv_dtype": "f16", "accumulate": "f32",
-            "ctx": "uniform[128,4096] seed %d" % args.seed,
-            "mean_ctx": float(ctx_step[W:].mean()),
-            "parallelism": "single GPU",
-        },
-        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "append_tokens_per_s": round(append_tok_s, 1),
-        "append_token_layers_per_s": round(append_tok_s * L, 1),
-        "bulk_append": {
-            "tokens_per_launch": int(n_fill),
-            "ms_per_launch": round(bulk_append_ms, 4),
-            "token_layers_per_s": round(n_fill / (bulk_append_ms * 1e-3), 1),
-            "gbs": round(append_bytes(n_fill, hkv, d, 2) / (bulk_append_ms * 1e-3) / 1e9, 2),
-        },
-        "device_copy_gbs": round(copy_gbs, 1),
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "fkv_decode_attention (attn_split_kernel + attn_combine_kernel)",
-            "achieved": round(achieved, 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": traffic,
-            "bytes_per_launch": int(launch_bytes),
-            "ms_per_launch": round(launch_ms, 5),
-        },
-        "cpu_baseline": None,
-    }
-
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(pool, tables, ctx_step[W + K - 1], q, out,
-                                              L - 1, hq, hkv, d, bs, args)
+    run = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload]
+    result = run(args, torch, fa, lib, dev)
     print(json.dumps(result), flush=True)
-
-
-def cpu_baseline(pool, tables, ctx, q, out, layer, hq, hkv, d, bs, args):
-    """Oracle AVX2 restatement of the reference attention loop on one full layer
-    of the same pool (copied to host), at 1 thread and at `threads` threads.
-    Also counts GPU outputs outside tolerance on that layer."""
-    from oracle import ref
-    import ferrum_amd as fa
-
-    n_seqs = tables.shape[0]
-    nb = (ctx + bs - 1) // bs
-    used = [int(b) for s in range(n_seqs) for b in tables[s, : nb[s]]]
-    remap = {b: i for i, b in enumerate(used)}
-    lay = ref.Layout(1, hkv, d, bs, len(used), dtype=1)
-    region = lay.block_bytes
-    image = np.empty(lay.pool_bytes, np.uint8)
-    for b, i in remap.items():
-        src = b * pool.block_bytes + layer * region
-        image[i * region:(i + 1) * region] = pool.read(src, region)
-    tab = np.zeros_like(tables)
-    for s in range(n_seqs):
-        tab[s, : nb[s]] = [remap[int(b)] for b in tables[s, : nb[s]]]
-    qh = q[layer].cpu().numpy()
-    gpu_out = out[layer].cpu().numpy()
-    scale = fa.default_scale(d)
-    if not ref.avx2_available():
-        return None
-    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-    bytes_layer = attn_bytes(ctx, hq, hkv, d, 2)
-    t0 = time.perf_counter()
-    o1 = ref.avx2_attention(lay, image, 0, qh, tab, ctx.astype(np.int32), scale, 1)
-    t1 = time.perf_counter() - t0
-    reps = 3
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        on = ref.avx2_attention(lay, image, 0, qh, tab, ctx.astype(np.int32), scale, threads)
-    tn = (time.perf_counter() - t0) / reps
-    err = np.abs(gpu_out.astype(np.float64) - o1)
-    bad = int((err > 2e-3 + 1e-2 * np.abs(o1)).sum())
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    assert np.array_equal(o1, on)
-    return {
-        "value": round(bytes_layer / tn / 1e9, 3),
-        "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
-        "sample": (f"1 of 32 layers (all {n_seqs} seqs, {int(ctx.sum())} tokens, "
-                   f"{bytes_layer / 1e6:.1f} MB algorithmic), AVX2 restatement of "
-                   "llama.rs:220-247 (per query head, no GQA reuse); "
-                   f"{reps} reps at {threads} threads"),
-        "value_1thread": round(bytes_layer / t1 / 1e9, 3),
-        "seconds_1thread": round(t1, 3),
-        "seconds_threads": round(tn, 3),
-        "cpu_model": model,
-        "host_cpus": os.cpu_count(),
-        "gpu_vs_cpu_out_of_tolerance": bad,
-        "gpu_vs_cpu_max_abs_err": float(err.max()),
-    }
 
 
 if __name__ == "__main__":

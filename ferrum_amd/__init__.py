@@ -4,15 +4,17 @@ The product is ``libferrum_kv.so`` (HIP kernels + C ABI, include/ferrum_kv.h);
 this package binds it and mirrors Ferrum's KvPool interface on the host.
 """
 from . import _lib
-from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8_0, GATHER_F32, GATHER_RAW,
-                   ROUND_HALF_AWAY, ROUND_NEAREST_EVEN)
+from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8_0, FAULT_BLOCK_RANGE, FAULT_CTX_RANGE,
+                   FAULT_SLOT_RANGE, GATHER_F32, GATHER_RAW, ROUND_HALF_AWAY,
+                   ROUND_NEAREST_EVEN)
 from .errors import (CacheError, FerrumError, InternalError, InvalidRequest, KernelError,
                      Unavailable)
 from .kvcache import (KvPoolConfig, PagedConfig, PagedKvPool, PreallocatedKvPool,
                       default_scale, device_copy)
 
 __all__ = [
-    "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
+    "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "FAULT_BLOCK_RANGE", "FAULT_CTX_RANGE",
+    "FAULT_SLOT_RANGE", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
     "ROUND_NEAREST_EVEN", "CacheError", "FerrumError", "InternalError", "InvalidRequest",
     "KernelError", "Unavailable", "KvPoolConfig", "PagedConfig", "PagedKvPool",
     "PreallocatedKvPool", "default_scale", "device_copy", "load_library",

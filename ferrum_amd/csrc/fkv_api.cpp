@@ -415,11 +415,12 @@ int32_t fkv_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_hea
   return ok();
 }
 
-int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,
-                             float* out, const int32_t* block_tables,
-                             uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
-                             uint32_t n_seqs, uint32_t max_ctx_len, float scale,
-                             void* workspace, uint64_t workspace_bytes, void* stream) {
+static int32_t decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                                const float* k_new, const float* v_new, const float* q,
+                                float* out, const int32_t* block_tables,
+                                uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                                uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                                void* workspace, uint64_t workspace_bytes, void* stream) {
   if (!pool) return fail(FKV_ERR_INVALID, "null argument");
   if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
   int32_t st = check_attention(pool, n_heads, max_ctx_len);
@@ -433,14 +434,48 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, c
     return fail(FKV_ERR_INVALID, "max_ctx_len exceeds the block table");
   DeviceGuard dg(pool->cfg.device);
   const uint64_t need =
-      fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
+      k_new ? fkv::append_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len)
+            : fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
   if (workspace_bytes < need || (need && !workspace))
     return fail(FKV_ERR_INVALID, "attention workspace too small");
   FKV_HIP(fkv::launch_decode_attention(pool->geom, layer, n_heads, q, out, block_tables,
                                        max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale,
-                                       workspace, (hipStream_t)stream),
+                                       workspace, k_new, v_new, (hipStream_t)stream),
           "decode_attention");
   return ok();
+}
+
+int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,
+                             float* out, const int32_t* block_tables,
+                             uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                             uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                             void* workspace, uint64_t workspace_bytes, void* stream) {
+  return decode_attention(pool, layer, n_heads, nullptr, nullptr, q, out, block_tables,
+                          max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale, workspace,
+                          workspace_bytes, stream);
+}
+
+int32_t fkv_append_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                                   uint32_t n_seqs, uint32_t max_ctx_len,
+                                                   uint64_t* bytes_out) {
+  if (!pool || !bytes_out) return fail(FKV_ERR_INVALID, "null argument");
+  int32_t st = check_attention(pool, n_heads, max_ctx_len);
+  if (st) return st;
+  DeviceGuard dg(pool->cfg.device);
+  *bytes_out = fkv::append_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
+  return ok();
+}
+
+int32_t fkv_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                                    const float* k_new, const float* v_new, const float* q,
+                                    float* out, const int32_t* block_tables,
+                                    uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                                    uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                                    void* workspace, uint64_t workspace_bytes, void* stream) {
+  if (n_seqs && (!k_new || !v_new)) return fail(FKV_ERR_INVALID, "null argument");
+  return decode_attention(pool, layer, n_heads, k_new, v_new, q, out, block_tables,
+                          max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale, workspace,
+                          workspace_bytes, stream);
 }
 
 int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,

@@ -862,14 +862,19 @@ struct AttnPlan {
 inline uint64_t align256(uint64_t x) { return (x + 255) / 256 * 256; }
 
 // Split length: long enough that the final cross-split merge stays small
-// (<= 64 splits at the longest context), short enough that mixed batches give
-// several workgroups per CU. FKV_ATTN_SPLIT_TOKENS (a multiple of 256) overrides.
-uint32_t choose_split_tokens(uint32_t max_ctx_len) {
+// (<= 64 splits per sequence when there are many sequences), short enough that
+// the launch has thousands of workgroups: a batch of few sequences may split
+// further, up to ~4096 (sequence, KV head, split) workgroups, never below 512
+// tokens. FKV_ATTN_SPLIT_TOKENS (a multiple of 16) overrides.
+uint32_t choose_split_tokens(uint32_t max_ctx_len, uint32_t n_seqs, uint32_t n_kv_heads) {
   if (const char* e = getenv("FKV_ATTN_SPLIT_TOKENS")) {
     long v = strtol(e, nullptr, 10);
     if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) return (uint32_t)v;
   }
-  uint64_t st = ((uint64_t)max_ctx_len / 64 + 255) / 256 * 256;
+  const uint64_t segs = (uint64_t)n_seqs * (n_kv_heads ? n_kv_heads : 1);
+  uint64_t max_splits = segs ? 4096 / segs : 64;
+  if (max_splits < 64) max_splits = 64;
+  uint64_t st = (((uint64_t)max_ctx_len + max_splits - 1) / max_splits + 255) / 256 * 256;
   if (st < 512) st = 512;
   if (st > 8192) st = 8192;
   return (uint32_t)st;
@@ -895,7 +900,8 @@ AttnPlan plan_attention(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32
   }
   p.mfma_path = g.dtype == kDtypeF16 && G >= 1 && G <= 16;
   p.split_path = g.dtype == kDtypeQ8 && G >= 1 && G <= 8;
-  p.split_tokens = (p.mfma_path || p.split_path) ? choose_split_tokens(max_ctx_len) : kAttnPartTokens;
+  p.split_tokens = (p.mfma_path || p.split_path) ? choose_split_tokens(max_ctx_len, n_seqs, g.n_kv_heads)
+                                                    : kAttnPartTokens;
   p.max_splits = max_ctx_len ? (max_ctx_len + p.split_tokens - 1) / p.split_tokens : 1;
   if (p.max_splits <= 1) return p;  // single split: no workspace
   const uint64_t items = (uint64_t)n_seqs * n_heads * p.max_splits;
@@ -943,15 +949,63 @@ uint64_t attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_s
   return plan_attention(g, n_heads, n_seqs, max_ctx_len).total;
 }
 
+uint64_t append_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
+                                          uint32_t max_ctx_len) {
+  const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
+  if (p.mfma_path) return p.total;  // appended inside the attention kernel
+  return p.total + align256((uint64_t)n_seqs * sizeof(int64_t));
+}
+
+namespace {
+
+__global__ void __launch_bounds__(256) tail_slots_kernel(Geom g, const int32_t* __restrict__ tables,
+                                                         uint32_t max_blocks,
+                                                         const int32_t* __restrict__ ctx_lens,
+                                                         uint32_t n_seqs, int64_t* __restrict__ slots) {
+  const uint32_t s = blockIdx.x * 256u + threadIdx.x;
+  if (s >= n_seqs) return;
+  const int32_t ctx = ctx_lens[s];
+  const int64_t cap = (int64_t)max_blocks * g.block_size;
+  int64_t slot = -1;
+  if (ctx > 0 && ctx <= cap) {
+    const int32_t pos = ctx - 1;
+    const int32_t pb = tables[(uint64_t)s * max_blocks + (uint32_t)pos / g.block_size];
+    if (pb >= 0 && (uint64_t)pb < g.num_blocks)
+      slot = (int64_t)pb * g.block_size + pos % (int32_t)g.block_size;
+    else
+      raise_fault(g.fault, kFaultBlock);
+  }
+  slots[s] = slot;
+}
+
+}  // namespace
+
+hipError_t launch_tail_slots(const Geom& g, const int32_t* tables, uint32_t max_blocks,
+                             const int32_t* ctx_lens, uint32_t n_seqs, int64_t* slots,
+                             hipStream_t s) {
+  tail_slots_kernel<<<(n_seqs + 255) / 256, 256, 0, s>>>(g, tables, max_blocks, ctx_lens, n_seqs,
+                                                          slots);
+  return hipGetLastError();
+}
+
 hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
                                    const float* q, float* out, const int32_t* tables,
                                    uint32_t max_blocks, const int32_t* ctx_lens,
                                    uint32_t n_seqs, uint32_t max_ctx_len, float scale,
-                                   void* workspace, hipStream_t s) {
+                                   void* workspace, const float* k_new, const float* v_new,
+                                   hipStream_t s) {
   if (n_seqs == 0) return hipSuccess;
   const uint32_t G = n_heads / g.n_kv_heads;
   const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
   uint8_t* ws = (uint8_t*)workspace;
+  if (k_new != nullptr && !p.mfma_path) {
+    // Separate append launch: slots derived from the block tables first.
+    int64_t* slots = (int64_t*)(ws + p.total);
+    hipError_t e = launch_tail_slots(g, tables, max_blocks, ctx_lens, n_seqs, slots, s);
+    if (e == hipSuccess) e = launch_append(g, layer, k_new, v_new, slots, n_seqs, s);
+    if (e != hipSuccess) return e;
+    k_new = v_new = nullptr;
+  }
   if (p.stream_path)
     return launch_attention_stream(g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
                                    n_seqs, scale, p.stream_waves, (uint32_t*)(ws + p.pre_off),
@@ -961,7 +1015,7 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
     float* ws_ml = ws ? (float*)(ws + p.ml_off) : nullptr;
     hipError_t e = launch_attention_mfma(g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
                                          n_seqs, p.max_splits, p.split_tokens, scale, ws_o,
-                                         ws_ml, s);
+                                         ws_ml, k_new, v_new, s);
     if (e != hipSuccess || p.max_splits <= 1) return e;
     return launch_attention_combine(g.head_dim, ctx_lens, n_seqs, n_heads, max_blocks,
                                     p.max_splits, p.split_tokens, ws_o, ws_ml, out, s);

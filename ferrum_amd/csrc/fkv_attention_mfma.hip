@@ -562,18 +562,21 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
     const int32_t* __restrict__ ctx_lens, uint32_t max_splits, int32_t split_tokens,
-    float scale, float* __restrict__ ws_o, float* __restrict__ ws_ml) {
+    float scale, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    const float* __restrict__ k_new, const float* __restrict__ v_new) {
   constexpr int NC = D / 32, NM = D / 16;
 
   __shared__ float s_o[kAttnWaves][kHeads * D];
   __shared__ float s_m[kAttnWaves][kHeads];
   __shared__ float s_l[kAttnWaves][kHeads];
+  __shared__ __align__(16) uint16_t s_app[2][D];  // fused append: encoded K, V rows
 
   const uint32_t sk = blockIdx.x;
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int32_t cap = (int32_t)(max_blocks * B);
   int32_t ctx = ctx_lens[seq];
-  if (ctx < 0 || ctx > cap) {
+  const bool ctx_ok = ctx >= 0 && ctx <= cap;
+  if (!ctx_ok) {
     if (blockIdx.y == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
     ctx = ctx < 0 ? 0 : cap;
   }
@@ -593,6 +596,31 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
   const int32_t blk0 = s0 / B;
+
+  // Fused append (k_new != nullptr): the token at position ctx - 1 of this KV
+  // head is stored by the wave of the last split that reads its block. That wave
+  // encodes the token (f32 -> binary16 with the pool's rounding) up front and,
+  // when it reaches the block, puts the encoded values into its K and V operands
+  // in place of what it loaded and stores them to the pool. No other workgroup
+  // reads the position, and this one never reads back what it stores, so the
+  // stores need no ordering.
+  const bool app = k_new != nullptr && split == nsplits - 1 && ctx > 0 && ctx_ok;
+  const int32_t app_pos = ctx - 1;
+  const int32_t app_lb = app ? app_pos / B - blk0 : -1;  // block of the split
+  const bool app_wave = app && app_lb % kAttnWaves == wave;
+  const int32_t app_t = app_lb / kAttnWaves;             // the wave's block index
+  const int32_t app_off = app_pos % B;                   // token within the block
+  if (app_wave) {  // encoded K and V rows of the token to s_app (the wave's own LDS use)
+    const float* ksrc = k_new + ((uint64_t)seq * g.n_kv_heads + kvh) * D;
+    const float* vsrc = v_new + ((uint64_t)seq * g.n_kv_heads + kvh) * D;
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) {
+      const int dd = i * 64 + ln.lane;
+      s_app[0][dd] = (uint16_t)encode_f16(ksrc[dd], g.rounding);
+      s_app[1][dd] = (uint16_t)encode_f16(vsrc[dd], g.rounding);
+    }
+  }
+
   Accum<D> st;
   st.reset();
 
@@ -631,6 +659,15 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     const bool live = blive[b];
     const bool refill = t + NBUF < nt;
     const int32_t t0 = s0 + (wave + kAttnWaves * t) * B;  // first token of the block
+    const bool patch = app_wave && t == app_t && live;
+    if (patch && ln.col == app_off) {  // K tile [D/8][B][8]: run c*4 + grp of the token
+      uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        kr[b][c] = *(const uint4*)&s_app[0][c * 32 + ln.grp * 8];
+        *(uint4*)(kt + ((uint64_t)(c * 4 + ln.grp) * B + app_off) * 16) = kr[b][c];
+      }
+    }
     float s[4];
     qk_block<D>(kr[b], qh, ql, hscale, ln, live, t0, s1, s);
     if (refill) {
@@ -638,6 +675,18 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
       load_k<D>(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln, kr[b]);
     }
     const f16x4 pw = softmax_block<D>(s, ln, st);
+    if (patch && ln.grp == app_off / 4) {  // V tile [D][B]: dim 16m + col, token app_off
+      uint16_t* vt = (uint16_t*)tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
+      const int sh = (app_off & 1) * 16;
+      const uint32_t keep = ~(0xffffu << sh);
+#pragma unroll
+      for (int m = 0; m < NM; m++) {
+        const uint32_t h = s_app[1][m * 16 + ln.col];
+        if (app_off & 2) vr[b][m].y = (vr[b][m].y & keep) | (h << sh);
+        else vr[b][m].x = (vr[b][m].x & keep) | (h << sh);
+        vt[(uint64_t)(m * 16 + ln.col) * B + app_off] = (uint16_t)h;
+      }
+    }
     if (live) pv_block<D>(vr[b], pw, ln, t0, s1, st);
     if (refill) load_v<D>(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln, vr[b]);
   };
@@ -891,18 +940,21 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
                                  const float* q, float* out, const int32_t* tables,
                                  uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
                                  uint32_t max_splits, uint32_t split_tokens, float scale,
-                                 float* ws_o, float* ws_ml, hipStream_t s) {
+                                 float* ws_o, float* ws_ml, const float* k_new,
+                                 const float* v_new, hipStream_t s) {
   const uint32_t G = n_heads / g.n_kv_heads;
   dim3 grid(n_seqs * g.n_kv_heads, max_splits);
   constexpr int NBUF = FKV_MFMA_RING;
   if (g.head_dim == 128)
     attn_mfma_kernel<128, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,
                                                      max_blocks, ctx_lens, max_splits,
-                                                     (int32_t)split_tokens, scale, ws_o, ws_ml);
+                                                     (int32_t)split_tokens, scale, ws_o, ws_ml,
+                                                     k_new, v_new);
   else
     attn_mfma_kernel<64, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,
                                                     max_blocks, ctx_lens, max_splits,
-                                                    (int32_t)split_tokens, scale, ws_o, ws_ml);
+                                                    (int32_t)split_tokens, scale, ws_o, ws_ml,
+                                                     k_new, v_new);
   return hipGetLastError();
 }
 

@@ -70,12 +70,14 @@ hipError_t launch_device_copy(void* dst, const void* src, uint64_t bytes, hipStr
 // Returns hipErrorInvalidValue when no kernel is instantiated for the shape.
 bool attention_supported(int dtype, uint32_t head_dim, uint32_t group);
 // F16 decode attention on the matrix cores (fkv_attention_mfma.hip); head_dim 64
-// or 128, any group size 1..16.
+// or 128, any group size 1..16. With k_new/v_new (f32 [n_seqs][n_kv_heads][D])
+// the kernel first appends each sequence's token at position ctx_lens[s] - 1.
 hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads,
                                  const float* q, float* out, const int32_t* tables,
                                  uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
                                  uint32_t max_splits, uint32_t split_tokens, float scale,
-                                 float* ws_o, float* ws_ml, hipStream_t s);
+                                 float* ws_o, float* ws_ml, const float* k_new,
+                                 const float* v_new, hipStream_t s);
 // F16 decode attention, persistent schedule (fkv_attention_mfma.hip): n_waves
 // waves share the flattened (sequence, KV head, block) list equally; needs
 // 1 <= n_seqs <= kStreamMaxSeqs (the LDS prefix table). ws_pre holds n_seqs + 1
@@ -105,14 +107,26 @@ hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
                                     uint32_t max_splits, uint32_t split_tokens,
                                     const float* ws_o, const float* ws_ml, float* out,
                                     hipStream_t s);
+// k_new/v_new non-null: append each sequence's token at position ctx_lens[s] - 1
+// (through its block table) before attending; one launch for F16 storage.
 hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
                                    const float* q, float* out, const int32_t* tables,
                                    uint32_t max_blocks, const int32_t* ctx_lens,
                                    uint32_t n_seqs, uint32_t max_ctx_len, float scale,
-                                   void* workspace, hipStream_t s);
+                                   void* workspace, const float* k_new, const float* v_new,
+                                   hipStream_t s);
+// Slot of position ctx_lens[s] - 1 through the block table (-1 for an empty
+// context or an entry outside the pool, which raises kFaultBlock).
+hipError_t launch_tail_slots(const Geom& g, const int32_t* tables, uint32_t max_blocks,
+                             const int32_t* ctx_lens, uint32_t n_seqs, int64_t* slots,
+                             hipStream_t s);
 // Device scratch one call needs (0 when every sequence fits one split): the
 // split partials, which need no initialisation.
 uint64_t attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
                                    uint32_t max_ctx_len);
+// Workspace of the fused append + attention call: the above, plus the derived
+// slots for the storage types whose append is a separate launch.
+uint64_t append_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
+                                          uint32_t max_ctx_len);
 
 }  // namespace fkv

@@ -254,6 +254,29 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
                              uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                              void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* Decode step of one layer in one call: the append of Llama::forward_one_token
+ * (crates/model/src/llama.rs:218, KvPool::append_layer of kv.rs:30-38) followed by
+ * its attention loop (:220-247), which reads the token just appended. For each
+ * sequence s with ctx_lens[s] > 0, k_new[s] and v_new[s] (device f32
+ * [n_seqs][n_kv_heads][head_dim], post-RoPE K) are stored at position
+ * ctx_lens[s] - 1 through block_tables (encoded like fkv_append), then decode
+ * attention runs over ctx_lens[s] positions exactly as fkv_decode_attention.
+ * The block holding that position must belong to sequence s alone (copy it with
+ * fkv_copy_blocks first if it is shared). For F16 storage this is one kernel
+ * launch: the workgroup that reads the sequence's last context split stores the
+ * token before loading it. Other storage types use an append launch first.
+ * workspace: fkv_append_decode_attention_workspace_size() bytes, same rules as
+ * the decode-attention workspace. */
+int32_t fkv_append_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                                   uint32_t n_seqs, uint32_t max_ctx_len,
+                                                   uint64_t* bytes_out);
+int32_t fkv_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                                    const float* k_new, const float* v_new, const float* q,
+                                    float* out, const int32_t* block_tables,
+                                    uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                                    uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                                    void* workspace, uint64_t workspace_bytes, void* stream);
+
 /* Chunked-prefill attention over F16 storage: the reference's token-by-token
  * prefill (crates/model/src/llama.rs:363-378, each token running the attention
  * loop of :220-247 over positions 0 ..= its own) for a chunk whose K/V are
