@@ -330,6 +330,8 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 // One wave per (sequence, query head), four per workgroup, no LDS: lane p holds
 // partition p's (m, l) (64 partitions per pass), every lane holds D/64 dims, and
 // the partial-output loads of a pass are issued before its maximum is known.
+// Heads with many partitions (few sequences, long contexts) use
+// attn_combine_wide_kernel instead.
 template <int D>
 __global__ void __launch_bounds__(256) attn_combine_kernel(
     const int32_t* __restrict__ ctx_lens, uint32_t n_seq_heads, uint32_t n_heads,
@@ -417,6 +419,85 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
   const float inv = 1.0f / lsum;
 #pragma unroll
   for (int i = 0; i < DPL; i++) o[i] = acc[i] * inv;
+}
+
+// The same merge with one 16-wave workgroup per (sequence, query head): wave w
+// takes partitions w, w + 16, ..., each lane D/64 dims, and the waves' (l, o) are
+// summed through LDS. For heads with more than kWideParts partitions (few
+// sequences with long contexts), where one wave per head would walk hundreds of
+// partitions one latency after another.
+constexpr uint32_t kWideParts = 32;
+constexpr int kWideWaves = 16;
+template <int D>
+__global__ void __launch_bounds__(64 * kWideWaves) attn_combine_wide_kernel(
+    const int32_t* __restrict__ ctx_lens, uint32_t n_heads, uint32_t max_blocks,
+    uint32_t max_parts, int32_t part_tokens, const float* __restrict__ ws_o,
+    const float* __restrict__ ws_ml, float* __restrict__ out) {
+  constexpr int DPL = D / 64;
+  constexpr int kUnroll = 8;
+  constexpr int W = kWideWaves;
+  __shared__ float s_l[W];
+  __shared__ float s_acc[W][D];
+  const uint32_t head = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const uint32_t seq = head / n_heads;
+  const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
+  int32_t ctx = ctx_lens[seq];
+  ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int32_t nparts = ctx > 0 ? (ctx + part_tokens - 1) / part_tokens : 1;
+  if (nparts == 1) return;
+  const float* ml = ws_ml + (uint64_t)head * max_parts * 2;
+  const float* po = ws_o + (uint64_t)head * max_parts * D + lane * DPL;
+  float* o = out + (uint64_t)head * D;
+
+  // maximum over all partitions (every wave computes it; the loads hit in cache)
+  float M = -__builtin_inff();
+  for (int32_t p = lane; p < nparts; p += 64) M = __builtin_fmaxf(M, ml[2 * p]);
+  M = wave_max(M);
+  if (!__builtin_isfinite(M)) {
+    if (wave == 0)
+#pragma unroll
+      for (int i = 0; i < DPL; i++) o[lane * DPL + i] = 0.0f;
+    return;
+  }
+  float acc[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; i++) acc[i] = 0.0f;
+  float lsum = 0.0f;
+  for (int32_t p0 = wave; p0 < nparts; p0 += W * kUnroll) {
+    float v[kUnroll][DPL], w[kUnroll], l[kUnroll];
+#pragma unroll
+    for (int j = 0; j < kUnroll; j++) {
+      const int32_t p = p0 + W * j;
+      const bool ok = p < nparts;
+      w[j] = ok ? ml[2 * p] : -__builtin_inff();
+      l[j] = ok ? ml[2 * p + 1] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < DPL; i++) v[j][i] = ok ? po[(uint64_t)p * D + i] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < kUnroll; j++) {
+      if (p0 + W * j < nparts) {
+        const float wt = __builtin_amdgcn_exp2f((w[j] - M) * kLog2e);
+        lsum = __builtin_fmaf(wt, l[j], lsum);
+#pragma unroll
+        for (int i = 0; i < DPL; i++) acc[i] = __builtin_fmaf(wt, v[j][i], acc[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < DPL; i++) s_acc[wave][lane * DPL + i] = acc[i];
+  if (lane == 0) s_l[wave] = lsum;
+  __syncthreads();
+  if (threadIdx.x < D) {
+    float a = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int k = 0; k < W; k++) {
+      a += s_acc[k][threadIdx.x];
+      L += s_l[k];
+    }
+    o[threadIdx.x] = a * (1.0f / L);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -836,6 +917,15 @@ hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
                                     const float* ws_o, const float* ws_ml, float* out,
                                     hipStream_t s) {
   const uint32_t nh = n_seqs * n_heads, grid = (nh + 3) / 4;
+  if (max_splits > kWideParts) {
+    if (head_dim == 128)
+      attn_combine_wide_kernel<128><<<nh, 64 * kWideWaves, 0, s>>>(
+          ctx_lens, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
+    else
+      attn_combine_wide_kernel<64><<<nh, 64 * kWideWaves, 0, s>>>(
+          ctx_lens, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
+    return hipGetLastError();
+  }
   if (head_dim == 128)
     attn_combine_kernel<128><<<grid, 256, 0, s>>>(
         ctx_lens, nh, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);
