@@ -917,7 +917,7 @@ hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
                                     const float* ws_o, const float* ws_ml, float* out,
                                     hipStream_t s) {
   const uint32_t nh = n_seqs * n_heads, grid = (nh + 3) / 4;
-  if (max_splits > kWideParts) {
+  if (max_splits > kWideParts && nh < 2048) {  // few heads with many splits each
     if (head_dim == 128)
       attn_combine_wide_kernel<128><<<nh, 64 * kWideWaves, 0, s>>>(
           ctx_lens, n_heads, max_blocks, max_splits, (int32_t)split_tokens, ws_o, ws_ml, out);

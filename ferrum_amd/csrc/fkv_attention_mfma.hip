@@ -51,6 +51,13 @@
 #include "fkv_device.h"
 #include "fkv_internal.h"
 
+// K/V blocks in flight (register stages) of the chunked-prefill kernel. One
+// measured fastest on MI355X: deeper rings cost a wave per SIMD of occupancy and
+// the kernel is bound by issue, not by memory latency.
+#ifndef FKV_PREFILL_STAGES
+#define FKV_PREFILL_STAGES 1
+#endif
+
 // Blocks in flight per wave (the load ring depth) of attn_mfma_kernel.
 #ifndef FKV_MFMA_RING
 #define FKV_MFMA_RING 1
@@ -761,22 +768,34 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
 // The reference prefills token by token (crates/model/src/llama.rs:363-378), each
 // token running the attention loop of :220-247 over positions 0 ..= its own.
 // Here the chunk's K/V are already in the pool, and the 16 MFMA columns carry
-// query rows instead of heads: column c of a tile is (token c / G, head c % G)
-// for 16 / G consecutive query tokens, each with its own causal end. QK, the
-// softmax reductions (over the 4 lanes of a column) and PV are the decode step
-// unchanged. One wave per tile; 4 tiles per workgroup, no LDS.
-template <int D>
+// query rows instead of heads: column c of a wave's tile is (token c / G, head
+// c % G) for 16 / G consecutive query tokens, each with its own causal end. QK,
+// the softmax reductions (over the 4 lanes of a column) and PV are the decode
+// step unchanged.
+//
+// A workgroup holds 4 consecutive tiles (4 waves) of one (sequence, KV head) and
+// streams the blocks up to its furthest causal end once: the 256 threads load
+// block j + 1 (K and V tiles, 16 bytes per thread per load) into registers while
+// the waves compute block j from LDS, then store it to the other half of a
+// double buffer. Every K/V byte is read from memory once per 4 tiles instead of
+// once per tile; the operand reads come from LDS in the same orders as the
+// decode kernel's global loads.
+template <int D, int NS>
 __global__ void __launch_bounds__(256) attn_prefill_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
     const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ q_lens,
     const int64_t* __restrict__ q_offsets, float scale) {
   constexpr int NC = D / 32, NM = D / 16;
+  constexpr int kTileBytes = B * D * 2;             // one f16 K or V tile
+  constexpr int kLoads = 2 * kTileBytes / (256 * 16);  // 16-byte loads per thread per block
+  static_assert(kLoads >= 1 && kLoads * 256 * 16 == 2 * kTileBytes, "block staging");
+  __shared__ __align__(16) uint8_t s_kv[2][2 * kTileBytes];  // [buffer][K tile | V tile]
+
   const uint32_t sk = blockIdx.x;
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int32_t tile = (int32_t)blockIdx.y * kAttnWaves + wave;
-  const int32_t T = 16 / (int32_t)G;  // query tokens per tile
+  const int32_t T = 16 / (int32_t)G;  // query tokens per wave tile
   const int32_t cap = (int32_t)(max_blocks * B);
   int32_t ctx = ctx_lens[seq];
   int32_t ql = q_lens[seq];
@@ -785,19 +804,25 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
     ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
     ql = ql < 0 ? 0 : (ql > ctx ? ctx : ql);
   }
-  if (tile * T >= ql) return;
+  const int32_t tile0 = (int32_t)blockIdx.y * kAttnWaves;  // first tile of the workgroup
+  if (tile0 * T >= ql) return;                              // uniform over the workgroup
+  const int32_t tile = tile0 + wave;
   const int32_t p0 = ctx - ql;  // position of query 0
+  const bool wave_on = tile * T < ql;
 
   Lane ln;
   ln.lane = threadIdx.x & 63;
   ln.col = ln.lane & 15;
   ln.grp = ln.lane >> 4;
   const int32_t jcol = tile * T + ln.col / (int32_t)G;  // query token of this column
-  ln.real = ln.col < T * (int32_t)G && jcol < ql;
+  ln.real = wave_on && ln.col < T * (int32_t)G && jcol < ql;
   const int32_t end_col = p0 + jcol + 1;                // causal end of the column
   const int32_t jlast = tile * T + T - 1 < ql - 1 ? tile * T + T - 1 : ql - 1;
-  const int32_t end_max = p0 + jlast + 1;              // furthest end in the tile
-  const int32_t nblk = (end_max + B - 1) / B;
+  const int32_t end_max = wave_on ? p0 + jlast + 1 : 0;  // furthest end of the wave's tile
+  const int32_t nblk_w = (end_max + B - 1) / B;
+  // the workgroup's furthest end: its last tile's last query (or the chunk's last)
+  const int32_t wg_last = (tile0 + kAttnWaves) * T - 1 < ql - 1 ? (tile0 + kAttnWaves) * T - 1 : ql - 1;
+  const int32_t nblk = (p0 + wg_last + 1 + B - 1) / B;
   const int64_t qrow0 = q_offsets[seq];
   auto row_of = [&](int32_t colv) {  // q/out row of column colv (clamped for padding)
     const int32_t j = tile * T + colv / (int32_t)G;
@@ -806,42 +831,103 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   };
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
+  // Physical block j (uniform); an entry outside the pool raises the fault flag,
+  // stages block 0 instead and is skipped.
   auto phys = [&](int32_t j, bool& ok) {
     const int32_t p = __builtin_amdgcn_readfirstlane(table[j]);
     ok = p >= 0 && (uint64_t)p < g.num_blocks;
-    if (!ok && ln.lane == 0) raise_fault(g.fault, kFaultBlock);
+    if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
     return ok ? (uint64_t)p : 0;
   };
+  // Thread t stages bytes [t*16, t*16 + 16) of every 4 KiB of the block's K|V pair.
+  // Pipeline: block j is computed from LDS buffer j & 1 while blocks j+1 .. j+NS
+  // are in flight in a ring of NS register stages (block b >= 1 in stage
+  // (b - 1) % NS). At the end of step j, block j+1 goes from its stage to the other
+  // LDS buffer (its loads were issued NS steps earlier), the barrier publishes it,
+  // and the freed stage takes block j+1+NS.
+  uint4 stage[NS][kLoads];
+  bool slive[NS];
+  auto load_block = [&](uint4 (&st_)[kLoads], uint64_t p) {
+    const uint8_t* kt = tile_ptr(g, p, layer, 0, kvh);
+    const uint8_t* vt = tile_ptr(g, p, layer, 1, kvh);
+#pragma unroll
+    for (int i = 0; i < kLoads; i++) {
+      const uint32_t off = (uint32_t)(i * 256 + threadIdx.x) * 16u;
+      st_[i] = load_stream16(off < (uint32_t)kTileBytes ? kt + off : vt + (off - kTileBytes));
+    }
+  };
+  // K is staged as loaded. V rows (one dim, 16 tokens = four 8-byte chunks) are
+  // stored with chunk c at c ^ ((dim >> 2) & 3), so the P.V operand reads (lanes
+  // 16 dims x 4 chunks) hit distinct banks; a 16-byte pair of chunks stays one
+  // aligned 16-byte unit, its halves swapped when the swizzle is odd.
+  auto store_block = [&](const uint4 (&st_)[kLoads], int buf) {
+#pragma unroll
+    for (int i = 0; i < kLoads; i++) {
+      const uint32_t off = (uint32_t)(i * 256 + threadIdx.x) * 16u;
+      if (off < (uint32_t)kTileBytes) {
+        *(uint4*)&s_kv[buf][off] = st_[i];
+      } else {
+        const uint32_t v = off - kTileBytes, dim = v / 32u, unit = (v % 32u) / 16u;
+        const uint32_t sw = (dim >> 2) & 3u;
+        const uint4 x = st_[i];
+        *(uint4*)&s_kv[buf][kTileBytes + dim * 32u + ((unit ^ (sw >> 1)) * 16u)] =
+            (sw & 1u) ? make_uint4(x.z, x.w, x.x, x.y) : x;
+      }
+    }
+  };
 
-  uint4 kr[NC];
-  u32x2_t vr[NM];
-  bool live = false;
+  bool live = false;  // block in the LDS buffer being computed
   {
-    const uint64_t p = phys(0, live);
-    load_k<D>(tile_ptr(g, p, layer, 0, kvh), ln, kr);
-    load_v<D>(tile_ptr(g, p, layer, 1, kvh), ln, vr);
+    uint4 st0[kLoads];
+    load_block(st0, nblk > 0 ? phys(0, live) : 0);
+#pragma unroll
+    for (int sl = 0; sl < NS; sl++)
+      if (1 + sl < nblk) load_block(stage[sl], phys(1 + sl, slive[sl]));
+    store_block(st0, 0);
   }
   f16x8 qh[NC], qlo[NC];
   float hscale;
   prep_q<D>(q + row_of(ln.real ? ln.col : 0), ln, scale * kLog2e, qh, qlo, hscale);
   Accum<D> st;
   st.reset();
+  __syncthreads();
 
-  for (int32_t j = 0; j < nblk; j++) {
-    const bool more = j + 1 < nblk;
-    const int32_t t0 = j * B;
-    float s[4];
-    qk_block<D>(kr, qh, qlo, hscale, ln, live, t0, end_col, s);
-    const bool cur_live = live;
-    uint64_t np = 0;
-    if (more) {
-      np = phys(j + 1, live);
-      load_k<D>(tile_ptr(g, np, layer, 0, kvh), ln, kr);
+  for (int32_t j0 = 0; j0 < nblk; j0 += NS) {
+#pragma unroll
+    for (int sl = 0; sl < NS; sl++) {
+      const int32_t j = j0 + sl;
+      if (j < nblk) {
+        const int buf = j & 1;
+        if (j < nblk_w) {  // wave-uniform: blocks past the wave's tile are skipped
+          const uint8_t* ks = s_kv[buf];
+          const uint8_t* vs = s_kv[buf] + kTileBytes;
+          uint4 kr[NC];
+          u32x2_t vr[NM];
+#pragma unroll
+          for (int c = 0; c < NC; c++)
+            kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
+          const int32_t t0 = j * B;
+          float sc[4];
+          qk_block<D>(kr, qh, qlo, hscale, ln, live, t0, end_col, sc);
+#pragma unroll
+          for (int m = 0; m < NM; m++) {
+            const uint32_t dim = (uint32_t)(m * 16 + ln.col);
+            vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((uint32_t)ln.grp ^ ((dim >> 2) & 3u)) * 8u));
+          }
+          const f16x4 pw = softmax_block<D>(sc, ln, st);
+          if (live) pv_block<D>(vr, pw, ln, t0, end_max, st);
+        }
+        if (j + 1 < nblk) {
+          // the other buffer was last read before the previous barrier
+          store_block(stage[sl], buf ^ 1);
+          live = slive[sl];
+          __syncthreads();
+          if (j + 1 + NS < nblk) load_block(stage[sl], phys(j + 1 + NS, slive[sl]));
+        }
+      }
     }
-    const f16x4 pw = softmax_block<D>(s, ln, st);
-    if (cur_live) pv_block<D>(vr, pw, ln, t0, end_max, st);
-    if (more) load_v<D>(tile_ptr(g, np, layer, 1, kvh), ln, vr);
   }
+  if (!wave_on) return;
 
   float lsum = st.l_part;
   lsum += __shfl_xor(lsum, 16);
@@ -928,10 +1014,10 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
   const uint32_t tiles = (max_q_len + T - 1) / T;
   dim3 grid(n_seqs * g.n_kv_heads, (tiles + kAttnWaves - 1) / kAttnWaves);
   if (g.head_dim == 128)
-    attn_prefill_kernel<128><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
+    attn_prefill_kernel<128, FKV_PREFILL_STAGES><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
                                                   ctx_lens, q_lens, q_offsets, scale);
   else
-    attn_prefill_kernel<64><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
+    attn_prefill_kernel<64, FKV_PREFILL_STAGES><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
                                                  ctx_lens, q_lens, q_offsets, scale);
   return hipGetLastError();
 }
