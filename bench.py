@@ -376,7 +376,7 @@ def decode_workload(args, torch, fa, lib, dev, *, name, L, n_seqs, hq, hkv, d, d
     wall, region_ms = dl.run(W, K)
     e = elem_bytes(dtype)
     kname = ("fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)" if dtype == 1
-             else "fkv_append_decode_attention (tail slots + append + attn_split_kernel + combine)")
+             else "fkv_append_decode_attention (tail slots + append + attn_mfma_kernel<q8_0> + combine)")
     res = decode_result(args, dl, W, K, wall, region_ms, e, name, dict(extra_cfg or {}), kname,
                         None)
     if fill_ms:

@@ -5,7 +5,7 @@ this package binds it and mirrors Ferrum's KvPool interface on the host.
 """
 from . import _lib
 from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8_0, FAULT_BLOCK_RANGE, FAULT_CTX_RANGE,
-                   FAULT_SLOT_RANGE, GATHER_F32, GATHER_RAW, ROUND_HALF_AWAY,
+                   FAULT_SLOT_RANGE, FAULT_VALUE_RANGE, GATHER_F32, GATHER_RAW, ROUND_HALF_AWAY,
                    ROUND_NEAREST_EVEN)
 from .errors import (CacheError, FerrumError, InternalError, InvalidRequest, KernelError,
                      Unavailable)
@@ -14,7 +14,7 @@ from .kvcache import (KvPoolConfig, PagedConfig, PagedKvPool, PreallocatedKvPool
 
 __all__ = [
     "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "FAULT_BLOCK_RANGE", "FAULT_CTX_RANGE",
-    "FAULT_SLOT_RANGE", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
+    "FAULT_SLOT_RANGE", "FAULT_VALUE_RANGE", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
     "ROUND_NEAREST_EVEN", "CacheError", "FerrumError", "InternalError", "InvalidRequest",
     "KernelError", "Unavailable", "KvPoolConfig", "PagedConfig", "PagedKvPool",
     "PreallocatedKvPool", "default_scale", "device_copy", "load_library",

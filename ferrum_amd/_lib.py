@@ -32,6 +32,7 @@ GATHER_RAW = 1
 FAULT_SLOT_RANGE = 1
 FAULT_BLOCK_RANGE = 2
 FAULT_CTX_RANGE = 4
+FAULT_VALUE_RANGE = 8
 
 c_void_p = ctypes.c_void_p
 u32, u64, i32, i64 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_int64

@@ -107,6 +107,9 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
     return fail(FKV_ERR_KERNEL, "unsupported dtype");
   if (c.kv_dtype == FKV_DTYPE_Q8_0 && c.head_dim % 32 != 0)
     return fail(FKV_ERR_KERNEL, "q8_0 k is not a multiple of 32");
+  // The Q8_0 tile order (16-token sub-tiles of 1 KiB operand runs) needs these.
+  if (c.kv_dtype == FKV_DTYPE_Q8_0 && (c.head_dim % 64 != 0 || c.block_size % 16 != 0))
+    return fail(FKV_ERR_KERNEL, "q8_0 kv needs head_dim % 64 == 0 and block_size % 16 == 0");
   if (c.f16_rounding != FKV_ROUND_NEAREST_EVEN && c.f16_rounding != FKV_ROUND_HALF_AWAY)
     return fail(FKV_ERR_INVALID, "unknown f16 rounding mode");
   if (c.num_blocks > 0x7fffffffull) return fail(FKV_ERR_CACHE, "kv pool size overflow");

@@ -72,6 +72,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kHeads = 16;            // MFMA column count: query heads of one group
 constexpr float kRescaleLog2 = 8.0f;  // rescale when a score passes the reference max by 2^8
@@ -252,6 +253,124 @@ __device__ __forceinline__ void load_v(const uint8_t* vtile, const Lane& ln,
 #pragma unroll
   for (int m = 0; m < D / 16; m++) vr[m] = load_stream8(t + m * 16 * B * 2);
 }
+
+// Registers of one block's K and V tiles as loaded, and their f16 MFMA operands
+// (the operand orders of load_k / load_v above).
+template <int DT, int D>
+struct BlockRegs;
+
+template <int D>
+struct BlockRegs<kDtypeF16, D> {
+  uint4 k[D / 32];
+  u32x2_t v[D / 16];
+  __device__ __forceinline__ void load_k_tile(const uint8_t* kt, const Lane& ln) {
+    load_k<D>(kt, ln, k);
+  }
+  __device__ __forceinline__ void load_v_tile(const uint8_t* vt, const Lane& ln) {
+    load_v<D>(vt, ln, v);
+  }
+  __device__ __forceinline__ void k_operand(uint4 (&kr)[D / 32]) const {
+#pragma unroll
+    for (int c = 0; c < D / 32; c++) kr[c] = k[c];
+  }
+  __device__ __forceinline__ void v_operand(u32x2_t (&vr)[D / 16]) const {
+#pragma unroll
+    for (int m = 0; m < D / 16; m++) vr[m] = v[m];
+  }
+};
+
+// int8 pair -> exact binary16 pair. u holds four int8 with the sign bit flipped
+// (x + 128 as unsigned); sel picks bytes (0, 1) or (2, 3). Each picked byte
+// becomes the low mantissa byte of binary16 0x64XX = 1024 + (x + 128), and
+// subtracting 1152 leaves x exactly.
+__device__ __forceinline__ f16x2 i8_pair_to_f16(uint32_t u, uint32_t sel) {
+  const uint32_t b = __builtin_amdgcn_perm(0x64646464u, u, sel);
+  return __builtin_bit_cast(f16x2, b) - (f16x2){(_Float16)1152.0f, (_Float16)1152.0f};
+}
+constexpr uint32_t kSelLo = 0x04010400u;  // bytes 0, 1 under 0x64
+constexpr uint32_t kSelHi = 0x04030402u;  // bytes 2, 3 under 0x64
+
+// Q8_0 tiles: int8 quants in the operand order (q8_quant_offset: lane l = grp*16 +
+// col holds 32 contiguous bytes of the block, 1 KiB per load instruction), then
+// the f16 scales [B][D/32] (one per 32-dim group of a token). The operands are
+// the dequantised values as binary16: the int8 -> binary16 step is exact and the
+// product with the scale is rounded once (v_pk_mul_f16), which is the value an
+// f16 pool would hold for the reference's f32 dequant
+// (f16_to_f32(scale) * (i8 as f32), crates/kernels/src/scalar.rs:268-275).
+template <int D>
+struct BlockRegs<kDtypeQ8, D> {
+  static constexpr int NG = D / 32;  // scale groups per token (= QK chunks)
+  static_assert(D % 64 == 0, "Q8_0 tiles pair the 32-dim chunks");
+  u32x2_t kq[NG];       // chunk c: dims c*32 + grp*8 .. +7 of token col
+  uint32_t ks[NG / 2];  // the NG scales of token col
+  uint32_t vq[D / 16];  // tile m: tokens grp*4 .. +3 of dim 16m + col
+  uint32_t vs[2 * NG];  // the scales of tokens grp*4 .. +3: [4][NG]
+  __device__ __forceinline__ void load_k_tile(const uint8_t* kt, const Lane& ln) {
+    const uint8_t* lp = kt + (uint64_t)ln.lane * 16;
+#pragma unroll
+    for (int p = 0; p < NG / 2; p++) {  // chunks 2p, 2p + 1
+      const uint4 w = load_stream16(lp + p * 1024);
+      kq[2 * p] = (u32x2_t){w.x, w.y};
+      kq[2 * p + 1] = (u32x2_t){w.z, w.w};
+    }
+    const uint8_t* sc = kt + (uint64_t)B * D + (uint64_t)ln.col * NG * 2;
+    if constexpr (NG == 4) {
+      const u32x2_t w = load_stream8(sc);
+      ks[0] = w.x;
+      ks[1] = w.y;
+    } else {
+      ks[0] = __builtin_nontemporal_load((const uint32_t*)sc);
+    }
+  }
+  __device__ __forceinline__ void load_v_tile(const uint8_t* vt, const Lane& ln) {
+    const uint8_t* lp = vt + (uint64_t)ln.lane * 16;
+#pragma unroll
+    for (int p = 0; p < D / 64; p++) {  // dim tiles 4p .. 4p + 3
+      const uint4 w = load_stream16(lp + p * 1024);
+      vq[4 * p] = w.x;
+      vq[4 * p + 1] = w.y;
+      vq[4 * p + 2] = w.z;
+      vq[4 * p + 3] = w.w;
+    }
+    const uint8_t* sc = vt + (uint64_t)B * D + (uint64_t)ln.grp * 4 * NG * 2;
+#pragma unroll
+    for (int i = 0; i < NG / 2; i++) {
+      const uint4 w = load_stream16(sc + i * 16);
+      vs[4 * i] = w.x;
+      vs[4 * i + 1] = w.y;
+      vs[4 * i + 2] = w.z;
+      vs[4 * i + 3] = w.w;
+    }
+  }
+  __device__ __forceinline__ void k_operand(uint4 (&kr)[D / 32]) const {
+#pragma unroll
+    for (int c = 0; c < NG; c++) {
+      const uint32_t sw = ks[c / 2];
+      const f16x2 s2 = __builtin_bit_cast(
+          f16x2, __builtin_amdgcn_perm(sw, sw, (c & 1) ? 0x03020302u : 0x01000100u));
+      const uint32_t w0 = kq[c].x ^ 0x80808080u, w1 = kq[c].y ^ 0x80808080u;
+      kr[c] = make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelLo) * s2),
+                         __builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelHi) * s2),
+                         __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelLo) * s2),
+                         __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelHi) * s2));
+    }
+  }
+  __device__ __forceinline__ void v_operand(u32x2_t (&vr)[D / 16]) const {
+#pragma unroll
+    for (int m = 0; m < D / 16; m++) {
+      const int gg = m / 2;  // dims 16m .. 16m + 15 lie in group m / 2
+      // scale of (token r, group gg) is half (gg & 1) of dword r * NG / 2 + gg / 2
+      const uint32_t sel = (gg & 1) ? 0x07060302u : 0x05040100u;
+      const f16x2 s01 = __builtin_bit_cast(
+          f16x2, __builtin_amdgcn_perm(vs[NG / 2 + gg / 2], vs[gg / 2], sel));
+      const f16x2 s23 = __builtin_bit_cast(
+          f16x2, __builtin_amdgcn_perm(vs[3 * NG / 2 + gg / 2], vs[NG + gg / 2], sel));
+      const uint32_t w = vq[m] ^ 0x80808080u;
+      vr[m].x = __builtin_bit_cast(uint32_t, i8_pair_to_f16(w, kSelLo) * s01);
+      vr[m].y = __builtin_bit_cast(uint32_t, i8_pair_to_f16(w, kSelHi) * s23);
+    }
+  }
+};
 
 // ---------------------------------------------------------------------------
 // Persistent streaming kernel
@@ -563,7 +682,7 @@ __global__ void __launch_bounds__(256) attn_stream_combine_kernel(
 #define FKV_MFMA_WAVES_PER_EU 3
 #endif
 
-template <int D, int NBUF>
+template <int DT, int D, int NBUF>
 __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
@@ -611,7 +730,8 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   // in place of what it loaded and stores them to the pool. No other workgroup
   // reads the position, and this one never reads back what it stores, so the
   // stores need no ordering.
-  const bool app = k_new != nullptr && split == nsplits - 1 && ctx > 0 && ctx_ok;
+  const bool app =
+      DT == kDtypeF16 && k_new != nullptr && split == nsplits - 1 && ctx > 0 && ctx_ok;
   const int32_t app_pos = ctx - 1;
   const int32_t app_lb = app ? app_pos / B - blk0 : -1;  // block of the split
   const bool app_wave = app && app_lb % kAttnWaves == wave;
@@ -635,8 +755,7 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   // split; block t of the wave lives in buffer t % NBUF. Block t + NBUF's K load
   // is issued as soon as block t's QK has consumed the buffer, and its V load
   // once block t's P.V has.
-  uint4 kr[NBUF][NC];
-  u32x2_t vr[NBUF][NM];
+  BlockRegs<DT, D> ring[NBUF];
   int32_t bid[NBUF];
   bool blive[NBUF];
   f16x8 qh[NC], ql[NC];
@@ -666,22 +785,26 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     const bool live = blive[b];
     const bool refill = t + NBUF < nt;
     const int32_t t0 = s0 + (wave + kAttnWaves * t) * B;  // first token of the block
-    const bool patch = app_wave && t == app_t && live;
+    const bool patch = app_wave && t == app_t && live;  // (F16 storage only)
+    uint4 kr[NC];
+    ring[b].k_operand(kr);
     if (patch && ln.col == app_off) {  // K tile [D/8][B][8]: run c*4 + grp of the token
       uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
 #pragma unroll
       for (int c = 0; c < NC; c++) {
-        kr[b][c] = *(const uint4*)&s_app[0][c * 32 + ln.grp * 8];
-        *(uint4*)(kt + ((uint64_t)(c * 4 + ln.grp) * B + app_off) * 16) = kr[b][c];
+        kr[c] = *(const uint4*)&s_app[0][c * 32 + ln.grp * 8];
+        *(uint4*)(kt + ((uint64_t)(c * 4 + ln.grp) * B + app_off) * 16) = kr[c];
       }
     }
     float s[4];
-    qk_block<D>(kr[b], qh, ql, hscale, ln, live, t0, s1, s);
+    qk_block<D>(kr, qh, ql, hscale, ln, live, t0, s1, s);
     if (refill) {
       fetch(t + NBUF, b);
-      load_k<D>(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln, kr[b]);
+      ring[b].load_k_tile(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln);
     }
     const f16x4 pw = softmax_block<D>(s, ln, st);
+    u32x2_t vr[NM];
+    ring[b].v_operand(vr);
     if (patch && ln.grp == app_off / 4) {  // V tile [D][B]: dim 16m + col, token app_off
       uint16_t* vt = (uint16_t*)tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
       const int sh = (app_off & 1) * 16;
@@ -689,21 +812,21 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
 #pragma unroll
       for (int m = 0; m < NM; m++) {
         const uint32_t h = s_app[1][m * 16 + ln.col];
-        if (app_off & 2) vr[b][m].y = (vr[b][m].y & keep) | (h << sh);
-        else vr[b][m].x = (vr[b][m].x & keep) | (h << sh);
+        if (app_off & 2) vr[m].y = (vr[m].y & keep) | (h << sh);
+        else vr[m].x = (vr[m].x & keep) | (h << sh);
         vt[(uint64_t)(m * 16 + ln.col) * B + app_off] = (uint16_t)h;
       }
     }
-    if (live) pv_block<D>(vr[b], pw, ln, t0, s1, st);
-    if (refill) load_v<D>(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln, vr[b]);
+    if (live) pv_block<D>(vr, pw, ln, t0, s1, st);
+    if (refill) ring[b].load_v_tile(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln);
   };
 
 #pragma unroll
   for (int b = 0; b < NBUF; b++) {
     if (b < nt) {
       fetch(b, b);
-      load_k<D>(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln, kr[b]);
-      load_v<D>(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln, vr[b]);
+      ring[b].load_k_tile(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln);
+      ring[b].load_v_tile(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln);
     }
   }
   // q is read after the first K/V loads are issued, so its latency overlaps theirs.
@@ -1031,16 +1154,19 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
   const uint32_t G = n_heads / g.n_kv_heads;
   dim3 grid(n_seqs * g.n_kv_heads, max_splits);
   constexpr int NBUF = FKV_MFMA_RING;
-  if (g.head_dim == 128)
-    attn_mfma_kernel<128, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,
-                                                     max_blocks, ctx_lens, max_splits,
-                                                     (int32_t)split_tokens, scale, ws_o, ws_ml,
-                                                     k_new, v_new);
-  else
-    attn_mfma_kernel<64, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,
-                                                    max_blocks, ctx_lens, max_splits,
-                                                    (int32_t)split_tokens, scale, ws_o, ws_ml,
-                                                     k_new, v_new);
+  const int32_t st = (int32_t)split_tokens;
+#define FKV_LAUNCH_MFMA(DT_, D_)                                                              \
+  attn_mfma_kernel<DT_, D_, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,  \
+                                                       max_blocks, ctx_lens, max_splits, st,  \
+                                                       scale, ws_o, ws_ml, k_new, v_new)
+  if (g.dtype == kDtypeQ8) {
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128);
+    else FKV_LAUNCH_MFMA(kDtypeQ8, 64);
+  } else {
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128);
+    else FKV_LAUNCH_MFMA(kDtypeF16, 64);
+  }
+#undef FKV_LAUNCH_MFMA
   return hipGetLastError();
 }
 

@@ -30,6 +30,27 @@ __device__ __forceinline__ uint4 load_stream16(const uint8_t* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Byte offset of the int8 quant of (token off, dim d) in a Q8_0 tile of kind kv.
+// Quants come in 16-token sub-tiles of 16*D bytes, in the operand order of the
+// matrix-core attention (each lane's 32 bytes of a block contiguous, 1 KiB per
+// load instruction); with t = off % 16:
+//   K: d = c*32 + g*8 + e -> (c/2)*1024 + (g*16 + t)*16 + (c%2)*8 + e
+//   V: d = m*16 + j, t = q*4 + r -> (m/4)*1024 + (q*16 + j)*16 + (m%4)*4 + r
+// (pools need D % 64 == 0 and B % 16 == 0). The f16 scales [B][D/32] follow.
+__device__ __forceinline__ uint64_t q8_quant_offset(uint32_t kv, uint32_t off, uint32_t d,
+                                                    uint32_t D) {
+  const uint64_t sub = (uint64_t)(off / 16u) * 16u * D;
+  const uint32_t t = off % 16u;
+  if (kv) {
+    const uint32_t m = d / 16u, j = d % 16u;
+    return sub + (uint64_t)(m / 4u) * 1024u + (uint64_t)((t / 4u) * 16u + j) * 16u +
+           (m % 4u) * 4u + t % 4u;
+  }
+  const uint32_t c = d / 32u, g = (d % 32u) / 8u;
+  return sub + (uint64_t)(c / 2u) * 1024u + (uint64_t)(g * 16u + t) * 16u + (c % 2u) * 8u +
+         d % 8u;
+}
+
 // ---------------------------------------------------------------------------
 // binary16 <-> binary32
 // ---------------------------------------------------------------------------

@@ -10,8 +10,9 @@ namespace fkv {
 // Geometry of one paged pool, passed by value to every kernel.
 // pool[block][layer][kv][head][tile]; tile = [B][D] elements (F32), [D/8][B][8]
 // (F16 K: 16-byte runs of 8 dims, token-contiguous per run), [D][B] (F16 V), or
-// [B*D int8][B*D/32 f16 scales] (Q8_0), padded to a multiple of 16 bytes. The
-// F16 orders are the QK and P.V operand orders of the MFMA decode kernel.
+// int8 quants ([B][D] for K, [D][B] for V) then f16 scales [B][D/32] (Q8_0),
+// padded to a multiple of 16 bytes. The F16 and Q8_0 orders are the QK and P.V
+// operand orders of the MFMA decode kernel.
 struct Geom {
   uint8_t* base;
   uint64_t tile_bytes;
@@ -33,6 +34,7 @@ constexpr int kDtypeQ8 = 8;
 constexpr uint32_t kFaultSlot = 1u;
 constexpr uint32_t kFaultBlock = 2u;
 constexpr uint32_t kFaultCtx = 4u;
+constexpr uint32_t kFaultRange = 8u;
 
 // Decode attention partitioning: 4 waves per workgroup, each wave owns 4 blocks
 // of 16 tokens, so one workgroup covers a 256-token partition of one

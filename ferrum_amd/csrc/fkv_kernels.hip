@@ -218,10 +218,20 @@ __global__ void __launch_bounds__(256) append_q8_kernel(Geom g, uint32_t layer,
     uint32_t sc = q8_quantize(x, g.rounding, q);
     uint32_t off = (uint32_t)((uint64_t)slot % B);
     uint8_t* tile = tile_ptr(g, (uint64_t)slot / B, layer, kv, h);
-    uint4* qdst = (uint4*)(tile + (uint64_t)off * D + c * 32u);
-    qdst[0] = make_uint4(q[0], q[1], q[2], q[3]);
-    qdst[1] = make_uint4(q[4], q[5], q[6], q[7]);
+    if (kv == 0) {  // K: dims c*32 + g*8 .. +7 are one 8-byte run per g
+#pragma unroll
+      for (uint32_t gg = 0; gg < 4; gg++)
+        *(uint2*)(tile + q8_quant_offset(0, off, c * 32u + gg * 8u, D)) =
+            make_uint2(q[2 * gg], q[2 * gg + 1]);
+    } else {  // V: one byte per dim
+#pragma unroll
+      for (uint32_t j = 0; j < 32; j++)
+        tile[q8_quant_offset(1, off, c * 32u + j, D)] = (uint8_t)(q[j / 4] >> (8 * (j % 4)));
+    }
     ((uint16_t*)(tile + (uint64_t)B * D))[off * cpr + c] = (uint16_t)sc;
+    // A finite scale >= 512 can dequantise past 65504, beyond the binary16
+    // operands of the matrix-core attention: stored exactly, but flagged.
+    if ((sc & 0x7fffu) >= 0x6000u && (sc & 0x7fffu) < 0x7c00u) raise_fault(g.fault, kFaultRange);
   }
 }
 
@@ -238,17 +248,17 @@ __device__ __forceinline__ void gather_chunk(const Geom& g, uint32_t layer, uint
   const uint32_t D = g.head_dim;
   const uint8_t* tile = tile_ptr(g, blk, layer, kv, h);
   if (g.dtype == kDtypeQ8) {
-    const uint8_t* qs = tile + (uint64_t)off * D + c * 32u;
     uint32_t sc = ((const uint16_t*)(tile + (uint64_t)g.block_size * D))[off * (D / 32u) + c];
+    auto qv = [&](uint32_t j) { return tile[q8_quant_offset(kv, off, c * 32u + j, D)]; };
     if (format == 0) {
       float s = f16_bits_to_f32(sc);
       float* o = (float*)dst_row + c * 32u;
-      for (int j = 0; j < 32; j++) o[j] = s * (float)(int8_t)qs[j];
+      for (uint32_t j = 0; j < 32; j++) o[j] = s * (float)(int8_t)qv(j);
     } else {
       // Ferrum's 34-byte Q8_0 block: f16 scale (LE) then 32 x i8 (dtype.rs:19-21).
       uint16_t* o = (uint16_t*)(dst_row + (uint64_t)c * 34u);
       o[0] = (uint16_t)sc;
-      for (int j = 0; j < 16; j++) o[1 + j] = (uint16_t)(qs[2 * j] | (qs[2 * j + 1] << 8));
+      for (uint32_t j = 0; j < 16; j++) o[1 + j] = (uint16_t)(qv(2 * j) | (qv(2 * j + 1) << 8));
     }
     return;
   }

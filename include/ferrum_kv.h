@@ -36,9 +36,15 @@
  *   tile (F16 K) : [head_dim/8][block_size][8]: 16-byte runs of 8 dims, token-
  *                  contiguous per run (head_dim padded to a multiple of 8)
  *   tile (F16 V) : [head_dim][block_size]: dim-major
- *   tile (Q8_0)  : [block_size*head_dim int8 quants][block_size*head_dim/32 f16 scales]
- * The F16 orders are the operand orders of the MFMA attention kernels: one load
- * instruction reads 1 KiB of K or 512 B of V of consecutive bytes. A block holds
+ *   tile (Q8_0)  : int8 quants in 16-token sub-tiles of 16*head_dim bytes, each in
+ *                  the matrix-core operand order (t = token % 16):
+ *                    K dim c*32+g*8+e at (c/2)*1024 + (g*16+t)*16 + (c%2)*8 + e
+ *                    V dim m*16+j     at (m/4)*1024 + ((t/4)*16+j)*16 + (m%4)*4 + t%4
+ *                  then f16 scales [block_size][head_dim/32] (one per 32-value run
+ *                  of a token row, Ferrum's Q8_0 block). Needs head_dim % 64 == 0
+ *                  and block_size % 16 == 0.
+ * The F16 and Q8_0 orders are the operand orders of the MFMA attention kernels: one
+ * load instruction reads 1 KiB of K or 512 B of V of consecutive bytes (F16). A block holds
  * every layer of block_size consecutive tokens, and the (block, layer, kv, head)
  * tile is contiguous (4 KiB for f16, D=128, B=16). Slot = block * block_size +
  * offset_in_block (the vLLM slot-mapping convention). The gather entry points
@@ -85,6 +91,9 @@ extern "C" {
 #define FKV_FAULT_SLOT_RANGE 1u   /* append/gather slot >= num_blocks*block_size */
 #define FKV_FAULT_BLOCK_RANGE 2u  /* block table / copy pair id outside [0, num_blocks) */
 #define FKV_FAULT_CTX_RANGE 4u    /* ctx_len > max_blocks_per_seq * block_size or < 0 */
+#define FKV_FAULT_VALUE_RANGE 8u  /* Q8_0 append stored a block scale >= 512: its values can
+                                     dequantise past 65504, the binary16 range of the
+                                     matrix-core attention (storage itself is exact) */
 
 /* Version of this ABI; equals FKV_ABI_VERSION of the header the library was built with. */
 int32_t fkv_abi_version(void);
@@ -237,8 +246,9 @@ int32_t fkv_swap_in(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void
  * A non-finite maximum score gives zeros (kernels/src/scalar.rs:125-130).
  * q, out: device f32 [n_seqs][n_heads][head_dim]. block_tables: device int32
  * [n_seqs][max_blocks_per_seq]; ctx_lens: device int32 [n_seqs], each
- * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, and g <= 16 (F16,
- * matrix cores), g in {1,2,4,8,16} (F32) or g in {1,2,4,8} (Q8_0).
+ * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, and g <= 16 (F16 and
+ * Q8_0, matrix cores; Q8_0 values are dequantised to binary16 operands, see
+ * FKV_FAULT_VALUE_RANGE) or g in {1,2,4,8,16} (F32).
  * workspace: device scratch of fkv_decode_attention_workspace_size() bytes
  * holding the split partials (running max, sum and unnormalised output per
  * query head and context split) that the merge pass reads; it may be NULL when

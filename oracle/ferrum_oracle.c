@@ -225,6 +225,24 @@ static uint64_t f16_index(const fo_layout* l, int kv, uint32_t off, uint32_t d) 
   return ((uint64_t)(d / 8) * l->block_size + off) * 8 + d % 8;
 }
 
+/* Byte index of the int8 quant of (token off, dim d) inside a Q8_0 tile of kind
+ * kv. The quants come in 16-token sub-tiles of 16*D bytes, each in 1 KiB runs;
+ * with t = off % 16:
+ *   K: d = c*32 + g*8 + e -> (c/2)*1024 + (g*16 + t)*16 + (c%2)*8 + e
+ *   V: d = m*16 + j, t = q*4 + r -> (m/4)*1024 + (q*16 + j)*16 + (m%4)*4 + r
+ * (needs D % 64 == 0 and B % 16 == 0). The f16 scales of both follow the quants
+ * as [B][D/32]. */
+static uint64_t q8_index(const fo_layout* l, int kv, uint32_t off, uint32_t d) {
+  const uint64_t sub = (uint64_t)(off / 16) * 16 * l->head_dim;
+  const uint32_t t = off % 16;
+  if (kv) {
+    const uint32_t m = d / 16, j = d % 16, q = t / 4, r = t % 4;
+    return sub + (uint64_t)(m / 4) * 1024 + (uint64_t)(q * 16 + j) * 16 + (m % 4) * 4 + r;
+  }
+  const uint32_t c = d / 32, g = (d % 32) / 8, e = d % 8;
+  return sub + (uint64_t)(c / 2) * 1024 + (uint64_t)(g * 16 + t) * 16 + (c % 2) * 8 + e;
+}
+
 /* Encode one row of D values into token `off` of a tile of kind kv (0 K, 1 V). */
 static void encode_row(const fo_layout* l, int kv, uint8_t* tile, uint32_t off, const float* src) {
   uint32_t D = l->head_dim;
@@ -234,13 +252,12 @@ static void encode_row(const fo_layout* l, int kv, uint8_t* tile, uint32_t off, 
     uint16_t* dst = (uint16_t*)tile;
     for (uint32_t d = 0; d < D; d++) dst[f16_index(l, kv, off, d)] = fo_f32_to_f16(src[d], l->rounding);
   } else {
-    uint8_t* qs = tile + (uint64_t)off * D;
     uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
     for (uint32_t g = 0; g < D / 32; g++) {
       uint16_t s;
       int8_t q[32];
       fo_q8_quantize_block(src + g * 32, l->rounding, &s, q);
-      memcpy(qs + g * 32, q, 32);
+      for (uint32_t j = 0; j < 32; j++) tile[q8_index(l, kv, off, g * 32 + j)] = (uint8_t)q[j];
       sc[g * 2] = (uint8_t)(s & 0xff);
       sc[g * 2 + 1] = (uint8_t)(s >> 8);
     }
@@ -256,11 +273,11 @@ static void decode_row(const fo_layout* l, int kv, const uint8_t* tile, uint32_t
     const uint16_t* src = (const uint16_t*)tile;
     for (uint32_t d = 0; d < D; d++) dst[d] = fo_f16_to_f32(src[f16_index(l, kv, off, d)]);
   } else {
-    const uint8_t* qs = tile + (uint64_t)off * D;
     const uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
     for (uint32_t g = 0; g < D / 32; g++) {
       float scale = fo_f16_to_f32((uint16_t)(sc[g * 2] | (sc[g * 2 + 1] << 8)));
-      for (int j = 0; j < 32; j++) dst[g * 32 + j] = scale * (float)(int8_t)qs[g * 32 + j];
+      for (uint32_t j = 0; j < 32; j++)
+        dst[g * 32 + j] = scale * (float)(int8_t)tile[q8_index(l, kv, off, g * 32 + j)];
     }
   }
 }
@@ -275,12 +292,11 @@ static void raw_row(const fo_layout* l, int kv, const uint8_t* tile, uint32_t of
     const uint16_t* src = (const uint16_t*)tile;
     for (uint32_t d = 0; d < D; d++) ((uint16_t*)dst)[d] = src[f16_index(l, kv, off, d)];
   } else {
-    const uint8_t* qs = tile + (uint64_t)off * D;
     const uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
     for (uint32_t g = 0; g < D / 32; g++) {
       dst[g * 34] = sc[g * 2];
       dst[g * 34 + 1] = sc[g * 2 + 1];
-      memcpy(dst + g * 34 + 2, qs + g * 32, 32);
+      for (uint32_t j = 0; j < 32; j++) dst[g * 34 + 2 + j] = tile[q8_index(l, kv, off, g * 32 + j)];
     }
   }
 }

@@ -55,6 +55,10 @@ def test_zero_dimension_is_cache_error(field):
 def test_config_validation_messages():
     with pytest.raises(fa.KernelError, match="^kernel: q8_0 k is not a multiple of 32$"):
         _create(kv_dtype=fa.DTYPE_Q8_0, head_dim=48)
+    # the Q8_0 tile order works in 16-token sub-tiles of 64-dim operand runs
+    for bad in ({"head_dim": 96}, {"block_size": 8}):
+        with pytest.raises(fa.KernelError, match="^kernel: q8_0 kv needs head_dim % 64 == 0"):
+            _create(kv_dtype=fa.DTYPE_Q8_0, **bad)
     with pytest.raises(fa.KernelError, match="^kernel: unsupported dtype$"):
         _create(kv_dtype=3)
     with pytest.raises(fa.InvalidRequest, match="unknown f16 rounding mode"):

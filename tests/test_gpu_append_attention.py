@@ -49,7 +49,7 @@ def _setup(dtype, d, hkv, ctxs, rounding=0, seed=0, layers=2):
 
 
 SHAPES = [(1, 128, 8, 4), (1, 64, 4, 8), (1, 128, 2, 1), (1, 128, 1, 16),
-          (8, 128, 2, 4), (0, 64, 2, 2)]
+          (8, 128, 2, 4), (8, 64, 2, 16), (0, 64, 2, 2)]
 
 
 @pytest.mark.parametrize("rounding", [0, 1])
