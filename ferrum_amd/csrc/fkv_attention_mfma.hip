@@ -786,8 +786,16 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     const bool refill = t + NBUF < nt;
     const int32_t t0 = s0 + (wave + kAttnWaves * t) * B;  // first token of the block
     const bool patch = app_wave && t == app_t && live;  // (F16 storage only)
-    uint4 kr[NC];
-    ring[b].k_operand(kr);
+    // F16 operands are the ring registers themselves; Q8_0 ones are dequantised.
+    uint4 kdq[DT == kDtypeF16 ? 1 : NC];
+    uint4(&kr)[NC] = *[&]() -> uint4(*)[NC] {
+      if constexpr (DT == kDtypeF16) {
+        return &ring[b].k;
+      } else {
+        ring[b].k_operand(kdq);
+        return &kdq;
+      }
+    }();
     if (patch && ln.col == app_off) {  // K tile [D/8][B][8]: run c*4 + grp of the token
       uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
 #pragma unroll
@@ -803,8 +811,15 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
       ring[b].load_k_tile(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln);
     }
     const f16x4 pw = softmax_block<D>(s, ln, st);
-    u32x2_t vr[NM];
-    ring[b].v_operand(vr);
+    u32x2_t vdq[DT == kDtypeF16 ? 1 : NM];
+    u32x2_t(&vr)[NM] = *[&]() -> u32x2_t(*)[NM] {
+      if constexpr (DT == kDtypeF16) {
+        return &ring[b].v;
+      } else {
+        ring[b].v_operand(vdq);
+        return &vdq;
+      }
+    }();
     if (patch && ln.grp == app_off / 4) {  // V tile [D][B]: dim 16m + col, token app_off
       uint16_t* vt = (uint16_t*)tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
       const int sh = (app_off & 1) * 16;
