@@ -286,8 +286,7 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 // skipped); a non-finite M gives zeros (scalar.rs:127-130); otherwise
 // out = sum_p w_p o_p / sum_p w_p l_p with w_p = exp(m_p - M).
 // One wave per (sequence, query head), four per workgroup, no LDS: lane p holds
-// partition p's (m, l) (64 partitions per pass), every lane holds D/64 dims, and
-// the partial-output loads of a pass are issued before its maximum is known.
+// partition p's (m, l) (64 partitions per pass) and every lane holds D/64 dims.
 // Heads with many partitions (few sequences, long contexts) use
 // attn_combine_wide_kernel instead.
 template <int D>
@@ -303,19 +302,14 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
   const uint32_t seq = head / n_heads;
   const float* ml = ws_ml + (uint64_t)head * max_parts * 2;
   const float* po = ws_o + (uint64_t)head * max_parts * D + lane * DPL;
-  // The context length, the first 64 partitions' (m, l) and the first kChunk
-  // partial outputs are loaded together: slots past the head's partition count
-  // hold stale bytes and are masked once the count is known (the workspace has
-  // max_parts slots per head, so every load is in bounds).
+  // The context length and the first 64 partitions' (m, l) are loaded together:
+  // slots past the head's partition count hold stale bytes and are masked once
+  // the count is known (the workspace has max_parts slots per head, so every load
+  // is in bounds). Partial outputs are read only for the head's own partitions.
   const int32_t raw_ctx = ctx_lens[seq];
   const int32_t n0 = (int32_t)max_parts < 64 ? (int32_t)max_parts : 64;
   float mp = lane < n0 ? ml[2 * lane] : -__builtin_inff();
   float lp = lane < n0 ? ml[2 * lane + 1] : 0.0f;
-  float v0[kChunk][DPL];
-#pragma unroll
-  for (int j = 0; j < kChunk; j++)
-#pragma unroll
-    for (int i = 0; i < DPL; i++) v0[j][i] = j < (int)max_parts ? po[(uint64_t)j * D + i] : 0.0f;
 
   const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
   const int32_t ctx = raw_ctx < 0 ? 0 : (raw_ctx > cap ? cap : raw_ctx);
@@ -351,18 +345,11 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
     const int32_t n = nparts - p0 < 64 ? nparts - p0 : 64;
     for (int32_t c0 = 0; c0 < n; c0 += kChunk) {
       float v[kChunk][DPL];
-      if (p0 == 0 && c0 == 0) {
 #pragma unroll
-        for (int j = 0; j < kChunk; j++)
+      for (int j = 0; j < kChunk; j++)
 #pragma unroll
-          for (int i = 0; i < DPL; i++) v[j][i] = v0[j][i];
-      } else {
-#pragma unroll
-        for (int j = 0; j < kChunk; j++)
-#pragma unroll
-          for (int i = 0; i < DPL; i++)
-            v[j][i] = c0 + j < n ? po[(uint64_t)(p0 + c0 + j) * D + i] : 0.0f;
-      }
+        for (int i = 0; i < DPL; i++)
+          v[j][i] = c0 + j < n ? po[(uint64_t)(p0 + c0 + j) * D + i] : 0.0f;
 #pragma unroll
       for (int j = 0; j < kChunk; j++) {
         if (c0 + j < n) {
