@@ -62,3 +62,26 @@ def attention_f64(q, k_rows, v_rows, scale):
     m = s.max()
     e = np.exp(s - m)
     return (e[:, None] * v_rows.astype(np.float64)).sum(0) / e.sum()
+
+
+def layer_image(pool, layout_cls, tables, ctxs, layer, seqs):
+    """Host copy of one layer of the blocks the sampled sequences use, as a compact
+    one-layer pool for the oracle. Returns (layout, image, remapped tables)."""
+    cfg = pool.config
+    bs = cfg.block_size
+    ctxs = np.asarray(ctxs, np.int64)
+    nb = [(int(ctxs[s]) + bs - 1) // bs for s in seqs]
+    used = []
+    for s, n in zip(seqs, nb):
+        used.extend(int(b) for b in tables[s, :n])
+    remap = {b: i for i, b in enumerate(dict.fromkeys(used))}
+    lay = layout_cls(1, cfg.n_kv_heads, cfg.head_dim, bs, max(1, len(remap)), cfg.kv_dtype,
+                     cfg.f16_rounding)
+    region = lay.block_bytes
+    image = np.zeros(lay.pool_bytes, np.uint8)
+    for b, i in remap.items():
+        image[i * region:(i + 1) * region] = pool.read(b * pool.block_bytes + layer * region, region)
+    tab = np.zeros((len(seqs), max(1, max(nb))), np.int32)
+    for j, (s, n) in enumerate(zip(seqs, nb)):
+        tab[j, :n] = [remap[int(b)] for b in tables[s, :n]]
+    return lay, image, tab
