@@ -700,19 +700,9 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   const uint32_t sk = blockIdx.x;
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int32_t cap = (int32_t)(max_blocks * B);
-  int32_t ctx = ctx_lens[seq];
-  const bool ctx_ok = ctx >= 0 && ctx <= cap;
-  if (!ctx_ok) {
-    if (blockIdx.y == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
-    ctx = ctx < 0 ? 0 : cap;
-  }
-  const int32_t nsplits = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 1;
   const int32_t split = (int32_t)blockIdx.y;
-  if (split >= nsplits) return;
-  const int32_t s0 = (int32_t)split * split_tokens;
-  const int32_t s1 = ctx - s0 < split_tokens ? ctx : s0 + split_tokens;
-  const int32_t nblk = s1 > s0 ? (s1 - s0 + B - 1) / B : 0;
-
+  const int32_t s0 = split * split_tokens;
+  const int32_t blk0 = s0 / B;  // < max_blocks for every grid row
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   Lane ln;
   ln.lane = threadIdx.x & 63;
@@ -720,8 +710,31 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   ln.grp = ln.lane >> 4;
   ln.real = ln.col < (int)G;
 
+  // The wave's block-table entries, 64 at a time: lane j holds the entry of the
+  // wave's block (t & ~63) + j. A block's physical id then comes from a register
+  // (readlane) instead of a load that its K/V loads would have to wait for. The
+  // first 64 are loaded before the context length is known (indices clamped to
+  // the table row; entries past the split are never used), so the two loads'
+  // latencies overlap.
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
-  const int32_t blk0 = s0 / B;
+  int32_t tabv = 0;
+  auto load_tab = [&](int tb) {
+    int64_t j = (int64_t)blk0 + wave + (int64_t)kAttnWaves * (tb + ln.lane);
+    if (j > (int64_t)max_blocks - 1) j = (int64_t)max_blocks - 1;
+    tabv = j >= 0 ? table[j] : 0;
+  };
+  load_tab(0);
+
+  int32_t ctx = ctx_lens[seq];
+  const bool ctx_ok = ctx >= 0 && ctx <= cap;
+  if (!ctx_ok) {
+    if (split == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
+    ctx = ctx < 0 ? 0 : cap;
+  }
+  const int32_t nsplits = ctx > 0 ? (ctx + split_tokens - 1) / split_tokens : 1;
+  if (split >= nsplits) return;
+  const int32_t s1 = ctx - s0 < split_tokens ? ctx : s0 + split_tokens;
+  const int32_t nblk = s1 > s0 ? (s1 - s0 + B - 1) / B : 0;
 
   // Fused append (k_new != nullptr): the token at position ctx - 1 of this KV
   // head is stored by the wave of the last split that reads its block. That wave
@@ -762,15 +775,6 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   float hscale;
   const int32_t nt = wave < nblk ? (nblk - wave + kAttnWaves - 1) / kAttnWaves : 0;
 
-  // The wave's block-table entries, 64 at a time: lane j holds the entry of the
-  // wave's block (t & ~63) + j. A block's physical id then comes from a register
-  // (readlane) instead of a load that its K/V loads would have to wait for.
-  int32_t tabv = 0;
-  auto load_tab = [&](int tb) {
-    const int j = tb + ln.lane;
-    tabv = j < nt ? table[blk0 + wave + kAttnWaves * j] : 0;
-  };
-  load_tab(0);
   // Physical block of the wave's block t (wave-uniform). A block-table entry
   // outside the pool raises the fault flag, loads block 0 instead and is skipped.
   auto fetch = [&](int t, int b) {
