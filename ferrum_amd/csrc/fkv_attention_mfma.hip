@@ -47,6 +47,7 @@
 //        because XCDs stream at different rates.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "fkv_device.h"
 #include "fkv_internal.h"
@@ -677,6 +678,131 @@ __global__ void __launch_bounds__(256) attn_stream_combine_kernel(
 // Split kernel (one workgroup per (sequence, KV head, split))
 // ---------------------------------------------------------------------------
 
+// Work order of the split grid.
+//
+// Within each XCD, the hardware hands a launch's workgroups to the shader engines
+// in a fixed rotation, whatever their load; each engine then runs its share on
+// its own CUs. With one workgroup per (sequence, KV head, split) in grid order,
+// every split of a sequence falls to the same engine. The engines' loads then
+// differ as much as sums of random context lengths do, and the most loaded engine
+// sets the kernel's end.
+//
+// In the longest-first order, workgroup r of the launch takes unit r / n_kv_heads
+// (KV head r % n_kv_heads) of this list:
+// - every full split (split_tokens positions) of every sequence, sequence-major;
+// - then each sequence's last, partial split, including the zero-length one of an
+//   empty context. These are taken by block count, largest first, ties by
+//   sequence (n_seqs <= 256); for larger batches, in sequence order.
+// Ranks past the list exit at once. A rotation dealing from a list sorted this
+// way gives every engine the same work to within about one item.
+enum : uint32_t { kOrderGrid = 0, kOrderFullFirst = 1, kOrderLongestFirst = 2 };
+constexpr uint32_t kOrderMaxSeqs = 1024;    // contiguous runs of <= 4 sequences per thread
+constexpr uint32_t kOrderSortSeqs = 256;    // one sequence per thread for the block-count ranks
+
+struct OrderedItem {
+  int32_t seq;    // < 0: past the list
+  int32_t split;
+  int32_t ctx;    // ctx_lens[seq] as read (unclamped)
+};
+
+// Unit u of the longest-first list. Every thread of the workgroup calls this with
+// the same u and receives the same item.
+__device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_lens,
+                                    uint32_t n_seqs, int32_t cap, int32_t split_tokens,
+                                    uint32_t order, int32_t* s_scan, int32_t* s_key,
+                                    int32_t* s_res) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int K = (int)((n_seqs + 255u) / 256u);  // <= 4
+  int32_t raw[4], full[4], part[4];
+  int32_t fsum = 0, psum = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int s = tid * K + k;
+    raw[k] = 0;
+    full[k] = part[k] = 0;
+    if (k < K && s < (int)n_seqs) {
+      raw[k] = ctx_lens[s];
+      const int32_t c = raw[k] < 0 ? 0 : (raw[k] > cap ? cap : raw[k]);
+      full[k] = c / split_tokens;
+      part[k] = (c == 0 || c % split_tokens != 0) ? 1 : 0;
+    }
+    fsum += full[k];
+    psum += part[k];
+  }
+  if (order == kOrderLongestFirst) {  // K == 1: sort key of the thread's partial split
+    const int32_t c = raw[0] < 0 ? 0 : (raw[0] > cap ? cap : raw[0]);
+    const int32_t nb = (c - full[0] * split_tokens + B - 1) / B;  // <= 65536 blocks
+    s_key[tid] = part[0] ? (((65536 - nb) << 10) | tid) : 0x7fffffff;
+  }
+  // Exclusive scans of the full and partial counts over the threads.
+  int32_t fin = fsum, pin = psum;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t a = __shfl_up(fin, o), b = __shfl_up(pin, o);
+    if (lane >= o) {
+      fin += a;
+      pin += b;
+    }
+  }
+  if (lane == 63) {
+    s_scan[wave] = fin;
+    s_scan[kAttnWaves + wave] = pin;
+  }
+  if (tid == 0) s_res[0] = -1;
+  __syncthreads();
+  int32_t fpre = fin - fsum, ppre = pin - psum, F = 0, P = 0;
+#pragma unroll
+  for (int w = 0; w < kAttnWaves; w++) {
+    if (w < wave) {
+      fpre += s_scan[w];
+      ppre += s_scan[kAttnWaves + w];
+    }
+    F += s_scan[w];
+    P += s_scan[kAttnWaves + w];
+  }
+  if ((int64_t)u < F) {  // a full split: the thread whose run holds unit u
+    if ((int32_t)u >= fpre && (int32_t)u < fpre + fsum) {
+      int32_t base = fpre;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        if ((int32_t)u >= base && (int32_t)u < base + full[k]) {
+          s_res[0] = tid * K + k;
+          s_res[1] = (int32_t)u - base;
+          s_res[2] = raw[k];
+        }
+        base += full[k];
+      }
+    }
+  } else if ((int64_t)u < (int64_t)F + P) {  // a sequence's last, partial split
+    const int32_t p = (int32_t)u - F;
+    if (order == kOrderLongestFirst) {
+      if (part[0]) {
+        const int32_t key = s_key[tid];
+        int32_t rank = 0;
+        for (int j = 0; j < (int)n_seqs; j++) rank += s_key[j] < key ? 1 : 0;
+        if (rank == p) {
+          s_res[0] = tid;
+          s_res[1] = full[0];
+          s_res[2] = raw[0];
+        }
+      }
+    } else if (p >= ppre && p < ppre + psum) {
+      int32_t base = ppre;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        if (part[k] && p == base) {
+          s_res[0] = tid * K + k;
+          s_res[1] = full[k];
+          s_res[2] = raw[k];
+        }
+        base += part[k];
+      }
+    }
+  }
+  __syncthreads();
+  return OrderedItem{s_res[0], s_res[1], s_res[2]};
+}
+
 // Waves per SIMD the split kernel is compiled for (the VGPR budget: 4 -> 128).
 #ifndef FKV_MFMA_WAVES_PER_EU
 #define FKV_MFMA_WAVES_PER_EU 3
@@ -687,20 +813,34 @@ __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
-    const int32_t* __restrict__ ctx_lens, uint32_t max_splits, int32_t split_tokens,
-    float scale, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    const float* __restrict__ k_new, const float* __restrict__ v_new) {
+    const int32_t* __restrict__ ctx_lens, uint32_t n_seqs, uint32_t max_splits,
+    int32_t split_tokens, uint32_t order, float scale, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml, const float* __restrict__ k_new, const float* __restrict__ v_new) {
   constexpr int NC = D / 32, NM = D / 16;
 
   __shared__ float s_o[kAttnWaves][kHeads * D];
   __shared__ float s_m[kAttnWaves][kHeads];
   __shared__ float s_l[kAttnWaves][kHeads];
   __shared__ __align__(16) uint16_t s_app[2][D];  // fused append: encoded K, V rows
+  __shared__ int32_t s_ord[2 * kAttnWaves + 4 + kOrderSortSeqs];  // work order: scans, item, keys
 
-  const uint32_t sk = blockIdx.x;
-  const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int32_t cap = (int32_t)(max_blocks * B);
-  const int32_t split = (int32_t)blockIdx.y;
+  const uint32_t kvh = blockIdx.x % g.n_kv_heads;
+  uint32_t seq;
+  int32_t split, ctx = 0;
+  if (order != kOrderGrid) {
+    const OrderedItem it =
+        ordered_item(blockIdx.x / g.n_kv_heads, ctx_lens, n_seqs, cap, split_tokens, order,
+                     s_ord, s_ord + 2 * kAttnWaves + 4, s_ord + 2 * kAttnWaves);
+    if (it.seq < 0) return;
+    seq = (uint32_t)it.seq;
+    split = it.split;
+    ctx = it.ctx;
+  } else {
+    const uint32_t segs = n_seqs * g.n_kv_heads;
+    seq = (blockIdx.x % segs) / g.n_kv_heads;
+    split = (int32_t)(blockIdx.x / segs);
+  }
   const int32_t s0 = split * split_tokens;
   const int32_t blk0 = s0 / B;  // < max_blocks for every grid row
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -712,10 +852,10 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
 
   // The wave's block-table entries, 64 at a time: lane j holds the entry of the
   // wave's block (t & ~63) + j. A block's physical id then comes from a register
-  // (readlane) instead of a load that its K/V loads would have to wait for. The
-  // first 64 are loaded before the context length is known (indices clamped to
-  // the table row; entries past the split are never used), so the two loads'
-  // latencies overlap.
+  // (readlane) instead of a load that its K/V loads would have to wait for. In
+  // grid order the first 64 are loaded before the context length is known
+  // (indices clamped to the table row; entries past the split are never used),
+  // so the two loads' latencies overlap.
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
   int32_t tabv = 0;
   auto load_tab = [&](int tb) {
@@ -725,7 +865,7 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   };
   load_tab(0);
 
-  int32_t ctx = ctx_lens[seq];
+  if (order == kOrderGrid) ctx = ctx_lens[seq];
   const bool ctx_ok = ctx >= 0 && ctx <= cap;
   if (!ctx_ok) {
     if (split == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
@@ -1171,13 +1311,24 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
                                  float* ws_o, float* ws_ml, const float* k_new,
                                  const float* v_new, hipStream_t s) {
   const uint32_t G = n_heads / g.n_kv_heads;
-  dim3 grid(n_seqs * g.n_kv_heads, max_splits);
+  const dim3 grid(n_seqs * g.n_kv_heads * max_splits);
   constexpr int NBUF = FKV_MFMA_RING;
   const int32_t st = (int32_t)split_tokens;
-#define FKV_LAUNCH_MFMA(DT_, D_)                                                              \
-  attn_mfma_kernel<DT_, D_, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables,  \
-                                                       max_blocks, ctx_lens, max_splits, st,  \
-                                                       scale, ws_o, ws_ml, k_new, v_new)
+  // Longest-first order when the batch is small enough for every workgroup to
+  // rank it; FKV_ATTN_ORDER=0/1/2 forces grid / full-first / longest-first.
+  uint32_t order = n_seqs <= kOrderSortSeqs   ? kOrderLongestFirst
+                   : n_seqs <= kOrderMaxSeqs ? kOrderFullFirst
+                                             : kOrderGrid;
+  if (const char* e = getenv("FKV_ATTN_ORDER")) {
+    const long v = strtol(e, nullptr, 10);
+    if (v == 0 || (v == 1 && n_seqs <= kOrderMaxSeqs) || (v == 2 && n_seqs <= kOrderSortSeqs))
+      order = (uint32_t)v;
+  }
+#define FKV_LAUNCH_MFMA(DT_, D_)                                                             \
+  attn_mfma_kernel<DT_, D_, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
+                                                       max_blocks, ctx_lens, n_seqs,         \
+                                                       max_splits, st, order, scale, ws_o,   \
+                                                       ws_ml, k_new, v_new)
   if (g.dtype == kDtypeQ8) {
     if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128);
     else FKV_LAUNCH_MFMA(kDtypeQ8, 64);

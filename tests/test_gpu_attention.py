@@ -103,6 +103,81 @@ def test_attention_long_context_uses_combine(f16_schedule):
     assert_close(got, want)
 
 
+ORDER_CTXS = [0, 1, 511, 512, 513, 1024, 1500, 3000, 17, 4100, 0, 2048, 700]
+
+
+@pytest.mark.parametrize("dtype", [1, 8])
+def test_work_orders_are_bit_identical(dtype, monkeypatch):
+    """The split kernel's workgroups take the (sequence, KV head, split) items in
+    grid order, full-first order or longest-first order (FKV_ATTN_ORDER=0/1/2).
+    An item is computed the same way whichever workgroup takes it, so the three
+    outputs agree bit for bit; empty contexts, contexts of whole splits and a
+    9-split context are in the batch."""
+    import ferrum_amd as fa
+    from oracle import ref
+    hkv, g, d = 2, 4, 128
+    pool, layout, tab = _build(dtype, d, hkv, ORDER_CTXS, seed=21, layers=1)
+    q = np.random.default_rng(8).standard_normal((len(ORDER_CTXS), hkv * g, d), dtype=np.float32)
+    outs = []
+    for order in ("0", "1", "2"):
+        monkeypatch.setenv("FKV_ATTN_ORDER", order)
+        outs.append(_run(pool, 0, q, tab, ORDER_CTXS))
+    assert pool.take_fault_flags() == 0
+    assert np.all(outs[0][0] == 0.0) and np.all(outs[0][10] == 0.0)
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array(ORDER_CTXS), fa.default_scale(d))
+    assert_close(outs[2], want)
+    pool.close()
+
+
+@pytest.mark.parametrize("order", ["0", "1", "2"])
+def test_context_outside_the_table_is_flagged(order, monkeypatch):
+    """A context length past the table row (or negative) raises FKV_FAULT_CTX_RANGE in
+    every work order; the sequence is read up to the row's end (or not at all, with
+    a zero output) and the other sequences are unaffected."""
+    import ferrum_amd as fa
+    from oracle import ref
+    monkeypatch.setenv("FKV_ATTN_ORDER", order)
+    ctxs = [40, 1100, 600]
+    pool, layout, tab = _build(1, 128, 2, ctxs, seed=6, layers=1)
+    cap = tab.shape[1] * 16
+    q = np.random.default_rng(2).standard_normal((3, 8, 128), dtype=np.float32)
+    bad = [40, cap + 5, -3]
+    import torch
+    out = torch.full(q.shape, 123.0, dtype=torch.float32, device="cuda")
+    # max_ctx_len is checked on the host; the device-side lengths are not
+    pool.decode_attention(0, to_dev(q), out, to_dev(tab), to_dev(np.array(bad, np.int32)), cap)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert pool.take_fault_flags() & fa.FAULT_CTX_RANGE
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array([40, cap, 0]), fa.default_scale(128))
+    assert_close(got, want)
+    assert np.all(got[2] == 0.0)
+    pool.close()
+
+
+@pytest.mark.parametrize("n_seqs", [300, 1100])
+def test_large_batches_match_oracle(n_seqs, monkeypatch):
+    """300 sequences take the full-first order (three or fewer per thread of the
+    ranking), 1,100 the grid order; both against the oracle and the grid order."""
+    import ferrum_amd as fa
+    from oracle import ref
+    hkv, g, d = 1, 4, 64
+    ctxs = [int(c) for c in np.random.default_rng(n_seqs).integers(0, 1100, n_seqs)]
+    pool, layout, tab = _build(1, d, hkv, ctxs, seed=2, layers=1)
+    q = np.random.default_rng(4).standard_normal((n_seqs, hkv * g, d), dtype=np.float32)
+    monkeypatch.delenv("FKV_ATTN_ORDER", raising=False)
+    got = _run(pool, 0, q, tab, ctxs)
+    monkeypatch.setenv("FKV_ATTN_ORDER", "0")
+    grid = _run(pool, 0, q, tab, ctxs)
+    assert pool.take_fault_flags() == 0
+    assert np.array_equal(got.view(np.uint32), grid.view(np.uint32))
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array(ctxs), fa.default_scale(d))
+    assert_close(got, want)
+    pool.close()
+
+
 def test_attention_is_invariant_to_block_placement():
     q = np.random.default_rng(9).standard_normal((len(CTXS), 8, 128), dtype=np.float32)
     outs = []
