@@ -531,20 +531,26 @@ struct AttnPlan {
 
 inline uint64_t align256(uint64_t x) { return (x + 255) / 256 * 256; }
 
-// Split length: long enough that the final cross-split merge stays small
-// (<= 64 splits per sequence when there are many sequences), short enough that
-// the launch has thousands of workgroups: a batch of few sequences may split
-// further, up to ~4096 (sequence, KV head, split) workgroups, never below 512
-// tokens. FKV_ATTN_SPLIT_TOKENS (a multiple of 16) overrides.
+// Split length. A workgroup pays a fixed cost (its start, the latency of its first
+// block-table and K/V loads, the merge of its 4 waves, the partial it writes, and
+// the combine's read of it) that a longer split spreads over more bytes, while
+// the last workgroups' lengths set how ragged the kernel's end is. Measured on
+// MI355X with the longest-first order, the best lengths made about 2,048 (sequence,
+// KV head, split) workgroups at the longest context in the batch (64 x U[128, 4096]
+// tokens: 1,024; 128 x 8,192: 4,096; 256 log-normal contexts up to 32k: 8,192),
+// with at most about 64 splits per head (1 x 131,072 tokens: 2,048; longer splits
+// leave CUs idle there). So: the larger of max_ctx * segments / 2048 and
+// max_ctx / 64, to the nearest multiple of 256, within [512, 8192].
+// FKV_ATTN_SPLIT_TOKENS (a multiple of 16) overrides.
 uint32_t choose_split_tokens(uint32_t max_ctx_len, uint32_t n_seqs, uint32_t n_kv_heads) {
   if (const char* e = getenv("FKV_ATTN_SPLIT_TOKENS")) {
     long v = strtol(e, nullptr, 10);
     if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) return (uint32_t)v;
   }
   const uint64_t segs = (uint64_t)n_seqs * (n_kv_heads ? n_kv_heads : 1);
-  uint64_t max_splits = segs ? 4096 / segs : 64;
-  if (max_splits < 64) max_splits = 64;
-  uint64_t st = (((uint64_t)max_ctx_len + max_splits - 1) / max_splits + 255) / 256 * 256;
+  const uint64_t by_items = (uint64_t)max_ctx_len * segs / 2048;
+  const uint64_t by_head = ((uint64_t)max_ctx_len + 63) / 64;
+  uint64_t st = ((by_items > by_head ? by_items : by_head) + 128) / 256 * 256;
   if (st < 512) st = 512;
   if (st > 8192) st = 8192;
   return (uint32_t)st;
