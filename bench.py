@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
+    ap.add_argument("--rope-dim", type=int, default=0,
+                    help="> 0: time fkv_rope_append_decode_attention (q and k before RoPE)")
+    ap.add_argument("--rope-theta", type=float, default=500000.0)
     return ap.parse_args()
 
 
@@ -181,7 +184,7 @@ class DecodeLoop:
     ctx_step[t] holds every sequence's context after step t's append."""
 
     def __init__(self, torch, fa, lib, pool, L, n_seqs, hq, hkv, d, tables, ctx0, n_steps, gen,
-                 dev, seqs=None):
+                 dev, seqs=None, rope=(0, 0.0)):
         self.torch, self.fa, self.lib, self.pool, self.L = torch, fa, lib, pool, L
         self.n_seqs, self.hq, self.hkv, self.d = n_seqs, hq, hkv, d
         self.q = torch.randn((L, n_seqs, hq, d), generator=gen, device=dev)
@@ -194,9 +197,12 @@ class DecodeLoop:
         self.tables_d = torch.from_numpy(tables).to(dev)
         self.max_blocks = tables.shape[1]
         self.max_ctx = int(self.ctx_step.max())
+        self.rope_dim, self.rope_theta = int(rope[0]), float(rope[1])
         n = ctypes.c_uint64()
-        fa.errors.check(lib.fkv_append_decode_attention_workspace_size(
-            ctypes.c_void_p(pool.handle), hq, n_seqs, self.max_ctx, ctypes.byref(n)))
+        size_fn = (lib.fkv_rope_append_decode_attention_workspace_size if self.rope_dim
+                   else lib.fkv_append_decode_attention_workspace_size)
+        fa.errors.check(size_fn(ctypes.c_void_p(pool.handle), hq, n_seqs, self.max_ctx,
+                                ctypes.byref(n)))
         self.ws_bytes = n.value
         self.ws = torch.zeros(max(self.ws_bytes, 16), dtype=torch.uint8, device=dev)
         self.scale = fa.default_scale(d)
@@ -209,9 +215,15 @@ class DecodeLoop:
         tp = self.tables_d.data_ptr()
         for l in range(self.L):
             qp, op, kp, vp = self.ptrs[l]
-            rc = self.lib.fkv_append_decode_attention(
-                self.h, l, self.hq, kp, vp, qp, op, tp, self.max_blocks, cl, self.n_seqs,
-                self.max_ctx, self.scale, self.ws.data_ptr(), self.ws_bytes, sp)
+            if self.rope_dim:
+                rc = self.lib.fkv_rope_append_decode_attention(
+                    self.h, l, self.hq, self.rope_dim, self.rope_theta, kp, vp, qp, op, tp,
+                    self.max_blocks, cl, self.n_seqs, self.max_ctx, self.scale,
+                    self.ws.data_ptr(), self.ws_bytes, sp)
+            else:
+                rc = self.lib.fkv_append_decode_attention(
+                    self.h, l, self.hq, kp, vp, qp, op, tp, self.max_blocks, cl, self.n_seqs,
+                    self.max_ctx, self.scale, self.ws.data_ptr(), self.ws_bytes, sp)
             if rc:
                 self.fa.errors.check(rc)
 
@@ -308,6 +320,9 @@ def cpu_baseline(args, pool, tables, ctx, q_layer, out_layer, layer, hq, hkv, d,
     for j, (s, n) in enumerate(zip(seqs, nb)):
         tab[j, :n] = [remap[int(b)] for b in tables[s, :n]]
     qh = np.ascontiguousarray(q_layer[seqs])
+    if args.rope_dim:  # the step attended with q rotated at position ctx - 1
+        for j, c in enumerate(ctx):
+            qh[j] = ref.rope(qh[j], args.rope_dim, int(c) - 1 if c > 0 else 0, args.rope_theta)
     gpu_out = out_layer[seqs]
     scale = fa.default_scale(d)
     threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -372,8 +387,11 @@ def decode_workload(args, torch, fa, lib, dev, *, name, L, n_seqs, hq, hkv, d, d
     fill_ms = []
     n_fill = fill_context(torch, pool, range(L), tables, ctx0, hkv, d, gen, dev,
                           outlier_frac=outlier_frac, timer=fill_ms)
-    dl = DecodeLoop(torch, fa, lib, pool, L, n_seqs, hq, hkv, d, tables, ctx0, W + K, gen, dev)
+    dl = DecodeLoop(torch, fa, lib, pool, L, n_seqs, hq, hkv, d, tables, ctx0, W + K, gen, dev,
+                    rope=(args.rope_dim, args.rope_theta))
     wall, region_ms = dl.run(W, K)
+    if args.rope_dim:
+        extra_cfg = dict(extra_cfg or {}, rope_dim=args.rope_dim, rope_theta=args.rope_theta)
     e = elem_bytes(dtype)
     kname = ("fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)" if dtype == 1
              else "fkv_append_decode_attention (tail slots + append + attn_mfma_kernel<q8_0> + combine)")
@@ -517,7 +535,7 @@ def run_c3(args, torch, fa, lib, dev):
     fill_context(torch, pool, range(L), tables, np.concatenate([ctx_dec, pre_prior]), hkv, d,
                  gen, dev)
     dl = DecodeLoop(torch, fa, lib, pool, L, n_dec, hq, hkv, d, tables[:n_dec], ctx_dec, W + K,
-                    gen, dev)
+                    gen, dev, rope=(args.rope_dim, args.rope_theta))
     # prefill inputs: chunk t of sequence p covers positions prior + t*chunk .. +chunk-1
     tab_pre = torch.from_numpy(np.ascontiguousarray(tables[n_dec:])).to(dev)
     kp = torch.randn((L, n_pre * chunk, hkv, d), generator=gen, device=dev)
@@ -615,7 +633,8 @@ def run_c1(args, torch, fa, lib, dev):
     fill_ms = []
     fill_context(torch, pool, range(L), tables, np.array([512]), hkv, d, gen, dev, timer=fill_ms)
     K = 64
-    dl = DecodeLoop(torch, fa, lib, pool, L, 1, hq, hkv, d, tables, np.array([512]), K, gen, dev)
+    dl = DecodeLoop(torch, fa, lib, pool, L, 1, hq, hkv, d, tables, np.array([512]), K, gen, dev,
+                    rope=(args.rope_dim, args.rope_theta))
     wall, region_ms = dl.run(0, K)
     res = decode_result(args, dl, 0, K, wall, region_ms, 2.0, "tinyllama prefill 512 + 64 "
                         "decode steps (BASELINE configs[0])", {"kv_dtype": "f16"},

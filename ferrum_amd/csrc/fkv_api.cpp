@@ -6,6 +6,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -423,7 +424,8 @@ static int32_t decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads
                                 float* out, const int32_t* block_tables,
                                 uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
                                 uint32_t n_seqs, uint32_t max_ctx_len, float scale,
-                                void* workspace, uint64_t workspace_bytes, void* stream) {
+                                void* workspace, uint64_t workspace_bytes, void* stream,
+                                const fkv::RopeTable* rope = nullptr) {
   if (!pool) return fail(FKV_ERR_INVALID, "null argument");
   if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
   int32_t st = check_attention(pool, n_heads, max_ctx_len);
@@ -437,13 +439,14 @@ static int32_t decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads
     return fail(FKV_ERR_INVALID, "max_ctx_len exceeds the block table");
   DeviceGuard dg(pool->cfg.device);
   const uint64_t need =
-      k_new ? fkv::append_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len)
-            : fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
+      rope    ? fkv::rope_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len)
+      : k_new ? fkv::append_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len)
+              : fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
   if (workspace_bytes < need || (need && !workspace))
     return fail(FKV_ERR_INVALID, "attention workspace too small");
   FKV_HIP(fkv::launch_decode_attention(pool->geom, layer, n_heads, q, out, block_tables,
                                        max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale,
-                                       workspace, k_new, v_new, (hipStream_t)stream),
+                                       workspace, k_new, v_new, (hipStream_t)stream, rope),
           "decode_attention");
   return ok();
 }
@@ -479,6 +482,49 @@ int32_t fkv_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_h
   return decode_attention(pool, layer, n_heads, k_new, v_new, q, out, block_tables,
                           max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale, workspace,
                           workspace_bytes, stream);
+}
+
+// Kernels::rope's checks, in its order (crates/kernels/src/validate.rs:64-87: theta,
+// then parity, then shape), and the per-pair denominators theta^(2i / rope_dim)
+// computed in f32 as math.rs:31-34 does.
+static int32_t rope_table(const fkv_pool* pool, uint32_t rope_dim, float theta,
+                          fkv::RopeTable* t) {
+  if (!(theta > 0.0f)) return fail(FKV_ERR_KERNEL, "theta must be positive");
+  if (rope_dim % 2 != 0) return fail(FKV_ERR_KERNEL, "rope_dim must be even");
+  if (rope_dim > pool->cfg.head_dim) return fail(FKV_ERR_KERNEL, "rope_dim exceeds head_dim");
+  *t = fkv::RopeTable{};
+  t->rope_dim = (int32_t)rope_dim;
+  for (uint32_t i = 0; i < rope_dim / 2; i++)
+    t->den[i] = powf(theta, (float)(2 * i) / (float)rope_dim);
+  return FKV_OK;
+}
+
+int32_t fkv_rope_append_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                                        uint32_t n_seqs, uint32_t max_ctx_len,
+                                                        uint64_t* bytes_out) {
+  if (!pool || !bytes_out) return fail(FKV_ERR_INVALID, "null argument");
+  int32_t st = check_attention(pool, n_heads, max_ctx_len);
+  if (st) return st;
+  DeviceGuard dg(pool->cfg.device);
+  *bytes_out = fkv::rope_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
+  return ok();
+}
+
+int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                                         uint32_t rope_dim, float theta, const float* k_new,
+                                         const float* v_new, const float* q, float* out,
+                                         const int32_t* block_tables, uint32_t max_blocks_per_seq,
+                                         const int32_t* ctx_lens, uint32_t n_seqs,
+                                         uint32_t max_ctx_len, float scale, void* workspace,
+                                         uint64_t workspace_bytes, void* stream) {
+  if (!pool) return fail(FKV_ERR_INVALID, "null argument");
+  fkv::RopeTable rope;
+  int32_t st = rope_table(pool, rope_dim, theta, &rope);
+  if (st) return st;
+  if (n_seqs && (!k_new || !v_new)) return fail(FKV_ERR_INVALID, "null argument");
+  return decode_attention(pool, layer, n_heads, k_new, v_new, q, out, block_tables,
+                          max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale, workspace,
+                          workspace_bytes, stream, &rope);
 }
 
 int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,

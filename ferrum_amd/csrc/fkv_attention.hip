@@ -600,7 +600,51 @@ uint64_t append_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint3
   return p.total + align256((uint64_t)n_seqs * sizeof(int64_t));
 }
 
+uint64_t rope_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
+                                        uint32_t max_ctx_len) {
+  const uint64_t base = append_attention_workspace_bytes(g, n_heads, n_seqs, max_ctx_len);
+  const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
+  if (p.mfma_path && g.dtype == kDtypeF16) return base;  // rotated inside the kernel
+  return base +
+         align256((uint64_t)n_seqs * (n_heads + g.n_kv_heads) * g.head_dim * sizeof(float));
+}
+
 namespace {
+
+// RoPE rows for storage the decode kernels do not rotate in place: pair p of row
+// (s, h) of q [n_seqs][n_heads][D] and of k [n_seqs][n_kv][D], rotated at position
+// ctx_lens[s] - 1 as the reference does (crates/kernels/src/scalar.rs:167-189).
+__global__ void __launch_bounds__(256) rope_rows_kernel(RopeTable rope, const int32_t* __restrict__ ctx_lens,
+                                                        int32_t cap, uint32_t n_seqs, uint32_t n_heads,
+                                                        uint32_t n_kv, uint32_t D,
+                                                        const float* __restrict__ q,
+                                                        const float* __restrict__ k,
+                                                        float* __restrict__ q_out,
+                                                        float* __restrict__ k_out) {
+  const uint32_t half = D / 2, rows = n_heads + n_kv;
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= (uint64_t)n_seqs * rows * half) return;
+  const uint32_t pr = (uint32_t)(i % half);
+  const uint64_t row = i / half;
+  const uint32_t s = (uint32_t)(row / rows), h = (uint32_t)(row % rows);
+  const uint64_t off = h < n_heads ? ((uint64_t)s * n_heads + h) * D + 2 * pr
+                                   : ((uint64_t)s * n_kv + (h - n_heads)) * D + 2 * pr;
+  const float* src = h < n_heads ? q : k;
+  float* dst = h < n_heads ? q_out : k_out;
+  float a = src[off], b = src[off + 1];
+  if ((int32_t)(2 * pr) < rope.rope_dim) {
+    int32_t c = ctx_lens[s];
+    c = c < 0 ? 0 : (c > cap ? cap : c);
+    const float freq = (float)(c > 0 ? c - 1 : 0) / rope.den[pr];
+    float sn, cs;
+    sincosf(freq, &sn, &cs);
+    const float a2 = a * cs - b * sn, b2 = a * sn + b * cs;
+    a = a2;
+    b = b2;
+  }
+  dst[off] = a;
+  dst[off + 1] = b;
+}
 
 __global__ void __launch_bounds__(256) tail_slots_kernel(Geom g, const int32_t* __restrict__ tables,
                                                          uint32_t max_blocks,
@@ -637,11 +681,25 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
                                    uint32_t max_blocks, const int32_t* ctx_lens,
                                    uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                                    void* workspace, const float* k_new, const float* v_new,
-                                   hipStream_t s) {
+                                   hipStream_t s, const RopeTable* rope) {
   if (n_seqs == 0) return hipSuccess;
   const uint32_t G = n_heads / g.n_kv_heads;
   const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
   uint8_t* ws = (uint8_t*)workspace;
+  if (rope != nullptr && rope->rope_dim > 0 && !(p.mfma_path && g.dtype == kDtypeF16)) {
+    // Rotate q and the new K rows into the workspace, then run the unrotated step.
+    float* q_rot = (float*)(ws + append_attention_workspace_bytes(g, n_heads, n_seqs, max_ctx_len));
+    float* k_rot = q_rot + (uint64_t)n_seqs * n_heads * g.head_dim;
+    const uint64_t pairs = (uint64_t)n_seqs * (n_heads + g.n_kv_heads) * (g.head_dim / 2);
+    rope_rows_kernel<<<(uint32_t)((pairs + 255) / 256), 256, 0, s>>>(
+        *rope, ctx_lens, (int32_t)(max_blocks * g.block_size), n_seqs, n_heads, g.n_kv_heads,
+        g.head_dim, q, k_new, q_rot, k_rot);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    q = q_rot;
+    k_new = k_rot;
+    rope = nullptr;
+  }
   if (k_new != nullptr && !(p.mfma_path && g.dtype == kDtypeF16)) {
     // Separate append launch: slots derived from the block tables first.
     int64_t* slots = (int64_t*)(ws + p.total);
@@ -659,7 +717,7 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
     float* ws_ml = ws ? (float*)(ws + p.ml_off) : nullptr;
     hipError_t e = launch_attention_mfma(g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
                                          n_seqs, p.max_splits, p.split_tokens, scale, ws_o,
-                                         ws_ml, k_new, v_new, s);
+                                         ws_ml, k_new, v_new, s, rope);
     if (e != hipSuccess || p.max_splits <= 1) return e;
     return launch_attention_combine(g.head_dim, ctx_lens, n_seqs, n_heads, max_blocks,
                                     p.max_splits, p.split_tokens, ws_o, ws_ml, out, s);

@@ -96,10 +96,16 @@ struct Lane {
 // gets a power-of-two scaling (its largest |q * scale * log2 e| lands in
 // [2^14, 2^15), far from f16 overflow), then an f16 hi + lo split; hscale undoes
 // the scaling.
-template <int D>
+//
+// ROPE: q is before RoPE. Lane p of the wave holds (sin, cos) of pair p (dims 2p,
+// 2p + 1) in rsin / rcos; the lane's eight dims are four whole pairs, rotated as
+// the reference does (a' = a cos - b sin, b' = a sin + b cos, each product rounded)
+// before the scaling.
+template <int D, bool ROPE = false>
 __device__ __forceinline__ void prep_q(const float* qrow, const Lane& ln, float qscale,
                                        f16x8 (&qh)[D / 32], f16x8 (&ql)[D / 32],
-                                       float& hscale) {
+                                       float& hscale, float rsin = 0.0f, float rcos = 1.0f,
+                                       int rope_dim = 0) {
   constexpr int NC = D / 32;
   const float* qb = qrow + ln.grp * 8;
   float x[NC][8];
@@ -108,7 +114,19 @@ __device__ __forceinline__ void prep_q(const float* qrow, const Lane& ln, float 
   for (int c = 0; c < NC; c++) {
     const float4 a = *(const float4*)(qb + c * 32);
     const float4 b = *(const float4*)(qb + c * 32 + 4);
-    const float v8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    float v8[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    if constexpr (ROPE) {
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const int dim = c * 32 + ln.grp * 8 + e;
+        const float sn = __shfl(rsin, dim >> 1), cs = __shfl(rcos, dim >> 1);
+        if (dim < rope_dim) {
+          const float u = v8[e], w = v8[e + 1];
+          v8[e] = u * cs - w * sn;
+          v8[e + 1] = u * sn + w * cs;
+        }
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       x[c][e] = ln.real ? v8[e] * qscale : 0.0f;
@@ -808,14 +826,15 @@ __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_
 #define FKV_MFMA_WAVES_PER_EU 3
 #endif
 
-template <int DT, int D, int NBUF>
+template <int DT, int D, int NBUF, bool ROPE>
 __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
     const int32_t* __restrict__ ctx_lens, uint32_t n_seqs, uint32_t max_splits,
     int32_t split_tokens, uint32_t order, float scale, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, const float* __restrict__ k_new, const float* __restrict__ v_new) {
+    float* __restrict__ ws_ml, const float* __restrict__ k_new, const float* __restrict__ v_new,
+    const RopeTable rope) {
   constexpr int NC = D / 32, NM = D / 16;
 
   __shared__ float s_o[kAttnWaves][kHeads * D];
@@ -876,6 +895,16 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   const int32_t s1 = ctx - s0 < split_tokens ? ctx : s0 + split_tokens;
   const int32_t nblk = s1 > s0 ? (s1 - s0 + B - 1) / B : 0;
 
+  // RoPE at the new token's position ctx - 1: lane p holds (sin, cos) of pair p,
+  // pos / den[p] as the reference computes it (f32 division, then sin and cos).
+  float rsin = 0.0f, rcos = 1.0f;
+  if constexpr (ROPE) {
+    if (2 * ln.lane < rope.rope_dim) {
+      const float freq = (float)(ctx > 0 ? ctx - 1 : 0) / rope.den[ln.lane];
+      sincosf(freq, &rsin, &rcos);
+    }
+  }
+
   // Fused append (k_new != nullptr): the token at position ctx - 1 of this KV
   // head is stored by the wave of the last split that reads its block. That wave
   // encodes the token (f32 -> binary16 with the pool's rounding) up front and,
@@ -896,7 +925,13 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
 #pragma unroll
     for (int i = 0; i < D / 64; i++) {
       const int dd = i * 64 + ln.lane;
-      s_app[0][dd] = (uint16_t)encode_f16(ksrc[dd], g.rounding);
+      float kv = ksrc[dd];
+      if constexpr (ROPE) {  // dims (dd & ~1, dd | 1) are a pair on adjacent lanes
+        const float other = __shfl_xor(kv, 1);
+        const float sn = __shfl(rsin, dd >> 1), cs = __shfl(rcos, dd >> 1);
+        if (dd < rope.rope_dim) kv = (dd & 1) ? other * sn + kv * cs : kv * cs - other * sn;
+      }
+      s_app[0][dd] = (uint16_t)encode_f16(kv, g.rounding);
       s_app[1][dd] = (uint16_t)encode_f16(vsrc[dd], g.rounding);
     }
   }
@@ -989,8 +1024,8 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     }
   }
   // q is read after the first K/V loads are issued, so its latency overlaps theirs.
-  prep_q<D>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D, ln,
-            scale * kLog2e, qh, ql, hscale);
+  prep_q<D, ROPE>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D,
+                  ln, scale * kLog2e, qh, ql, hscale, rsin, rcos, rope.rope_dim);
   for (int t = 0; t < nt; t += NBUF) {
 #pragma unroll
     for (int b = 0; b < NBUF; b++)
@@ -1309,7 +1344,7 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
                                  uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
                                  uint32_t max_splits, uint32_t split_tokens, float scale,
                                  float* ws_o, float* ws_ml, const float* k_new,
-                                 const float* v_new, hipStream_t s) {
+                                 const float* v_new, hipStream_t s, const RopeTable* rope) {
   const uint32_t G = n_heads / g.n_kv_heads;
   const dim3 grid(n_seqs * g.n_kv_heads * max_splits);
   constexpr int NBUF = FKV_MFMA_RING;
@@ -1324,17 +1359,26 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
     if (v == 0 || (v == 1 && n_seqs <= kOrderMaxSeqs) || (v == 2 && n_seqs <= kOrderSortSeqs))
       order = (uint32_t)v;
   }
-#define FKV_LAUNCH_MFMA(DT_, D_)                                                             \
-  attn_mfma_kernel<DT_, D_, NBUF><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
-                                                       max_blocks, ctx_lens, n_seqs,         \
-                                                       max_splits, st, order, scale, ws_o,   \
-                                                       ws_ml, k_new, v_new)
+  // RoPE in the kernel: F16 storage only (other storage rotates q and k_new into
+  // the workspace before the launch).
+  const bool roped = rope != nullptr && rope->rope_dim > 0;
+  if (roped && g.dtype != kDtypeF16) return hipErrorInvalidValue;
+  RopeTable rt{};
+  if (roped) rt = *rope;
+#define FKV_LAUNCH_MFMA(DT_, D_, R_)                                                             \
+  attn_mfma_kernel<DT_, D_, NBUF, R_><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
+                                                           max_blocks, ctx_lens, n_seqs,         \
+                                                           max_splits, st, order, scale, ws_o,   \
+                                                           ws_ml, k_new, v_new, rt)
   if (g.dtype == kDtypeQ8) {
-    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128);
-    else FKV_LAUNCH_MFMA(kDtypeQ8, 64);
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, false);
+    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, false);
+  } else if (roped) {
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128, true);
+    else FKV_LAUNCH_MFMA(kDtypeF16, 64, true);
   } else {
-    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128);
-    else FKV_LAUNCH_MFMA(kDtypeF16, 64);
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128, false);
+    else FKV_LAUNCH_MFMA(kDtypeF16, 64, false);
   }
 #undef FKV_LAUNCH_MFMA
   return hipGetLastError();

@@ -31,6 +31,15 @@ constexpr int kDtypeF32 = 0;
 constexpr int kDtypeF16 = 1;
 constexpr int kDtypeQ8 = 8;
 
+// RoPE of the decode step's new token (GGML_ROPE_TYPE_NORMAL: dims (2i, 2i+1)
+// rotate by pos / den[i], den[i] = theta^(2i / rope_dim) computed on the host
+// exactly as the reference computes it in f32; crates/kernels/src/math.rs:27-34,
+// scalar.rs:167-189). rope_dim = 0: no rotation.
+struct RopeTable {
+  int32_t rope_dim;  // even, <= head_dim <= 128
+  float den[64];
+};
+
 constexpr uint32_t kFaultSlot = 1u;
 constexpr uint32_t kFaultBlock = 2u;
 constexpr uint32_t kFaultCtx = 4u;
@@ -79,7 +88,8 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
                                  uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
                                  uint32_t max_splits, uint32_t split_tokens, float scale,
                                  float* ws_o, float* ws_ml, const float* k_new,
-                                 const float* v_new, hipStream_t s);
+                                 const float* v_new, hipStream_t s,
+                                 const RopeTable* rope = nullptr);
 // F16 decode attention, persistent schedule (fkv_attention_mfma.hip): n_waves
 // waves share the flattened (sequence, KV head, block) list equally; needs
 // 1 <= n_seqs <= kStreamMaxSeqs (the LDS prefix table). ws_pre holds n_seqs + 1
@@ -111,12 +121,19 @@ hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
                                     hipStream_t s);
 // k_new/v_new non-null: append each sequence's token at position ctx_lens[s] - 1
 // (through its block table) before attending; one launch for F16 storage.
+// rope non-null (with rope->rope_dim > 0): q and k_new are before RoPE; each
+// sequence's are rotated at position ctx_lens[s] - 1 (in the kernel for F16
+// storage; through the workspace's RoPE rows otherwise).
 hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
                                    const float* q, float* out, const int32_t* tables,
                                    uint32_t max_blocks, const int32_t* ctx_lens,
                                    uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                                    void* workspace, const float* k_new, const float* v_new,
-                                   hipStream_t s);
+                                   hipStream_t s, const RopeTable* rope = nullptr);
+// Workspace of a RoPE decode step: append_attention_workspace_bytes, plus room for
+// the rotated q and k rows when the storage is not F16.
+uint64_t rope_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
+                                        uint32_t max_ctx_len);
 // Slot of position ctx_lens[s] - 1 through the block table (-1 for an empty
 // context or an entry outside the pool, which raises kFaultBlock).
 hipError_t launch_tail_slots(const Geom& g, const int32_t* tables, uint32_t max_blocks,

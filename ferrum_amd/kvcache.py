@@ -350,6 +350,41 @@ class PagedKvPool:
             block_tables.shape[1], _dev(ctx_lens, torch.int32, "ctx_lens"), n_seqs, max_ctx_len,
             scale, ws_ptr, ws_bytes, _stream_ptr(stream)))
 
+    def rope_append_decode_attention(self, layer: int, k_new, v_new, q, out, block_tables,
+                                     ctx_lens, max_ctx_len: int, rope_dim: int, theta: float,
+                                     scale: Optional[float] = None, workspace=None,
+                                     stream=None) -> None:
+        """append_decode_attention with q and k_new before RoPE (llama.rs:207-247):
+        each sequence's q and k_new are rotated at position ctx_lens[s] - 1 (dims
+        (2i, 2i+1) below rope_dim, angle pos / theta^(2i/rope_dim); scalar.rs:167-189)
+        before the append and the attention. q is not written back."""
+        import torch
+        n_seqs, n_heads, d = q.shape
+        if d != self.config.head_dim or tuple(out.shape) != tuple(q.shape):
+            raise ValueError("q/out must be [n_seqs, n_heads, head_dim]")
+        kv_shape = (n_seqs, self.config.n_kv_heads, d)
+        if tuple(k_new.shape) != kv_shape or tuple(v_new.shape) != kv_shape:
+            raise ValueError("k_new/v_new must be [n_seqs, n_kv_heads, head_dim]")
+        if block_tables.shape[0] != n_seqs or ctx_lens.numel() != n_seqs:
+            raise ValueError("block_tables/ctx_lens must have one row per sequence")
+        if scale is None:
+            scale = default_scale(d)
+        n = ctypes.c_uint64()
+        check(self._lib.fkv_rope_append_decode_attention_workspace_size(
+            self._h, n_heads, n_seqs, max_ctx_len, ctypes.byref(n)))
+        need = n.value
+        ws_ptr, ws_bytes = 0, 0
+        if need:
+            if workspace is None:
+                workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+            ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
+        check(self._lib.fkv_rope_append_decode_attention(
+            self._h, layer, n_heads, rope_dim, theta, _dev(k_new, torch.float32, "k_new"),
+            _dev(v_new, torch.float32, "v_new"), _dev(q, torch.float32, "q"),
+            _dev(out, torch.float32, "out"), _dev(block_tables, torch.int32, "block_tables"),
+            block_tables.shape[1], _dev(ctx_lens, torch.int32, "ctx_lens"), n_seqs, max_ctx_len,
+            scale, ws_ptr, ws_bytes, _stream_ptr(stream)))
+
     def prefill_attention(self, layer: int, q, out, block_tables, ctx_lens, q_lens, q_offsets,
                           max_q_len: int, max_ctx_len: int, scale: Optional[float] = None,
                           stream=None) -> None:

@@ -287,6 +287,33 @@ int32_t fkv_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_h
                                     uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                                     void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* fkv_append_decode_attention with q and k_new before RoPE: the layer's
+ * Kernels::rope call (crates/model/src/llama.rs:207-216; scalar.rs:77-82,167-189,
+ * math.rs:27-34), then its append and attention loop. Every query head of q[s]
+ * and every KV head of k_new[s] is rotated at position pos = ctx_lens[s] - 1:
+ * dims (2i, 2i+1) with 2i < rope_dim (GGML_ROPE_TYPE_NORMAL) turn by
+ * f = pos / theta^(2i / rope_dim), all in f32 as the reference computes it
+ * (a' = a cos f - b sin f, b' = a sin f + b cos f); dims from rope_dim on are
+ * unchanged; rope_dim = 0 rotates nothing. The rotated K is what the pool stores;
+ * q is read only (the rotation is not written back). Checks, in the reference's
+ * order (validate.rs:64-87), before any other: FKV_ERR_KERNEL "kernel: theta must
+ * be positive" (theta <= 0 or NaN), "kernel: rope_dim must be even", "kernel:
+ * rope_dim exceeds head_dim". F16 storage rotates inside the one kernel launch;
+ * Q8_0 and F32 storage rotate q and k_new into the workspace first. sin and cos
+ * come from the device's sincosf, so stored K can differ from a CPU rotation by
+ * one f16 rounding step where a value sits on a rounding boundary.
+ * workspace: fkv_rope_append_decode_attention_workspace_size() bytes. */
+int32_t fkv_rope_append_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                                        uint32_t n_seqs, uint32_t max_ctx_len,
+                                                        uint64_t* bytes_out);
+int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                                         uint32_t rope_dim, float theta, const float* k_new,
+                                         const float* v_new, const float* q, float* out,
+                                         const int32_t* block_tables, uint32_t max_blocks_per_seq,
+                                         const int32_t* ctx_lens, uint32_t n_seqs,
+                                         uint32_t max_ctx_len, float scale, void* workspace,
+                                         uint64_t workspace_bytes, void* stream);
+
 /* Chunked-prefill attention over F16 storage: the reference's token-by-token
  * prefill (crates/model/src/llama.rs:363-378, each token running the attention
  * loop of :220-247 over positions 0 ..= its own) for a chunk whose K/V are

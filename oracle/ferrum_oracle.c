@@ -197,6 +197,28 @@ static float softmax_max(const float* x, uint64_t n) {
   return max;
 }
 
+/* rope_tensor, crates/kernels/src/scalar.rs:167-189, with the angle of
+ * math.rs:31-34: in every head_dim row, dims (2i, 2i+1) with 2i < rope_dim
+ * (GGML_ROPE_TYPE_NORMAL) rotate by f = pos / theta^(2i / rope_dim), everything in
+ * f32 and each product rounded (a' = a cos f - b sin f, b' = a sin f + b cos f).
+ * Returns without change when head_dim == 0, rope_dim == 0 or rope_dim > head_dim
+ * (scalar.rs:174-176). */
+void fo_rope(float* data, uint64_t n_rows, uint32_t head_dim, uint32_t rope_dim, uint32_t pos,
+             float theta) {
+  if (head_dim == 0 || rope_dim == 0 || rope_dim > head_dim) return;
+  for (uint64_t r = 0; r < n_rows; r++) {
+    float* h = data + r * head_dim;
+    for (uint32_t i = 0; i < rope_dim; i += 2) {
+      const uint32_t pair = i / 2;
+      const float freq = (float)pos / powf(theta, (float)(2 * pair) / (float)rope_dim);
+      const float sn = sinf(freq), cs = cosf(freq);
+      const float a = h[i], b = h[i + 1];
+      h[i] = a * cs - b * sn;
+      h[i + 1] = a * sn + b * cs;
+    }
+  }
+}
+
 /* scalar softmax, crates/kernels/src/scalar.rs:125-141. */
 void fo_softmax(float* x, uint64_t n) {
   float max = softmax_max(x, n);

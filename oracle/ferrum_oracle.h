@@ -22,6 +22,9 @@
  *                          invariants (|q|<=127, amax lane = +-127, error <= d/2)
  *   fo_q8_dequant          every code x 65,536 scales (kernels_contract.rs:700-744)
  *   fo_dot, fo_softmax     KATs tests.rs:178-195, kernels_contract.rs:437-467
+ *   fo_rope                KATs tests.rs:197-239 (pos 0 bit-identity, dims past rope_dim
+ *                          untouched, NORMAL pairing); the rotation against an f64
+ *                          evaluation of the same angle formula; pair norms kept
  *   fo_attention           numpy f64 brute force + closed forms (ctx=1, equal keys,
  *                          dominant key, non-finite max)
  *   fo_prefill_attention   equals fo_attention run once per query position (the
@@ -66,6 +69,8 @@ void fo_q8_dequant(const uint8_t* blocks, uint64_t n, float* out);
 
 float fo_dot(const float* a, const float* b, uint64_t n);
 void fo_softmax(float* x, uint64_t n);
+void fo_rope(float* data, uint64_t n_rows, uint32_t head_dim, uint32_t rope_dim, uint32_t pos,
+             float theta);
 
 /* Returns the number of skipped out-of-range slots. */
 uint64_t fo_append(const fo_layout* l, uint8_t* pool, uint32_t layer, const float* k,

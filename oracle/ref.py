@@ -36,6 +36,7 @@ _SIGS = {
     "fo_q8_dequant": (None, [c_void_p, u64, c_void_p]),
     "fo_dot": (ctypes.c_float, [c_void_p, c_void_p, u64]),
     "fo_softmax": (None, [c_void_p, u64]),
+    "fo_rope": (None, [c_void_p, u64, u32, u32, u32, ctypes.c_float]),
     "fo_append": (u64, [c_void_p, c_void_p, u32, c_void_p, c_void_p, c_void_p, u64]),
     "fo_gather_slots": (None, [c_void_p, c_void_p, u32, c_void_p, u64, i32, c_void_p, c_void_p]),
     "fo_gather_tables": (None, [c_void_p, c_void_p, u32, c_void_p, u32, c_void_p, c_void_p, u32,
@@ -173,6 +174,26 @@ def softmax(x) -> np.ndarray:
     a = np.array(x, dtype=np.float32, copy=True)
     lib().fo_softmax(_p(a), a.size)
     return a
+
+
+def rope(x, rope_dim: int, pos: int, theta: float) -> np.ndarray:
+    """A copy of x (f32 [..., head_dim]) with every row rotated at position pos."""
+    a = np.array(x, dtype=np.float32, copy=True, order="C")
+    d = a.shape[-1]
+    lib().fo_rope(_p(a), a.size // d if d else 0, d, rope_dim, pos, theta)
+    return a
+
+
+def rope_step(q, k, ctx_lens, rope_dim: int, theta: float):
+    """q [n_seqs][Hq][D] and k [n_seqs][Hkv][D] rotated per sequence at position
+    ctx_lens[s] - 1 (0 for an empty context), as the RoPE decode step does."""
+    q = np.array(q, dtype=np.float32, copy=True)
+    k = np.array(k, dtype=np.float32, copy=True)
+    for s, c in enumerate(np.asarray(ctx_lens)):
+        pos = int(c) - 1 if int(c) > 0 else 0
+        q[s] = rope(q[s], rope_dim, pos, theta)
+        k[s] = rope(k[s], rope_dim, pos, theta)
+    return q, k
 
 
 def avx2_available() -> bool:
