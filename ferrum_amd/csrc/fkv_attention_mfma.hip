@@ -97,10 +97,40 @@ struct Lane {
 // [2^14, 2^15), far from f16 overflow), then an f16 hi + lo split; hscale undoes
 // the scaling.
 //
-// ROPE: q is before RoPE. Lane p of the wave holds (sin, cos) of pair p (dims 2p,
-// 2p + 1) in rsin / rcos; the lane's eight dims are four whole pairs, rotated as
-// the reference does (a' = a cos - b sin, b' = a sin + b cos, each product rounded)
-// before the scaling.
+// ROPE: q is before RoPE. The lane's eight dims of chunk c are the four whole pairs
+// c*16 + grp*4 + e' (e' < 4), rotated as the reference does (a' = a cos - b sin,
+// b' = a sin + b cos, each product rounded) before the scaling. rsin / rcos hold
+// the (sin, cos) of pair rope_pair(lane): lane c*4 + e' of each 16-lane row has the
+// pair its row needs, broadcast to the row with DPP.
+// Lane L of each 16-lane row, broadcast to the row (DPP row_newbcast). L must
+// fold to a constant (an unrolled loop index): the switch then leaves one move.
+template <int L>
+__device__ __forceinline__ float row_bcast_c(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + L, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row_bcast(float v, int l) {
+  switch (l) {
+#define FKV_ROW_BCAST(L_) \
+  case L_:                \
+    return row_bcast_c<L_>(v);
+    FKV_ROW_BCAST(0) FKV_ROW_BCAST(1) FKV_ROW_BCAST(2) FKV_ROW_BCAST(3)
+    FKV_ROW_BCAST(4) FKV_ROW_BCAST(5) FKV_ROW_BCAST(6) FKV_ROW_BCAST(7)
+    FKV_ROW_BCAST(8) FKV_ROW_BCAST(9) FKV_ROW_BCAST(10) FKV_ROW_BCAST(11)
+    FKV_ROW_BCAST(12) FKV_ROW_BCAST(13) FKV_ROW_BCAST(14) FKV_ROW_BCAST(15)
+#undef FKV_ROW_BCAST
+    default: return v;
+  }
+}
+
+// The RoPE pair whose (sin, cos) a lane holds: c*16 + grp*4 + e' for lane
+// (col = c*4 + e', grp), so that every 16-lane row holds the 16 pairs prep_q needs
+// for its 8 dims of each 32-dim chunk.
+__device__ __forceinline__ int rope_pair(int lane) {
+  const int col = lane & 15, grp = lane >> 4;
+  return (col >> 2) * 16 + grp * 4 + (col & 3);
+}
+
 template <int D, bool ROPE = false>
 __device__ __forceinline__ void prep_q(const float* qrow, const Lane& ln, float qscale,
                                        f16x8 (&qh)[D / 32], f16x8 (&ql)[D / 32],
@@ -119,7 +149,7 @@ __device__ __forceinline__ void prep_q(const float* qrow, const Lane& ln, float 
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
         const int dim = c * 32 + ln.grp * 8 + e;
-        const float sn = __shfl(rsin, dim >> 1), cs = __shfl(rcos, dim >> 1);
+        const float sn = row_bcast(rsin, c * 4 + e / 2), cs = row_bcast(rcos, c * 4 + e / 2);
         if (dim < rope_dim) {
           const float u = v8[e], w = v8[e + 1];
           v8[e] = u * cs - w * sn;
@@ -895,15 +925,18 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   const int32_t s1 = ctx - s0 < split_tokens ? ctx : s0 + split_tokens;
   const int32_t nblk = s1 > s0 ? (s1 - s0 + B - 1) / B : 0;
 
-  // RoPE at the new token's position ctx - 1: lane p holds (sin, cos) of pair p,
-  // pos / den[p] as the reference computes it (f32 division, then sin and cos).
+  // RoPE at the new token's position ctx - 1: the lane holds (sin, cos) of pair
+  // rope_pair(lane), pos / den[p] as the reference computes it (f32 division, then
+  // sin and cos). Computed after the first K/V loads are issued, so the range
+  // reduction of large angles overlaps their latency.
   float rsin = 0.0f, rcos = 1.0f;
-  if constexpr (ROPE) {
-    if (2 * ln.lane < rope.rope_dim) {
-      const float freq = (float)(ctx > 0 ? ctx - 1 : 0) / rope.den[ln.lane];
+  auto rope_angles = [&]() {
+    const int pr = rope_pair(ln.lane);
+    if (2 * pr < rope.rope_dim) {
+      const float freq = (float)(ctx > 0 ? ctx - 1 : 0) / rope.den[pr];
       sincosf(freq, &rsin, &rcos);
     }
-  }
+  };
 
   // Fused append (k_new != nullptr): the token at position ctx - 1 of this KV
   // head is stored by the wave of the last split that reads its block. That wave
@@ -919,21 +952,29 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   const bool app_wave = app && app_lb % kAttnWaves == wave;
   const int32_t app_t = app_lb / kAttnWaves;             // the wave's block index
   const int32_t app_off = app_pos % B;                   // token within the block
-  if (app_wave) {  // encoded K and V rows of the token to s_app (the wave's own LDS use)
+  // Encoded K and V rows of the token to s_app (the appending wave's own LDS use).
+  // With RoPE the K row is rotated first; dims (dd & ~1, dd | 1) are a pair on
+  // adjacent lanes.
+  auto encode_app = [&]() {
     const float* ksrc = k_new + ((uint64_t)seq * g.n_kv_heads + kvh) * D;
     const float* vsrc = v_new + ((uint64_t)seq * g.n_kv_heads + kvh) * D;
 #pragma unroll
     for (int i = 0; i < D / 64; i++) {
       const int dd = i * 64 + ln.lane;
       float kv = ksrc[dd];
-      if constexpr (ROPE) {  // dims (dd & ~1, dd | 1) are a pair on adjacent lanes
+      if constexpr (ROPE) {
+        const int pr = dd >> 1;  // held by lane (pr%16/4)*16 + (pr/16)*4 + pr%4
+        const int src = ((pr & 15) >> 2) * 16 + (pr >> 4) * 4 + (pr & 3);
         const float other = __shfl_xor(kv, 1);
-        const float sn = __shfl(rsin, dd >> 1), cs = __shfl(rcos, dd >> 1);
+        const float sn = __shfl(rsin, src), cs = __shfl(rcos, src);
         if (dd < rope.rope_dim) kv = (dd & 1) ? other * sn + kv * cs : kv * cs - other * sn;
       }
       s_app[0][dd] = (uint16_t)encode_f16(kv, g.rounding);
       s_app[1][dd] = (uint16_t)encode_f16(vsrc[dd], g.rounding);
     }
+  };
+  if constexpr (!ROPE) {
+    if (app_wave) encode_app();
   }
 
   Accum<D> st;
@@ -1022,6 +1063,10 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
       ring[b].load_k_tile(tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh), ln);
       ring[b].load_v_tile(tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh), ln);
     }
+  }
+  if constexpr (ROPE) {
+    rope_angles();
+    if (app_wave) encode_app();
   }
   // q is read after the first K/V loads are issued, so its latency overlaps theirs.
   prep_q<D, ROPE>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D,
