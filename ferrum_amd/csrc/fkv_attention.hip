@@ -523,7 +523,7 @@ struct AttnPlan {
   bool stream_path = false; // attn_mfma_stream_kernel (F16) + stream combine
   uint32_t stream_waves = 0;
   uint64_t pre_off = 0;
-  bool mfma_path = false;   // attn_mfma_kernel (F16) + combine
+  bool mfma_path = false;   // attn_mfma_kernel (F16, Q8_0) + combine
   uint32_t split_tokens = kAttnPartTokens;
   uint32_t max_splits = 1;
   uint64_t o_off = 0, ml_off = 0, total = 0;
@@ -596,7 +596,7 @@ uint64_t attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_s
 uint64_t append_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
                                           uint32_t max_ctx_len) {
   const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
-  if (p.mfma_path && g.dtype == kDtypeF16) return p.total;  // appended inside the kernel
+  if (p.mfma_path) return p.total;  // appended inside the kernel
   return p.total + align256((uint64_t)n_seqs * sizeof(int64_t));
 }
 
@@ -604,7 +604,7 @@ uint64_t rope_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_
                                         uint32_t max_ctx_len) {
   const uint64_t base = append_attention_workspace_bytes(g, n_heads, n_seqs, max_ctx_len);
   const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
-  if (p.mfma_path && g.dtype == kDtypeF16) return base;  // rotated inside the kernel
+  if (p.mfma_path) return base;  // rotated inside the kernel
   return base +
          align256((uint64_t)n_seqs * (n_heads + g.n_kv_heads) * g.head_dim * sizeof(float));
 }
@@ -686,7 +686,7 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
   const uint32_t G = n_heads / g.n_kv_heads;
   const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
   uint8_t* ws = (uint8_t*)workspace;
-  if (rope != nullptr && rope->rope_dim > 0 && !(p.mfma_path && g.dtype == kDtypeF16)) {
+  if (rope != nullptr && rope->rope_dim > 0 && !p.mfma_path) {
     // Rotate q and the new K rows into the workspace, then run the unrotated step.
     float* q_rot = (float*)(ws + append_attention_workspace_bytes(g, n_heads, n_seqs, max_ctx_len));
     float* k_rot = q_rot + (uint64_t)n_seqs * n_heads * g.head_dim;
@@ -700,7 +700,7 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
     k_new = k_rot;
     rope = nullptr;
   }
-  if (k_new != nullptr && !(p.mfma_path && g.dtype == kDtypeF16)) {
+  if (k_new != nullptr && !p.mfma_path) {
     // Separate append launch: slots derived from the block tables first.
     int64_t* slots = (int64_t*)(ws + p.total);
     hipError_t e = launch_tail_slots(g, tables, max_blocks, ctx_lens, n_seqs, slots, s);

@@ -870,7 +870,9 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   __shared__ float s_o[kAttnWaves][kHeads * D];
   __shared__ float s_m[kAttnWaves][kHeads];
   __shared__ float s_l[kAttnWaves][kHeads];
-  __shared__ __align__(16) uint16_t s_app[2][D];  // fused append: encoded K, V rows
+  __shared__ __align__(16) uint16_t s_app[2][D];  // fused append: K, V operand values
+  __shared__ uint8_t s_appq[2][D];                 // fused Q8_0 append: quants
+  __shared__ uint16_t s_apps[2][D / 32];           // and scales
   __shared__ int32_t s_ord[2 * kAttnWaves + 4 + kOrderSortSeqs];  // work order: scans, item, keys
 
   const int32_t cap = (int32_t)(max_blocks * B);
@@ -940,13 +942,16 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
 
   // Fused append (k_new != nullptr): the token at position ctx - 1 of this KV
   // head is stored by the wave of the last split that reads its block. That wave
-  // encodes the token (f32 -> binary16 with the pool's rounding) up front and,
-  // when it reaches the block, puts the encoded values into its K and V operands
-  // in place of what it loaded and stores them to the pool. No other workgroup
+  // encodes the token up front (F16: f32 -> binary16 with the pool's rounding;
+  // Q8_0: each 32-dim group quantised as append_q8_kernel does) and, when it
+  // reaches the block, puts the operand values of the token (F16: the binary16
+  // values; Q8_0: scale x quant rounded once to binary16, what the block's operand
+  // conversion gives for the stored bytes) into its K and V operands in place of
+  // what it loaded, and stores the encoded token to the pool. No other workgroup
   // reads the position, and this one never reads back what it stores, so the
   // stores need no ordering.
-  const bool app =
-      DT == kDtypeF16 && k_new != nullptr && split == nsplits - 1 && ctx > 0 && ctx_ok;
+  const bool app = (DT == kDtypeF16 || DT == kDtypeQ8) && k_new != nullptr &&
+                   split == nsplits - 1 && ctx > 0 && ctx_ok;
   const int32_t app_pos = ctx - 1;
   const int32_t app_lb = app ? app_pos / B - blk0 : -1;  // block of the split
   const bool app_wave = app && app_lb % kAttnWaves == wave;
@@ -969,8 +974,35 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
         const float sn = __shfl(rsin, src), cs = __shfl(rcos, src);
         if (dd < rope.rope_dim) kv = (dd & 1) ? other * sn + kv * cs : kv * cs - other * sn;
       }
-      s_app[0][dd] = (uint16_t)encode_f16(kv, g.rounding);
-      s_app[1][dd] = (uint16_t)encode_f16(vsrc[dd], g.rounding);
+      const float vv = vsrc[dd];
+      if constexpr (DT == kDtypeQ8) {
+        // Group dd / 32 is this half of the wave: amax over its 32 lanes.
+        float ka = __builtin_fabsf(kv), va = __builtin_fabsf(vv);
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) {
+          ka = __builtin_fmaxf(ka, __shfl_xor(ka, o));
+          va = __builtin_fmaxf(va, __shfl_xor(va, o));
+        }
+        float kid, vid;
+        const uint32_t ksc = encode_f16(q8_scale(ka, kid), g.rounding);
+        const uint32_t vsc = encode_f16(q8_scale(va, vid), g.rounding);
+        const int kq = q8_quant(kv, kid), vq = q8_quant(vv, vid);
+        s_appq[0][dd] = (uint8_t)kq;
+        s_appq[1][dd] = (uint8_t)vq;
+        s_app[0][dd] = __builtin_bit_cast(uint16_t, (_Float16)(f16_bits_to_f32(ksc) * (float)kq));
+        s_app[1][dd] = __builtin_bit_cast(uint16_t, (_Float16)(f16_bits_to_f32(vsc) * (float)vq));
+        if ((ln.lane & 31) == 0) {
+          s_apps[0][dd / 32] = (uint16_t)ksc;
+          s_apps[1][dd / 32] = (uint16_t)vsc;
+          // A finite scale >= 512 can dequantise past 65504 (append_q8_kernel's rule).
+          if (((ksc & 0x7fffu) >= 0x6000u && (ksc & 0x7fffu) < 0x7c00u) ||
+              ((vsc & 0x7fffu) >= 0x6000u && (vsc & 0x7fffu) < 0x7c00u))
+            raise_fault(g.fault, kFaultRange);
+        }
+      } else {
+        s_app[0][dd] = (uint16_t)encode_f16(kv, g.rounding);
+        s_app[1][dd] = (uint16_t)encode_f16(vv, g.rounding);
+      }
     }
   };
   if constexpr (!ROPE) {
@@ -1005,7 +1037,23 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     const bool live = blive[b];
     const bool refill = t + NBUF < nt;
     const int32_t t0 = s0 + (wave + kAttnWaves * t) * B;  // first token of the block
-    const bool patch = app_wave && t == app_t && live;  // (F16 storage only)
+    const bool patch = app_wave && t == app_t && live;
+    if constexpr (DT == kDtypeQ8) {
+      if (patch) {  // the token's quants and scales to the pool (the whole wave)
+        uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
+        uint8_t* vt = tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
+#pragma unroll
+        for (int i = 0; i < D / 64; i++) {
+          const int dd = i * 64 + ln.lane;
+          kt[q8_quant_offset(0, app_off, dd, D)] = s_appq[0][dd];
+          vt[q8_quant_offset(1, app_off, dd, D)] = s_appq[1][dd];
+        }
+        if (ln.lane < D / 32) {
+          ((uint16_t*)(kt + B * D))[app_off * (D / 32) + ln.lane] = s_apps[0][ln.lane];
+          ((uint16_t*)(vt + B * D))[app_off * (D / 32) + ln.lane] = s_apps[1][ln.lane];
+        }
+      }
+    }
     // F16 operands are the ring registers themselves; Q8_0 ones are dequantised.
     uint4 kdq[DT == kDtypeF16 ? 1 : NC];
     uint4(&kr)[NC] = *[&]() -> uint4(*)[NC] {
@@ -1016,12 +1064,14 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
         return &kdq;
       }
     }();
-    if (patch && ln.col == app_off) {  // K tile [D/8][B][8]: run c*4 + grp of the token
-      uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
+    if (patch && ln.col == app_off) {  // K operand: run c*4 + grp of the token
 #pragma unroll
       for (int c = 0; c < NC; c++) {
         kr[c] = *(const uint4*)&s_app[0][c * 32 + ln.grp * 8];
-        *(uint4*)(kt + ((uint64_t)(c * 4 + ln.grp) * B + app_off) * 16) = kr[c];
+        if constexpr (DT == kDtypeF16) {  // F16 K tile [D/8][B][8]
+          uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
+          *(uint4*)(kt + ((uint64_t)(c * 4 + ln.grp) * B + app_off) * 16) = kr[c];
+        }
       }
     }
     float s[4];
@@ -1040,8 +1090,7 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
         return &vdq;
       }
     }();
-    if (patch && ln.grp == app_off / 4) {  // V tile [D][B]: dim 16m + col, token app_off
-      uint16_t* vt = (uint16_t*)tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
+    if (patch && ln.grp == app_off / 4) {  // V operand: dim 16m + col, token app_off
       const int sh = (app_off & 1) * 16;
       const uint32_t keep = ~(0xffffu << sh);
 #pragma unroll
@@ -1049,7 +1098,10 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
         const uint32_t h = s_app[1][m * 16 + ln.col];
         if (app_off & 2) vr[m].y = (vr[m].y & keep) | (h << sh);
         else vr[m].x = (vr[m].x & keep) | (h << sh);
-        vt[(uint64_t)(m * 16 + ln.col) * B + app_off] = (uint16_t)h;
+        if constexpr (DT == kDtypeF16) {  // F16 V tile [D][B]
+          uint16_t* vt = (uint16_t*)tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
+          vt[(uint64_t)(m * 16 + ln.col) * B + app_off] = (uint16_t)h;
+        }
       }
     }
     if (live) pv_block<D>(vr, pw, ln, t0, s1, st);
@@ -1404,10 +1456,8 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
     if (v == 0 || (v == 1 && n_seqs <= kOrderMaxSeqs) || (v == 2 && n_seqs <= kOrderSortSeqs))
       order = (uint32_t)v;
   }
-  // RoPE in the kernel: F16 storage only (other storage rotates q and k_new into
-  // the workspace before the launch).
+  // RoPE in the kernel for F16 and Q8_0 storage.
   const bool roped = rope != nullptr && rope->rope_dim > 0;
-  if (roped && g.dtype != kDtypeF16) return hipErrorInvalidValue;
   RopeTable rt{};
   if (roped) rt = *rope;
 #define FKV_LAUNCH_MFMA(DT_, D_, R_)                                                             \
@@ -1415,7 +1465,10 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
                                                            max_blocks, ctx_lens, n_seqs,         \
                                                            max_splits, st, order, scale, ws_o,   \
                                                            ws_ml, k_new, v_new, rt)
-  if (g.dtype == kDtypeQ8) {
+  if (g.dtype == kDtypeQ8 && roped) {
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, true);
+    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, true);
+  } else if (g.dtype == kDtypeQ8) {
     if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, false);
     else FKV_LAUNCH_MFMA(kDtypeQ8, 64, false);
   } else if (roped) {

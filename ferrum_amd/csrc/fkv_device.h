@@ -129,5 +129,29 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 
+// ---------------------------------------------------------------------------
+// Q8_0 quantiser steps (crates/kernels/src/q8_dot.rs:46-59)
+// ---------------------------------------------------------------------------
+
+// Rust's f32::round: half away from zero.
+__device__ __forceinline__ float round_half_away(float y) {
+  float t = __builtin_truncf(y);
+  return (__builtin_fabsf(y - t) >= 0.5f) ? t + __builtin_copysignf(1.0f, y) : t;
+}
+
+// d = amax / 127 and id = 1 / d (0 when d is 0), both in f32.
+__device__ __forceinline__ float q8_scale(float amax, float& id) {
+  const float d = amax / 127.0f;
+  id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  return d;
+}
+
+// round(x * id) as Rust's `as i32` takes it (saturating, NaN -> 0), clamped to
+// [-128, 127].
+__device__ __forceinline__ int q8_quant(float x, float id) {
+  const float r = round_half_away(x * id);
+  return (r != r) ? 0 : (r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int)r));
+}
+
 }  // namespace dev
 }  // namespace fkv

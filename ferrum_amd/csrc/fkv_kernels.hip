@@ -24,29 +24,19 @@ using namespace dev;
 // Q8_0 block quantiser (q8_dot.rs:46-59)
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float round_half_away(float y) {
-  float t = __builtin_truncf(y);
-  return (__builtin_fabsf(y - t) >= 0.5f) ? t + __builtin_copysignf(1.0f, y) : t;
-}
-
 // x[32] -> 32 int8 packed in q[8] (little-endian bytes) and the f16 scale bits.
 __device__ __forceinline__ uint32_t q8_quantize(const float (&x)[32], int rounding,
                                                 uint32_t (&q)[8]) {
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 32; j++) amax = __builtin_fmaxf(amax, __builtin_fabsf(x[j]));
-  float d = amax / 127.0f;
-  float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  float id;
+  const float d = q8_scale(amax, id);
 #pragma unroll
   for (int w = 0; w < 8; w++) {
     uint32_t packed = 0;
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-      float r = round_half_away(x[w * 4 + b] * id);
-      // Rust `as i32` saturates and maps NaN to 0; then clamp to [-128, 127].
-      int qi = (r != r) ? 0 : (r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int)r));
-      packed |= ((uint32_t)qi & 0xffu) << (8 * b);
-    }
+    for (int b = 0; b < 4; b++) packed |= ((uint32_t)q8_quant(x[w * 4 + b], id) & 0xffu) << (8 * b);
     q[w] = packed;
   }
   return encode_f16(d, rounding);

@@ -272,9 +272,11 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
  * ctx_lens[s] - 1 through block_tables (encoded like fkv_append), then decode
  * attention runs over ctx_lens[s] positions exactly as fkv_decode_attention.
  * The block holding that position must belong to sequence s alone (copy it with
- * fkv_copy_blocks first if it is shared). For F16 storage this is one kernel
- * launch: the workgroup that reads the sequence's last context split stores the
- * token before loading it. Other storage types use an append launch first.
+ * fkv_copy_blocks first if it is shared). For F16 and Q8_0 storage this is one
+ * kernel launch: the workgroup that reads the sequence's last context split
+ * encodes the token (Q8_0: quantised as fkv_append does, FKV_FAULT_VALUE_RANGE
+ * included), stores it and uses its encoded values in place of what it loaded.
+ * F32 storage uses an append launch first.
  * workspace: fkv_append_decode_attention_workspace_size() bytes, same rules as
  * the decode-attention workspace. */
 int32_t fkv_append_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
@@ -298,8 +300,8 @@ int32_t fkv_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_h
  * q is read only (the rotation is not written back). Checks, in the reference's
  * order (validate.rs:64-87), before any other: FKV_ERR_KERNEL "kernel: theta must
  * be positive" (theta <= 0 or NaN), "kernel: rope_dim must be even", "kernel:
- * rope_dim exceeds head_dim". F16 storage rotates inside the one kernel launch;
- * Q8_0 and F32 storage rotate q and k_new into the workspace first. sin and cos
+ * rope_dim exceeds head_dim". F16 and Q8_0 storage rotate inside the one kernel
+ * launch; F32 storage rotates q and k_new into the workspace first. sin and cos
  * come from the device's sincosf, so stored K can differ from a CPU rotation by
  * one f16 rounding step where a value sits on a rounding boundary.
  * workspace: fkv_rope_append_decode_attention_workspace_size() bytes. */
