@@ -1175,6 +1175,94 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   }
 }
 
+// Prefill versions of qk_block and softmax_block. The prefill kernel is bound by
+// the VALU work around its MFMAs, so the work that is rare per block sits behind
+// wave-uniform branches: the lo-chain NaN repair (only when a score is NaN), the
+// causal mask (only on a block that crosses some column's causal end) and the
+// empty-column rule (only while a real column has seen no finite score). The
+// accumulator rescale stays unconditional (x 1.0 when no column's max moved): in
+// the branch it costs 32 VGPRs, 4 -> 3 waves per SIMD, and 180 -> 222 us on a C3
+// layer. Padding columns (ln.real false) are not masked: their q is zero, their
+// accumulator rows are their own (an MFMA output row depends on its A row only)
+// and never written.
+template <int D>
+__device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
+                                            const f16x8 (&ql)[D / 32], float hscale,
+                                            const Lane& ln, bool live, bool full, int32_t t0,
+                                            int32_t end, float (&s)[4]) {
+  f32x4 ah = {0.0f, 0.0f, 0.0f, 0.0f}, al = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < D / 32; c++) {
+    const f16x8 kv = __builtin_bit_cast(f16x8, kr[c]);
+    ah = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qh[c], ah, 0, 0, 0);
+    al = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], al, 0, 0, 0);
+  }
+  float x[4];
+  bool nan = false;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    x[r] = ah[r] + al[r];
+    nan = nan || x[r] != x[r];
+  }
+  if (__builtin_amdgcn_ballot_w64(nan) != 0) {  // see qk_block: the inf * 0 case
+#pragma unroll
+    for (int r = 0; r < 4; r++) x[r] = (al[r] != al[r] && ah[r] == ah[r]) ? ah[r] : x[r];
+  }
+  if (live && full) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) s[r] = x[r] * hscale;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const bool ok = ln.real && live && t0 + ln.grp * 4 + r < end;
+      s[r] = ok ? x[r] * hscale : -__builtin_inff();
+    }
+  }
+}
+
+template <int D>
+__device__ __forceinline__ f16x4 softmax_block_pf(const float (&s)[4], const Lane& ln,
+                                                  Accum<D>& st) {
+  const float lmax = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), __builtin_fmaxf(s[2], s[3]));
+  const bool bad =
+      ln.real && (!(lmax <= st.m_ref + kRescaleLog2) || !__builtin_isfinite(st.m_ref));
+  float ar[4] = {1.0f, 1.0f, 1.0f, 1.0f};
+  if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+    float x = lmax;
+    x = __builtin_fmaxf(x, __shfl_xor(x, 16));
+    x = __builtin_fmaxf(x, __shfl_xor(x, 32));
+    const float mn = __builtin_fmaxf(st.m_ref, x);
+    const float alpha = (mn == -__builtin_inff()) ? 1.0f : __builtin_amdgcn_exp2f(st.m_ref - mn);
+    st.l_part *= alpha;
+    st.m_ref = mn;
+#pragma unroll
+    for (int r = 0; r < 4; r++) ar[r] = __shfl(alpha, ln.grp * 4 + r);
+  }
+#pragma unroll
+  for (int m = 0; m < D / 16; m++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) st.acc[m][r] *= ar[r];
+  f16x4 pw;
+  if (__builtin_amdgcn_ballot_w64(ln.real && st.m_ref == -__builtin_inff()) == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float e = __builtin_amdgcn_exp2f(s[r] - st.m_ref);
+      st.l_part += e;
+      pw[r] = (_Float16)e;
+    }
+  } else {
+    const bool dead = (st.m_ref == -__builtin_inff());
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float sv = s[r];
+      const float e = dead ? (sv != sv ? sv : 0.0f) : __builtin_amdgcn_exp2f(sv - st.m_ref);
+      st.l_part += e;
+      pw[r] = (_Float16)e;
+    }
+  }
+  return pw;
+}
+
 // ---------------------------------------------------------------------------
 // Chunked-prefill attention
 // ---------------------------------------------------------------------------
@@ -1233,6 +1321,8 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   const int32_t end_col = p0 + jcol + 1;                // causal end of the column
   const int32_t jlast = tile * T + T - 1 < ql - 1 ? tile * T + T - 1 : ql - 1;
   const int32_t end_max = wave_on ? p0 + jlast + 1 : 0;  // furthest end of the wave's tile
+  const int32_t end_min = p0 + tile * T + 1;             // nearest end: blocks before it
+                                                         // need no causal mask
   const int32_t nblk_w = (end_max + B - 1) / B;
   // the workgroup's furthest end: its last tile's last query (or the chunk's last)
   const int32_t wg_last = (tile0 + kAttnWaves) * T - 1 < ql - 1 ? (tile0 + kAttnWaves) * T - 1 : ql - 1;
@@ -1322,13 +1412,13 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
             kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
           const int32_t t0 = j * B;
           float sc[4];
-          qk_block<D>(kr, qh, qlo, hscale, ln, live, t0, end_col, sc);
+          qk_block_pf<D>(kr, qh, qlo, hscale, ln, live, t0 + B <= end_min, t0, end_col, sc);
 #pragma unroll
           for (int m = 0; m < NM; m++) {
             const uint32_t dim = (uint32_t)(m * 16 + ln.col);
             vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((uint32_t)ln.grp ^ ((dim >> 2) & 3u)) * 8u));
           }
-          const f16x4 pw = softmax_block<D>(sc, ln, st);
+          const f16x4 pw = softmax_block_pf<D>(sc, ln, st);
           if (live) pv_block<D>(vr, pw, ln, t0, end_max, st);
         }
         if (j + 1 < nblk) {
