@@ -10,14 +10,14 @@ from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8_0, FAULT_BLOCK_RANGE, FAULT_CT
 from .errors import (CacheError, FerrumError, InternalError, InvalidRequest, KernelError,
                      Unavailable)
 from .kvcache import (KvPoolConfig, PagedConfig, PagedKvPool, PreallocatedKvPool,
-                      default_scale, device_copy)
+                      SequenceManager, default_scale, device_copy)
 
 __all__ = [
     "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "FAULT_BLOCK_RANGE", "FAULT_CTX_RANGE",
     "FAULT_SLOT_RANGE", "FAULT_VALUE_RANGE", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
     "ROUND_NEAREST_EVEN", "CacheError", "FerrumError", "InternalError", "InvalidRequest",
     "KernelError", "Unavailable", "KvPoolConfig", "PagedConfig", "PagedKvPool",
-    "PreallocatedKvPool", "default_scale", "device_copy", "load_library",
+    "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "load_library",
 ]
 
 

@@ -107,6 +107,19 @@ SIGNATURES = {
     "fkv_prefill_attention": (i32, [c_void_p, u32, u32, c_void_p, c_void_p, c_void_p, u32,
                                     c_void_p, c_void_p, c_void_p, u32, u32, u32, f32, c_void_p]),
     "fkv_device_copy": (i32, [c_void_p, c_void_p, u64, c_void_p]),
+    "fkv_seqs_create": (i32, [c_void_p, P(c_void_p)]),
+    "fkv_seqs_destroy": (i32, [c_void_p]),
+    "fkv_seqs_add": (i32, [c_void_p, u64, P(u32)]),
+    "fkv_seqs_reserve": (i32, [c_void_p, u32, u64, c_void_p]),
+    "fkv_seqs_slots": (i32, [c_void_p, u32, u64, u64, c_void_p]),
+    "fkv_seqs_commit": (i32, [c_void_p, u32, u64]),
+    "fkv_seqs_truncate": (i32, [c_void_p, u32, u64]),
+    "fkv_seqs_fork": (i32, [c_void_p, u32, P(u32)]),
+    "fkv_seqs_free": (i32, [c_void_p, u32]),
+    "fkv_seqs_len": (i32, [c_void_p, u32, P(u64), P(i32)]),
+    "fkv_seqs_swap_out": (i32, [c_void_p, u32, c_void_p]),
+    "fkv_seqs_swap_in": (i32, [c_void_p, u32, c_void_p]),
+    "fkv_seqs_tables": (i32, [c_void_p, c_void_p, u32, u32, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

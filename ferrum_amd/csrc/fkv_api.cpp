@@ -69,7 +69,10 @@ struct fkv_pool {
   uint32_t* fault = nullptr;
   std::vector<int32_t> free_list;  // stack; LIFO reuse, as a fragmented pool would see
   std::vector<uint32_t> refcount;
+  std::vector<fkv_seqs*> managers;  // detached when the pool is destroyed
 };
+
+static void detach_manager(fkv_seqs* m);
 
 struct fkv_kvpool {
   fkv_kvpool_config cfg{};
@@ -162,6 +165,7 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
 
 int32_t fkv_paged_destroy(fkv_pool* pool) {
   if (!pool) return ok();
+  for (fkv_seqs* m : pool->managers) detach_manager(m);
   DeviceGuard dg(pool->cfg.device);
   (void)hipDeviceSynchronize();
   if (pool->dev) (void)hipFree(pool->dev);
@@ -776,6 +780,308 @@ int32_t fkv_kvpool_uncommit_token(fkv_kvpool* pool, uint32_t slot) {
   if (pool->seq_len[slot] == 0) return fail(FKV_ERR_CACHE, "nothing to uncommit");
   pool->seq_len[slot] -= 1;
   pool->layers_appended[slot] = 0;
+  return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Sequence block manager: the scheduler's KV bookkeeping on paged
+// storage. crates/scheduler/src/batcher.rs admits while a dense slot is free
+// (:108-129), rolls back by freeing the slot and re-running the prefix
+// (restore_kv, :291-308) and frees the slot on finish (:329-338). Here a sequence
+// is a list of blocks: admission asks for the blocks its tokens need, a fork
+// shares blocks by reference and copies a shared block before its first write,
+// a rollback truncates the list, and preemption moves the blocks to the pool's
+// host storage and back.
+// ---------------------------------------------------------------------------
+
+}  // extern "C"
+
+struct fkv_seqs {
+  struct Seq {
+    bool used = false;
+    bool swapped = false;
+    uint64_t len = 0;             // committed tokens
+    std::vector<int32_t> blocks;  // device blocks; host blocks while swapped out
+  };
+  fkv_pool* pool = nullptr;
+  std::vector<Seq> seqs;
+  std::vector<uint32_t> free_ids;  // sequence ids to reuse
+  std::vector<int32_t> host_free;  // the pool's free host blocks (LIFO)
+};
+
+// The pool is being destroyed: the manager keeps only its own memory.
+static void detach_manager(fkv_seqs* m) { m->pool = nullptr; }
+
+namespace {
+
+fkv_seqs::Seq* seq_at(fkv_seqs* m, uint32_t id) {
+  return m->pool && id < m->seqs.size() && m->seqs[id].used ? &m->seqs[id] : nullptr;
+}
+const fkv_seqs::Seq* seq_at(const fkv_seqs* m, uint32_t id) {
+  return m->pool && id < m->seqs.size() && m->seqs[id].used ? &m->seqs[id] : nullptr;
+}
+uint64_t blocks_for(const fkv_pool* p, uint64_t tokens) {
+  return (tokens + p->cfg.block_size - 1) / p->cfg.block_size;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t fkv_seqs_create(fkv_pool* pool, fkv_seqs** out) {
+  if (!pool || !out) return fail(FKV_ERR_INVALID, "null argument");
+  auto* m = new fkv_seqs();
+  m->pool = pool;
+  pool->managers.push_back(m);
+  for (uint64_t i = pool->cfg.num_host_blocks; i > 0; i--) m->host_free.push_back((int32_t)(i - 1));
+  *out = m;
+  return ok();
+}
+
+int32_t fkv_seqs_destroy(fkv_seqs* m) {
+  if (!m) return ok();
+  if (m->pool) {  // a destroyed pool has detached its managers: nothing to release
+    for (auto& s : m->seqs)
+      if (s.used && !s.swapped && !s.blocks.empty())
+        (void)fkv_block_free(m->pool, (uint32_t)s.blocks.size(), s.blocks.data());
+    auto& ms = m->pool->managers;
+    ms.erase(std::remove(ms.begin(), ms.end(), m), ms.end());
+  }
+  delete m;
+  return ok();
+}
+
+int32_t fkv_seqs_add(fkv_seqs* m, uint64_t n_tokens, uint32_t* seq_out) {
+  if (!m || !seq_out) return fail(FKV_ERR_INVALID, "null argument");
+  if (!m->pool) return fail(FKV_ERR_INVALID, "pool destroyed");
+  const uint64_t nb = blocks_for(m->pool, n_tokens);
+  if (nb > m->pool->free_list.size()) return fail(FKV_ERR_UNAVAILABLE, "no free kv blocks");
+  std::vector<int32_t> ids(nb);
+  if (nb) {
+    int32_t st = fkv_block_alloc(m->pool, (uint32_t)nb, ids.data());
+    if (st) return st;
+  }
+  uint32_t id;
+  if (!m->free_ids.empty()) {
+    id = m->free_ids.back();
+    m->free_ids.pop_back();
+  } else {
+    id = (uint32_t)m->seqs.size();
+    m->seqs.emplace_back();
+  }
+  fkv_seqs::Seq& s = m->seqs[id];
+  s = fkv_seqs::Seq();
+  s.used = true;
+  s.blocks = std::move(ids);
+  *seq_out = id;
+  return ok();
+}
+
+int32_t fkv_seqs_reserve(fkv_seqs* m, uint32_t seq, uint64_t n, int64_t* copy_pair) {
+  if (!m || !copy_pair) return fail(FKV_ERR_INVALID, "null argument");
+  fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (s->swapped) return fail(FKV_ERR_CACHE, "sequence is swapped out");
+  copy_pair[0] = copy_pair[1] = -1;
+  fkv_pool* p = m->pool;
+  const uint64_t B = p->cfg.block_size, have = s->blocks.size();
+  const uint64_t need = blocks_for(p, s->len + n);
+  // Only the block holding position len can be shared and partly written (a fork
+  // shares the blocks of the committed tokens): it is copied before the write.
+  const uint64_t first = s->len / B;
+  const bool cow = n > 0 && s->len % B != 0 && first < have &&
+                   p->refcount[(size_t)s->blocks[first]] > 1;
+  const uint64_t extra = (need > have ? need - have : 0) + (cow ? 1 : 0);
+  if (extra > p->free_list.size()) return fail(FKV_ERR_UNAVAILABLE, "no free kv blocks");
+  std::vector<int32_t> ids(extra);
+  if (extra) {
+    int32_t st = fkv_block_alloc(p, (uint32_t)extra, ids.data());
+    if (st) return st;
+  }
+  size_t k = 0;
+  if (cow) {
+    const int32_t src = s->blocks[first];
+    s->blocks[first] = ids[k++];
+    copy_pair[0] = src;
+    copy_pair[1] = s->blocks[first];
+    int32_t st = fkv_block_free(p, 1, &src);  // this sequence's reference to the shared block
+    if (st) return st;
+  }
+  for (; k < ids.size(); k++) s->blocks.push_back(ids[k]);
+  return ok();
+}
+
+int32_t fkv_seqs_commit(fkv_seqs* m, uint32_t seq, uint64_t n) {
+  if (!m) return fail(FKV_ERR_INVALID, "null argument");
+  fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (s->swapped) return fail(FKV_ERR_CACHE, "sequence is swapped out");
+  if (s->len + n > (uint64_t)s->blocks.size() * m->pool->cfg.block_size)
+    return fail(FKV_ERR_CACHE, "commit past the reserved blocks");
+  s->len += n;
+  return ok();
+}
+
+int32_t fkv_seqs_slots(const fkv_seqs* m, uint32_t seq, uint64_t pos, uint64_t n,
+                       int64_t* slots_out) {
+  if (!m || (n && !slots_out)) return fail(FKV_ERR_INVALID, "null argument");
+  const fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (s->swapped) return fail(FKV_ERR_CACHE, "sequence is swapped out");
+  const uint64_t B = m->pool->cfg.block_size;
+  if (pos + n > (uint64_t)s->blocks.size() * B)
+    return fail(FKV_ERR_CACHE, "position beyond the reserved blocks");
+  for (uint64_t i = 0; i < n; i++) {
+    const uint64_t q = pos + i;
+    slots_out[i] = (int64_t)s->blocks[q / B] * (int64_t)B + (int64_t)(q % B);
+  }
+  return ok();
+}
+
+int32_t fkv_seqs_truncate(fkv_seqs* m, uint32_t seq, uint64_t n_tokens) {
+  if (!m) return fail(FKV_ERR_INVALID, "null argument");
+  fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (s->swapped) return fail(FKV_ERR_CACHE, "sequence is swapped out");
+  if (n_tokens > s->len) return fail(FKV_ERR_CACHE, "truncate past the sequence length");
+  const uint64_t keep = blocks_for(m->pool, n_tokens);
+  if (keep < s->blocks.size()) {
+    int32_t st = fkv_block_free(m->pool, (uint32_t)(s->blocks.size() - keep), s->blocks.data() + keep);
+    if (st) return st;
+    s->blocks.resize(keep);
+  }
+  s->len = n_tokens;
+  return ok();
+}
+
+int32_t fkv_seqs_fork(fkv_seqs* m, uint32_t parent, uint32_t* child_out) {
+  if (!m || !child_out) return fail(FKV_ERR_INVALID, "null argument");
+  fkv_seqs::Seq* s = seq_at(m, parent);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (s->swapped) return fail(FKV_ERR_CACHE, "sequence is swapped out");
+  const uint64_t nb = blocks_for(m->pool, s->len);
+  std::vector<int32_t> shared(s->blocks.begin(), s->blocks.begin() + (ptrdiff_t)nb);
+  if (nb) {
+    int32_t st = fkv_block_ref(m->pool, (uint32_t)nb, shared.data());
+    if (st) return st;
+  }
+  const uint64_t len = s->len;  // s may move when seqs grows
+  uint32_t id;
+  if (!m->free_ids.empty()) {
+    id = m->free_ids.back();
+    m->free_ids.pop_back();
+  } else {
+    id = (uint32_t)m->seqs.size();
+    m->seqs.emplace_back();
+  }
+  fkv_seqs::Seq& c = m->seqs[id];
+  c = fkv_seqs::Seq();
+  c.used = true;
+  c.len = len;
+  c.blocks = std::move(shared);
+  *child_out = id;
+  return ok();
+}
+
+int32_t fkv_seqs_free(fkv_seqs* m, uint32_t seq) {
+  if (!m) return fail(FKV_ERR_INVALID, "null argument");
+  fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (s->swapped) {
+    for (int32_t h : s->blocks) m->host_free.push_back(h);
+  } else if (!s->blocks.empty()) {
+    int32_t st = fkv_block_free(m->pool, (uint32_t)s->blocks.size(), s->blocks.data());
+    if (st) return st;
+  }
+  *s = fkv_seqs::Seq();
+  m->free_ids.push_back(seq);
+  return ok();
+}
+
+int32_t fkv_seqs_len(const fkv_seqs* m, uint32_t seq, uint64_t* len_out, int32_t* swapped_out) {
+  if (!m || !len_out) return fail(FKV_ERR_INVALID, "null argument");
+  const fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  *len_out = s->len;
+  if (swapped_out) *swapped_out = s->swapped ? 1 : 0;
+  return ok();
+}
+
+int32_t fkv_seqs_swap_out(fkv_seqs* m, uint32_t seq, void* stream) {
+  if (!m) return fail(FKV_ERR_INVALID, "null argument");
+  fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (s->swapped) return fail(FKV_ERR_CACHE, "sequence is swapped out");
+  const uint64_t nb = blocks_for(m->pool, s->len);
+  if (nb > m->host_free.size()) return fail(FKV_ERR_UNAVAILABLE, "no free host blocks");
+  std::vector<int64_t> pairs(2 * nb);
+  std::vector<int32_t> host(nb);
+  for (uint64_t i = 0; i < nb; i++) {
+    host[i] = m->host_free[m->host_free.size() - 1 - i];
+    pairs[2 * i] = s->blocks[i];
+    pairs[2 * i + 1] = host[i];
+  }
+  if (nb) {
+    int32_t st = fkv_swap_out(m->pool, pairs.data(), (uint32_t)nb, stream);
+    if (st) return st;
+  }
+  m->host_free.resize(m->host_free.size() - nb);
+  if (!s->blocks.empty()) {
+    int32_t st = fkv_block_free(m->pool, (uint32_t)s->blocks.size(), s->blocks.data());
+    if (st) return st;
+  }
+  s->blocks = std::move(host);
+  s->swapped = true;
+  return ok();
+}
+
+int32_t fkv_seqs_swap_in(fkv_seqs* m, uint32_t seq, void* stream) {
+  if (!m) return fail(FKV_ERR_INVALID, "null argument");
+  fkv_seqs::Seq* s = seq_at(m, seq);
+  if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+  if (!s->swapped) return fail(FKV_ERR_CACHE, "sequence is not swapped out");
+  const uint64_t nb = s->blocks.size();
+  if (nb > m->pool->free_list.size()) return fail(FKV_ERR_UNAVAILABLE, "no free kv blocks");
+  std::vector<int32_t> dev(nb);
+  if (nb) {
+    int32_t st = fkv_block_alloc(m->pool, (uint32_t)nb, dev.data());
+    if (st) return st;
+  }
+  std::vector<int64_t> pairs(2 * nb);
+  for (uint64_t i = 0; i < nb; i++) {
+    pairs[2 * i] = s->blocks[i];
+    pairs[2 * i + 1] = dev[i];
+  }
+  if (nb) {
+    int32_t st = fkv_swap_in(m->pool, pairs.data(), (uint32_t)nb, stream);
+    if (st) {
+      (void)fkv_block_free(m->pool, (uint32_t)nb, dev.data());
+      return st;
+    }
+  }
+  for (int32_t h : s->blocks) m->host_free.push_back(h);
+  s->blocks = std::move(dev);
+  s->swapped = false;
+  return ok();
+}
+
+int32_t fkv_seqs_tables(const fkv_seqs* m, const uint32_t* seqs, uint32_t n, uint32_t max_blocks,
+                        int32_t* tables_out, int32_t* ctx_out) {
+  if (!m || (n && (!seqs || !tables_out || !ctx_out))) return fail(FKV_ERR_INVALID, "null argument");
+  for (uint32_t i = 0; i < n; i++) {
+    const fkv_seqs::Seq* s = seq_at(m, seqs[i]);
+    if (!s) return fail(FKV_ERR_CACHE, "unknown sequence");
+    if (s->swapped) return fail(FKV_ERR_CACHE, "sequence is swapped out");
+    if (s->blocks.size() > max_blocks) return fail(FKV_ERR_INVALID, "block table too narrow");
+    if (s->len > 0x7fffffffull) return fail(FKV_ERR_INVALID, "sequence too long");
+  }
+  for (uint32_t i = 0; i < n; i++) {
+    const fkv_seqs::Seq& s = m->seqs[seqs[i]];
+    int32_t* row = tables_out + (uint64_t)i * max_blocks;
+    std::copy(s.blocks.begin(), s.blocks.end(), row);
+    std::fill(row + s.blocks.size(), row + max_blocks, 0);
+    ctx_out[i] = (int32_t)s.len;
+  }
   return ok();
 }
 

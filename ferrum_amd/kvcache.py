@@ -408,6 +408,82 @@ class PagedKvPool:
             _stream_ptr(stream)))
 
 
+class SequenceManager:
+    """Per-sequence block lists over one PagedKvPool (fkv_seqs_*): the scheduler's KV
+    bookkeeping on paged storage (crates/scheduler/src/batcher.rs: admission :108-129,
+    rollback :291-308, finish :329-338), with copy-on-write forks and swap preemption."""
+
+    def __init__(self, pool: PagedKvPool):
+        self._lib = pool._lib
+        self.pool = pool
+        h = ctypes.c_void_p()
+        check(self._lib.fkv_seqs_create(pool.handle, ctypes.byref(h)))
+        self._h = h.value
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.fkv_seqs_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def add(self, n_tokens: int) -> int:
+        """Admission: a new sequence with blocks for n_tokens (Unavailable if none)."""
+        sid = ctypes.c_uint32()
+        check(self._lib.fkv_seqs_add(self._h, n_tokens, ctypes.byref(sid)))
+        return sid.value
+
+    def reserve(self, seq: int, n: int):
+        """Blocks for n more tokens; returns the copy-on-write (src, dst) pair or None."""
+        pair = np.full(2, -1, dtype=np.int64)
+        check(self._lib.fkv_seqs_reserve(self._h, seq, n, pair.ctypes.data))
+        return None if pair[0] < 0 else (int(pair[0]), int(pair[1]))
+
+    def slots(self, seq: int, pos: int, n: int) -> np.ndarray:
+        out = np.empty(n, dtype=np.int64)
+        check(self._lib.fkv_seqs_slots(self._h, seq, pos, n, out.ctypes.data))
+        return out
+
+    def commit(self, seq: int, n: int) -> None:
+        check(self._lib.fkv_seqs_commit(self._h, seq, n))
+
+    def truncate(self, seq: int, n_tokens: int) -> None:
+        check(self._lib.fkv_seqs_truncate(self._h, seq, n_tokens))
+
+    def fork(self, parent: int) -> int:
+        sid = ctypes.c_uint32()
+        check(self._lib.fkv_seqs_fork(self._h, parent, ctypes.byref(sid)))
+        return sid.value
+
+    def free(self, seq: int) -> None:
+        check(self._lib.fkv_seqs_free(self._h, seq))
+
+    def length(self, seq: int):
+        """(committed length, swapped out)."""
+        n, sw = ctypes.c_uint64(), ctypes.c_int32()
+        check(self._lib.fkv_seqs_len(self._h, seq, ctypes.byref(n), ctypes.byref(sw)))
+        return n.value, bool(sw.value)
+
+    def swap_out(self, seq: int, stream=None) -> None:
+        check(self._lib.fkv_seqs_swap_out(self._h, seq, _stream_ptr(stream)))
+
+    def swap_in(self, seq: int, stream=None) -> None:
+        check(self._lib.fkv_seqs_swap_in(self._h, seq, _stream_ptr(stream)))
+
+    def tables(self, seqs: Sequence[int], max_blocks: int):
+        """Host block-table rows [n, max_blocks] (padded with block 0) and lengths [n]."""
+        ids = np.ascontiguousarray(seqs, dtype=np.uint32)
+        tab = np.empty((ids.size, max_blocks), dtype=np.int32)
+        ctx = np.empty(ids.size, dtype=np.int32)
+        check(self._lib.fkv_seqs_tables(self._h, ids.ctypes.data, ids.size, max_blocks,
+                                        tab.ctypes.data, ctx.ctypes.data))
+        return tab, ctx
+
+
 def device_copy(dst, src, nbytes: int, stream=None) -> None:
     """16-byte vector device copy (the HBM calibration kernel)."""
     lib = _lib.load()

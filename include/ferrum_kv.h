@@ -339,6 +339,57 @@ int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, 
  * pool kernels; used to calibrate HBM counters and to measure copy bandwidth. */
 int32_t fkv_device_copy(void* dst, const void* src, uint64_t bytes, void* stream);
 
+/* ------------------------------------------------------------------------- */
+/* Sequence block manager: the scheduler's KV bookkeeping on the paged pool.   */
+/* ------------------------------------------------------------------------- */
+
+/* Per-sequence block lists over one paged pool. This is the paged replacement for
+ * how crates/scheduler/src/batcher.rs uses KV slots: admission stops on
+ * Unavailable (:108-129), rollback frees the slot and re-runs the prefix
+ * (restore_kv, :291-308), finish frees the slot (:329-338). Here admission asks
+ * for the blocks a sequence's tokens need; fkv_seqs_fork shares blocks by
+ * reference (copy-on-write); rollback truncates the block list; preemption moves
+ * a sequence's blocks to the pool's pinned host blocks and back. One manager per
+ * pool (it owns the pool's host blocks); single writer, like the pool.
+ * Errors: FKV_ERR_CACHE "cache: unknown sequence", "cache: sequence is swapped
+ * out", ...; FKV_ERR_UNAVAILABLE "no free kv blocks" / "no free host blocks", with
+ * nothing changed. */
+typedef struct fkv_seqs fkv_seqs;
+int32_t fkv_seqs_create(fkv_pool* pool, fkv_seqs** out);
+/* Releases every sequence's blocks. */
+int32_t fkv_seqs_destroy(fkv_seqs* m);
+/* Admission: a new sequence (length 0) with blocks for n_tokens tokens. */
+int32_t fkv_seqs_add(fkv_seqs* m, uint64_t n_tokens, uint32_t* seq_out);
+/* Blocks for n more tokens after the committed length. If the block that holds
+ * position len is shared with another sequence (after a fork) and already holds
+ * some of this sequence's tokens, the sequence takes a private copy: copy_pair
+ * (host int64[2]) receives (shared block, new block), which the caller copies
+ * with fkv_copy_blocks before it appends; otherwise copy_pair is (-1, -1). */
+int32_t fkv_seqs_reserve(fkv_seqs* m, uint32_t seq, uint64_t n, int64_t* copy_pair);
+/* Slots of positions pos .. pos + n - 1 (within the reserved blocks) for fkv_append. */
+int32_t fkv_seqs_slots(const fkv_seqs* m, uint32_t seq, uint64_t pos, uint64_t n,
+                       int64_t* slots_out);
+/* len += n: the tokens' K/V are in the pool (KvPool::commit_token, pool.rs:155-172). */
+int32_t fkv_seqs_commit(fkv_seqs* m, uint32_t seq, uint64_t n);
+/* Rollback: len = n_tokens (<= len); blocks past the new length are released. */
+int32_t fkv_seqs_truncate(fkv_seqs* m, uint32_t seq, uint64_t n_tokens);
+/* A new sequence of the parent's length sharing its committed blocks. */
+int32_t fkv_seqs_fork(fkv_seqs* m, uint32_t parent, uint32_t* child_out);
+/* Finish: releases the sequence's blocks (device or host). */
+int32_t fkv_seqs_free(fkv_seqs* m, uint32_t seq);
+/* Committed length; *swapped_out (may be NULL) is 1 while swapped out. */
+int32_t fkv_seqs_len(const fkv_seqs* m, uint32_t seq, uint64_t* len_out, int32_t* swapped_out);
+/* Preemption. swap_out copies the committed blocks to host blocks (fkv_swap_out)
+ * and releases the device blocks; swap_in copies them into new device blocks
+ * (fkv_swap_in). The copies are asynchronous on stream: released blocks may be
+ * written again only by work ordered after them (the same stream). */
+int32_t fkv_seqs_swap_out(fkv_seqs* m, uint32_t seq, void* stream);
+int32_t fkv_seqs_swap_in(fkv_seqs* m, uint32_t seq, void* stream);
+/* Host block-table rows (padded with block 0) and committed lengths of a batch,
+ * for upload to the decode and gather entry points. */
+int32_t fkv_seqs_tables(const fkv_seqs* m, const uint32_t* seqs, uint32_t n, uint32_t max_blocks,
+                        int32_t* tables_out, int32_t* ctx_out);
+
 #ifdef __cplusplus
 }
 #endif
