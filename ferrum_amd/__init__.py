@@ -1,7 +1,8 @@
 """ferrum_amd — MI355X (gfx950) paged KV-cache hot path of the Ferrum engine.
 
-The product is ``libferrum_kv.so`` (HIP kernels + C ABI, include/ferrum_kv.h);
-this package binds it and mirrors Ferrum's KvPool interface on the host.
+The product is ``libferrum_kv.so`` (HIP kernels + C ABI, include/ferrum_kv.h and
+include/ferrum_q8.h); this package binds it and mirrors Ferrum's KvPool interface
+and the Q8_0 Kernels::gemv/gemm on the host.
 """
 from . import _lib
 from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8_0, FAULT_BLOCK_RANGE, FAULT_CTX_RANGE,
@@ -11,13 +12,15 @@ from .errors import (CacheError, FerrumError, InternalError, InvalidRequest, Ker
                      Unavailable)
 from .kvcache import (KvPoolConfig, PagedConfig, PagedKvPool, PreallocatedKvPool,
                       SequenceManager, default_scale, device_copy)
+from .q8 import gemm_q8_0, gemv_q8_0, q8_0_row_bytes
 
 __all__ = [
     "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "FAULT_BLOCK_RANGE", "FAULT_CTX_RANGE",
     "FAULT_SLOT_RANGE", "FAULT_VALUE_RANGE", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
     "ROUND_NEAREST_EVEN", "CacheError", "FerrumError", "InternalError", "InvalidRequest",
     "KernelError", "Unavailable", "KvPoolConfig", "PagedConfig", "PagedKvPool",
-    "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "load_library",
+    "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "gemm_q8_0",
+    "gemv_q8_0", "load_library", "q8_0_row_bytes",
 ]
 
 

@@ -57,7 +57,7 @@ class PagedInfoC(ctypes.Structure):
                 ("free_blocks", u64), ("device_base", c_void_p), ("host_base", c_void_p)]
 
 
-# name -> (restype, argtypes). Must list every function include/ferrum_kv.h declares.
+# name -> (restype, argtypes). Must list every function include/*.h declares.
 SIGNATURES = {
     "fkv_abi_version": (i32, []),
     "fkv_last_error": (ctypes.c_char_p, []),
@@ -120,6 +120,9 @@ SIGNATURES = {
     "fkv_seqs_swap_out": (i32, [c_void_p, u32, c_void_p]),
     "fkv_seqs_swap_in": (i32, [c_void_p, u32, c_void_p]),
     "fkv_seqs_tables": (i32, [c_void_p, c_void_p, u32, u32, c_void_p, c_void_p]),
+    "fkv_gemv_q8_0": (i32, [c_void_p, u64, u64, u64, c_void_p, u64, c_void_p, u64, c_void_p]),
+    "fkv_gemm_q8_0": (i32, [c_void_p, u64, u64, u64, c_void_p, u64, u64, c_void_p, u64,
+                            c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -13,6 +13,7 @@
 #include <vector>
 
 #include "../../include/ferrum_kv.h"
+#include "../../include/ferrum_q8.h"
 #include "fkv_internal.h"
 
 namespace {
@@ -1083,6 +1084,59 @@ int32_t fkv_seqs_tables(const fkv_seqs* m, const uint32_t* seqs, uint32_t n, uin
     ctx_out[i] = (int32_t)s.len;
   }
   return ok();
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0 weight GEMV/GEMM (Kernels::gemv / Kernels::gemm for DType::Q8_0)
+// ---------------------------------------------------------------------------
+
+// check_matrix then the x/y lengths (crates/kernels/src/validate.rs:110-150), in
+// that order and with those strings; then what the device boundary adds.
+static int32_t check_gemm_q8(const void* w, uint64_t w_len, uint64_t rows, uint64_t cols,
+                             const float* x, uint64_t x_len, uint64_t n_tokens, float* y,
+                             uint64_t y_len) {
+  if (cols == 0) return fail(FKV_ERR_KERNEL, "empty dot");
+  if (cols % 32 != 0) return fail(FKV_ERR_KERNEL, "q8_0 k is not a multiple of 32");
+  uint64_t row_bytes, w_bytes, xn, yn;
+  if (mul_ovf(cols / 32, 34, &row_bytes) || mul_ovf(rows, row_bytes, &w_bytes))
+    return fail(FKV_ERR_KERNEL, "shape overflow");
+  if (w_len != w_bytes) return fail(FKV_ERR_KERNEL, "length mismatch");
+  if (mul_ovf(n_tokens, cols, &xn) || mul_ovf(n_tokens, rows, &yn))
+    return fail(FKV_ERR_KERNEL, "shape overflow");
+  if (x_len != xn || y_len != yn) return fail(FKV_ERR_KERNEL, "length mismatch");
+  if (rows == 0) return FKV_OK;
+  if (!w || !x || !y) return fail(FKV_ERR_INVALID, "null argument");
+  if ((uintptr_t)w % 2 != 0) return fail(FKV_ERR_INVALID, "w must be 2-byte aligned");
+  if ((uintptr_t)x % 4 != 0 || (uintptr_t)y % 4 != 0)
+    return fail(FKV_ERR_INVALID, "x and y must be 4-byte aligned");
+  if (rows > 0x7fff0000ull || n_tokens > 0x7fff0000ull || cols > 0xffffffffull ||
+      fkv::gemv_lds_bytes(1, (uint32_t)cols) > fkv::kGemvMaxLds)
+    return fail(FKV_ERR_INVALID, "matrix too large for one launch");
+  return FKV_OK;
+}
+
+static int32_t gemm_q8(const void* w, uint64_t w_len, uint64_t rows, uint64_t cols,
+                       const float* x, uint64_t x_len, uint64_t n_tokens, float* y,
+                       uint64_t y_len, void* stream) {
+  int32_t st = check_gemm_q8(w, w_len, rows, cols, x, x_len, n_tokens, y, y_len);
+  if (st) return st;
+  if (rows == 0) return ok();
+  FKV_HIP(fkv::launch_gemv_q8((const uint8_t*)w, (uint32_t)rows, (uint32_t)cols, x,
+                              (uint32_t)n_tokens, y, (hipStream_t)stream),
+          "gemv launch");
+  return ok();
+}
+
+int32_t fkv_gemv_q8_0(const void* w, uint64_t w_len, uint64_t rows, uint64_t cols,
+                      const float* x, uint64_t x_len, float* y, uint64_t y_len, void* stream) {
+  return gemm_q8(w, w_len, rows, cols, x, x_len, 1, y, y_len, stream);
+}
+
+int32_t fkv_gemm_q8_0(const void* w, uint64_t w_len, uint64_t rows, uint64_t cols,
+                      const float* x, uint64_t x_len, uint64_t n_tokens, float* y,
+                      uint64_t y_len, void* stream) {
+  if (n_tokens == 0) return ok();
+  return gemm_q8(w, w_len, rows, cols, x, x_len, n_tokens, y, y_len, stream);
 }
 
 }  // extern "C"

@@ -1,0 +1,336 @@
+// Q8_0 weight GEMV/GEMM on gfx950: Ferrum's ggml q8_0 x q8_0 product
+// (crates/kernels/src/q8_dot.rs:35-109; scalar.rs:84-116,191-204), bit for bit.
+//
+// Per token the f32 activation row is quantized as Q8Activation::quantize_into
+// (q8_dot.rs:35-61): per 32 values amax = max|v| (NaN ignored), d = amax/127,
+// id = d != 0 ? 1/d : 0, q = clamp(round_half_away(v * id)), and the scale kept is
+// f16(d) through the reference's own ties-away encoder (q8_dot.rs:111-139). Every
+// output is then dot_q8_row_q8_act (q8_dot.rs:72-109):
+//   acc = 0; for b = 0, 1, ...: acc += f32(sumi_b) * (w_scale_b * x_scale_b)
+// where sumi_b is the int32 dot of the two 32-byte runs. The integer dots have no
+// rounding, so any order gives the same sumi_b; w_scale * x_scale is exact (two
+// binary16 significands fit in 22 bits); f32(sumi_b) * that rounds once, as in the
+// reference (no FMA anywhere: -ffp-contract=off); and the f32 sum keeps the
+// reference's left-to-right block order through a DPP broadcast chain.
+//
+// Layout: weights row-major, row r = cols/32 blocks of 34 bytes ([f16 scale LE]
+// [32 x i8]) at w + r * (cols/32) * 34 (Ferrum's tensor bytes, dtype.rs:19-21); x is
+// [n_tokens][cols] f32, y is [n_tokens][rows] f32 (GemmArgs, par.rs:9-26).
+//
+// Work split: a workgroup of 4 waves owns 16 consecutive rows, a wave 4 rows, one
+// per 16-lane DPP row. Lane l of a row group takes blocks l, l+16, l+32, ... of its
+// row, so a 16-block step of the wave reads four runs of 544 contiguous bytes.
+// Up to kPipe steps of loads are in flight per wave.
+//
+// Alignment without realignment: a block is only 2-byte aligned (34 = 2 mod 4), and
+// the parity of its address is the same for every step of a lane (16 * 34 = 0 mod
+// 4). A lane reads the 8 dwords that start at the first dword boundary of its block
+// and the 16-bit word they leave out, and dots those 9 dwords as they are against
+// one of two copies of the quantized activation block kept in LDS:
+//   block at 2 mod 4: dwords = q0..q31, word = scale -> aligned copy (x0..x31, 0)
+//   block at 0 mod 4: dwords = (scale, q0 q1), (q2..q5) ... (q26..q29), word = (q30,
+//                     q31) -> copy shifted by two bytes ((0, 0, x0, x1), ..., (x30,
+//                     x31, 0, 0)); the scale bytes meet zeros.
+// The activation is quantized into LDS by each workgroup; its loads are issued
+// before any weight load (loads retire in issue order, so activation loads behind
+// a wave's weight prefetch would wait for all of it).
+#include <utility>
+
+#include "fkv_device.h"
+
+namespace fkv {
+namespace {
+
+typedef unsigned int u32x4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef float f32x4a __attribute__((ext_vector_type(4), aligned(4)));
+// Global-memory views of a device address (global_load, not flat_load: a flat load
+// also counts against the LDS wait counter and would hold the LDS reads back).
+typedef const __attribute__((address_space(1))) u32x4a g_u32x4a;
+typedef const __attribute__((address_space(1))) uint16_t g_u16;
+
+constexpr uint32_t kQ8Bytes = 34;
+constexpr int kGemvWaves = 4;
+constexpr int kGemvThreads = 64 * kGemvWaves;
+constexpr int kRowsPerWave = 4;                             // 16 lanes per row
+constexpr uint32_t kRowsPerWg = kGemvWaves * kRowsPerWave;  // 16
+constexpr int kPipe = 8;                                    // 16-block steps in flight
+// LDS dwords per (token, block): aligned q[0..8) | shifted q[0..8) | aligned q[8] (= 0),
+// xs | shifted q[8], xs. Each copy's first 8 dwords are 16-byte aligned.
+constexpr uint32_t kXDw = 20;
+constexpr int kXRegs = 4;  // activation passes (8 values a lane) loaded up front
+
+struct RawBlock {
+  uint32_t d[8];
+  uint32_t tail;
+};
+
+// Block at device address s (even): 8 dwords from the dword boundary at s (scale
+// first, s = 0 mod 4) or s + 2 (quants first, s = 2 mod 4), and the 16-bit word the
+// dwords leave out: the last two quants (s + 32) or the scale (s).
+__device__ __forceinline__ void load_block(uint64_t s, RawBlock& rb) {
+  const uint64_t base = (s + 2u) & ~(uint64_t)3u;
+  const u32x4a a = *(g_u32x4a*)base;
+  const u32x4a b = *(g_u32x4a*)(base + 16u);
+  rb.d[0] = a.x; rb.d[1] = a.y; rb.d[2] = a.z; rb.d[3] = a.w;
+  rb.d[4] = b.x; rb.d[5] = b.y; rb.d[6] = b.z; rb.d[7] = b.w;
+  rb.tail = *(g_u16*)((s & 2u) ? s : s + 32u);
+}
+
+template <int L>
+__device__ __forceinline__ float row_bcast(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + L, 0xf, 0xf, true));
+}
+
+// acc + p(lane 0) + p(lane 1) + ... + p(lane 15) of this lane's 16-lane row, in that
+// order, one rounding per add (one v_add_f32_dpp row_newbcast each).
+template <int... L>
+__device__ __forceinline__ float chain16(float acc, float p, std::integer_sequence<int, L...>) {
+  ((acc = acc + row_bcast<L>(p)), ...);
+  return acc;
+}
+
+// Rust's f32::max with a NaN-free left side: a NaN right side leaves it unchanged.
+__device__ __forceinline__ float max_keep(float m, float a) { return a > m ? a : m; }
+
+// amax / 127 correctly rounded for every amax >= 0: q = amax * RN(1/127) corrected
+// once by its FMA residual equals the IEEE quotient for all finite amax (checked
+// exhaustively over all 2^31 of them); +Inf, where the residual is NaN, maps to +Inf.
+__device__ __forceinline__ float div127(float a) {
+  const float c = 1.0f / 127.0f;
+  const float q = a * c;
+  const float r = __builtin_fmaf(-q, 127.0f, a);
+  const float q1 = __builtin_fmaf(r, c, q);
+  return a == __builtin_inff() ? a : q1;
+}
+
+// Rust's round (half away from zero) as trunc(y + copysign(0.5 - 2^-25, y)): equal
+// for every f32 y (checked exhaustively over all 2^32).
+__device__ __forceinline__ float round_away(float y) {
+  return __builtin_truncf(y + __builtin_copysignf(0.49999997f, y));
+}
+
+// clamp(round(y) as i32, -128, 127) with Rust's `as i32` taking NaN to 0, as a byte.
+__device__ __forceinline__ uint32_t q8_byte(float y) {
+  const float r = round_away(y);
+  const float c = (r == r) ? __builtin_amdgcn_fmed3f(r, -128.0f, 127.0f) : 0.0f;
+  return (uint32_t)(int)c & 0xffu;
+}
+
+// binary16 bits of d >= 0 (never NaN), ties away from zero (q8_dot.rs:111-139): the
+// round-toward-zero neighbour and the next binary16 up, compared by distance (both
+// differences exact near a tie). 65504 < d < 65520 stays 65504; d >= 65520 -> Inf.
+__device__ __forceinline__ uint32_t f16_bits_away(float d) {
+  auto pk = __builtin_amdgcn_cvt_pkrtz(d, 0.0f);
+  const uint32_t lo = __builtin_bit_cast(uint32_t, pk) & 0xffffu;
+  const float lo_v = dev::f16_bits_to_f32(lo);
+  const float hi_v = (lo == 0x7bffu) ? 65536.0f : dev::f16_bits_to_f32(lo + 1u);
+  return (hi_v - d <= d - lo_v) ? lo + 1u : lo;
+}
+
+// Activation quantization into LDS. A pass gives thread i (i < total) values
+// 8 * (i % (cols/8)) .. +8 of token i / (cols/8): four consecutive lanes (a quad)
+// own one 32-value block.
+struct XRegs {
+  f32x4a v[2 * kXRegs];
+};
+
+// Issues the loads of passes [p0, p0 + kXRegs). Items past the end read the last
+// item instead (in bounds; never stored), so no load sits under a branch.
+__device__ __forceinline__ void load_x(const float* x, uint32_t cols, uint32_t t0,
+                                       uint32_t total, uint32_t p0, XRegs& r) {
+  const uint32_t per_tok = cols / 8u;
+#pragma unroll
+  for (int k = 0; k < kXRegs; ++k) {
+    uint32_t i = (p0 + (uint32_t)k) * kGemvThreads + threadIdx.x;
+    i = i < total ? i : total - 1u;
+    const uint32_t t = i / per_tok, j = i - t * per_tok;
+    const float* src = x + (uint64_t)(t0 + t) * cols + 8u * j;
+    r.v[2 * k] = *(const f32x4a*)src;
+    r.v[2 * k + 1] = *(const f32x4a*)(src + 4);
+  }
+}
+
+__device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, uint32_t total,
+                                           uint32_t p0, uint32_t* lds) {
+  const uint32_t per_tok = nb * 4u;
+#pragma unroll
+  for (int k = 0; k < kXRegs; ++k) {
+    if ((p0 + (uint32_t)k) * kGemvThreads >= total) break;  // uniform
+    const uint32_t i = (p0 + (uint32_t)k) * kGemvThreads + threadIdx.x;
+    const f32x4a a = r.v[2 * k], b = r.v[2 * k + 1];
+    float m = 0.0f;
+    m = max_keep(m, __builtin_fabsf(a.x));
+    m = max_keep(m, __builtin_fabsf(a.y));
+    m = max_keep(m, __builtin_fabsf(a.z));
+    m = max_keep(m, __builtin_fabsf(a.w));
+    m = max_keep(m, __builtin_fabsf(b.x));
+    m = max_keep(m, __builtin_fabsf(b.y));
+    m = max_keep(m, __builtin_fabsf(b.z));
+    m = max_keep(m, __builtin_fabsf(b.w));
+    // max over the quad (partial maxima are never NaN, so v_max_f32 keeps max_keep's
+    // meaning); a quad is entirely below or entirely past `total` (multiples of 4).
+    m = __builtin_fmaxf(m, dev::dpp<0xB1>(m));
+    m = __builtin_fmaxf(m, dev::dpp<0x4E>(m));
+    const float d = div127(m);
+    const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+    const uint32_t qa = q8_byte(a.x * id) | (q8_byte(a.y * id) << 8) |
+                        (q8_byte(a.z * id) << 16) | (q8_byte(a.w * id) << 24);
+    const uint32_t qb = q8_byte(b.x * id) | (q8_byte(b.y * id) << 8) |
+                        (q8_byte(b.z * id) << 16) | (q8_byte(b.w * id) << 24);
+    // the previous lane's qb (quad_perm [0,0,1,2]); nothing before the first lane
+    const uint32_t sub = threadIdx.x & 3u;
+    uint32_t prev = (uint32_t)__builtin_amdgcn_mov_dpp((int)qb, 0x90, 0xf, 0xf, true);
+    prev = sub == 0u ? 0u : prev;
+    if (i < total) {
+      const uint32_t t = i / per_tok, j = i - t * per_tok;
+      uint32_t* blk = lds + ((uint64_t)t * nb + j / 4u) * kXDw;
+      *(uint2*)(blk + 2u * sub) = make_uint2(qa, qb);
+      *(uint2*)(blk + 8u + 2u * sub) = make_uint2(__builtin_amdgcn_alignbit(qa, prev, 16),
+                                                  __builtin_amdgcn_alignbit(qb, qa, 16));
+      const float xs = dev::f16_bits_to_f32(f16_bits_away(d));
+      if (sub == 0u) {
+        *(uint2*)(blk + 16u) = make_uint2(0u, __float_as_uint(xs));
+        blk[19] = __float_as_uint(xs);
+      }
+      if (sub == 3u) blk[18] = qb >> 16;
+    }
+  }
+}
+
+template <int T>
+__global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(
+    const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* x,
+    uint32_t n_tokens, float* __restrict__ y) {
+  extern __shared__ uint32_t lds[];  // [T][nb][kXDw]
+  const uint32_t nb = cols / 32u;
+  const uint32_t t0 = blockIdx.y * T;
+  const uint32_t nt = n_tokens - t0 < (uint32_t)T ? n_tokens - t0 : (uint32_t)T;
+
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+  const uint32_t l = lane & 15u;
+  const uint32_t row = blockIdx.x * kRowsPerWg + wave * kRowsPerWave + (lane >> 4);
+  const bool row_ok = row < rows;
+  // Loads never branch: a lane past the last row or block reads the last block of
+  // the last row in range (a cache hit) and its product is masked to +0. Branches
+  // around loads would cost the pipeline (the wait counts cannot be tracked through
+  // them) and split the DPP chain from its moves.
+  const uint64_t row_off =
+      (uint64_t)(uintptr_t)w + (uint64_t)(row_ok ? row : rows - 1u) * nb * kQ8Bytes;
+  const uint32_t n_it = (nb + 15u) / 16u;
+  const uint32_t n_pad = (n_it + kPipe - 1u) / kPipe * kPipe;
+  auto block_off = [&](uint32_t it) -> uint64_t {  // device address of the block
+    const uint32_t b = it * 16u + l;
+    return row_off + (uint64_t)(b < nb ? b : nb - 1u) * kQ8Bytes;
+  };
+  // Which activation copy this lane's (unclamped) blocks pair with, as LDS dword
+  // offsets of its 8 quant dwords and of its (9th dword, scale) pair.
+  const bool aligned = ((row_off + l * kQ8Bytes) & 2u) != 0u;
+  const uint32_t q_dw = aligned ? 0u : 8u, tail_dw = aligned ? 16u : 18u;
+
+  const uint32_t x_total = nt * (cols / 8u);  // 8-value items of this launch's tokens
+  XRegs xr;
+  load_x(x, cols, t0, x_total, 0, xr);
+  // Keep these loads ahead of the weight prefetch: no load moves across an asm
+  // statement that may touch memory (x is not __restrict__, so that covers it).
+  __asm__ volatile("" ::: "memory");
+
+  RawBlock buf[kPipe];
+#pragma unroll
+  for (int k = 0; k < kPipe; ++k) load_block(block_off((uint32_t)k), buf[k]);
+
+  quantize_x(xr, nb, x_total, 0, lds);
+  for (uint32_t p0 = kXRegs; p0 * kGemvThreads < x_total; p0 += kXRegs) {
+    load_x(x, cols, t0, x_total, p0, xr);
+    quantize_x(xr, nb, x_total, p0, lds);
+  }
+  __syncthreads();
+
+  float acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = 0.0f;
+
+  // Blocks it*16 .. it*16+15 into acc, lane L's block L-th. Steps past the last
+  // block add +0: acc starts at +0 and a zero sum is +0 under round-to-nearest, so
+  // acc is never -0 and acc + 0 == acc.
+  auto consume = [&](uint32_t it, const RawBlock& rb) {
+    const uint32_t b = it * 16u + l;
+    const bool ok = row_ok && b < nb;
+    const uint32_t bx = b < nb ? b : nb - 1u;
+    const float ws = dev::f16_bits_to_f32(aligned ? rb.tail : rb.d[0]);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t* xb = lds + ((uint64_t)t * nb + bx) * kXDw;
+      const uint4 x0 = *(const uint4*)(xb + q_dw);
+      const uint4 x1 = *(const uint4*)(xb + q_dw + 4u);
+      const uint2 xt = *(const uint2*)(xb + tail_dw);
+      int s = 0;
+      s = __builtin_amdgcn_sdot4((int)rb.d[0], (int)x0.x, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.d[1], (int)x0.y, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.d[2], (int)x0.z, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.d[3], (int)x0.w, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.d[4], (int)x1.x, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.d[5], (int)x1.y, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.d[6], (int)x1.z, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.d[7], (int)x1.w, s, false);
+      s = __builtin_amdgcn_sdot4((int)rb.tail, (int)xt.x, s, false);
+      float p = (float)s * (ws * __uint_as_float(xt.y));
+      p = ok ? p : 0.0f;
+      acc[t] = chain16(acc[t], p, std::make_integer_sequence<int, 16>{});
+    }
+  };
+
+  // The last kPipe reloads re-read the row's last block (cache hits): one loop body
+  // keeps the code small and every chain folded into v_add_f32_dpp.
+  for (uint32_t base = 0; base < n_pad; base += kPipe) {
+#pragma unroll
+    for (int k = 0; k < kPipe; ++k) {
+      consume(base + (uint32_t)k, buf[k]);
+      load_block(block_off(base + (uint32_t)k + kPipe), buf[k]);
+    }
+  }
+
+  if (row_ok && l == 0u) {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      if ((uint32_t)t < nt) y[(uint64_t)(t0 + t) * rows + row] = acc[t];
+  }
+}
+
+template <int T>
+hipError_t launch_t(const uint8_t* w, uint32_t rows, uint32_t cols, const float* x,
+                    uint32_t n_tokens, float* y, hipStream_t s) {
+  const dim3 grid((rows + kRowsPerWg - 1u) / kRowsPerWg, (n_tokens + T - 1u) / T);
+  const size_t lds = gemv_lds_bytes(T, cols);
+  if (lds > 65536u) {
+    const hipError_t e = hipFuncSetAttribute((const void*)gemv_q8_kernel<T>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                                             (int)lds);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(gemv_q8_kernel<T>, grid, dim3(kGemvThreads), lds, s, w, rows, cols, x,
+                     n_tokens, y);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t gemv_lds_bytes(uint32_t tokens, uint32_t cols) {
+  return (size_t)tokens * (cols / 32u) * kXDw * 4u;
+}
+
+uint32_t gemv_tokens_per_launch(uint32_t n_tokens, uint32_t cols) {
+  uint32_t t = n_tokens >= 3u ? 4u : (n_tokens == 2u ? 2u : 1u);
+  while (t > 1u && gemv_lds_bytes(t, cols) > 65536u) t /= 2u;
+  return t;
+}
+
+hipError_t launch_gemv_q8(const uint8_t* w, uint32_t rows, uint32_t cols, const float* x,
+                          uint32_t n_tokens, float* y, hipStream_t s) {
+  switch (gemv_tokens_per_launch(n_tokens, cols)) {
+    case 4: return launch_t<4>(w, rows, cols, x, n_tokens, y, s);
+    case 2: return launch_t<2>(w, rows, cols, x, n_tokens, y, s);
+    default: return launch_t<1>(w, rows, cols, x, n_tokens, y, s);
+  }
+}
+
+}  // namespace fkv

@@ -148,4 +148,14 @@ uint64_t attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_s
 uint64_t append_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
                                           uint32_t max_ctx_len);
 
+// Q8_0 weight GEMV/GEMM (fkv_gemv.hip): y[t][r] = dot_q8_row_q8_act(w row r, x[t]
+// quantized) for t < n_tokens, r < rows; w rows of cols/32 34-byte blocks (w even,
+// x 4-byte aligned, cols % 32 == 0, gemv_lds_bytes(1, cols) <= kGemvMaxLds: the
+// LDS one workgroup may hold on gfx950).
+constexpr size_t kGemvMaxLds = 163840;
+size_t gemv_lds_bytes(uint32_t tokens, uint32_t cols);
+uint32_t gemv_tokens_per_launch(uint32_t n_tokens, uint32_t cols);
+hipError_t launch_gemv_q8(const uint8_t* w, uint32_t rows, uint32_t cols, const float* x,
+                          uint32_t n_tokens, float* y, hipStream_t s);
+
 }  // namespace fkv

@@ -178,6 +178,44 @@ void fo_q8_dequant(const uint8_t* blocks, uint64_t n, float* out) {
   }
 }
 
+/* Kernels::gemm for DType::Q8_0 (crates/kernels/src/scalar.rs:98-116,191-204 through
+ * par.rs:9-26; Kernels::gemv is n_tokens = 1, scalar.rs:84-96). For every token the
+ * activation row is quantized by Q8Activation::quantize_into (q8_dot.rs:35-61):
+ * fo_q8_quantize_block with the reference's ties-away f32_to_f16_bits
+ * (q8_dot.rs:111-139), the scale kept as f16_to_f32 of those bits. Each weight row
+ * is then dot_q8_row_q8_act (q8_dot.rs:72-109): acc = 0, and for every block in
+ * order acc += (float)sumi * (w_scale * x_scale), sumi the int32 dot of the two i8
+ * runs. y[t * rows + r]. The caller has validated the shapes (cols % 32 == 0,
+ * w holds rows * (cols/32) * 34 bytes). */
+void fo_q8_gemm(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
+                uint64_t n_tokens, float* y) {
+  const uint64_t nb = cols / 32;
+  int8_t* xq = (int8_t*)malloc(cols ? cols : 1);
+  float* xs = (float*)malloc((nb ? nb : 1) * sizeof(float));
+  for (uint64_t t = 0; t < n_tokens; t++) {
+    for (uint64_t b = 0; b < nb; b++) {
+      uint16_t bits;
+      fo_q8_quantize_block(x + t * cols + b * 32, 1, &bits, xq + b * 32);
+      xs[b] = fo_f16_to_f32(bits);
+    }
+#pragma omp parallel for schedule(static)
+    for (uint64_t r = 0; r < rows; r++) {
+      const uint8_t* row = w + r * nb * 34;
+      float acc = 0.0f;
+      for (uint64_t b = 0; b < nb; b++) {
+        const uint8_t* blk = row + b * 34;
+        const float ws = fo_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+        int32_t sumi = 0;
+        for (int j = 0; j < 32; j++) sumi += (int32_t)(int8_t)blk[2 + j] * (int32_t)xq[b * 32 + j];
+        acc += (float)sumi * (ws * xs[b]);
+      }
+      y[t * rows + r] = acc;
+    }
+  }
+  free(xq);
+  free(xs);
+}
+
 /* ------------------------------------------------------------------------- */
 /* dot / softmax (scalar reference backend)                                    */
 /* ------------------------------------------------------------------------- */

@@ -21,6 +21,11 @@
  *   fo_q8_quantize_*       reference KAT tests.rs:299-309, tie/rounding cases,
  *                          invariants (|q|<=127, amax lane = +-127, error <= d/2)
  *   fo_q8_dequant          every code x 65,536 scales (kernels_contract.rs:700-744)
+ *   fo_q8_gemm             the reference KAT tests.rs:291-309; exact closed forms
+ *                          (power-of-two scales: integer matmul; a 4-block row whose
+ *                          left-to-right f32 sum differs from every other order; an
+ *                          f16 tie of the activation scale, which rounds away);
+ *                          sign and power-of-two scaling symmetries; f64 bound
  *   fo_dot, fo_softmax     KATs tests.rs:178-195, kernels_contract.rs:437-467
  *   fo_rope                KATs tests.rs:197-239 (pos 0 bit-identity, dims past rope_dim
  *                          untouched, NORMAL pairing); the rotation against an f64
@@ -66,6 +71,9 @@ void fo_q8_quantize_block(const float* x32, int32_t rounding, uint16_t* scale_ou
 /* Ferrum 34-byte blocks ([f16 scale LE][32 x i8]) for n values (n % 32 == 0). */
 void fo_q8_quantize_row(const float* x, uint64_t n, int32_t rounding, uint8_t* out);
 void fo_q8_dequant(const uint8_t* blocks, uint64_t n, float* out);
+/* Q8_0 weight GEMM/GEMV (ggml q8_0 . q8_0): y[t*rows + r], x [n_tokens][cols]. */
+void fo_q8_gemm(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
+                uint64_t n_tokens, float* y);
 
 float fo_dot(const float* a, const float* b, uint64_t n);
 void fo_softmax(float* x, uint64_t n);
