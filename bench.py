@@ -12,7 +12,9 @@ N(0,1), synthetic (no checkpoint).
 
 --workload picks another BASELINE config (c1 TinyLlama prefill + 64 decode steps,
 c3 continuous batching with chunked prefill in a fragmented 60%-of-HBM pool, c4
-Q8_0 KV, c5 70B long context plus copy_blocks and swap); each prints its own line.
+Q8_0 KV, c5 70B long context plus copy_blocks and swap), or q8gemv, the decode
+layer's Q8_0 weight projections (fkv_gemm_q8_0 over Llama-3-8B's 32 layers); each
+prints its own line.
 
 Printed JSON line: value = algorithmic HBM bytes of the step's calls (attention +
 append) / wall time per step, timed over K steps bracketed by synchronisation.
@@ -45,7 +47,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "q8gemv"])
+    ap.add_argument("--tokens", type=int, default=1,
+                    help="q8gemv: activation rows a call (1 = Kernels::gemv, more = gemm)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
     ap.add_argument("--rope-dim", type=int, default=0,
@@ -648,6 +652,148 @@ def run_c1(args, torch, fa, lib, dev):
     return res
 
 
+# Llama-3-8B projection shapes (rows, cols) of one layer, in forward_one_token's order
+# (crates/model/src/llama.rs:185-205 attn_q/k/v, :249-255 attn_output, then the FFN).
+LLAMA3_8B_PROJ = [("attn_q", 4096, 4096), ("attn_k", 1024, 4096), ("attn_v", 1024, 4096),
+                  ("attn_output", 4096, 4096), ("ffn_gate", 14336, 4096),
+                  ("ffn_up", 14336, 4096), ("ffn_down", 4096, 14336)]
+
+
+def q8_weights(torch, rows, cols, gen, dev):
+    """Synthetic Q8_0 tensor bytes: random int8 quants, binary16 scales of random sign
+    and mantissa in [2^-10, 2^-6) (the range of trained Llama Q8_0 weight scales)."""
+    nb = rows * (cols // 32)
+    w = torch.randint(-128, 128, (nb * 34,), dtype=torch.int8, device=dev, generator=gen)
+    w = w.view(torch.uint8)
+    sc = torch.randint(0x1400, 0x2400, (nb,), dtype=torch.int32, device=dev, generator=gen)
+    sc |= torch.randint(0, 2, (nb,), dtype=torch.int32, device=dev, generator=gen) << 15
+    blk = w.view(nb, 34)
+    blk[:, 0] = (sc & 0xFF).to(torch.uint8)
+    blk[:, 1] = ((sc >> 8) & 0xFF).to(torch.uint8)
+    return w
+
+
+def run_q8gemv(args, torch, fa, lib, dev):
+    """The decode layer's projections with Q8_0 weights: one step = Kernels::gemv of
+    attn_q/k/v/output and ffn_gate/up/down for each of Llama-3-8B's 32 layers (one token;
+    --tokens n: Kernels::gemm of n tokens), distinct synthetic weights per layer (7.4 GB,
+    so no launch reads weights another left in a cache). value = weight + activation +
+    output bytes a step / wall time a step."""
+    from oracle import ref
+
+    L, T = 32, max(1, args.tokens)
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    xs = {c: torch.randn(T, c, device=dev, generator=gen) for c in (4096, 14336)}
+    ys = {r: torch.empty(T, r, device=dev) for r in (1024, 4096, 14336)}
+    calls, weights = [], []
+    step_bytes = 0.0
+    for _ in range(L):
+        for name, rows, cols in LLAMA3_8B_PROJ:
+            w = q8_weights(torch, rows, cols, gen, dev)
+            weights.append((name, rows, cols, w))
+            calls.append((w.data_ptr(), w.numel(), rows, cols, xs[cols].data_ptr(), T * cols, T,
+                          ys[rows].data_ptr(), T * rows))
+            step_bytes += w.numel() + T * cols * 4 + T * rows * 4
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    f = lib.fkv_gemm_q8_0
+
+    def step():
+        for c in calls:
+            if f(*c, sp) != 0:
+                raise RuntimeError(lib.fkv_last_error().decode())
+
+    W, K = args.warmup, args.steps
+    for _ in range(W):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(K):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    region_ms = e0.elapsed_time(e1)
+    n_launch = K * len(calls)
+    value = step_bytes * K / wall / 1e9
+    achieved = step_bytes / len(calls) / (region_ms * 1e-3 / n_launch) / 1e9
+    kname = "gemv_q8_kernel<%d>" % (4 if T >= 3 else T)
+    res = {
+        "metric": "Q8_0 weight GEMV HBM GB/s (Llama-3-8B decode projections), 1xMI355X",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0 x q8_0 -> i32, f32 accumulate",
+        "data": "synthetic: random int8 quants, f16 scales in [2^-10, 2^-6); x ~ N(0,1)",
+        "config": {"workload": "q8gemv", "model_shapes": "Llama-3-8B", "n_layers": L,
+                   "tokens": T, "calls_per_step": len(calls),
+                   "weight_bytes_per_step": int(sum(w[3].numel() for w in weights)),
+                   "parallelism": "single GPU"},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "kernel": kname,
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": int(step_bytes / len(calls)),
+            "ms_per_launch": round(region_ms / n_launch, 5),
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        # the oracle's restatement of scalar.rs:191-204 + q8_dot.rs on layer 0's seven
+        # matrices, on host cores; the GPU's outputs for the same inputs must equal it
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        x_h = {c: xs[c].cpu().numpy() for c in xs}
+        mats = [(r, c, wd, wd.cpu().numpy()) for _, r, c, wd in weights[:len(LLAMA3_8B_PROJ)]]
+        nbytes = sum(w.size + T * c * 4 + T * r * 4 for r, c, _, w in mats)
+        mism = 0
+        for r, c, wd, w in mats:
+            y = torch.empty(T, r, device=dev)
+            if lib.fkv_gemm_q8_0(wd.data_ptr(), w.size, r, c, xs[c].data_ptr(), T * c, T,
+                                 y.data_ptr(), T * r, sp):
+                raise RuntimeError(lib.fkv_last_error().decode())
+            torch.cuda.synchronize()
+            want = ref.q8_gemm(w, r, c, x_h[c], threads)
+            mism += int((y.cpu().numpy().view(np.uint32) != want.view(np.uint32)).sum())
+        t0 = time.perf_counter()
+        for r, c, _, w in mats:
+            ref.q8_gemm(w, r, c, x_h[c], 1)
+        t1 = time.perf_counter() - t0
+        reps = 3
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            for r, c, _, w in mats:
+                ref.q8_gemm(w, r, c, x_h[c], threads)
+        tn = (time.perf_counter() - t0) / reps
+        res["cpu_baseline"] = {
+            "value": round(nbytes / tn / 1e9, 3),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (f"layer 0's 7 projections ({nbytes / 1e6:.1f} MB), {T} token(s): the "
+                       f"oracle's restatement of q8_dot.rs:35-109 / scalar.rs:191-204, "
+                       f"{reps} reps at {threads} threads"),
+            "value_1thread": round(nbytes / t1 / 1e9, 3),
+            "seconds_1thread": round(t1, 3),
+            "seconds_threads": round(tn, 3),
+            "gpu_vs_cpu_bit_mismatches": mism,
+        }
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -663,7 +809,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     lib = _lib.load()
-    run = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5}[args.workload]
+    run = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5,
+           "q8gemv": run_q8gemv}[args.workload]
     result = run(args, torch, fa, lib, dev)
     print(json.dumps(result), flush=True)
 

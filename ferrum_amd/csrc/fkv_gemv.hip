@@ -41,40 +41,36 @@
 namespace fkv {
 namespace {
 
-typedef unsigned int u32x4a __attribute__((ext_vector_type(4), aligned(4)));
 typedef float f32x4a __attribute__((ext_vector_type(4), aligned(4)));
-// Global-memory views of a device address (global_load, not flat_load: a flat load
-// also counts against the LDS wait counter and would hold the LDS reads back).
-typedef const __attribute__((address_space(1))) u32x4a g_u32x4a;
-typedef const __attribute__((address_space(1))) uint16_t g_u16;
 
 constexpr uint32_t kQ8Bytes = 34;
 constexpr int kGemvWaves = 4;
 constexpr int kGemvThreads = 64 * kGemvWaves;
 constexpr int kRowsPerWave = 4;                             // 16 lanes per row
 constexpr uint32_t kRowsPerWg = kGemvWaves * kRowsPerWave;  // 16
-constexpr int kPipe = 8;                                    // 16-block steps in flight
+constexpr int kPipe = 4;                                    // 16-block steps in flight
 // LDS dwords per (token, block): aligned q[0..8) | shifted q[0..8) | aligned q[8] (= 0),
 // xs | shifted q[8], xs. Each copy's first 8 dwords are 16-byte aligned.
 constexpr uint32_t kXDw = 20;
-constexpr int kXRegs = 4;  // activation passes (8 values a lane) loaded up front
+constexpr int kXRegs = 2;  // activation passes (8 values a lane) loaded up front
+
+// LDS blocks a token: the step count rounded up to whole groups of kPipe steps, so
+// every step a group runs reads inside the array.
+__host__ __device__ constexpr uint32_t gemv_padded_blocks(uint32_t nb) {
+  return (nb + 16u * kPipe - 1u) / (16u * kPipe) * (16u * kPipe);
+}
 
 struct RawBlock {
   uint32_t d[8];
   uint32_t tail;
 };
 
-// Block at device address s (even): 8 dwords from the dword boundary at s (scale
-// first, s = 0 mod 4) or s + 2 (quants first, s = 2 mod 4), and the 16-bit word the
-// dwords leave out: the last two quants (s + 32) or the scale (s).
-__device__ __forceinline__ void load_block(uint64_t s, RawBlock& rb) {
-  const uint64_t base = (s + 2u) & ~(uint64_t)3u;
-  const u32x4a a = *(g_u32x4a*)base;
-  const u32x4a b = *(g_u32x4a*)(base + 16u);
-  rb.d[0] = a.x; rb.d[1] = a.y; rb.d[2] = a.z; rb.d[3] = a.w;
-  rb.d[4] = b.x; rb.d[5] = b.y; rb.d[6] = b.z; rb.d[7] = b.w;
-  rb.tail = *(g_u16*)((s & 2u) ? s : s + 32u);
-}
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+// Buffer descriptor word 3 for raw 32-bit access on gfx9 (the data format that
+// makes out-of-range reads return zero); offsets at or past kOobOffset are out of
+// range (the resource never spans more than kOobOffset - 1 bytes).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr uint32_t kOobOffset = 0x80000000u;
 
 template <int L>
 __device__ __forceinline__ float row_bcast(float v) {
@@ -88,9 +84,6 @@ __device__ __forceinline__ float chain16(float acc, float p, std::integer_sequen
   ((acc = acc + row_bcast<L>(p)), ...);
   return acc;
 }
-
-// Rust's f32::max with a NaN-free left side: a NaN right side leaves it unchanged.
-__device__ __forceinline__ float max_keep(float m, float a) { return a > m ? a : m; }
 
 // amax / 127 correctly rounded for every amax >= 0: q = amax * RN(1/127) corrected
 // once by its FMA residual equals the IEEE quotient for all finite amax (checked
@@ -109,11 +102,13 @@ __device__ __forceinline__ float round_away(float y) {
   return __builtin_truncf(y + __builtin_copysignf(0.49999997f, y));
 }
 
-// clamp(round(y) as i32, -128, 127) with Rust's `as i32` taking NaN to 0, as a byte.
+// clamp(round(y) as i32, -128, 127) as a byte. v_cvt_i32_f32 is Rust's `as i32`:
+// it saturates and takes NaN to 0 (written as asm: the C++ cast of NaN is undefined).
 __device__ __forceinline__ uint32_t q8_byte(float y) {
-  const float r = round_away(y);
-  const float c = (r == r) ? __builtin_amdgcn_fmed3f(r, -128.0f, 127.0f) : 0.0f;
-  return (uint32_t)(int)c & 0xffu;
+  int q;
+  __asm__("v_cvt_i32_f32 %0, %1" : "=v"(q) : "v"(round_away(y)));
+  q = q < -128 ? -128 : (q > 127 ? 127 : q);  // v_med3_i32
+  return (uint32_t)q & 0xffu;
 }
 
 // binary16 bits of d >= 0 (never NaN), ties away from zero (q8_dot.rs:111-139): the
@@ -127,48 +122,57 @@ __device__ __forceinline__ uint32_t f16_bits_away(float d) {
   return (hi_v - d <= d - lo_v) ? lo + 1u : lo;
 }
 
-// Activation quantization into LDS. A pass gives thread i (i < total) values
-// 8 * (i % (cols/8)) .. +8 of token i / (cols/8): four consecutive lanes (a quad)
-// own one 32-value block.
+// Activation quantization into LDS. Pass q covers token t = q / C of the launch
+// (C = ceil((cols/8) / 256) passes a token), items j = (q % C) * 256 + thread:
+// values 8j .. 8j+8 of the token; four consecutive lanes (a quad) own one 32-value
+// block. Token and chunk are uniform, so no lane divides.
 struct XRegs {
   f32x4a v[2 * kXRegs];
 };
 
-// Issues the loads of passes [p0, p0 + kXRegs). Items past the end read the last
-// item instead (in bounds; never stored), so no load sits under a branch.
+struct XPlan {
+  uint32_t per_tok;  // cols / 8 items a token
+  uint32_t chunks;   // passes a token
+  uint32_t passes;   // nt * chunks
+};
+
+// Issues the loads of passes [q0, q0 + kXRegs). Items past a token's end read its
+// last item (in bounds; never stored), so no load sits under a branch.
 __device__ __forceinline__ void load_x(const float* x, uint32_t cols, uint32_t t0,
-                                       uint32_t total, uint32_t p0, XRegs& r) {
-  const uint32_t per_tok = cols / 8u;
+                                       const XPlan& pl, uint32_t q0, XRegs& r) {
 #pragma unroll
   for (int k = 0; k < kXRegs; ++k) {
-    uint32_t i = (p0 + (uint32_t)k) * kGemvThreads + threadIdx.x;
-    i = i < total ? i : total - 1u;
-    const uint32_t t = i / per_tok, j = i - t * per_tok;
+    uint32_t q = q0 + (uint32_t)k;
+    q = q < pl.passes ? q : pl.passes - 1u;
+    const uint32_t t = q / pl.chunks, c = q - t * pl.chunks;
+    uint32_t j = c * kGemvThreads + threadIdx.x;
+    j = j < pl.per_tok ? j : pl.per_tok - 1u;
     const float* src = x + (uint64_t)(t0 + t) * cols + 8u * j;
     r.v[2 * k] = *(const f32x4a*)src;
     r.v[2 * k + 1] = *(const f32x4a*)(src + 4);
   }
 }
 
-__device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, uint32_t total,
-                                           uint32_t p0, uint32_t* lds) {
-  const uint32_t per_tok = nb * 4u;
+__device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, const XPlan& pl,
+                                           uint32_t q0, uint32_t* lds) {
 #pragma unroll
   for (int k = 0; k < kXRegs; ++k) {
-    if ((p0 + (uint32_t)k) * kGemvThreads >= total) break;  // uniform
-    const uint32_t i = (p0 + (uint32_t)k) * kGemvThreads + threadIdx.x;
+    const uint32_t q = q0 + (uint32_t)k;
+    if (q >= pl.passes) break;  // uniform
+    const uint32_t t = q / pl.chunks, c = q - t * pl.chunks;
+    const uint32_t j = c * kGemvThreads + threadIdx.x;
     const f32x4a a = r.v[2 * k], b = r.v[2 * k + 1];
-    float m = 0.0f;
-    m = max_keep(m, __builtin_fabsf(a.x));
-    m = max_keep(m, __builtin_fabsf(a.y));
-    m = max_keep(m, __builtin_fabsf(a.z));
-    m = max_keep(m, __builtin_fabsf(a.w));
-    m = max_keep(m, __builtin_fabsf(b.x));
-    m = max_keep(m, __builtin_fabsf(b.y));
-    m = max_keep(m, __builtin_fabsf(b.z));
-    m = max_keep(m, __builtin_fabsf(b.w));
-    // max over the quad (partial maxima are never NaN, so v_max_f32 keeps max_keep's
-    // meaning); a quad is entirely below or entirely past `total` (multiples of 4).
+    // Rust's max ignores NaN; so does fmaxf (maxnum: a NaN operand, quiet or
+    // signaling, yields the other one).
+    float m = __builtin_fmaxf(__builtin_fabsf(a.x), __builtin_fabsf(a.y));
+    m = __builtin_fmaxf(m, __builtin_fabsf(a.z));
+    m = __builtin_fmaxf(m, __builtin_fabsf(a.w));
+    m = __builtin_fmaxf(m, __builtin_fabsf(b.x));
+    m = __builtin_fmaxf(m, __builtin_fabsf(b.y));
+    m = __builtin_fmaxf(m, __builtin_fabsf(b.z));
+    m = __builtin_fmaxf(m, __builtin_fabsf(b.w));
+    m = __builtin_fmaxf(m, 0.0f);  // all NaN: 0, as the reference's amax = 0 start
+    // max over the quad; a quad is entirely below or past per_tok (a multiple of 4)
     m = __builtin_fmaxf(m, dev::dpp<0xB1>(m));
     m = __builtin_fmaxf(m, dev::dpp<0x4E>(m));
     const float d = div127(m);
@@ -181,14 +185,13 @@ __device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, uint32_t
     const uint32_t sub = threadIdx.x & 3u;
     uint32_t prev = (uint32_t)__builtin_amdgcn_mov_dpp((int)qb, 0x90, 0xf, 0xf, true);
     prev = sub == 0u ? 0u : prev;
-    if (i < total) {
-      const uint32_t t = i / per_tok, j = i - t * per_tok;
+    if (j < pl.per_tok) {
       uint32_t* blk = lds + ((uint64_t)t * nb + j / 4u) * kXDw;
       *(uint2*)(blk + 2u * sub) = make_uint2(qa, qb);
       *(uint2*)(blk + 8u + 2u * sub) = make_uint2(__builtin_amdgcn_alignbit(qa, prev, 16),
                                                   __builtin_amdgcn_alignbit(qb, qa, 16));
-      const float xs = dev::f16_bits_to_f32(f16_bits_away(d));
       if (sub == 0u) {
+        const float xs = dev::f16_bits_to_f32(f16_bits_away(d));
         *(uint2*)(blk + 16u) = make_uint2(0u, __float_as_uint(xs));
         blk[19] = __float_as_uint(xs);
       }
@@ -197,8 +200,11 @@ __device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, uint32_t
   }
 }
 
+// Four waves a SIMD (at most 128 VGPRs) keep every wave of a 14336-row matrix
+// resident at once, so its weight stream never pauses between rounds of waves.
 template <int T>
-__global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(
+__global__ __launch_bounds__(kGemvThreads) 
+void gemv_q8_kernel(
     const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* x,
     uint32_t n_tokens, float* __restrict__ y) {
   extern __shared__ uint32_t lds[];  // [T][nb][kXDw]
@@ -210,38 +216,63 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(
   const uint32_t l = lane & 15u;
   const uint32_t row = blockIdx.x * kRowsPerWg + wave * kRowsPerWave + (lane >> 4);
   const bool row_ok = row < rows;
-  // Loads never branch: a lane past the last row or block reads the last block of
-  // the last row in range (a cache hit) and its product is masked to +0. Branches
-  // around loads would cost the pipeline (the wait counts cannot be tracked through
-  // them) and split the DPP chain from its moves.
-  const uint64_t row_off =
-      (uint64_t)(uintptr_t)w + (uint64_t)(row_ok ? row : rows - 1u) * nb * kQ8Bytes;
-  const uint32_t n_it = (nb + 15u) / 16u;
-  const uint32_t n_pad = (n_it + kPipe - 1u) / kPipe * kPipe;
-  auto block_off = [&](uint32_t it) -> uint64_t {  // device address of the block
-    const uint32_t b = it * 16u + l;
-    return row_off + (uint64_t)(b < nb ? b : nb - 1u) * kQ8Bytes;
-  };
-  // Which activation copy this lane's (unclamped) blocks pair with, as LDS dword
-  // offsets of its 8 quant dwords and of its (9th dword, scale) pair.
-  const bool aligned = ((row_off + l * kQ8Bytes) & 2u) != 0u;
-  const uint32_t q_dw = aligned ? 0u : 8u, tail_dw = aligned ? 16u : 18u;
+  const uint32_t n_it = (nb + 15u) / 16u;      // 16-block steps a row
+  const uint32_t nbp = gemv_padded_blocks(nb);  // LDS blocks a token (whole groups)
 
-  const uint32_t x_total = nt * (cols / 8u);  // 8-value items of this launch's tokens
+  // Weights through a buffer resource based at this workgroup's first row: a lane
+  // whose block lies past its row's end asks for an offset beyond the resource, which
+  // reads zeros without touching memory. So no load is clamped or branched around,
+  // and every step's loads are a lane offset plus an immediate.
+  const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
+  const uint32_t row0 = blockIdx.x * kRowsPerWg;
+  const uint64_t base = (uint64_t)(uintptr_t)w + row0 * row_bytes;
+  const uint64_t left = (uint64_t)rows * row_bytes - row0 * row_bytes;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(uintptr_t)base, (short)0, (int)(left < kOobOffset ? left : kOobOffset - 1u),
+      kBufferWord3);
+  // A row past the end reads the last row (its results are not stored).
+  const uint32_t lane_off =
+      (uint32_t)((uint64_t)((row_ok ? row : rows - 1u) - row0) * row_bytes) + l * kQ8Bytes;
+  // Which activation copy this lane's blocks pair with (the parity of a lane's block
+  // addresses is the same at every step), as LDS dword offsets of its 8 quant dwords
+  // and of its (9th dword, scale) pair; and its byte offsets of the 8 dwords and of
+  // the 16-bit word.
+  const bool aligned = ((base + lane_off) & 2u) != 0u;
+  const uint32_t q_dw = aligned ? 0u : 8u, tail_dw = aligned ? 16u : 18u;
+  const uint32_t dw_off = lane_off + (aligned ? 2u : 0u);
+  const uint32_t tail_off = lane_off + (aligned ? 0u : 32u);
+
+  XPlan pl;
+  pl.per_tok = cols / 8u;
+  pl.chunks = (pl.per_tok + kGemvThreads - 1u) / kGemvThreads;
+  pl.passes = nt * pl.chunks;
   XRegs xr;
-  load_x(x, cols, t0, x_total, 0, xr);
+  load_x(x, cols, t0, pl, 0, xr);
   // Keep these loads ahead of the weight prefetch: no load moves across an asm
   // statement that may touch memory (x is not __restrict__, so that covers it).
   __asm__ volatile("" ::: "memory");
 
+  // Step it's loads: blocks it*16 + l; beyond the row (or the step count) none.
+  auto load_step = [&](uint32_t it, RawBlock& rb) {
+    const bool in = it * 16u + l < nb;
+    const uint32_t o = it * (16u * kQ8Bytes);
+    const uint32_t od = in ? dw_off + o : kOobOffset;
+    const uint32_t ot = in ? tail_off + o : kOobOffset;
+    const v4u a = __builtin_amdgcn_raw_buffer_load_b128(rsrc, od, 0, 0);
+    const v4u b = __builtin_amdgcn_raw_buffer_load_b128(rsrc, od + 16u, 0, 0);
+    rb.d[0] = a[0]; rb.d[1] = a[1]; rb.d[2] = a[2]; rb.d[3] = a[3];
+    rb.d[4] = b[0]; rb.d[5] = b[1]; rb.d[6] = b[2]; rb.d[7] = b[3];
+    rb.tail = __builtin_amdgcn_raw_buffer_load_b16(rsrc, ot, 0, 0);
+  };
+
   RawBlock buf[kPipe];
 #pragma unroll
-  for (int k = 0; k < kPipe; ++k) load_block(block_off((uint32_t)k), buf[k]);
+  for (int k = 0; k < kPipe; ++k) load_step((uint32_t)k, buf[k]);
 
-  quantize_x(xr, nb, x_total, 0, lds);
-  for (uint32_t p0 = kXRegs; p0 * kGemvThreads < x_total; p0 += kXRegs) {
-    load_x(x, cols, t0, x_total, p0, xr);
-    quantize_x(xr, nb, x_total, p0, lds);
+  quantize_x(xr, nbp, pl, 0, lds);
+  for (uint32_t q0 = kXRegs; q0 < pl.passes; q0 += kXRegs) {
+    load_x(x, cols, t0, pl, q0, xr);
+    quantize_x(xr, nbp, pl, q0, lds);
   }
   __syncthreads();
 
@@ -249,17 +280,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(
 #pragma unroll
   for (int t = 0; t < T; ++t) acc[t] = 0.0f;
 
-  // Blocks it*16 .. it*16+15 into acc, lane L's block L-th. Steps past the last
-  // block add +0: acc starts at +0 and a zero sum is +0 under round-to-nearest, so
-  // acc is never -0 and acc + 0 == acc.
+  // Step it into acc: lane L's block is the L-th added. Blocks past the row's end
+  // (loaded as zeros, paired with LDS padding) add +0: acc starts at +0 and a zero
+  // sum is +0 under round-to-nearest, so acc is never -0 and acc + 0 == acc.
+  const uint32_t* lane_x = lds + (uint64_t)l * kXDw;
   auto consume = [&](uint32_t it, const RawBlock& rb) {
-    const uint32_t b = it * 16u + l;
-    const bool ok = row_ok && b < nb;
-    const uint32_t bx = b < nb ? b : nb - 1u;
+    const bool ok = it * 16u + l < nb;
     const float ws = dev::f16_bits_to_f32(aligned ? rb.tail : rb.d[0]);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const uint32_t* xb = lds + ((uint64_t)t * nb + bx) * kXDw;
+      const uint32_t* xb = lane_x + ((uint64_t)t * nbp + it * 16u) * kXDw;
       const uint4 x0 = *(const uint4*)(xb + q_dw);
       const uint4 x1 = *(const uint4*)(xb + q_dw + 4u);
       const uint2 xt = *(const uint2*)(xb + tail_dw);
@@ -279,13 +309,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(
     }
   };
 
-  // The last kPipe reloads re-read the row's last block (cache hits): one loop body
-  // keeps the code small and every chain folded into v_add_f32_dpp.
-  for (uint32_t base = 0; base < n_pad; base += kPipe) {
+  // Groups of kPipe steps: consume each step, then load the step kPipe ahead into
+  // its buffer (loads past the last step read nothing).
+  for (uint32_t g = 0; g < n_it; g += kPipe) {
 #pragma unroll
     for (int k = 0; k < kPipe; ++k) {
-      consume(base + (uint32_t)k, buf[k]);
-      load_block(block_off(base + (uint32_t)k + kPipe), buf[k]);
+      consume(g + (uint32_t)k, buf[k]);
+      load_step(g + (uint32_t)k + kPipe, buf[k]);
     }
   }
 
@@ -315,7 +345,7 @@ hipError_t launch_t(const uint8_t* w, uint32_t rows, uint32_t cols, const float*
 }  // namespace
 
 size_t gemv_lds_bytes(uint32_t tokens, uint32_t cols) {
-  return (size_t)tokens * (cols / 32u) * kXDw * 4u;
+  return (size_t)tokens * gemv_padded_blocks(cols / 32u) * kXDw * 4u;
 }
 
 uint32_t gemv_tokens_per_launch(uint32_t n_tokens, uint32_t cols) {

@@ -188,7 +188,8 @@ void fo_q8_dequant(const uint8_t* blocks, uint64_t n, float* out) {
  * runs. y[t * rows + r]. The caller has validated the shapes (cols % 32 == 0,
  * w holds rows * (cols/32) * 34 bytes). */
 void fo_q8_gemm(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
-                uint64_t n_tokens, float* y) {
+                uint64_t n_tokens, float* y, int32_t threads) {
+  if (threads <= 0) threads = omp_get_max_threads();
   const uint64_t nb = cols / 32;
   int8_t* xq = (int8_t*)malloc(cols ? cols : 1);
   float* xs = (float*)malloc((nb ? nb : 1) * sizeof(float));
@@ -198,7 +199,7 @@ void fo_q8_gemm(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
       fo_q8_quantize_block(x + t * cols + b * 32, 1, &bits, xq + b * 32);
       xs[b] = fo_f16_to_f32(bits);
     }
-#pragma omp parallel for schedule(static)
+#pragma omp parallel for schedule(static) num_threads(threads)
     for (uint64_t r = 0; r < rows; r++) {
       const uint8_t* row = w + r * nb * 34;
       float acc = 0.0f;

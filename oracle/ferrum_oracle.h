@@ -73,7 +73,7 @@ void fo_q8_quantize_row(const float* x, uint64_t n, int32_t rounding, uint8_t* o
 void fo_q8_dequant(const uint8_t* blocks, uint64_t n, float* out);
 /* Q8_0 weight GEMM/GEMV (ggml q8_0 . q8_0): y[t*rows + r], x [n_tokens][cols]. */
 void fo_q8_gemm(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
-                uint64_t n_tokens, float* y);
+                uint64_t n_tokens, float* y, int32_t threads);
 
 float fo_dot(const float* a, const float* b, uint64_t n);
 void fo_softmax(float* x, uint64_t n);

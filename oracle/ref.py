@@ -34,7 +34,7 @@ _SIGS = {
     "fo_q8_quantize_block": (None, [c_void_p, i32, c_void_p, c_void_p]),
     "fo_q8_quantize_row": (None, [c_void_p, u64, i32, c_void_p]),
     "fo_q8_dequant": (None, [c_void_p, u64, c_void_p]),
-    "fo_q8_gemm": (None, [c_void_p, u64, u64, c_void_p, u64, c_void_p]),
+    "fo_q8_gemm": (None, [c_void_p, u64, u64, c_void_p, u64, c_void_p, i32]),
     "fo_dot": (ctypes.c_float, [c_void_p, c_void_p, u64]),
     "fo_softmax": (None, [c_void_p, u64]),
     "fo_rope": (None, [c_void_p, u64, u32, u32, u32, ctypes.c_float]),
@@ -165,14 +165,14 @@ def q8_dequant(blocks: np.ndarray, n: int) -> np.ndarray:
     return out
 
 
-def q8_gemm(w: np.ndarray, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+def q8_gemm(w: np.ndarray, rows: int, cols: int, x: np.ndarray, threads: int = 0) -> np.ndarray:
     """Kernels::gemm/gemv for Q8_0 weights (fo_q8_gemm): x [n_tokens, cols] (or
-    [cols]) -> y [n_tokens, rows] float32."""
+    [cols]) -> y [n_tokens, rows] float32, rows split over `threads` (0: default)."""
     wb = np.ascontiguousarray(w, dtype=np.uint8).ravel()
     xa = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
     assert cols % 32 == 0 and wb.size == rows * (cols // 32) * 34
     y = np.empty((xa.shape[0], rows), dtype=np.float32)
-    lib().fo_q8_gemm(_p(wb), rows, cols, _p(xa), xa.shape[0], _p(y))
+    lib().fo_q8_gemm(_p(wb), rows, cols, _p(xa), xa.shape[0], _p(y), threads)
     return y
 
 
