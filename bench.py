@@ -746,7 +746,9 @@ def run_q8gemv(args, torch, fa, lib, dev):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": read_traffic(os.path.join(ROOT, "profiles",
+                                                 "q8_gemv_llama3_8b_decode_kernel_stats.md"))
+            if T == 1 else None,
             "bytes_per_launch": int(step_bytes / len(calls)),
             "ms_per_launch": round(region_ms / n_launch, 5),
         },
