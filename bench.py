@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "q8gemv"])
     ap.add_argument("--tokens", type=int, default=1,
                     help="q8gemv: activation rows a call (1 = Kernels::gemv, more = gemm)")
+    ap.add_argument("--gemv-fused", action="store_true",
+                    help="q8gemv: q/k/v and gate/up each in one fkv_gemm_q8_0_multi launch")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
     ap.add_argument("--rope-dim", type=int, default=0,
@@ -685,23 +687,46 @@ def run_q8gemv(args, torch, fa, lib, dev):
     gen = torch.Generator(device=dev).manual_seed(args.seed)
     xs = {c: torch.randn(T, c, device=dev, generator=gen) for c in (4096, 14336)}
     ys = {r: torch.empty(T, r, device=dev) for r in (1024, 4096, 14336)}
+    ys_of = {name: torch.empty(T, rows, device=dev) for name, rows, _ in LLAMA3_8B_PROJ}
     calls, weights = [], []
     step_bytes = 0.0
+    groups = ([["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"],
+               ["ffn_down"]] if args.gemv_fused else [[n] for n, _, _ in LLAMA3_8B_PROJ])
+    shape = {n: (r, c) for n, r, c in LLAMA3_8B_PROJ}
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    keep = []  # ctypes arrays of the multi calls
     for _ in range(L):
+        layer_w = {}
         for name, rows, cols in LLAMA3_8B_PROJ:
             w = q8_weights(torch, rows, cols, gen, dev)
             weights.append((name, rows, cols, w))
-            calls.append((w.data_ptr(), w.numel(), rows, cols, xs[cols].data_ptr(), T * cols, T,
-                          ys[rows].data_ptr(), T * rows))
+            layer_w[name] = w
             step_bytes += w.numel() + T * cols * 4 + T * rows * 4
+        for g in groups:
+            cols = shape[g[0]][1]
+            if len(g) == 1:
+                r = shape[g[0]][0]
+                w = layer_w[g[0]]
+                calls.append((lib.fkv_gemm_q8_0, (w.data_ptr(), w.numel(), r, cols,
+                                                  xs[cols].data_ptr(), T * cols, T,
+                                                  ys_of[g[0]].data_ptr(), T * r, sp)))
+            else:
+                n = len(g)
+                arr_p, arr_u = ctypes.c_void_p * n, ctypes.c_uint64 * n
+                a = (arr_p(*[layer_w[m].data_ptr() for m in g]),
+                     arr_u(*[layer_w[m].numel() for m in g]), arr_u(*[shape[m][0] for m in g]),
+                     arr_p(*[ys_of[m].data_ptr() for m in g]),
+                     arr_u(*[T * shape[m][0] for m in g]))
+                keep.append(a)
+                calls.append((lib.fkv_gemm_q8_0_multi, (n, a[0], a[1], a[2], cols,
+                                                        xs[cols].data_ptr(), T * cols, T, a[3],
+                                                        a[4], sp)))
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-    f = lib.fkv_gemm_q8_0
 
     def step():
-        for c in calls:
-            if f(*c, sp) != 0:
+        for f, c in calls:
+            if f(*c) != 0:
                 raise RuntimeError(lib.fkv_last_error().decode())
 
     W, K = args.warmup, args.steps
@@ -736,6 +761,7 @@ def run_q8gemv(args, torch, fa, lib, dev):
         "data": "synthetic: random int8 quants, f16 scales in [2^-10, 2^-6); x ~ N(0,1)",
         "config": {"workload": "q8gemv", "model_shapes": "Llama-3-8B", "n_layers": L,
                    "tokens": T, "calls_per_step": len(calls),
+                   "fused": "q/k/v and gate/up one launch each" if args.gemv_fused else "none",
                    "weight_bytes_per_step": int(sum(w[3].numel() for w in weights)),
                    "parallelism": "single GPU"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
@@ -748,7 +774,7 @@ def run_q8gemv(args, torch, fa, lib, dev):
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": read_traffic(os.path.join(ROOT, "profiles",
                                                  "q8_gemv_llama3_8b_decode_kernel_stats.md"))
-            if T == 1 else None,
+            if T == 1 and not args.gemv_fused else None,
             "bytes_per_launch": int(step_bytes / len(calls)),
             "ms_per_launch": round(region_ms / n_launch, 5),
         },

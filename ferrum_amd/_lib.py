@@ -123,6 +123,8 @@ SIGNATURES = {
     "fkv_gemv_q8_0": (i32, [c_void_p, u64, u64, u64, c_void_p, u64, c_void_p, u64, c_void_p]),
     "fkv_gemm_q8_0": (i32, [c_void_p, u64, u64, u64, c_void_p, u64, u64, c_void_p, u64,
                             c_void_p]),
+    "fkv_gemm_q8_0_multi": (i32, [u32, c_void_p, c_void_p, c_void_p, u64, c_void_p, u64, u64,
+                                  c_void_p, c_void_p, c_void_p]),
 }
 
 _lock = threading.Lock()

@@ -1121,8 +1121,12 @@ static int32_t gemm_q8(const void* w, uint64_t w_len, uint64_t rows, uint64_t co
   int32_t st = check_gemm_q8(w, w_len, rows, cols, x, x_len, n_tokens, y, y_len);
   if (st) return st;
   if (rows == 0) return ok();
-  FKV_HIP(fkv::launch_gemv_q8((const uint8_t*)w, (uint32_t)rows, (uint32_t)cols, x,
-                              (uint32_t)n_tokens, y, (hipStream_t)stream),
+  fkv::GemvBatch b{};
+  b.n = 1;
+  b.m[0].w = (const uint8_t*)w;
+  b.m[0].y = y;
+  b.m[0].rows = (uint32_t)rows;
+  FKV_HIP(fkv::launch_gemv_q8(b, (uint32_t)cols, x, (uint32_t)n_tokens, (hipStream_t)stream),
           "gemv launch");
   return ok();
 }
@@ -1137,6 +1141,30 @@ int32_t fkv_gemm_q8_0(const void* w, uint64_t w_len, uint64_t rows, uint64_t col
                       uint64_t y_len, void* stream) {
   if (n_tokens == 0) return ok();
   return gemm_q8(w, w_len, rows, cols, x, x_len, n_tokens, y, y_len, stream);
+}
+
+int32_t fkv_gemm_q8_0_multi(uint32_t n_mats, const void* const* w, const uint64_t* w_len,
+                            const uint64_t* rows, uint64_t cols, const float* x,
+                            uint64_t x_len, uint64_t n_tokens, float* const* y,
+                            const uint64_t* y_len, void* stream) {
+  if (n_mats == 0 || n_mats > (uint32_t)fkv::kGemvMaxMats)
+    return fail(FKV_ERR_INVALID, "n_mats must be 1..4");
+  if (!w || !w_len || !rows || !y || !y_len) return fail(FKV_ERR_INVALID, "null argument");
+  if (n_tokens == 0) return ok();
+  fkv::GemvBatch b{};
+  for (uint32_t m = 0; m < n_mats; ++m) {
+    int32_t st = check_gemm_q8(w[m], w_len[m], rows[m], cols, x, x_len, n_tokens, y[m], y_len[m]);
+    if (st) return st;
+    if (rows[m] == 0) continue;
+    b.m[b.n].w = (const uint8_t*)w[m];
+    b.m[b.n].y = y[m];
+    b.m[b.n].rows = (uint32_t)rows[m];
+    b.n++;
+  }
+  if (b.n == 0) return ok();
+  FKV_HIP(fkv::launch_gemv_q8(b, (uint32_t)cols, x, (uint32_t)n_tokens, (hipStream_t)stream),
+          "gemv launch");
+  return ok();
 }
 
 }  // extern "C"

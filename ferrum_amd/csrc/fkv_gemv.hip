@@ -17,8 +17,9 @@
 // [32 x i8]) at w + r * (cols/32) * 34 (Ferrum's tensor bytes, dtype.rs:19-21); x is
 // [n_tokens][cols] f32, y is [n_tokens][rows] f32 (GemmArgs, par.rs:9-26).
 //
-// Work split: a workgroup of 4 waves owns 16 consecutive rows, a wave 4 rows, one
-// per 16-lane DPP row. Lane l of a row group takes blocks l, l+16, l+32, ... of its
+// Work split: a workgroup of 4 waves owns 16 consecutive rows of one of the launch's
+// matrices (up to four that share the activation), a wave 4 rows, one per 16-lane DPP
+// row. Lane l of a row group takes blocks l, l+16, l+32, ... of its
 // row, so a 16-block step of the wave reads four runs of 544 contiguous bytes.
 // Up to kPipe steps of loads are in flight per wave.
 //
@@ -203,10 +204,18 @@ __device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, const XP
 // Four waves a SIMD (at most 128 VGPRs) keep every wave of a 14336-row matrix
 // resident at once, so its weight stream never pauses between rounds of waves.
 template <int T>
-__global__ __launch_bounds__(kGemvThreads) 
-void gemv_q8_kernel(
-    const uint8_t* __restrict__ w, uint32_t rows, uint32_t cols, const float* x,
-    uint32_t n_tokens, float* __restrict__ y) {
+__global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch bat, uint32_t cols,
+                                                               const float* x, uint32_t n_tokens) {
+  // This workgroup's matrix (uniform: scalar selects over the launch's few matrices).
+  uint32_t mi = 0;
+#pragma unroll
+  for (int j = 1; j < kGemvMaxMats; ++j)
+    if ((uint32_t)j < bat.n && blockIdx.x >= bat.m[j].wg0) mi = (uint32_t)j;
+  const GemvMat M = mi == 0u ? bat.m[0] : mi == 1u ? bat.m[1] : mi == 2u ? bat.m[2] : bat.m[3];
+  const uint8_t* __restrict__ w = M.w;
+  float* __restrict__ y = M.y;
+  const uint32_t rows = M.rows;
+  const uint32_t wg = blockIdx.x - M.wg0;
   extern __shared__ uint32_t lds[];  // [T][nb][kXDw]
   const uint32_t nb = cols / 32u;
   const uint32_t t0 = blockIdx.y * T;
@@ -214,7 +223,7 @@ void gemv_q8_kernel(
 
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t l = lane & 15u;
-  const uint32_t row = blockIdx.x * kRowsPerWg + wave * kRowsPerWave + (lane >> 4);
+  const uint32_t row = wg * kRowsPerWg + wave * kRowsPerWave + (lane >> 4);
   const bool row_ok = row < rows;
   const uint32_t n_it = (nb + 15u) / 16u;      // 16-block steps a row
   const uint32_t nbp = gemv_padded_blocks(nb);  // LDS blocks a token (whole groups)
@@ -224,7 +233,7 @@ void gemv_q8_kernel(
   // reads zeros without touching memory. So no load is clamped or branched around,
   // and every step's loads are a lane offset plus an immediate.
   const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
-  const uint32_t row0 = blockIdx.x * kRowsPerWg;
+  const uint32_t row0 = wg * kRowsPerWg;
   const uint64_t base = (uint64_t)(uintptr_t)w + row0 * row_bytes;
   const uint64_t left = (uint64_t)rows * row_bytes - row0 * row_bytes;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -327,9 +336,9 @@ void gemv_q8_kernel(
 }
 
 template <int T>
-hipError_t launch_t(const uint8_t* w, uint32_t rows, uint32_t cols, const float* x,
-                    uint32_t n_tokens, float* y, hipStream_t s) {
-  const dim3 grid((rows + kRowsPerWg - 1u) / kRowsPerWg, (n_tokens + T - 1u) / T);
+hipError_t launch_t(const GemvBatch& b, uint32_t n_wg, uint32_t cols, const float* x,
+                    uint32_t n_tokens, hipStream_t s) {
+  const dim3 grid(n_wg, (n_tokens + T - 1u) / T);
   const size_t lds = gemv_lds_bytes(T, cols);
   if (lds > 65536u) {
     const hipError_t e = hipFuncSetAttribute((const void*)gemv_q8_kernel<T>,
@@ -337,8 +346,8 @@ hipError_t launch_t(const uint8_t* w, uint32_t rows, uint32_t cols, const float*
                                              (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(gemv_q8_kernel<T>, grid, dim3(kGemvThreads), lds, s, w, rows, cols, x,
-                     n_tokens, y);
+  hipLaunchKernelGGL(gemv_q8_kernel<T>, grid, dim3(kGemvThreads), lds, s, b, cols, x,
+                     n_tokens);
   return hipGetLastError();
 }
 
@@ -354,12 +363,18 @@ uint32_t gemv_tokens_per_launch(uint32_t n_tokens, uint32_t cols) {
   return t;
 }
 
-hipError_t launch_gemv_q8(const uint8_t* w, uint32_t rows, uint32_t cols, const float* x,
-                          uint32_t n_tokens, float* y, hipStream_t s) {
+hipError_t launch_gemv_q8(GemvBatch b, uint32_t cols, const float* x, uint32_t n_tokens,
+                          hipStream_t s) {
+  uint32_t n_wg = 0;
+  for (uint32_t m = 0; m < b.n; ++m) {
+    b.m[m].wg0 = n_wg;
+    n_wg += (b.m[m].rows + kRowsPerWg - 1u) / kRowsPerWg;
+  }
+  for (uint32_t m = b.n; m < (uint32_t)kGemvMaxMats; ++m) b.m[m] = b.m[0];
   switch (gemv_tokens_per_launch(n_tokens, cols)) {
-    case 4: return launch_t<4>(w, rows, cols, x, n_tokens, y, s);
-    case 2: return launch_t<2>(w, rows, cols, x, n_tokens, y, s);
-    default: return launch_t<1>(w, rows, cols, x, n_tokens, y, s);
+    case 4: return launch_t<4>(b, n_wg, cols, x, n_tokens, s);
+    case 2: return launch_t<2>(b, n_wg, cols, x, n_tokens, s);
+    default: return launch_t<1>(b, n_wg, cols, x, n_tokens, s);
   }
 }
 

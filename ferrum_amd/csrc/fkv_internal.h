@@ -155,7 +155,20 @@ uint64_t append_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint3
 constexpr size_t kGemvMaxLds = 163840;
 size_t gemv_lds_bytes(uint32_t tokens, uint32_t cols);
 uint32_t gemv_tokens_per_launch(uint32_t n_tokens, uint32_t cols);
-hipError_t launch_gemv_q8(const uint8_t* w, uint32_t rows, uint32_t cols, const float* x,
-                          uint32_t n_tokens, float* y, hipStream_t s);
+// Up to kGemvMaxMats weight matrices that share the activation x (cols columns): one
+// launch, workgroups [wg0, next wg0) on matrix m; each y[m] as its own launch would give.
+constexpr int kGemvMaxMats = 4;
+struct GemvMat {
+  const uint8_t* w;
+  float* y;
+  uint32_t rows;
+  uint32_t wg0;  // first workgroup of this matrix (filled by launch_gemv_q8)
+};
+struct GemvBatch {
+  GemvMat m[kGemvMaxMats];
+  uint32_t n;
+};
+hipError_t launch_gemv_q8(GemvBatch b, uint32_t cols, const float* x, uint32_t n_tokens,
+                          hipStream_t s);
 
 }  // namespace fkv

@@ -15,11 +15,14 @@ reference's slice lengths, so a wrongly sized tensor gets the reference's
 """
 from __future__ import annotations
 
+import ctypes
+
 from . import _lib
 from .errors import check
 from .kvcache import _stream_ptr
 
-__all__ = ["Q8_0_BLOCK", "Q8_0_BLOCK_BYTES", "gemv_q8_0", "gemm_q8_0", "q8_0_row_bytes"]
+__all__ = ["Q8_0_BLOCK", "Q8_0_BLOCK_BYTES", "gemv_q8_0", "gemm_q8_0", "gemm_q8_0_multi",
+           "q8_0_row_bytes"]
 
 Q8_0_BLOCK = 32        # crates/core-types/src/dtype.rs:19-21
 Q8_0_BLOCK_BYTES = 34
@@ -59,3 +62,20 @@ def gemm_q8_0(w, rows: int, cols: int, x, n_tokens: int, y, stream=None) -> None
     yp, yn = _dev_any(y, torch.float32, "y")
     check(_lib.load().fkv_gemm_q8_0(wp, wn, rows, cols, xp, xn, n_tokens, yp, yn,
                                     _stream_ptr(stream)))
+
+
+def gemm_q8_0_multi(ws, rows, cols: int, x, n_tokens: int, ys, stream=None) -> None:
+    """gemm_q8_0 of up to 4 matrices that take the same x (q/k/v, gate/up) in one launch;
+    ys[m] equals gemm_q8_0(ws[m], rows[m], cols, x, n_tokens, ys[m]) bit for bit."""
+    import torch
+    n = len(ws)
+    if len(rows) != n or len(ys) != n:
+        raise ValueError("ws, rows and ys must have one entry per matrix")
+    wp = [_dev_any(w, torch.uint8, "w") for w in ws]
+    yp = [_dev_any(y, torch.float32, "y") for y in ys]
+    xp, xn = _dev_any(x, torch.float32, "x")
+    arr_p = ctypes.c_void_p * max(n, 1)
+    arr_u = ctypes.c_uint64 * max(n, 1)
+    check(_lib.load().fkv_gemm_q8_0_multi(
+        n, arr_p(*[p for p, _ in wp]), arr_u(*[k for _, k in wp]), arr_u(*rows), cols, xp, xn,
+        n_tokens, arr_p(*[p for p, _ in yp]), arr_u(*[k for _, k in yp]), _stream_ptr(stream)))

@@ -60,6 +60,19 @@ int32_t fkv_gemm_q8_0(const void* w, uint64_t w_len, uint64_t rows, uint64_t col
                       const float* x, uint64_t x_len, uint64_t n_tokens, float* y,
                       uint64_t y_len, void* stream);
 
+/* Kernels::gemm of up to 4 Q8_0 matrices that take the same activation rows (the
+ * layer's attn_q/attn_k/attn_v of one normed row, crates/model/src/llama.rs:185-205, or
+ * ffn_gate/ffn_up), in one launch: y[m] is bit for bit what fkv_gemm_q8_0(w[m], ...) gives.
+ * No counterpart in the reference, which makes one gemv call per matrix; this saves the
+ * small matrices' per-launch cost. w, w_len, rows, y, y_len are host arrays of n_mats
+ * entries (the pointers in them are device pointers). Errors: n_mats outside 1..4 or a
+ * null array -> FKV_ERR_INVALID; then n_tokens == 0 succeeds; then each matrix's checks
+ * as fkv_gemm_q8_0's, in matrix order, the first failure returned and nothing launched. */
+int32_t fkv_gemm_q8_0_multi(uint32_t n_mats, const void* const* w, const uint64_t* w_len,
+                            const uint64_t* rows, uint64_t cols, const float* x,
+                            uint64_t x_len, uint64_t n_tokens, float* const* y,
+                            const uint64_t* y_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

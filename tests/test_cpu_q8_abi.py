@@ -72,3 +72,31 @@ def test_device_boundary_errors():
     cols = 65536 + 32                                    # one token's LDS beyond 160 KiB
     with pytest.raises(fa.InvalidRequest, match="^matrix too large for one launch$"):
         gemv(cols // 32 * 34, 1, cols, cols, 1)
+
+
+def multi(n, w_len, rows, cols, x_len, n_tokens, y_len, w=None, y=None):
+    arr_p = ctypes.c_void_p * max(n, 1)
+    arr_u = ctypes.c_uint64 * max(n, 1)
+    w = w if w is not None else [FAKE] * n
+    y = y if y is not None else [FAKE] * n
+    return check(_lib.load().fkv_gemm_q8_0_multi(
+        n, arr_p(*w), arr_u(*w_len), arr_u(*rows), cols, FAKE, x_len, n_tokens, arr_p(*y),
+        arr_u(*y_len), None))
+
+
+def test_multi_checks_each_matrix_in_order():
+    with pytest.raises(fa.InvalidRequest, match="^n_mats must be 1..4$"):
+        multi(0, [], [], 64, 64, 1, [])
+    with pytest.raises(fa.InvalidRequest, match="^n_mats must be 1..4$"):
+        multi(5, [68] * 5, [2] * 5, 32, 32, 1, [2] * 5)
+    # the second matrix's weight bytes are one block short: its length mismatch
+    with pytest.raises(fa.KernelError, match="^kernel: length mismatch$"):
+        multi(2, [68, 34], [2, 2], 32, 32, 1, [2, 2])
+    # a bad cols fails on the first matrix already
+    with pytest.raises(fa.KernelError, match="^kernel: q8_0 k is not a multiple of 32$"):
+        multi(2, [68, 68], [2, 2], 48, 48, 1, [2, 2])
+    with pytest.raises(fa.InvalidRequest, match="^null argument$"):
+        multi(2, [68, 68], [2, 2], 32, 32, 1, [2, 2], w=[FAKE, 0])
+    # n_tokens == 0 and all-empty matrices succeed without a launch
+    multi(2, [0, 0], [0, 0], 32, 0, 0, [0, 0])
+    multi(2, [0, 0], [0, 0], 32, 32, 1, [0, 0], w=[0, 0], y=[0, 0])

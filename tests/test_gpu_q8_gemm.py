@@ -157,3 +157,39 @@ def test_errors_and_no_work_cases():
     fa.gemm_q8_0(w, 2, 32, x, 0, y)                   # n_tokens == 0: nothing written
     torch.cuda.synchronize()
     assert y.cpu().tolist() == [5.0, 5.0]
+
+
+@pytest.mark.parametrize("n_tokens", [1, 3, 4])
+def test_multi_matrix_launch_equals_separate_calls(n_tokens):
+    """q/k/v (and gate/up) in one launch: each output bit-identical to its own call and to
+    the oracle, including a matrix with no rows in the middle of the batch."""
+    import torch
+    import ferrum_amd as fa
+    rng = np.random.default_rng(40 + n_tokens)
+    cols = 512
+    shapes = [64, 16, 0, 17]
+    ws = [_weights(rng, r, cols) if r else np.zeros(0, np.uint8) for r in shapes]
+    x = rng.standard_normal((n_tokens, cols)).astype(np.float32)
+    xd = _dev(x)
+    wd = [_dev(w) if w.size else torch.zeros(0, dtype=torch.uint8, device="cuda") for w in ws]
+    ys = [torch.full((n_tokens, r), 7.0, dtype=torch.float32, device="cuda") for r in shapes]
+    fa.gemm_q8_0_multi(wd, shapes, cols, xd, n_tokens, ys)
+    torch.cuda.synchronize()
+    for r, w, y in zip(shapes, ws, ys):
+        if not r:
+            continue
+        _same(y.cpu().numpy(), ref.q8_gemm(w, r, cols, x))
+        _same(y.cpu().numpy(), _run(w, r, cols, x))
+
+
+def test_multi_matrix_rejects_before_writing():
+    import torch
+    import ferrum_amd as fa
+    w = torch.zeros(68, dtype=torch.uint8, device="cuda")
+    short = torch.zeros(34, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(32, dtype=torch.float32, device="cuda")
+    ys = [torch.full((1, 2), 5.0, device="cuda") for _ in range(2)]
+    with pytest.raises(fa.KernelError, match="^kernel: length mismatch$"):
+        fa.gemm_q8_0_multi([w, short], [2, 2], 32, x, 1, ys)
+    torch.cuda.synchronize()
+    assert all(y.cpu().tolist() == [[5.0, 5.0]] for y in ys)
