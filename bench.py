@@ -12,9 +12,9 @@ N(0,1), synthetic (no checkpoint).
 
 --workload picks another BASELINE config (c1 TinyLlama prefill + 64 decode steps,
 c3 continuous batching with chunked prefill in a fragmented 60%-of-HBM pool, c4
-Q8_0 KV, c5 70B long context plus copy_blocks and swap), or q8gemv, the decode
-layer's Q8_0 weight projections (fkv_gemm_q8_0 over Llama-3-8B's 32 layers); each
-prints its own line.
+Q8_0 KV, c5 70B long context plus copy_blocks and swap), q8gemv, the decode layer's
+Q8_0 weight projections (fkv_gemm_q8_0 over Llama-3-8B's 32 layers), or gguf, the
+GGUF open + weight upload to HBM; each prints its own line.
 
 Printed JSON line: value = algorithmic HBM bytes of the step's calls (attention +
 append) / wall time per step, timed over K steps bracketed by synchronisation.
@@ -47,7 +47,11 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "q8gemv"])
+    ap.add_argument("--workload", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c5", "q8gemv", "gguf"])
+    ap.add_argument("--gguf-layers", type=int, default=4,
+                    help="gguf: Llama-3-8B layers in the synthetic file (232 MB of Q8_0 each)")
+    ap.add_argument("--gguf-threads", type=int, default=0, help="gguf: host threads (0 = the CPUs available, at most 16)")
     ap.add_argument("--tokens", type=int, default=1,
                     help="q8gemv: activation rows a call (1 = Kernels::gemv, more = gemm)")
     ap.add_argument("--gemv-fused", action="store_true",
@@ -822,6 +826,98 @@ def run_q8gemv(args, torch, fa, lib, dev):
     return res
 
 
+def run_gguf(args, torch, fa, lib, dev):
+    """gguf::load + weight upload (§8(f) F4): a synthetic Llama-3-8B-shaped Q8_0 GGUF
+    (--gguf-layers layers of the 7 projections, alignment 32) is written to a temporary
+    file, then opened (mmap + decode) and its data section uploaded to HBM through pinned
+    staging; K timed repeats after W warm-ups (the file stays in the page cache, as a
+    server restarting on the same model finds it). value = data-section bytes / time of
+    open + upload. The plain pinned host-to-device copy of the same size is measured
+    beside it as the link's ceiling."""
+    import tempfile
+    from tests import gguf_build as gb
+
+    rng = np.random.default_rng(args.seed)
+    tensors, cursor = [], 0
+    one = {}
+    for name, rows, cols in LLAMA3_8B_PROJ:  # random bytes a matrix, reused across layers
+        nb = rows * cols // 32
+        blk = rng.integers(0, 256, (nb, 34), dtype=np.uint8)
+        blk[:, 1] = rng.integers(0x14, 0x24, nb, dtype=np.uint8)
+        one[name] = blk.reshape(-1)
+    for layer in range(args.gguf_layers):
+        for name, rows, cols in LLAMA3_8B_PROJ:
+            off = gb.align_up(cursor, 32)
+            tensors.append((f"blk.{layer}.{name}.weight", [cols, rows], 8, off, one[name]))
+            cursor = off + one[name].size
+    head = gb.build(3, [("general.architecture", gb.Str("llama")),
+                        ("llama.block_count", gb.U32(args.gguf_layers))],
+                    [(n, d, g, o, b"") for n, d, g, o, _ in tensors], 32)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    try:
+        with os.fdopen(fd, "wb") as f:
+            f.write(head)
+            for n, d, g, o, data in tensors:
+                f.seek(len(head) + o)
+                f.write(data.tobytes())
+        with fa.GgufFile(path) as g:
+            nbytes = g.data_bytes
+        dst = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+        def once():
+            with fa.GgufFile(path) as g:
+                g.upload(dst, threads=args.gguf_threads)
+
+        for _ in range(args.warmup):
+            once()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            once()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / args.steps
+        # correctness of the last upload: every tensor's bytes in HBM are the file's
+        check = dst.cpu().numpy()
+        with fa.GgufFile(path) as g:
+            bad = sum(int(not np.array_equal(check[t.data_offset:t.data_offset + t.nbytes],
+                                             one[t.name.split(".")[2]]))
+                      for t in g.tensors)
+        # the link's ceiling: one pinned buffer of the same size, copied to the device
+        pinned = torch.empty(nbytes, dtype=torch.uint8).pin_memory()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            dst.copy_(pinned, non_blocking=True)
+        torch.cuda.synchronize()
+        link = (time.perf_counter() - t0) / 3
+    finally:
+        os.unlink(path)
+    return {
+        "metric": "GGUF open + weight upload to HBM GB/s, 1xMI355X",
+        "value": round(nbytes / wall / 1e9, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bytes (Q8_0 tensors copied as stored)",
+        "data": "synthetic Llama-3-8B-shaped Q8_0 GGUF in the page cache",
+        "config": {"workload": "gguf", "layers": args.gguf_layers, "tensors": len(tensors),
+                   "data_bytes": int(nbytes), "chunk_bytes": 32 << 20,
+                   "host_threads": args.gguf_threads or min(len(os.sched_getaffinity(0)), 16),
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "pcie", "achieved": round(nbytes / wall / 1e9, 2),
+                     "peak": round(nbytes / link / 1e9, 2), "unit": "GB/s",
+                     "frac": round(link / wall, 4), "traffic": None,
+                     "peak_is": "pinned host-to-device copy of the same size, measured"},
+        "tensors_differing_after_upload": bad,
+        "cpu_baseline": None,
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -838,7 +934,7 @@ def main():
     dev = torch.device("cuda:0")
     lib = _lib.load()
     run = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5,
-           "q8gemv": run_q8gemv}[args.workload]
+           "q8gemv": run_q8gemv, "gguf": run_gguf}[args.workload]
     result = run(args, torch, fa, lib, dev)
     print(json.dumps(result), flush=True)
 

@@ -8,8 +8,9 @@ from . import _lib
 from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8_0, FAULT_BLOCK_RANGE, FAULT_CTX_RANGE,
                    FAULT_SLOT_RANGE, FAULT_VALUE_RANGE, GATHER_F32, GATHER_RAW, ROUND_HALF_AWAY,
                    ROUND_NEAREST_EVEN)
-from .errors import (CacheError, FerrumError, InternalError, InvalidRequest, KernelError,
-                     Unavailable)
+from .errors import (CacheError, FerrumError, GgufError, InternalError, InvalidRequest,
+                     KernelError, Unavailable)
+from .gguf import GgufFile
 from .kvcache import (KvPoolConfig, PagedConfig, PagedKvPool, PreallocatedKvPool,
                       SequenceManager, default_scale, device_copy)
 from .q8 import gemm_q8_0, gemm_q8_0_multi, gemv_q8_0, q8_0_row_bytes
@@ -17,7 +18,8 @@ from .q8 import gemm_q8_0, gemm_q8_0_multi, gemv_q8_0, q8_0_row_bytes
 __all__ = [
     "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "FAULT_BLOCK_RANGE", "FAULT_CTX_RANGE",
     "FAULT_SLOT_RANGE", "FAULT_VALUE_RANGE", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
-    "ROUND_NEAREST_EVEN", "CacheError", "FerrumError", "InternalError", "InvalidRequest",
+    "ROUND_NEAREST_EVEN", "CacheError", "FerrumError", "GgufError", "GgufFile", "InternalError",
+    "InvalidRequest",
     "KernelError", "Unavailable", "KvPoolConfig", "PagedConfig", "PagedKvPool",
     "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "gemm_q8_0", "gemm_q8_0_multi",
     "gemv_q8_0", "load_library", "q8_0_row_bytes",

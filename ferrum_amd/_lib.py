@@ -18,6 +18,7 @@ FKV_ERR_UNAVAILABLE = 2
 FKV_ERR_KERNEL = 3
 FKV_ERR_INVALID = 4
 FKV_ERR_INTERNAL = 5
+FKV_ERR_GGUF = 6
 
 DTYPE_F32 = 0
 DTYPE_F16 = 1
@@ -55,6 +56,16 @@ class PagedConfigC(ctypes.Structure):
 class PagedInfoC(ctypes.Structure):
     _fields_ = [("tile_bytes", u64), ("block_bytes", u64), ("pool_bytes", u64),
                 ("free_blocks", u64), ("device_base", c_void_p), ("host_base", c_void_p)]
+
+
+class GgufTensorInfoC(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("name_len", u64), ("n_dims", u32),
+                ("ggml_type", u32), ("shape", u64 * 4), ("data_offset", u64), ("nbytes", u64)]
+
+
+class GgufValueC(ctypes.Structure):
+    _fields_ = [("type", u32), ("elem_type", u32), ("count", u64), ("u", u64), ("i", i64),
+                ("f", ctypes.c_double), ("str", ctypes.c_void_p), ("str_len", u64)]
 
 
 # name -> (restype, argtypes). Must list every function include/*.h declares.
@@ -125,6 +136,15 @@ SIGNATURES = {
                             c_void_p]),
     "fkv_gemm_q8_0_multi": (i32, [u32, c_void_p, c_void_p, c_void_p, u64, c_void_p, u64, u64,
                                   c_void_p, c_void_p, c_void_p]),
+    "fkv_gguf_open": (i32, [ctypes.c_char_p, P(c_void_p)]),
+    "fkv_gguf_close": (i32, [c_void_p]),
+    "fkv_gguf_info": (i32, [c_void_p, P(u32), P(u64), P(u64), P(u64), P(u64), P(u64)]),
+    "fkv_gguf_tensor": (i32, [c_void_p, u64, P(GgufTensorInfoC)]),
+    "fkv_gguf_find": (i32, [c_void_p, ctypes.c_char_p, u64, P(u64)]),
+    "fkv_gguf_meta": (i32, [c_void_p, ctypes.c_char_p, u64, P(GgufValueC)]),
+    "fkv_gguf_meta_array_elem": (i32, [c_void_p, ctypes.c_char_p, u64, u64, P(GgufValueC)]),
+    "fkv_gguf_dump": (i32, [c_void_p, ctypes.c_char_p, u64, P(u64)]),
+    "fkv_gguf_upload": (i32, [c_void_p, c_void_p, u64, u64, u32]),
 }
 
 _lock = threading.Lock()

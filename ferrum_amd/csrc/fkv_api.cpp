@@ -14,6 +14,7 @@
 
 #include "../../include/ferrum_kv.h"
 #include "../../include/ferrum_q8.h"
+#include "../../include/ferrum_gguf.h"
 #include "fkv_internal.h"
 
 namespace {
@@ -25,6 +26,7 @@ int32_t fail(int32_t code, const std::string& msg) {
   switch (code) {
     case FKV_ERR_CACHE: g_last_error = "cache: " + msg; break;
     case FKV_ERR_KERNEL: g_last_error = "kernel: " + msg; break;
+    case FKV_ERR_GGUF: g_last_error = "gguf: " + msg; break;
     default: g_last_error = msg; break;
   }
   return code;
@@ -61,6 +63,13 @@ struct DeviceGuard {
 bool mul_ovf(uint64_t a, uint64_t b, uint64_t* r) { return __builtin_mul_overflow(a, b, r); }
 
 }  // namespace
+
+namespace fkv {
+int32_t api_fail(int32_t code, const std::string& msg) { return fail(code, msg); }
+int32_t api_ok() { return ok(); }
+KeepLastError::KeepLastError() : saved(g_last_error) {}
+KeepLastError::~KeepLastError() { g_last_error = std::move(saved); }
+}  // namespace fkv
 
 struct fkv_pool {
   fkv_paged_config cfg{};
@@ -165,6 +174,7 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
 }
 
 int32_t fkv_paged_destroy(fkv_pool* pool) {
+  fkv::KeepLastError keep;
   if (!pool) return ok();
   for (fkv_seqs* m : pool->managers) detach_manager(m);
   DeviceGuard dg(pool->cfg.device);
@@ -623,6 +633,7 @@ int32_t fkv_kvpool_new(const fkv_kvpool_config* config, int32_t device, fkv_kvpo
 }
 
 int32_t fkv_kvpool_destroy(fkv_kvpool* pool) {
+  fkv::KeepLastError keep;
   if (!pool) return ok();
   {
     DeviceGuard dg(pool->paged ? pool->paged->cfg.device : 0);
@@ -840,6 +851,7 @@ int32_t fkv_seqs_create(fkv_pool* pool, fkv_seqs** out) {
 }
 
 int32_t fkv_seqs_destroy(fkv_seqs* m) {
+  fkv::KeepLastError keep;
   if (!m) return ok();
   if (m->pool) {  // a destroyed pool has detached its managers: nothing to release
     for (auto& s : m->seqs)

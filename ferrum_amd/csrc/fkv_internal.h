@@ -5,7 +5,23 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+#include <string>
+
 namespace fkv {
+
+// The C ABI's error state (fkv_api.cpp): set the thread's Display string for an
+// FKV_ERR_* code and return the code; clear it and return FKV_OK.
+int32_t api_fail(int32_t code, const std::string& msg);
+int32_t api_ok();
+// Restores the thread's last-error message when it goes out of scope. The destroy and
+// close entry points hold one: they run from finalizers (a garbage collector may call them
+// between a failing call and the caller's read of fkv_last_error), so they must not
+// change the message.
+struct KeepLastError {
+  KeepLastError();
+  ~KeepLastError();
+  std::string saved;
+};
 
 // Geometry of one paged pool, passed by value to every kernel.
 // pool[block][layer][kv][head][tile]; tile = [B][D] elements (F32), [D/8][B][8]

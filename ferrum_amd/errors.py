@@ -47,12 +47,17 @@ class InternalError(FerrumError):
     """FerrumError::Internal (a HIP runtime failure)."""
 
 
+class GgufError(FerrumError):
+    """FerrumError::Gguf ("gguf: {msg}", HTTP 500)."""
+
+
 _BY_CODE = {
     _lib.FKV_ERR_CACHE: CacheError,
     _lib.FKV_ERR_UNAVAILABLE: Unavailable,
     _lib.FKV_ERR_KERNEL: KernelError,
     _lib.FKV_ERR_INVALID: InvalidRequest,
     _lib.FKV_ERR_INTERNAL: InternalError,
+    _lib.FKV_ERR_GGUF: GgufError,
 }
 
 

@@ -98,7 +98,10 @@ extern "C" {
 /* Version of this ABI; equals FKV_ABI_VERSION of the header the library was built with. */
 int32_t fkv_abi_version(void);
 
-/* Thread-local message of the last failing call on this thread ("" if none). */
+/* Thread-local message of the last failing call on this thread ("" if none). The destroy
+ * and close entry points (fkv_paged_destroy, fkv_kvpool_destroy, fkv_seqs_destroy,
+ * fkv_gguf_close) leave it as it is, so finalizers that run between a failing call and
+ * this read cannot clear it. */
 const char* fkv_last_error(void);
 
 /* Number of visible HIP devices (0 when no GPU); never fails. */

@@ -4,6 +4,7 @@ reference's error variants and strings (no kernel is launched here)."""
 import ctypes
 import os
 import re
+import struct
 
 import pytest
 
@@ -78,8 +79,26 @@ def test_null_arguments_are_invalid_request():
     assert lib.fkv_append(None, 0, None, None, None, 0, None) == _lib.FKV_ERR_INVALID
     assert lib.fkv_device_copy(ctypes.c_void_p(16), ctypes.c_void_p(8), 16, None) == _lib.FKV_ERR_INVALID
     assert b"16-byte aligned" in lib.fkv_last_error()
-    # a successful no-op call clears the thread's message
-    assert lib.fkv_paged_destroy(None) == 0
+
+
+def test_destroy_and_close_keep_the_last_error(tmp_path):
+    # finalizers may run between a failing call and the read of its message
+    lib = _lib.load()
+    assert lib.fkv_paged_create(None, None) == _lib.FKV_ERR_INVALID
+    for destroy in (lib.fkv_paged_destroy, lib.fkv_kvpool_destroy, lib.fkv_seqs_destroy,
+                    lib.fkv_gguf_close):
+        assert destroy(None) == _lib.FKV_OK
+        assert lib.fkv_last_error() == b"null argument"
+    good = tmp_path / "ok.gguf"
+    good.write_bytes(b"GGUF" + struct.pack("<IQQ", 3, 0, 0) + bytes(8))  # data at 32
+    f = fa.GgufFile(str(good))
+    bad = tmp_path / "bad.gguf"
+    bad.write_bytes(b"GGUF" + struct.pack("<I", 3))
+    assert lib.fkv_gguf_open(str(bad).encode(), ctypes.byref(ctypes.c_void_p())) == _lib.FKV_ERR_GGUF
+    f.close()
+    assert lib.fkv_last_error().startswith(b"gguf: ")
+    # any other successful call clears the thread's message
+    fa.GgufFile(str(good)).close()
     assert lib.fkv_last_error() == b""
 
 
