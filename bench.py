@@ -51,7 +51,8 @@ def parse():
                     choices=["c1", "c2", "c3", "c4", "c5", "q8gemv", "gguf"])
     ap.add_argument("--gguf-layers", type=int, default=4,
                     help="gguf: Llama-3-8B layers in the synthetic file (232 MB of Q8_0 each)")
-    ap.add_argument("--gguf-threads", type=int, default=0, help="gguf: host threads (0 = the CPUs available, at most 16)")
+    ap.add_argument("--gguf-threads", type=int, default=0, help="gguf: host threads (0 = 4, fewer on fewer CPUs)")
+    ap.add_argument("--gguf-chunk-mib", type=int, default=0, help="gguf: staging chunk (0 = 8 MiB)")
     ap.add_argument("--tokens", type=int, default=1,
                     help="q8gemv: activation rows a call (1 = Kernels::gemv, more = gemm)")
     ap.add_argument("--gemv-fused", action="store_true",
@@ -827,7 +828,7 @@ def run_q8gemv(args, torch, fa, lib, dev):
 
 
 def run_gguf(args, torch, fa, lib, dev):
-    """gguf::load + weight upload (§8(f) F4): a synthetic Llama-3-8B-shaped Q8_0 GGUF
+    """gguf::load + weight upload to HBM: a synthetic Llama-3-8B-shaped Q8_0 GGUF
     (--gguf-layers layers of the 7 projections, alignment 32) is written to a temporary
     file, then opened (mmap + decode) and its data section uploaded to HBM through pinned
     staging; K timed repeats after W warm-ups (the file stays in the page cache, as a
@@ -866,7 +867,7 @@ def run_gguf(args, torch, fa, lib, dev):
 
         def once():
             with fa.GgufFile(path) as g:
-                g.upload(dst, threads=args.gguf_threads)
+                g.upload(dst, chunk_bytes=args.gguf_chunk_mib << 20, threads=args.gguf_threads)
 
         for _ in range(args.warmup):
             once()
@@ -906,8 +907,8 @@ def run_gguf(args, torch, fa, lib, dev):
         "dtype": "bytes (Q8_0 tensors copied as stored)",
         "data": "synthetic Llama-3-8B-shaped Q8_0 GGUF in the page cache",
         "config": {"workload": "gguf", "layers": args.gguf_layers, "tensors": len(tensors),
-                   "data_bytes": int(nbytes), "chunk_bytes": 32 << 20,
-                   "host_threads": args.gguf_threads or min(len(os.sched_getaffinity(0)), 16),
+                   "data_bytes": int(nbytes), "chunk_bytes": (args.gguf_chunk_mib or 8) << 20,
+                   "host_threads": args.gguf_threads or min(len(os.sched_getaffinity(0)), 4),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "pcie", "achieved": round(nbytes / wall / 1e9, 2),
                      "peak": round(nbytes / link / 1e9, 2), "unit": "GB/s",
@@ -922,7 +923,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding of the path is design-only, see DESIGN.md", file=sys.stderr)
+              "sharding the path over several GPUs is a design, not built here", file=sys.stderr)
         sys.exit(2)
 
     import torch

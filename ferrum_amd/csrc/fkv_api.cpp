@@ -796,7 +796,7 @@ int32_t fkv_kvpool_uncommit_token(fkv_kvpool* pool, uint32_t slot) {
 }
 
 // ---------------------------------------------------------------------------
-// Sequence block manager (SURVEY F2): the scheduler's KV bookkeeping on paged
+// Sequence block manager: the scheduler's KV bookkeeping on paged
 // storage. crates/scheduler/src/batcher.rs admits while a dense slot is free
 // (:108-129), rolls back by freeing the slot and re-running the prefix
 // (restore_kv, :291-308) and frees the slot on finish (:329-338). Here a sequence

@@ -102,11 +102,12 @@ int32_t fkv_gguf_meta_array_elem(const fkv_gguf* g, const char* key, uint64_t ke
 int32_t fkv_gguf_dump(const fkv_gguf* g, char* buf, uint64_t cap, uint64_t* len);
 
 /* Copy the data section (data_bytes bytes) into device memory at dst (dst_bytes >=
- * data_bytes) on the calling thread's current device. Four pinned staging buffers of
- * chunk_bytes (0: 32 MiB) are filled from the file by `threads` host threads (0: the
- * CPUs the process may run on, at most 16; pread of disjoint parts) and sent with hipMemcpyAsync while the next chunks fill;
- * returns when every copy is done. Tensor t's device bytes are then dst +
- * info(t).data_offset. A read failure is FKV_ERR_GGUF "failed to read tensor data: ...". */
+ * data_bytes) on the calling thread's current device. `threads` host threads (0: 4, fewer
+ * when the process may run on fewer CPUs) each own one pinned buffer of chunk_bytes (0:
+ * 8 MiB) and one stream, and move every threads-th chunk: pread from the file, then
+ * hipMemcpyAsync, reusing the buffer once that copy is done. Returns when every copy is
+ * done. Tensor t's device bytes are then dst + info(t).data_offset. A read failure is
+ * FKV_ERR_GGUF "failed to read tensor data: ..."; a HIP failure FKV_ERR_INTERNAL. */
 int32_t fkv_gguf_upload(const fkv_gguf* g, void* dst, uint64_t dst_bytes, uint64_t chunk_bytes,
                         uint32_t threads);
 

@@ -94,3 +94,19 @@ def test_upload_rejects_a_short_buffer(tmp_path):
             f.upload(dst)
         torch.cuda.synchronize()
         assert int(dst.count_nonzero()) == 0
+
+
+def test_upload_reports_a_file_cut_short_after_open(tmp_path):
+    # the directory was decoded at open; the data section is read at upload, so a file that
+    # shrinks in between is a read error, not a crash
+    import os
+    import torch
+    import ferrum_amd as fa
+    path = tmp_path / "m.gguf"
+    path.write_bytes(_model(np.random.default_rng(3)))
+    with fa.GgufFile(str(path)) as f:
+        dst = torch.zeros(f.data_bytes, dtype=torch.uint8, device="cuda")
+        os.truncate(path, f.data_start + f.data_bytes // 2)
+        with pytest.raises(fa.GgufError, match=r"^gguf: failed to read tensor data: .*\(os error 5\)$"):
+            f.upload(dst, chunk_bytes=1 << 16, threads=4)
+        torch.cuda.synchronize()
