@@ -50,9 +50,16 @@ constexpr int kGemvThreads = 64 * kGemvWaves;
 constexpr int kRowsPerWave = 4;                             // 16 lanes per row
 constexpr uint32_t kRowsPerWg = kGemvWaves * kRowsPerWave;  // 16
 constexpr int kPipe = 4;                                    // 16-block steps in flight
-// LDS dwords per (token, block): aligned q[0..8) | shifted q[0..8) | aligned q[8] (= 0),
-// xs | shifted q[8], xs. Each copy's first 8 dwords are 16-byte aligned.
+// LDS dwords per (token, block): aligned q[0..8) | shifted q[0..8) | two tail pairs,
+// aligned (q[8] = 0, xs) and shifted (q[8], xs). Each copy's first 8 dwords are
+// 16-byte aligned. The tail pairs trade places in blocks with bit 3 set
+// (kTailDw): lanes l and l + 8 read blocks 8 records = 160 dwords apart, a multiple
+// of 32 banks, and would otherwise hit the same banks with their 8-byte tail reads.
 constexpr uint32_t kXDw = 20;
+__device__ __forceinline__ uint32_t tail_dw(bool aligned, uint32_t block) {
+  const uint32_t swap = (block >> 3) & 1u;
+  return aligned ? 16u + 2u * swap : 18u - 2u * swap;
+}
 constexpr int kXRegs = 2;  // activation passes (8 values a lane) loaded up front
 
 // LDS blocks a token: the step count rounded up to whole groups of kPipe steps, so
@@ -191,12 +198,13 @@ __device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, const XP
       *(uint2*)(blk + 2u * sub) = make_uint2(qa, qb);
       *(uint2*)(blk + 8u + 2u * sub) = make_uint2(__builtin_amdgcn_alignbit(qa, prev, 16),
                                                   __builtin_amdgcn_alignbit(qb, qa, 16));
+      const uint32_t ta = tail_dw(true, j / 4u), ts = tail_dw(false, j / 4u);
       if (sub == 0u) {
         const float xs = dev::f16_bits_to_f32(f16_bits_away(d));
-        *(uint2*)(blk + 16u) = make_uint2(0u, __float_as_uint(xs));
-        blk[19] = __float_as_uint(xs);
+        *(uint2*)(blk + ta) = make_uint2(0u, __float_as_uint(xs));
+        blk[ts + 1u] = __float_as_uint(xs);
       }
-      if (sub == 3u) blk[18] = qb >> 16;
+      if (sub == 3u) blk[ts] = qb >> 16;
     }
   }
 }
@@ -247,7 +255,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
   // and of its (9th dword, scale) pair; and its byte offsets of the 8 dwords and of
   // the 16-bit word.
   const bool aligned = ((base + lane_off) & 2u) != 0u;
-  const uint32_t q_dw = aligned ? 0u : 8u, tail_dw = aligned ? 16u : 18u;
+  // a step's blocks start at a multiple of 16, so bit 3 of lane l's block is bit 3 of l
+  const uint32_t q_dw = aligned ? 0u : 8u, t_dw = tail_dw(aligned, l);
   const uint32_t dw_off = lane_off + (aligned ? 2u : 0u);
   const uint32_t tail_off = lane_off + (aligned ? 0u : 32u);
 
@@ -301,7 +310,7 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
       const uint32_t* xb = lane_x + ((uint64_t)t * nbp + it * 16u) * kXDw;
       const uint4 x0 = *(const uint4*)(xb + q_dw);
       const uint4 x1 = *(const uint4*)(xb + q_dw + 4u);
-      const uint2 xt = *(const uint2*)(xb + tail_dw);
+      const uint2 xt = *(const uint2*)(xb + t_dw);
       int s = 0;
       s = __builtin_amdgcn_sdot4((int)rb.d[0], (int)x0.x, s, false);
       s = __builtin_amdgcn_sdot4((int)rb.d[1], (int)x0.y, s, false);
