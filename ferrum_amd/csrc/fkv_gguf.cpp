@@ -18,6 +18,7 @@
 #include <atomic>
 #include <memory>
 #include <string>
+#include <system_error>
 #include <thread>
 #include <unordered_map>
 #include <unordered_set>
@@ -335,10 +336,15 @@ void parse(fkv_gguf* g) {
   for (uint64_t k = 0; k < g->tensors.size(); k++) g->by_name.emplace(g->tensors[k].name, k);
 }
 
+// io::Error's Display of an OS error: "<strerror> (os error N)". strerror_r (GNU form)
+// because upload workers format errors concurrently.
+std::string os_error_text(int err) {
+  char buf[256];
+  return std::string(strerror_r(err, buf, sizeof(buf))) + " (os error " + std::to_string(err) + ")";
+}
+
 std::string io_error(const char* what, const char* path, int err) {
-  // io::Error's Display: "<strerror> (os error N)"
-  return std::string("failed to ") + what + " " + path + ": " + strerror(err) + " (os error " +
-         std::to_string(err) + ")";
+  return std::string("failed to ") + what + " " + path + ": " + os_error_text(err);
 }
 
 void fill_value(const Value& v, fkv_gguf_value* out) {
@@ -547,8 +553,7 @@ int32_t fkv_gguf_upload(const fkv_gguf* g, void* dst, uint64_t dst_bytes, uint64
           if (r <= 0) {
             const int e = r < 0 ? errno : EIO;
             f.code = FKV_ERR_GGUF;
-            f.msg = std::string("failed to read tensor data: ") + strerror(e) + " (os error " +
-                    std::to_string(e) + ")";
+            f.msg = "failed to read tensor data: " + os_error_text(e);
             ok = false;
             break;
           }
@@ -570,8 +575,16 @@ int32_t fkv_gguf_upload(const fkv_gguf* g, void* dst, uint64_t dst_bytes, uint64
   };
   std::vector<std::thread> pool;
   pool.reserve(nthr);
-  for (uint32_t t = 0; t < nthr; t++) pool.emplace_back(worker, t);
+  bool spawned = true;
+  try {
+    for (uint32_t t = 0; t < nthr; t++) pool.emplace_back(worker, t);
+  } catch (const std::system_error&) {
+    // the workers started so far stop after their current chunk
+    stop.store(true, std::memory_order_relaxed);
+    spawned = false;
+  }
   for (auto& th : pool) th.join();
+  if (!spawned) return fkv::api_fail(FKV_ERR_INTERNAL, "failed to start upload threads");
   for (const Failure& f : fail)
     if (f.code != FKV_OK) return fkv::api_fail(f.code, f.msg);
   return fkv::api_ok();

@@ -110,3 +110,28 @@ def test_upload_reports_a_file_cut_short_after_open(tmp_path):
         with pytest.raises(fa.GgufError, match=r"^gguf: failed to read tensor data: .*\(os error 5\)$"):
             f.upload(dst, chunk_bytes=1 << 16, threads=4)
         torch.cuda.synchronize()
+
+
+def test_upload_past_four_gib(tmp_path):
+    # a sparse 5 GiB F32 tensor: offsets beyond 32 bits in the file, the staging and HBM
+    import torch
+    import ferrum_amd as fa
+    n = (5 << 30) // 4
+    hdr = gb.build(3, [], [("big", [n], 0, 0, b"")], 32)
+    marks = {0: b"head", (4 << 30) - 3: b"edge", (4 << 30) + 12345: b"past", n * 4 - 4: b"tail"}
+    path = tmp_path / "big.gguf"
+    with open(path, "wb") as f:
+        f.write(hdr)
+        f.truncate(len(hdr) + n * 4)
+        for off, m in marks.items():
+            f.seek(len(hdr) + off)
+            f.write(m)
+    with fa.GgufFile(str(path)) as g:
+        assert g.data_bytes == n * 4 and g.tensor("big").nbytes == n * 4
+        dst = torch.full((n * 4,), 0x5A, dtype=torch.uint8, device="cuda")
+        g.upload(dst)
+        torch.cuda.synchronize()
+        for off, m in marks.items():
+            assert bytes(dst[off:off + 4].cpu().numpy()) == m, off
+        # everything else is the file's zeros: the sum is the marks' bytes alone
+        assert int(dst.sum(dtype=torch.int64)) == sum(sum(m) for m in marks.values())

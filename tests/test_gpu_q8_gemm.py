@@ -83,6 +83,7 @@ def test_reference_known_answer():
     (2, 256, 4), (2, 4096, 4),                               # tests.rs:770-830
     (17, 96, 1), (33, 544, 3), (16, 512, 5), (100, 1056, 9), (1000, 4096, 1),
     (5, 8192, 7), (48, 2080, 8), (7, 57344, 2),
+    (3, 65536, 2),   # the widest accepted: one token's activation copies fill 160 KB of LDS
 ])
 def test_matches_oracle(rows, cols, n_tokens):
     rng = np.random.default_rng(rows * 7919 + cols + n_tokens)
