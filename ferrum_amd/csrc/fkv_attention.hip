@@ -80,7 +80,7 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
   const uint32_t sk = blockIdx.x;
   const uint32_t part = blockIdx.y;
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
-  const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
+  const int32_t cap = dev::split_ctx_cap(max_blocks, kAttnBlock, max_parts, kAttnPartTokens);
   int32_t ctx = ctx_lens[seq];
   if (ctx < 0 || ctx > cap) {
     if (part == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
@@ -311,7 +311,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(
   float mp = lane < n0 ? ml[2 * lane] : -__builtin_inff();
   float lp = lane < n0 ? ml[2 * lane + 1] : 0.0f;
 
-  const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
+  const int32_t cap = dev::split_ctx_cap(max_blocks, kAttnBlock, max_parts, (uint32_t)part_tokens);
   const int32_t ctx = raw_ctx < 0 ? 0 : (raw_ctx > cap ? cap : raw_ctx);
   const int32_t nparts = ctx > 0 ? (ctx + part_tokens - 1) / part_tokens : 1;
   if (nparts == 1) return;
@@ -386,7 +386,7 @@ __global__ void __launch_bounds__(64 * kWideWaves) attn_combine_wide_kernel(
   const uint32_t head = blockIdx.x;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const uint32_t seq = head / n_heads;
-  const int32_t cap = (int32_t)(max_blocks * kAttnBlock);
+  const int32_t cap = dev::split_ctx_cap(max_blocks, kAttnBlock, max_parts, (uint32_t)part_tokens);
   int32_t ctx = ctx_lens[seq];
   ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
   const int32_t nparts = ctx > 0 ? (ctx + part_tokens - 1) / part_tokens : 1;

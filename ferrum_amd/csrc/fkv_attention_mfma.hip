@@ -875,7 +875,9 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   __shared__ uint16_t s_apps[2][D / 32];           // and scales
   __shared__ int32_t s_ord[2 * kAttnWaves + 4 + kOrderSortSeqs];  // work order: scans, item, keys
 
-  const int32_t cap = (int32_t)(max_blocks * B);
+  // the work list and the split clamp share this bound, so the list never holds more
+  // items than the grid has workgroups
+  const int32_t cap = dev::split_ctx_cap(max_blocks, B, max_splits, (uint32_t)split_tokens);
   const uint32_t kvh = blockIdx.x % g.n_kv_heads;
   uint32_t seq;
   int32_t split, ctx = 0;

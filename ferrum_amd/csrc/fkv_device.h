@@ -17,6 +17,17 @@ __device__ __forceinline__ uint8_t* tile_ptr(const Geom& g, uint64_t block, uint
          ((uint64_t)(layer * 2u + kv) * g.n_kv_heads + head) * g.tile_bytes;
 }
 
+// The largest context a split-attention launch can hold: the block table's capacity and
+// the max_parts partitions of part_tokens its grid and workspace were sized for (from the
+// caller's max_ctx_len). A longer context is an input fault: every kernel of the launch
+// clamps to the same bound, so none reads another head's partitions or past the workspace.
+__device__ __forceinline__ int32_t split_ctx_cap(uint32_t max_blocks, uint32_t block,
+                                                 uint32_t max_parts, uint32_t part_tokens) {
+  const uint64_t a = (uint64_t)max_blocks * block, b = (uint64_t)max_parts * part_tokens;
+  const uint64_t c = a < b ? a : b;
+  return (int32_t)(c < 0x7fffffffull ? c : 0x7fffffffull);
+}
+
 __device__ __forceinline__ void raise_fault(uint32_t* f, uint32_t bit) {
   atomicOr(f, bit);
 }

@@ -90,7 +90,10 @@ extern "C" {
  * the kernels skipped instead of touching memory out of bounds. */
 #define FKV_FAULT_SLOT_RANGE 1u   /* append/gather slot >= num_blocks*block_size */
 #define FKV_FAULT_BLOCK_RANGE 2u  /* block table / copy pair id outside [0, num_blocks) */
-#define FKV_FAULT_CTX_RANGE 4u    /* ctx_len > max_blocks_per_seq * block_size or < 0 */
+#define FKV_FAULT_CTX_RANGE 4u    /* ctx_len < 0, > max_blocks_per_seq * block_size, or
+                                     (decode attention) longer than the call's splits
+                                     hold, which max_ctx_len sized: the context is
+                                     clamped to that bound */
 #define FKV_FAULT_VALUE_RANGE 8u  /* Q8_0 append stored a block scale >= 512: its values can
                                      dequantise past 65504, the binary16 range of the
                                      matrix-core attention (storage itself is exact) */

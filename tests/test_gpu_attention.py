@@ -157,6 +157,32 @@ def test_context_outside_the_table_is_flagged(order, monkeypatch):
     pool.close()
 
 
+@pytest.mark.parametrize("dtype,order", [(1, "0"), (1, "1"), (1, "2"), (8, "2"), (0, "2")])
+def test_context_past_max_ctx_len_is_flagged(dtype, order, monkeypatch):
+    """A device context longer than the call's max_ctx_len (but inside the table row)
+    is clamped to what the launch's splits hold (512 here for every path: 64-token
+    splits on the matrix cores, 256-token partitions on F32) and raises
+    FKV_FAULT_CTX_RANGE; the merge reads only the workspace slots the launch was sized
+    for (the offending sequence is the last, whose slots end the workspace), and the
+    other sequences are unaffected."""
+    import ferrum_amd as fa
+    from oracle import ref
+    monkeypatch.setenv("FKV_ATTN_ORDER", order)
+    ctxs = [40, 300, 1100]
+    pool, layout, tab = _build(dtype, 128, 2, ctxs, seed=11, layers=1)
+    q = np.random.default_rng(3).standard_normal((3, 8, 128), dtype=np.float32)
+    import torch
+    out = torch.full(q.shape, 123.0, dtype=torch.float32, device="cuda")
+    pool.decode_attention(0, to_dev(q), out, to_dev(tab), to_dev(np.array(ctxs, np.int32)), 512)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert pool.take_fault_flags() & fa.FAULT_CTX_RANGE
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array([40, 300, 512]),
+                         fa.default_scale(128))
+    assert_close(got, want)
+    pool.close()
+
+
 @pytest.mark.parametrize("n_seqs", [300, 1100])
 def test_large_batches_match_oracle(n_seqs, monkeypatch):
     """300 sequences take the full-first order (three or fewer per thread of the
