@@ -41,6 +41,17 @@ HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, vendor figure
 METRIC = "paged decode-attn HBM GB/s (% of peak) + KV append tokens/s, 1xMI355X"
 
 
+def cpu_timed(fn, min_seconds, min_reps=1):
+    """Seconds per call of fn, repeated until min_seconds have passed (at least min_reps
+    calls), and the number of calls."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if reps >= min_reps and el >= min_seconds:
+            return el / reps, reps
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -59,6 +70,8 @@ def parse():
                     help="q8gemv: q/k/v and gate/up each in one fkv_gemm_q8_0_multi launch")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="CPU baseline budget: a third at 1 thread, the rest at --cpu-threads")
     ap.add_argument("--rope-dim", type=int, default=0,
                     help="> 0: time fkv_rope_append_decode_attention (q and k before RoPE)")
     ap.add_argument("--rope-theta", type=float, default=500000.0)
@@ -339,14 +352,13 @@ def cpu_baseline(args, pool, tables, ctx, q_layer, out_layer, layer, hq, hkv, d,
     threads = args.cpu_threads or min(16, os.cpu_count() or 1)
     e = elem_bytes(dtype)
     nbytes = attn_bytes(ctx, hq, hkv, d, e)
-    t0 = time.perf_counter()
-    o1 = ref.avx2_attention(lay, image, 0, qh, tab, ctx.astype(np.int32), scale, 1)
-    t1 = time.perf_counter() - t0
-    reps = 3
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        on = ref.avx2_attention(lay, image, 0, qh, tab, ctx.astype(np.int32), scale, threads)
-    tn = (time.perf_counter() - t0) / reps
+    ctx32 = ctx.astype(np.int32)
+    o1 = ref.avx2_attention(lay, image, 0, qh, tab, ctx32, scale, 1)
+    t1, reps1 = cpu_timed(lambda: ref.avx2_attention(lay, image, 0, qh, tab, ctx32, scale, 1),
+                          args.cpu_seconds / 3)
+    on = ref.avx2_attention(lay, image, 0, qh, tab, ctx32, scale, threads)
+    tn, reps = cpu_timed(lambda: ref.avx2_attention(lay, image, 0, qh, tab, ctx32, scale, threads),
+                         args.cpu_seconds * 2 / 3)
     assert np.array_equal(o1, on)
     err = np.abs(gpu_out.astype(np.float64) - o1)
     bad = int((err > 2e-3 + 1e-2 * np.abs(o1)).sum())
@@ -366,7 +378,8 @@ def cpu_baseline(args, pool, tables, ctx, q_layer, out_layer, layer, hq, hkv, d,
         "kind": "port",
         "sample": (f"layer {layer}, {len(seqs)} seqs ({int(ctx.sum())} tokens, "
                    f"{nbytes / 1e6:.1f} MB algorithmic): AVX2 restatement of llama.rs:220-247 "
-                   f"(per query head, no GQA reuse); {reps} reps at {threads} threads"),
+                   f"(per query head, no GQA reuse); {reps1} reps at 1 thread, {reps} reps at "
+                   f"{threads} threads"),
         "value_1thread": round(nbytes / t1 / 1e9, 3),
         "seconds_1thread": round(t1, 3),
         "seconds_threads": round(tn, 3),
@@ -801,16 +814,11 @@ def run_q8gemv(args, torch, fa, lib, dev):
             torch.cuda.synchronize()
             want = ref.q8_gemm(w, r, c, x_h[c], threads)
             mism += int((y.cpu().numpy().view(np.uint32) != want.view(np.uint32)).sum())
-        t0 = time.perf_counter()
-        for r, c, _, w in mats:
-            ref.q8_gemm(w, r, c, x_h[c], 1)
-        t1 = time.perf_counter() - t0
-        reps = 3
-        t0 = time.perf_counter()
-        for _ in range(reps):
+        def cpu_pass(nthr):
             for r, c, _, w in mats:
-                ref.q8_gemm(w, r, c, x_h[c], threads)
-        tn = (time.perf_counter() - t0) / reps
+                ref.q8_gemm(w, r, c, x_h[c], nthr)
+        t1, reps1 = cpu_timed(lambda: cpu_pass(1), args.cpu_seconds / 3)
+        tn, reps = cpu_timed(lambda: cpu_pass(threads), args.cpu_seconds * 2 / 3)
         res["cpu_baseline"] = {
             "value": round(nbytes / tn / 1e9, 3),
             "unit": "GB/s",
@@ -818,7 +826,7 @@ def run_q8gemv(args, torch, fa, lib, dev):
             "kind": "port",
             "sample": (f"layer 0's 7 projections ({nbytes / 1e6:.1f} MB), {T} token(s): the "
                        f"oracle's restatement of q8_dot.rs:35-109 / scalar.rs:191-204, "
-                       f"{reps} reps at {threads} threads"),
+                       f"{reps1} reps at 1 thread, {reps} reps at {threads} threads"),
             "value_1thread": round(nbytes / t1 / 1e9, 3),
             "seconds_1thread": round(t1, 3),
             "seconds_threads": round(tn, 3),

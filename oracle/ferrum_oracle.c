@@ -645,17 +645,20 @@ AVX2_FN static void decode_row_avx2(const fo_layout* l, int kv, const uint8_t* t
       _mm256_storeu_ps(dst + d, _mm256_cvtph_ps(_mm_loadu_si128(
                                     (const __m128i*)(src + (uint64_t)(d / 8) * l->block_size * 8))));
   } else if (l->dtype == 8) {
-    const uint8_t* qs = tile + (uint64_t)off * D;
     const uint8_t* sc = tile + (uint64_t)l->block_size * D + (uint64_t)off * (D / 32) * 2;
     for (uint32_t g = 0; g < D / 32; g++) {
+      /* the block's 32 quants, gathered from the tile's operand order (q8_index) into
+       * the contiguous block the reference's loop reads */
+      uint8_t qs[32];
+      for (uint32_t j = 0; j < 32; j++) qs[j] = tile[q8_index(l, kv, off, g * 32 + j)];
       float scale = fo_f16_to_f32((uint16_t)(sc[g * 2] | (sc[g * 2 + 1] << 8)));
       if (!isfinite(scale)) {
-        for (int j = 0; j < 32; j++) dst[g * 32 + j] = scale * (float)(int8_t)qs[g * 32 + j];
+        for (int j = 0; j < 32; j++) dst[g * 32 + j] = scale * (float)(int8_t)qs[j];
         continue;
       }
       __m256 sv = _mm256_set1_ps(scale);
       for (int j = 0; j < 32; j += 8) {
-        __m128i qv = _mm_loadl_epi64((const __m128i*)(qs + g * 32 + j));
+        __m128i qv = _mm_loadl_epi64((const __m128i*)(qs + j));
         __m256 qf = _mm256_cvtepi32_ps(_mm256_cvtepi8_epi32(qv));
         _mm256_storeu_ps(dst + g * 32 + j, _mm256_mul_ps(qf, sv));
       }

@@ -260,11 +260,14 @@ def test_attention_gqa_mapping_and_block_placement():
     assert np.array_equal(o[:, 1], o[:, 0]) and not np.array_equal(o[:, g], o[:, 0])
 
 
-def test_avx2_attention_within_tolerance_of_oracle():
+@pytest.mark.parametrize("dtype", [1, 8, 0])
+def test_avx2_attention_within_tolerance_of_oracle(dtype):
+    """The CPU baseline's AVX2 port reads every storage type's tiles as the scalar oracle
+    does (Q8_0: the quants' operand order inside the tile)."""
     if not ref.avx2_available():
         pytest.skip("host has no AVX2/FMA/F16C")
     ctxs = [3, 129, 700]
-    lay, pool, tab = _pool_with(1, 128, 2, ctxs, seed=9)
+    lay, pool, tab = _pool_with(dtype, 128, 2, ctxs, seed=9)
     q = np.random.default_rng(1).standard_normal((3, 8, 128)).astype(np.float32)
     c = np.array(ctxs, np.int32)
     a = ref.attention(lay, pool, 0, q, tab, c, 0.088388346)
