@@ -35,6 +35,9 @@ FAULT_BLOCK_RANGE = 2
 FAULT_CTX_RANGE = 4
 FAULT_VALUE_RANGE = 8
 
+# FKV_STATIC_SCRATCH_BYTES: the per-GPU static scratch of fkv_append_decode_attention_noalloc.
+STATIC_SCRATCH_BYTES = 32 << 20
+
 c_void_p = ctypes.c_void_p
 u32, u64, i32, i64 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32, ctypes.c_int64
 f32 = ctypes.c_float
@@ -111,6 +114,9 @@ SIGNATURES = {
     "fkv_append_decode_attention": (i32, [c_void_p, u32, u32, c_void_p, c_void_p, c_void_p,
                                           c_void_p, c_void_p, u32, c_void_p, u32, u32, f32,
                                           c_void_p, u64, c_void_p]),
+    "fkv_append_decode_attention_noalloc": (i32, [c_void_p, u32, u32, c_void_p, c_void_p,
+                                                  c_void_p, c_void_p, c_void_p, u32, c_void_p,
+                                                  u32, u32, f32, c_void_p]),
     "fkv_rope_append_decode_attention_workspace_size": (i32, [c_void_p, u32, u32, u32, P(u64)]),
     "fkv_rope_append_decode_attention": (i32, [c_void_p, u32, u32, u32, f32, c_void_p, c_void_p,
                                                c_void_p, c_void_p, c_void_p, u32, c_void_p, u32,

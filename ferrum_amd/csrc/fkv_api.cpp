@@ -17,6 +17,9 @@
 #include "../../include/ferrum_gguf.h"
 #include "fkv_internal.h"
 
+static_assert(FKV_STATIC_SCRATCH_BYTES == fkv::kStaticScratchBytes,
+              "the header states the static scratch size the library holds");
+
 namespace {
 
 thread_local std::string g_last_error;
@@ -138,6 +141,9 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
 
   DeviceGuard dg(c.device);
   if (!dg.ok) return fail(FKV_ERR_INTERNAL, "hip: cannot select device");
+  // Set-up of the no-allocation decode step on this device: the address of the
+  // device's static scratch, taken once per device with the device current.
+  FKV_HIP(fkv::static_scratch_setup(c.device), "static scratch address");
   auto* p = new fkv_pool();
   p->cfg = c;
   hipError_t e = hipMalloc((void**)&p->dev, total);
@@ -440,7 +446,7 @@ static int32_t decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads
                                 uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
                                 uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                                 void* workspace, uint64_t workspace_bytes, void* stream,
-                                const fkv::RopeTable* rope = nullptr) {
+                                const fkv::RopeTable* rope = nullptr, bool use_static = false) {
   if (!pool) return fail(FKV_ERR_INVALID, "null argument");
   if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
   int32_t st = check_attention(pool, n_heads, max_ctx_len);
@@ -457,6 +463,16 @@ static int32_t decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads
       rope    ? fkv::rope_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len)
       : k_new ? fkv::append_attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len)
               : fkv::attention_workspace_bytes(pool->geom, n_heads, n_seqs, max_ctx_len);
+  if (use_static) {
+    if (need > fkv::kStaticScratchBytes)
+      return fail(FKV_ERR_INVALID,
+                  "decode step needs " + std::to_string(need) +
+                      " bytes of scratch; the static scratch holds " +
+                      std::to_string(fkv::kStaticScratchBytes));
+    workspace = fkv::static_scratch(pool->cfg.device);
+    workspace_bytes = fkv::kStaticScratchBytes;
+    if (!workspace) return fail(FKV_ERR_INTERNAL, "static scratch is not set up on the device");
+  }
   if (workspace_bytes < need || (need && !workspace))
     return fail(FKV_ERR_INVALID, "attention workspace too small");
   FKV_HIP(fkv::launch_decode_attention(pool->geom, layer, n_heads, q, out, block_tables,
@@ -497,6 +513,19 @@ int32_t fkv_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_h
   return decode_attention(pool, layer, n_heads, k_new, v_new, q, out, block_tables,
                           max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale, workspace,
                           workspace_bytes, stream);
+}
+
+int32_t fkv_append_decode_attention_noalloc(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                                            const float* k_new, const float* v_new,
+                                            const float* q, float* out,
+                                            const int32_t* block_tables,
+                                            uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                                            uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                                            void* stream) {
+  if (n_seqs && (!k_new || !v_new)) return fail(FKV_ERR_INVALID, "null argument");
+  return decode_attention(pool, layer, n_heads, k_new, v_new, q, out, block_tables,
+                          max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale, nullptr, 0,
+                          stream, nullptr, true);
 }
 
 // Kernels::rope's checks, in its order (crates/kernels/src/validate.rs:64-87: theta,

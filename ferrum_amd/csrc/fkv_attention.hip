@@ -12,12 +12,46 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "fkv_device.h"
 #include "fkv_internal.h"
 
+// Scratch of fkv_append_decode_attention_noalloc: the split partials (and, for F32
+// storage, the derived slots) that the workspace argument holds for the other entry
+// points. Every GPU the library runs on holds its own copy until the process ends.
+// In host code `scratch` is only a stand-in for the symbol: host code passes the
+// per-device address from static_scratch_setup to kernels, never the name itself.
+// Nothing in it has to start at zero (every partial is written before it is read).
+static __device__ __align__(256) uint8_t scratch[fkv::kStaticScratchBytes];
+
 namespace fkv {
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxScratchDevices];
+}  // namespace
+
+hipError_t static_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[device] != nullptr) return hipSuccess;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (p == nullptr) return hipErrorInvalidSymbol;
+  g_scratch_addr[device] = p;
+  return hipSuccess;
+}
+
+void* static_scratch(int device) {
+  if (device < 0 || device >= kMaxScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_addr[device];
+}
+
 namespace {
 
 using namespace dev;

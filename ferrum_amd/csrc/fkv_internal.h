@@ -164,6 +164,14 @@ uint64_t attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_s
 uint64_t append_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
                                           uint32_t max_ctx_len);
 
+// Static scratch of the no-allocation decode step (fkv_attention.hip): one device
+// array of kStaticScratchBytes per GPU, held until the process ends. setup takes
+// its address on `device` (which must be current) once; static_scratch returns it
+// (nullptr before setup). Calls that use it on one GPU share it.
+constexpr uint64_t kStaticScratchBytes = 32ull << 20;
+hipError_t static_scratch_setup(int device);
+void* static_scratch(int device);
+
 // Q8_0 weight GEMV/GEMM (fkv_gemv.hip): y[t][r] = dot_q8_row_q8_act(w row r, x[t]
 // quantized) for t < n_tokens, r < rows; w rows of cols/32 34-byte blocks (w even,
 // x 4-byte aligned, cols % 32 == 0, gemv_lds_bytes(1, cols) <= kGemvMaxLds: the

@@ -350,6 +350,30 @@ class PagedKvPool:
             block_tables.shape[1], _dev(ctx_lens, torch.int32, "ctx_lens"), n_seqs, max_ctx_len,
             scale, ws_ptr, ws_bytes, _stream_ptr(stream)))
 
+    def append_decode_attention_noalloc(self, layer: int, k_new, v_new, q, out, block_tables,
+                                        ctx_lens, max_ctx_len: int,
+                                        scale: Optional[float] = None, stream=None) -> None:
+        """append_decode_attention with no workspace and no allocation: the split
+        partials go to the library's static per-GPU scratch (STATIC_SCRATCH_BYTES).
+        Calls that overlap on one GPU race on it; a step needing more is InvalidRequest."""
+        import torch
+        n_seqs, n_heads, d = q.shape
+        if d != self.config.head_dim or tuple(out.shape) != tuple(q.shape):
+            raise ValueError("q/out must be [n_seqs, n_heads, head_dim]")
+        kv_shape = (n_seqs, self.config.n_kv_heads, d)
+        if tuple(k_new.shape) != kv_shape or tuple(v_new.shape) != kv_shape:
+            raise ValueError("k_new/v_new must be [n_seqs, n_kv_heads, head_dim]")
+        if block_tables.shape[0] != n_seqs or ctx_lens.numel() != n_seqs:
+            raise ValueError("block_tables/ctx_lens must have one row per sequence")
+        if scale is None:
+            scale = default_scale(d)
+        check(self._lib.fkv_append_decode_attention_noalloc(
+            self._h, layer, n_heads, _dev(k_new, torch.float32, "k_new"),
+            _dev(v_new, torch.float32, "v_new"), _dev(q, torch.float32, "q"),
+            _dev(out, torch.float32, "out"), _dev(block_tables, torch.int32, "block_tables"),
+            block_tables.shape[1], _dev(ctx_lens, torch.int32, "ctx_lens"), n_seqs, max_ctx_len,
+            scale, _stream_ptr(stream)))
+
     def rope_append_decode_attention(self, layer: int, k_new, v_new, q, out, block_tables,
                                      ctx_lens, max_ctx_len: int, rope_dim: int, theta: float,
                                      scale: Optional[float] = None, workspace=None,

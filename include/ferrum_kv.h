@@ -295,6 +295,27 @@ int32_t fkv_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_h
                                     uint32_t n_seqs, uint32_t max_ctx_len, float scale,
                                     void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* fkv_append_decode_attention without a workspace argument, and allocating nothing
+ * (no hipMalloc, hipFree or allocating library call). It has no counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation). The split
+ * partials go to a static device array of FKV_STATIC_SCRATCH_BYTES per GPU, held
+ * until the process ends, whose address the library takes when a pool is created on
+ * that GPU. A call whose fkv_append_decode_attention_workspace_size() exceeds that
+ * is FKV_ERR_INVALID "decode step needs <n> bytes of scratch; the static scratch
+ * holds <max>", with nothing launched. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other threads, other pools) race and
+ * must be ordered by the caller. Nothing in the array needs to start at zero.
+ * Outputs and pool bytes are bit-identical to fkv_append_decode_attention's. */
+#define FKV_STATIC_SCRATCH_BYTES (32ull << 20)
+int32_t fkv_append_decode_attention_noalloc(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
+                                            const float* k_new, const float* v_new,
+                                            const float* q, float* out,
+                                            const int32_t* block_tables,
+                                            uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
+                                            uint32_t n_seqs, uint32_t max_ctx_len, float scale,
+                                            void* stream);
+
 /* fkv_append_decode_attention with q and k_new before RoPE: the layer's
  * Kernels::rope call (crates/model/src/llama.rs:207-216; scalar.rs:77-82,167-189,
  * math.rs:27-34), then its append and attention loop. Every query head of q[s]

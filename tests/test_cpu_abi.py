@@ -107,3 +107,10 @@ def test_error_classes_mirror_ferrum_error():
     assert fa.Unavailable("no free kv blocks").http_status == 503
     assert fa.InvalidRequest("x").http_status == 400
     assert issubclass(fa.CacheError, fa.FerrumError)
+
+
+def test_static_scratch_size_matches_the_header():
+    text = open(os.path.join(ROOT, "include", "ferrum_kv.h")).read()
+    m = re.search(r"#define FKV_STATIC_SCRATCH_BYTES \((\d+)ull << (\d+)\)", text)
+    assert m, "FKV_STATIC_SCRATCH_BYTES missing from ferrum_kv.h"
+    assert int(m.group(1)) << int(m.group(2)) == _lib.STATIC_SCRATCH_BYTES
