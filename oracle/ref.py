@@ -384,3 +384,72 @@ class DensePool:
 
     def uncommit_token(self, slot):
         return self._call(self._l.fo_dense_uncommit_token, slot) + (None,)
+
+
+# -- Llama::forward's KV sequence (crates/model/src/llama.rs:345-389) ----------------
+
+# FerrumError::Model (crates/core-types/src/error.rs:38-39, Display "model: {0}"): raised
+# by the model's own logic, never by a KV pool. Codes 0-6 are the pools' (FKV_* / fo_*).
+MODEL = 7
+
+
+def forward_kv(pool, slot, position0, tokens, fail=None):
+    """The KV calls `Llama::forward` makes (llama.rs:345-381) and its rewind on error
+    (`rewind_forward`, :383-389), with the model's arithmetic left out.
+
+    tokens[t][layer] = (k, v): the rows `append_layer` receives for token t
+    (post-RoPE K, llama.rs:207-218). fail = (t, layer, where) makes the model fail at
+    token t: where "embed" (embed_token, :367-370), "before" (an error of layer
+    `layer` before its append, e.g. a projection, :183-206) or "after" (after its
+    append, e.g. attn_output, :249-255). pool follows DensePool's protocol: every
+    method returns (code, message, value). Returns (code, message) of the call."""
+    code, msg, seq = pool.seq_len(slot)                                   # :354
+    if code:
+        return code, msg
+    if position0 != seq:                                                  # :355-360
+        return MODEL, f"model: position0 {position0} does not match sequence length {seq}"
+    for idx, layers in enumerate(tokens):                                 # :362
+        if position0 + idx > 0xFFFFFFFF:                                  # :363-365, no rewind
+            return MODEL, "model: position overflow"
+        if fail is not None and fail[0] == idx and fail[2] == "embed":    # :367-370
+            err = (MODEL, "model: injected failure")
+        else:
+            err = _forward_one_token_kv(pool, slot, idx, layers, fail)    # :371-376
+        if err[0]:
+            rw = rewind_forward(pool, slot, seq)
+            return rw if rw[0] else err
+    return 0, ""
+
+
+def _forward_one_token_kv(pool, slot, idx, layers, fail):
+    """forward_one_token's KV calls (llama.rs:150-293): abandon_partial (:166), one
+    append_layer per layer in order (:218), commit_token after the last (:291)."""
+    code, msg, _ = pool.abandon_partial(slot)
+    if code:
+        return code, msg
+    for layer, (k, v) in enumerate(layers):
+        if fail == (idx, layer, "before"):
+            return MODEL, "model: injected failure"
+        code, msg, _ = pool.append_layer(slot, layer, k, v)
+        if code:
+            return code, msg
+        if fail == (idx, layer, "after"):
+            return MODEL, "model: injected failure"
+    code, msg, _ = pool.commit_token(slot)
+    return code, msg
+
+
+def rewind_forward(pool, slot, committed):
+    """llama.rs:383-389: uncommit tokens until seq_len == committed, then drop the
+    partial token's layers."""
+    while True:
+        code, msg, n = pool.seq_len(slot)
+        if code:
+            return code, msg
+        if n <= committed:
+            break
+        code, msg, _ = pool.uncommit_token(slot)
+        if code:
+            return code, msg
+    code, msg, _ = pool.abandon_partial(slot)
+    return code, msg
