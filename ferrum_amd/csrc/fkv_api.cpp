@@ -151,8 +151,10 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
     delete p;
     return fail(FKV_ERR_UNAVAILABLE, "no device memory for kv pool");
   }
-  e = hipMalloc((void**)&p->fault, sizeof(uint32_t));
-  if (e == hipSuccess) e = hipMemset(p->fault, 0, sizeof(uint32_t));
+  // Two device words: the FKV_FAULT_* bits, and the sticky mark of a Q8_0 scale of 512
+  // or more (read by the attention kernels to pick their exact instance).
+  e = hipMalloc((void**)&p->fault, 2 * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemset(p->fault, 0, 2 * sizeof(uint32_t));
   if (e == hipSuccess && host_total) e = hipHostMalloc((void**)&p->host, host_total, hipHostMallocDefault);
   if (e != hipSuccess) {
     (void)hipFree(p->dev);
@@ -220,7 +222,30 @@ int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream) {
   FKV_HIP(fkv::launch_fill(pool->dev, byte, pool->geom.block_bytes * pool->geom.num_blocks,
                            (hipStream_t)stream),
           "fill");
+  if (pool->cfg.kv_dtype == FKV_DTYPE_Q8_0) {
+    // Every scale is now (byte << 8 | byte): the pool holds a scale of 512 or more
+    // exactly when that does (exponent bits 14 and 13 set), whatever it held before.
+    const uint8_t wide = (byte & 0x60u) == 0x60u ? 1 : 0;
+    FKV_HIP(fkv::launch_fill(pool->fault + 1, wide, sizeof(uint32_t), (hipStream_t)stream), "fill");
+  }
   return ok();
+}
+
+// Whether bytes [offset, offset + bytes) of a Q8_0 pool image (src) write a scale of
+// 512 or more. The f16 scales sit at the end of every tile ([B][D/32] little-endian
+// after the B*D quants), and whether one is that large depends on its high byte only
+// (exponent bits 14 and 13), so the high bytes the range covers decide.
+static bool q8_image_has_wide_scale(const fkv_pool* pool, uint64_t offset, uint64_t bytes,
+                                    const uint8_t* src) {
+  const uint64_t tile = pool->geom.tile_bytes;
+  const uint64_t q = (uint64_t)pool->cfg.block_size * pool->cfg.head_dim;
+  const uint64_t sc_end = q + q / 32 * 2;
+  const uint64_t end = offset + bytes;
+  for (uint64_t t0 = offset / tile * tile; t0 < end; t0 += tile) {
+    for (uint64_t x = t0 + q + 1; x < t0 + sc_end && x < end; x += 2)
+      if (x >= offset && (src[x - offset] & 0x60u) == 0x60u) return true;
+  }
+  return false;
 }
 
 static int32_t check_range(const fkv_pool* pool, uint64_t offset, uint64_t bytes) {
@@ -244,6 +269,11 @@ int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const v
   DeviceGuard dg(pool->cfg.device);
   FKV_HIP(hipDeviceSynchronize(), "synchronize");
   FKV_HIP(hipMemcpy(pool->dev + offset, host_src, bytes, hipMemcpyHostToDevice), "pool write");
+  if (pool->cfg.kv_dtype == FKV_DTYPE_Q8_0 &&
+      q8_image_has_wide_scale(pool, offset, bytes, (const uint8_t*)host_src)) {
+    const uint32_t one = 1;
+    FKV_HIP(hipMemcpy(pool->fault + 1, &one, sizeof one, hipMemcpyHostToDevice), "pool write");
+  }
   return ok();
 }
 

@@ -74,6 +74,7 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));  // bf16 MFMA operands
 
 constexpr int kHeads = 16;            // MFMA column count: query heads of one group
 constexpr float kRescaleLog2 = 8.0f;  // rescale when a score passes the reference max by 2^8
@@ -226,7 +227,7 @@ __device__ __forceinline__ void qk_block(const uint4 (&kr)[D / 32], const f16x8 
 // Lazy online softmax update and P (f16, the PV A operand) of one block.
 template <int D>
 __device__ __forceinline__ f16x4 softmax_block(const float (&s)[4], const Lane& ln,
-                                               Accum<D>& st) {
+                                               Accum<D>& st, float (&ef)[4]) {
   const float lmax = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), __builtin_fmaxf(s[2], s[3]));
   const bool bad =
       ln.real && (!(lmax <= st.m_ref + kRescaleLog2) || !__builtin_isfinite(st.m_ref));
@@ -258,9 +259,16 @@ __device__ __forceinline__ f16x4 softmax_block(const float (&s)[4], const Lane& 
     // all scores so far -inf/NaN: weight 0, but a NaN score stays NaN
     const float e = dead ? (sv != sv ? sv : 0.0f) : __builtin_amdgcn_exp2f(sv - st.m_ref);
     st.l_part += e;
+    ef[r] = e;
     pw[r] = (_Float16)e;
   }
   return pw;
+}
+template <int D>
+__device__ __forceinline__ f16x4 softmax_block(const float (&s)[4], const Lane& ln,
+                                               Accum<D>& st) {
+  float ef[4];
+  return softmax_block<D>(s, ln, st, ef);
 }
 
 // O += P . V for one block. Tokens at or past `end` carry weight 0 but their V
@@ -419,7 +427,143 @@ struct BlockRegs<kDtypeQ8, D> {
       vr[m].y = __builtin_bit_cast(uint32_t, i8_pair_to_f16(w, kSelHi) * s23);
     }
   }
+
+  // ---- exact path (qk_block_q8x / pv_block_q8x), for pools holding a scale >= 512 ----
+
+  // K operand of chunk c without its scale: the quants as binary16, exactly.
+  __device__ __forceinline__ uint4 k_quants_chunk(int c) const {
+    const uint32_t w0 = kq[c].x ^ 0x80808080u, w1 = kq[c].y ^ 0x80808080u;
+    return make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelLo)),
+                      __builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelHi)),
+                      __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelLo)),
+                      __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelHi)));
+  }
+  // Scale dwords of the QK output's tokens grp*4 + r: token t's are ks of lane t.
+  __device__ __forceinline__ void k_scales_out(const Lane& ln, uint32_t (&o)[4][NG / 2]) const {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+      for (int i = 0; i < NG / 2; i++) o[r][i] = (uint32_t)__shfl((int)ks[i], ln.grp * 4 + r);
+  }
+  // V quants of tile m (tokens grp*4 .. +3 of dim 16m + col) as bf16, exactly.
+  __device__ __forceinline__ s16x4 v_quants_bf16(int m) const {
+    const uint32_t w = vq[m];
+    const uint32_t f0 = __builtin_bit_cast(uint32_t, (float)(int8_t)(w & 0xffu));
+    const uint32_t f1 = __builtin_bit_cast(uint32_t, (float)(int8_t)((w >> 8) & 0xffu));
+    const uint32_t f2 = __builtin_bit_cast(uint32_t, (float)(int8_t)((w >> 16) & 0xffu));
+    const uint32_t f3 = __builtin_bit_cast(uint32_t, (float)(int8_t)(w >> 24));
+    const u32x2_t p = {__builtin_amdgcn_perm(f1, f0, 0x07060302u),
+                       __builtin_amdgcn_perm(f3, f2, 0x07060302u)};
+    return __builtin_bit_cast(s16x4, p);
+  }
+  // Scale (f16 bits) of V token grp*4 + r, group gg.
+  __device__ __forceinline__ uint32_t v_scale_bits(int r, int gg) const {
+    return (vs[r * NG / 2 + gg / 2] >> (16 * (gg & 1))) & 0xffffu;
+  }
+
+  // The fused append's token (quants q[kv][d], scales sc[kv][group]) in place of what
+  // was loaded for token off: lanes read it and keep it only if they hold token off.
+  __device__ __forceinline__ void patch_token(const Lane& ln, int off, const uint8_t (*q)[D],
+                                              const uint16_t (*sc)[D / 32]) {
+    const bool kme = ln.col == off, vme = ln.grp == off / 4;
+    const int r = off & 3, sh = 8 * r;
+#pragma unroll
+    for (int c = 0; c < NG; c++) {
+      const u32x2_t t = *(const u32x2_t*)&q[0][c * 32 + ln.grp * 8];
+      kq[c].x = kme ? t.x : kq[c].x;
+      kq[c].y = kme ? t.y : kq[c].y;
+    }
+#pragma unroll
+    for (int i = 0; i < NG / 2; i++) {
+      const uint32_t tk = *(const uint32_t*)&sc[0][2 * i], tv = *(const uint32_t*)&sc[1][2 * i];
+      ks[i] = kme ? tk : ks[i];
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++)
+        vs[rr * NG / 2 + i] = (vme && rr == r) ? tv : vs[rr * NG / 2 + i];
+    }
+#pragma unroll
+    for (int m = 0; m < D / 16; m++) {
+      const uint32_t t = (vq[m] & ~(0xffu << sh)) | ((uint32_t)q[1][m * 16 + ln.col] << sh);
+      vq[m] = vme ? t : vq[m];
+    }
+  }
 };
+
+// Exact Q8_0 scores of one block: the reference's dot over scale x quant in f32
+// (crates/kernels/src/scalar.rs:268-275), as sum over 32-dim chunks c of
+// scale[token][c] * (q . quants of chunk c). The quants are exact binary16 operands,
+// q is the hi + lo split of prep_q, and the scales multiply the chunk's f32 result, so
+// no value passes through the binary16 range whatever the scale.
+template <int D>
+__device__ __forceinline__ void qk_block_q8x(const BlockRegs<kDtypeQ8, D>& rg,
+                                             const f16x8 (&qh)[D / 32], const f16x8 (&ql)[D / 32],
+                                             float hscale, const Lane& ln, bool live, int32_t t0,
+                                             int32_t end, float (&s)[4]) {
+  constexpr int NG = D / 32;
+  uint32_t sc[4][NG / 2];
+  rg.k_scales_out(ln, sc);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // One chunk at a time (sched_barrier): the exact loop runs beside the fast loop's
+  // register allocation and must not hold every chunk's products at once.
+#pragma unroll
+  for (int c = 0; c < NG; c++) {
+    __builtin_amdgcn_sched_barrier(0);
+    const f16x8 kv = __builtin_bit_cast(f16x8, rg.k_quants_chunk(c));
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+    const f32x4 th = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qh[c], zero, 0, 0, 0);
+    const f32x4 tl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], zero, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float x = (tl[r] != tl[r] && th[r] == th[r]) ? th[r] : th[r] + tl[r];
+      const float d = f16_bits_to_f32((sc[r][c / 2] >> (16 * (c & 1))) & 0xffffu);
+      acc[r] = __builtin_fmaf(d, x, acc[r]);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const bool ok = ln.real && live && t0 + ln.grp * 4 + r < end;
+    s[r] = ok ? acc[r] * hscale : -__builtin_inff();
+  }
+}
+
+// Exact Q8_0 O += P . V of one block: per 32-dim group, the f32 softmax weight times
+// the token's V scale in f32, split into three bf16 parts (24 significant bits: the
+// f32 product to within its last bit, in bf16's range), against the quants as bf16
+// (exact). Tokens at or past `end` get weight 0 and their scales are not read.
+template <int D>
+__device__ __forceinline__ void pv_block_q8x(const BlockRegs<kDtypeQ8, D>& rg,
+                                             const float (&w)[4], const Lane& ln, int32_t t0,
+                                             int32_t end, Accum<D>& st) {
+  constexpr int NG = D / 32;
+  const int nvt = end - (t0 + ln.grp * 4);  // valid tokens among this lane's 4
+#pragma unroll
+  for (int gg = 0; gg < NG; gg++) {
+    __builtin_amdgcn_sched_barrier(0);
+    uint32_t part[3][4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      float y = r < nvt ? w[r] * f16_bits_to_f32(rg.v_scale_bits(r, gg)) : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 3; k++) {  // truncate to bf16, keep the exact remainder
+        const uint32_t yb = __builtin_bit_cast(uint32_t, y);
+        part[k][r] = yb >> 16;
+        y -= __builtin_bit_cast(float, yb & 0xffff0000u);
+      }
+    }
+    s16x4 p[3];
+#pragma unroll
+    for (int k = 0; k < 3; k++)
+      p[k] = __builtin_bit_cast(
+          s16x4, (u32x2_t){part[k][0] | (part[k][1] << 16), part[k][2] | (part[k][3] << 16)});
+#pragma unroll
+    for (int m = 2 * gg; m < 2 * gg + 2; m++) {
+      const s16x4 vb = rg.v_quants_bf16(m);
+#pragma unroll
+      for (int k = 0; k < 3; k++)
+        st.acc[m] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p[k], vb, st.acc[m], 0, 0, 0);
+    }
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Persistent streaming kernel
@@ -751,6 +895,7 @@ struct OrderedItem {
   int32_t seq;    // < 0: past the list
   int32_t split;
   int32_t ctx;    // ctx_lens[seq] as read (unclamped)
+  int32_t wide;   // *wide_word as thread 0 read it (0 without one)
 };
 
 // Unit u of the longest-first list. Every thread of the workgroup calls this with
@@ -758,7 +903,7 @@ struct OrderedItem {
 __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_lens,
                                     uint32_t n_seqs, int32_t cap, int32_t split_tokens,
                                     uint32_t order, int32_t* s_scan, int32_t* s_key,
-                                    int32_t* s_res) {
+                                    int32_t* s_res, const uint32_t* wide_word) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = (int)((n_seqs + 255u) / 256u);  // <= 4
   int32_t raw[4], full[4], part[4];
@@ -796,7 +941,10 @@ __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_
     s_scan[wave] = fin;
     s_scan[kAttnWaves + wave] = pin;
   }
-  if (tid == 0) s_res[0] = -1;
+  if (tid == 0) {
+    s_res[0] = -1;
+    s_res[3] = wide_word ? (int32_t)__atomic_load_n(wide_word, __ATOMIC_RELAXED) : 0;
+  }
   __syncthreads();
   int32_t fpre = fin - fsum, ppre = pin - psum, F = 0, P = 0;
 #pragma unroll
@@ -848,7 +996,7 @@ __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_
     }
   }
   __syncthreads();
-  return OrderedItem{s_res[0], s_res[1], s_res[2]};
+  return OrderedItem{s_res[0], s_res[1], s_res[2], s_res[3]};
 }
 
 // Waves per SIMD the split kernel is compiled for (the VGPR budget: 4 -> 128).
@@ -856,9 +1004,16 @@ __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_
 #define FKV_MFMA_WAVES_PER_EU 3
 #endif
 
-template <int DT, int D, int NBUF, bool ROPE>
+// EXACT (Q8_0 only): the instance for pools holding scales of 512 or more. Every Q8_0
+// call launches the fast instance and then this one over the same grid; each
+// workgroup of both reads the pool's sticky word once. The fast instance computes
+// when it is clear (a workgroup whose appended token has such a scale sets it), the
+// exact one when it is set, redoing every output and partial without binary16
+// dequantised operands (qk_block_q8x, pv_block_q8x). Its own register allocation
+// keeps the fast instance's at three waves per SIMD.
+template <int DT, int D, int NBUF, bool ROPE, bool EXACT>
 __global__ void __launch_bounds__(256)
-__attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
+__attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
     const int32_t* __restrict__ ctx_lens, uint32_t n_seqs, uint32_t max_splits,
@@ -874,21 +1029,33 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   __shared__ uint8_t s_appq[2][D];                 // fused Q8_0 append: quants
   __shared__ uint16_t s_apps[2][D / 32];           // and scales
   __shared__ int32_t s_ord[2 * kAttnWaves + 4 + kOrderSortSeqs];  // work order: scans, item, keys
+  __shared__ uint32_t s_wide;  // the pool's sticky word as this workgroup read it
 
   // the work list and the split clamp share this bound, so the list never holds more
   // items than the grid has workgroups
   const int32_t cap = dev::split_ctx_cap(max_blocks, B, max_splits, (uint32_t)split_tokens);
+  // The exact instance has work only over a pool marked wide; the word cannot change
+  // during its launch (only fast instances set it), so each wave reads it alone.
+  if constexpr (EXACT) {
+    if (!pool_has_wide_scales(g.fault)) return;
+  }
   const uint32_t kvh = blockIdx.x % g.n_kv_heads;
   uint32_t seq;
   int32_t split, ctx = 0;
+  // Fast Q8_0 instance: whether the pool has held a scale of 512 or more, read once
+  // per workgroup (a fast workgroup appending such a token sets the word during the
+  // launch, and the waves of one workgroup must agree before the merge barrier).
+  bool pool_wide = false;
   if (order != kOrderGrid) {
-    const OrderedItem it =
-        ordered_item(blockIdx.x / g.n_kv_heads, ctx_lens, n_seqs, cap, split_tokens, order,
-                     s_ord, s_ord + 2 * kAttnWaves + 4, s_ord + 2 * kAttnWaves);
+    const OrderedItem it = ordered_item(
+        blockIdx.x / g.n_kv_heads, ctx_lens, n_seqs, cap, split_tokens, order, s_ord,
+        s_ord + 2 * kAttnWaves + 4, s_ord + 2 * kAttnWaves,
+        DT == kDtypeQ8 && !EXACT ? g.fault + 1 : nullptr);
     if (it.seq < 0) return;
     seq = (uint32_t)it.seq;
     split = it.split;
     ctx = it.ctx;
+    pool_wide = it.wide != 0;
   } else {
     const uint32_t segs = n_seqs * g.n_kv_heads;
     seq = (blockIdx.x % segs) / g.n_kv_heads;
@@ -917,6 +1084,13 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     tabv = j >= 0 ? table[j] : 0;
   };
   load_tab(0);
+  if constexpr (DT == kDtypeQ8 && !EXACT) {
+    if (order == kOrderGrid) {  // no ordering pass to carry the word: one barrier
+      if (threadIdx.x == 0) s_wide = __atomic_load_n(g.fault + 1, __ATOMIC_RELAXED);
+      __syncthreads();
+      pool_wide = s_wide != 0;
+    }
+  }
 
   if (order == kOrderGrid) ctx = ctx_lens[seq];
   const bool ctx_ok = ctx >= 0 && ctx <= cap;
@@ -952,7 +1126,7 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   // what it loaded, and stores the encoded token to the pool. No other workgroup
   // reads the position, and this one never reads back what it stores, so the
   // stores need no ordering.
-  const bool app = (DT == kDtypeF16 || DT == kDtypeQ8) && k_new != nullptr &&
+  const bool app = (DT == kDtypeF16 || DT == kDtypeQ8) && !EXACT && k_new != nullptr &&
                    split == nsplits - 1 && ctx > 0 && ctx_ok;
   const int32_t app_pos = ctx - 1;
   const int32_t app_lb = app ? app_pos / B - blk0 : -1;  // block of the split
@@ -996,11 +1170,15 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
         if ((ln.lane & 31) == 0) {
           s_apps[0][dd / 32] = (uint16_t)ksc;
           s_apps[1][dd / 32] = (uint16_t)vsc;
-          // A finite scale >= 512 can dequantise past 65504 (append_q8_kernel's rule).
-          if (((ksc & 0x7fffu) >= 0x6000u && (ksc & 0x7fffu) < 0x7c00u) ||
-              ((vsc & 0x7fffu) >= 0x6000u && (vsc & 0x7fffu) < 0x7c00u))
+          // a scale past the binary16 range (append_q8_kernel's rule)
+          if ((ksc & 0x7c00u) == 0x7c00u || (vsc & 0x7c00u) == 0x7c00u)
             raise_fault(g.fault, kFaultRange);
         }
+        // A scale of 512 or more marks the pool (q8_wide_scale): the exact instance,
+        // launched after this one, then computes every output of the call.
+        if (__builtin_amdgcn_ballot_w64(q8_wide_scale(ksc) || q8_wide_scale(vsc)) != 0 &&
+            ln.lane == 0)
+          mark_wide(g.fault);
       } else {
         s_app[0][dd] = (uint16_t)encode_f16(kv, g.rounding);
         s_app[1][dd] = (uint16_t)encode_f16(vv, g.rounding);
@@ -1010,6 +1188,10 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   if constexpr (!ROPE) {
     if (app_wave) encode_app();
   }
+  // Q8_0 fast instance over a pool marked wide: the exact instance computes this
+  // workgroup's outputs; only the appended token is stored here.
+  bool store_only = false;
+  if constexpr (DT == kDtypeQ8 && !EXACT) store_only = pool_wide;
 
   Accum<D> st;
   st.reset();
@@ -1035,26 +1217,28 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
     blive[b] = okb;
     bid[b] = okb ? p : 0;
   };
+  // The Q8_0 token's quants and scales to the pool (the whole appending wave).
+  auto store_q8_token = [&](int b) {
+    uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
+    uint8_t* vt = tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
+#pragma unroll
+    for (int i = 0; i < D / 64; i++) {
+      const int dd = i * 64 + ln.lane;
+      kt[q8_quant_offset(0, app_off, dd, D)] = s_appq[0][dd];
+      vt[q8_quant_offset(1, app_off, dd, D)] = s_appq[1][dd];
+    }
+    if (ln.lane < D / 32) {
+      ((uint16_t*)(kt + B * D))[app_off * (D / 32) + ln.lane] = s_apps[0][ln.lane];
+      ((uint16_t*)(vt + B * D))[app_off * (D / 32) + ln.lane] = s_apps[1][ln.lane];
+    }
+  };
   auto process = [&](int t, int b) {
     const bool live = blive[b];
     const bool refill = t + NBUF < nt;
     const int32_t t0 = s0 + (wave + kAttnWaves * t) * B;  // first token of the block
     const bool patch = app_wave && t == app_t && live;
     if constexpr (DT == kDtypeQ8) {
-      if (patch) {  // the token's quants and scales to the pool (the whole wave)
-        uint8_t* kt = tile_ptr(g, (uint64_t)bid[b], layer, 0, kvh);
-        uint8_t* vt = tile_ptr(g, (uint64_t)bid[b], layer, 1, kvh);
-#pragma unroll
-        for (int i = 0; i < D / 64; i++) {
-          const int dd = i * 64 + ln.lane;
-          kt[q8_quant_offset(0, app_off, dd, D)] = s_appq[0][dd];
-          vt[q8_quant_offset(1, app_off, dd, D)] = s_appq[1][dd];
-        }
-        if (ln.lane < D / 32) {
-          ((uint16_t*)(kt + B * D))[app_off * (D / 32) + ln.lane] = s_apps[0][ln.lane];
-          ((uint16_t*)(vt + B * D))[app_off * (D / 32) + ln.lane] = s_apps[1][ln.lane];
-        }
-      }
+      if (patch) store_q8_token(b);
     }
     // F16 operands are the ring registers themselves; Q8_0 ones are dequantised.
     uint4 kdq[DT == kDtypeF16 ? 1 : NC];
@@ -1125,10 +1309,35 @@ __attribute__((amdgpu_waves_per_eu(FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
   // q is read after the first K/V loads are issued, so its latency overlaps theirs.
   prep_q<D, ROPE>(q + ((uint64_t)seq * n_heads + (uint64_t)kvh * G + (ln.real ? ln.col : 0)) * D,
                   ln, scale * kLog2e, qh, ql, hscale, rsin, rcos, rope.rope_dim);
-  for (int t = 0; t < nt; t += NBUF) {
+  if constexpr (DT == kDtypeQ8 && EXACT) {
+    // One block at a time: the ring's single buffer, refilled after each block.
+    for (int t = 0; t < nt; t++) {
+      if (t > 0) {
+        fetch(t, 0);
+        ring[0].load_k_tile(tile_ptr(g, (uint64_t)bid[0], layer, 0, kvh), ln);
+        ring[0].load_v_tile(tile_ptr(g, (uint64_t)bid[0], layer, 1, kvh), ln);
+      }
+      const int32_t t0 = s0 + (wave + kAttnWaves * t) * B;
+      float sc[4], w[4];
+      qk_block_q8x<D>(ring[0], qh, ql, hscale, ln, blive[0], t0, s1, sc);
+      (void)softmax_block<D>(sc, ln, st, w);
+      if (blive[0]) pv_block_q8x<D>(ring[0], w, ln, t0, s1, st);
+    }
+  } else if (store_only) {
+    if (app_wave && app_t < nt) {  // the block holding the token: the wave's block app_t
+      if (app_t >= 64) load_tab(app_t & ~63);
+      const int32_t p = __builtin_amdgcn_readlane(tabv, app_t & 63);
+      bid[0] = p;
+      if (p >= 0 && (uint64_t)p < g.num_blocks) store_q8_token(0);
+      else if (ln.lane == 0) raise_fault(g.fault, kFaultBlock);
+    }
+    return;  // the whole workgroup (pool_wide is the same in all its waves)
+  } else {
+    for (int t = 0; t < nt; t += NBUF) {
 #pragma unroll
-    for (int b = 0; b < NBUF; b++)
-      if (t + b < nt) process(t + b, b);
+      for (int b = 0; b < NBUF; b++)
+        if (t + b < nt) process(t + b, b);
+    }
   }
 
   // ---- per wave: l over the 4 lanes of each head; O rows to LDS.
@@ -1552,23 +1761,32 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
   const bool roped = rope != nullptr && rope->rope_dim > 0;
   RopeTable rt{};
   if (roped) rt = *rope;
-#define FKV_LAUNCH_MFMA(DT_, D_, R_)                                                             \
-  attn_mfma_kernel<DT_, D_, NBUF, R_><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
-                                                           max_blocks, ctx_lens, n_seqs,         \
-                                                           max_splits, st, order, scale, ws_o,   \
-                                                           ws_ml, k_new, v_new, rt)
+#define FKV_LAUNCH_MFMA(DT_, D_, R_, X_)                                                         \
+  attn_mfma_kernel<DT_, D_, NBUF, R_, X_><<<grid, 256, 0, s>>>(                                  \
+      g, layer, n_heads, G, q, out, tables, max_blocks, ctx_lens, n_seqs, max_splits, st, order, \
+      scale, ws_o, ws_ml, k_new, v_new, rt)
+  // Q8_0: the fast instance, then the exact one (each workgroup of which exits at once
+  // unless the pool's sticky word says it holds a scale of 512 or more).
   if (g.dtype == kDtypeQ8 && roped) {
-    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, true);
-    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, true);
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, true, false);
+    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, true, false);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, true, true);
+    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, true, true);
   } else if (g.dtype == kDtypeQ8) {
-    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, false);
-    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, false);
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, false, false);
+    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, false, false);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, false, true);
+    else FKV_LAUNCH_MFMA(kDtypeQ8, 64, false, true);
   } else if (roped) {
-    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128, true);
-    else FKV_LAUNCH_MFMA(kDtypeF16, 64, true);
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128, true, false);
+    else FKV_LAUNCH_MFMA(kDtypeF16, 64, true, false);
   } else {
-    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128, false);
-    else FKV_LAUNCH_MFMA(kDtypeF16, 64, false);
+    if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeF16, 128, false, false);
+    else FKV_LAUNCH_MFMA(kDtypeF16, 64, false, false);
   }
 #undef FKV_LAUNCH_MFMA
   return hipGetLastError();

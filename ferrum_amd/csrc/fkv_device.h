@@ -32,6 +32,18 @@ __device__ __forceinline__ void raise_fault(uint32_t* f, uint32_t bit) {
   atomicOr(f, bit);
 }
 
+// Q8_0 scales of 512 or more (binary16 exponent bits 14 and 13 set: 512 <= |s|,
+// inf, NaN): scale x quant of such a block can pass 65504, the binary16 range of the
+// fast attention operands. The pool's second fault word records, sticky, that one was
+// stored; attention over such a pool takes its exact loop.
+__device__ __forceinline__ bool q8_wide_scale(uint32_t bits) { return (bits & 0x6000u) == 0x6000u; }
+__device__ __forceinline__ void mark_wide(uint32_t* fault) {
+  if (__atomic_load_n(fault + 1, __ATOMIC_RELAXED) == 0u) atomicOr(fault + 1, 1u);
+}
+__device__ __forceinline__ bool pool_has_wide_scales(const uint32_t* fault) {
+  return __builtin_amdgcn_readfirstlane(__atomic_load_n(fault + 1, __ATOMIC_RELAXED)) != 0;
+}
+
 // 16-byte load of K/V bytes that are read once per launch: the nontemporal hint
 // keeps the stream from evicting reusable lines (block tables, q) and measured
 // 7.1 TB/s against 6.3 TB/s for plain loads in a read-only sweep on MI355X.

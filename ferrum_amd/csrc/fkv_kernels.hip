@@ -219,9 +219,13 @@ __global__ void __launch_bounds__(256) append_q8_kernel(Geom g, uint32_t layer,
         tile[q8_quant_offset(1, off, c * 32u + j, D)] = (uint8_t)(q[j / 4] >> (8 * (j % 4)));
     }
     ((uint16_t*)(tile + (uint64_t)B * D))[off * cpr + c] = (uint16_t)sc;
-    // A finite scale >= 512 can dequantise past 65504, beyond the binary16
-    // operands of the matrix-core attention: stored exactly, but flagged.
-    if ((sc & 0x7fffu) >= 0x6000u && (sc & 0x7fffu) < 0x7c00u) raise_fault(g.fault, kFaultRange);
+    // A scale of 512 or more sends later attention over the pool to its exact loop;
+    // one past the binary16 range (|x| >= 65520 * 127) is stored as +-inf, as the
+    // reference's encoder stores it, and flagged.
+    if (q8_wide_scale(sc)) {
+      mark_wide(g.fault);
+      if ((sc & 0x7c00u) == 0x7c00u) raise_fault(g.fault, kFaultRange);
+    }
   }
 }
 

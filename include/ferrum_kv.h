@@ -94,9 +94,10 @@ extern "C" {
                                      (decode attention) longer than the call's splits
                                      hold, which max_ctx_len sized: the context is
                                      clamped to that bound */
-#define FKV_FAULT_VALUE_RANGE 8u  /* Q8_0 append stored a block scale >= 512: its values can
-                                     dequantise past 65504, the binary16 range of the
-                                     matrix-core attention (storage itself is exact) */
+#define FKV_FAULT_VALUE_RANGE 8u  /* Q8_0 append stored a block scale past the binary16
+                                     range (a 32-value run with |x| >= 65520 * 127): the
+                                     scale is +-inf, as the reference's encoder stores it,
+                                     and attention over it is non-finite */
 
 /* Version of this ABI; equals FKV_ABI_VERSION of the header the library was built with. */
 int32_t fkv_abi_version(void);
@@ -253,8 +254,12 @@ int32_t fkv_swap_in(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void
  * q, out: device f32 [n_seqs][n_heads][head_dim]. block_tables: device int32
  * [n_seqs][max_blocks_per_seq]; ctx_lens: device int32 [n_seqs], each
  * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, and g <= 16 (F16 and
- * Q8_0, matrix cores; Q8_0 values are dequantised to binary16 operands, see
- * FKV_FAULT_VALUE_RANGE) or g in {1,2,4,8,16} (F32).
+ * Q8_0, matrix cores) or g in {1,2,4,8,16} (F32). Q8_0 follows the reference's f32
+ * dequantisation (kernels/src/scalar.rs:268-275) for every finite scale: while the
+ * pool has never held a scale of 512 or more, operands are scale x quant in
+ * binary16 (exact to one rounding); once it has (the append, fill or write that put
+ * one there marks the pool), a second kernel instance takes the quants as exact
+ * operands and applies the scales in f32.
  * workspace: device scratch of fkv_decode_attention_workspace_size() bytes
  * holding the split partials (running max, sum and unnormalised output per
  * query head and context split) that the merge pass reads; it may be NULL when
@@ -281,7 +286,9 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
  * fkv_copy_blocks first if it is shared). For F16 and Q8_0 storage this is one
  * kernel launch: the workgroup that reads the sequence's last context split
  * encodes the token (Q8_0: quantised as fkv_append does, FKV_FAULT_VALUE_RANGE
- * included), stores it and uses its encoded values in place of what it loaded.
+ * included), stores it and uses its encoded values in place of what it loaded; a
+ * Q8_0 token with a scale of 512 or more marks the pool, and the exact instance
+ * that every Q8_0 call launches after the first recomputes the call's outputs.
  * F32 storage uses an append launch first.
  * workspace: fkv_append_decode_attention_workspace_size() bytes, same rules as
  * the decode-attention workspace. */

@@ -263,27 +263,3 @@ def test_attention_non_finite_scores(ctx, dtype):
     q2[0, :, 0] = -1.0
     got2 = _run(pool, 0, q2, tab, [ctx])
     assert np.all(got2 == 0.0)
-
-
-def test_q8_scale_past_binary16_range_is_flagged():
-    """A Q8_0 block whose scale is >= 512 (values up to 127 * scale > 65504) is stored
-    exactly, but the append raises FKV_FAULT_VALUE_RANGE: the matrix-core attention
-    reads binary16 operands. Ordinary values raise nothing."""
-    import ferrum_amd as fa
-    import torch
-    pool, layout = make_pools(1, 1, 64, 2, dtype=8)
-    pool.fill(0)
-    k = np.ones((2, 1, 64), np.float32)
-    v = np.ones((2, 1, 64), np.float32)
-    slots = np.array([0, 1], np.int64)
-    pool.append(0, to_dev(k), to_dev(v), to_dev(slots))
-    torch.cuda.synchronize()
-    assert pool.take_fault_flags() == 0
-    v[1, 0, 40] = 70000.0  # scale = 70000 / 127 > 512
-    pool.append(0, to_dev(k), to_dev(v), to_dev(slots))
-    torch.cuda.synchronize()
-    assert pool.take_fault_flags() == fa.FAULT_VALUE_RANGE
-    from oracle import ref
-    want = ref.new_pool(layout)
-    ref.append(layout, want, 0, k, v, slots)
-    assert np.array_equal(pool.read(), want)
