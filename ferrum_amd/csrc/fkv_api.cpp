@@ -151,10 +151,12 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
     delete p;
     return fail(FKV_ERR_UNAVAILABLE, "no device memory for kv pool");
   }
-  // Two device words: the FKV_FAULT_* bits, and the sticky mark of a Q8_0 scale of 512
-  // or more (read by the attention kernels to pick their exact instance).
-  e = hipMalloc((void**)&p->fault, 2 * sizeof(uint32_t));
-  if (e == hipSuccess) e = hipMemset(p->fault, 0, 2 * sizeof(uint32_t));
+  // Four device words: the FKV_FAULT_* bits; the sticky mark of a Q8_0 scale of 512 or
+  // more (read by the attention kernels to pick their exact instance); the chunked
+  // prefill's mark of a non-finite V past a causal end and its workgroup count (the
+  // leak-safe instance clears both).
+  e = hipMalloc((void**)&p->fault, 4 * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemset(p->fault, 0, 4 * sizeof(uint32_t));
   if (e == hipSuccess && host_total) e = hipHostMalloc((void**)&p->host, host_total, hipHostMallocDefault);
   if (e != hipSuccess) {
     (void)hipFree(p->dev);
@@ -227,8 +229,29 @@ int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream) {
     // exactly when that does (exponent bits 14 and 13 set), whatever it held before.
     const uint8_t wide = (byte & 0x60u) == 0x60u ? 1 : 0;
     FKV_HIP(fkv::launch_fill(pool->fault + 1, wide, sizeof(uint32_t), (hipStream_t)stream), "fill");
+  } else if (pool->cfg.kv_dtype == FKV_DTYPE_F16) {
+    // Every V value is now (byte << 8 | byte): Inf/NaN exactly when its exponent bits are.
+    const uint8_t nonfinite = (byte & 0x7cu) == 0x7cu ? 1 : 0;
+    FKV_HIP(fkv::launch_fill(pool->fault + 2, nonfinite, sizeof(uint32_t), (hipStream_t)stream),
+            "fill");
   }
   return ok();
+}
+
+// Whether bytes [offset, offset + bytes) of an F16 pool image (src) write an Inf or NaN
+// into a V tile (tile i of the pool is V when (i / n_kv_heads) is odd; every 16-bit
+// word of it is a value, little-endian, so its high byte decides).
+static bool f16_image_has_nonfinite_v(const fkv_pool* pool, uint64_t offset, uint64_t bytes,
+                                      const uint8_t* src) {
+  const uint64_t tile = pool->geom.tile_bytes, hkv = pool->cfg.n_kv_heads;
+  const uint64_t end = offset + bytes;
+  for (uint64_t t = offset / tile; t * tile < end; t++) {
+    if ((t / hkv) % 2 == 0) continue;  // a K tile
+    const uint64_t a = std::max(t * tile, offset), b = std::min((t + 1) * tile, end);
+    for (uint64_t x = a + ((a - t * tile) % 2 == 0 ? 1 : 0); x < b; x += 2)
+      if ((src[x - offset] & 0x7cu) == 0x7cu) return true;
+  }
+  return false;
 }
 
 // Whether bytes [offset, offset + bytes) of a Q8_0 pool image (src) write a scale of
@@ -269,10 +292,15 @@ int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const v
   DeviceGuard dg(pool->cfg.device);
   FKV_HIP(hipDeviceSynchronize(), "synchronize");
   FKV_HIP(hipMemcpy(pool->dev + offset, host_src, bytes, hipMemcpyHostToDevice), "pool write");
-  if (pool->cfg.kv_dtype == FKV_DTYPE_Q8_0 &&
-      q8_image_has_wide_scale(pool, offset, bytes, (const uint8_t*)host_src)) {
+  const uint8_t* img = (const uint8_t*)host_src;
+  const int word = pool->cfg.kv_dtype == FKV_DTYPE_Q8_0 &&
+                           q8_image_has_wide_scale(pool, offset, bytes, img) ? 1
+                   : pool->cfg.kv_dtype == FKV_DTYPE_F16 &&
+                           f16_image_has_nonfinite_v(pool, offset, bytes, img) ? 2
+                                                                                : 0;
+  if (word) {
     const uint32_t one = 1;
-    FKV_HIP(hipMemcpy(pool->fault + 1, &one, sizeof one, hipMemcpyHostToDevice), "pool write");
+    FKV_HIP(hipMemcpy(pool->fault + word, &one, sizeof one, hipMemcpyHostToDevice), "pool write");
   }
   return ok();
 }
@@ -611,8 +639,8 @@ int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, 
   if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
   int32_t st = check_attention(pool, n_heads, max_ctx_len);
   if (st) return st;
-  if (pool->cfg.kv_dtype != FKV_DTYPE_F16)
-    return fail(FKV_ERR_KERNEL, "prefill attention needs f16 kv");
+  if (pool->cfg.kv_dtype != FKV_DTYPE_F16 && pool->cfg.kv_dtype != FKV_DTYPE_Q8_0)
+    return fail(FKV_ERR_KERNEL, "prefill attention needs f16 or q8_0 kv");
   if (n_seqs == 0 || max_q_len == 0) return ok();
   if (!q || !out || !block_tables || !ctx_lens || !q_lens || !q_offsets)
     return fail(FKV_ERR_INVALID, "null argument");

@@ -52,13 +52,6 @@
 #include "fkv_device.h"
 #include "fkv_internal.h"
 
-// K/V blocks in flight (register stages) of the chunked-prefill kernel. One
-// measured fastest on MI355X: deeper rings cost a wave per SIMD of occupancy and
-// the kernel is bound by issue, not by memory latency.
-#ifndef FKV_PREFILL_STAGES
-#define FKV_PREFILL_STAGES 1
-#endif
-
 // Blocks in flight per wave (the load ring depth) of attn_mfma_kernel.
 #ifndef FKV_MFMA_RING
 #define FKV_MFMA_RING 1
@@ -274,8 +267,8 @@ __device__ __forceinline__ f16x4 softmax_block(const float (&s)[4], const Lane& 
 // O += P . V for one block. Tokens at or past `end` carry weight 0 but their V
 // bytes may be anything (0 * NaN = NaN), so a partial block zeroes them first.
 template <int D>
-__device__ __forceinline__ void pv_block(u32x2_t (&vr)[D / 16], f16x4 pw, const Lane& ln,
-                                         int32_t t0, int32_t end, Accum<D>& st) {
+__device__ __forceinline__ void mask_v_tail(u32x2_t (&vr)[D / 16], const Lane& ln, int32_t t0,
+                                            int32_t end) {
   if (t0 + B > end) {
     const int nv = end - (t0 + ln.grp * 4);  // valid tokens among this lane's 4
     const uint32_t m0 = nv >= 2 ? 0xffffffffu : (nv == 1 ? 0x0000ffffu : 0u);
@@ -286,6 +279,12 @@ __device__ __forceinline__ void pv_block(u32x2_t (&vr)[D / 16], f16x4 pw, const 
       vr[m].y &= m1;
     }
   }
+}
+
+template <int D>
+__device__ __forceinline__ void pv_block(u32x2_t (&vr)[D / 16], f16x4 pw, const Lane& ln,
+                                         int32_t t0, int32_t end, Accum<D>& st) {
+  mask_v_tail<D>(vr, ln, t0, end);
 #pragma unroll
   for (int m = 0; m < D / 16; m++)
     st.acc[m] = __builtin_amdgcn_mfma_f32_16x16x16f16(pw, __builtin_bit_cast(f16x4, vr[m]),
@@ -362,28 +361,32 @@ struct BlockRegs<kDtypeQ8, D> {
   uint32_t ks[NG / 2];  // the NG scales of token col
   uint32_t vq[D / 16];  // tile m: tokens grp*4 .. +3 of dim 16m + col
   uint32_t vs[2 * NG];  // the scales of tokens grp*4 .. +3: [4][NG]
+  // LDS: the tile is a byte copy staged in shared memory (chunked prefill), read with
+  // ordinary loads; otherwise it is in the pool, read with the streaming hint.
+  template <bool LDS = false>
   __device__ __forceinline__ void load_k_tile(const uint8_t* kt, const Lane& ln) {
     const uint8_t* lp = kt + (uint64_t)ln.lane * 16;
 #pragma unroll
     for (int p = 0; p < NG / 2; p++) {  // chunks 2p, 2p + 1
-      const uint4 w = load_stream16(lp + p * 1024);
+      const uint4 w = LDS ? *(const uint4*)(lp + p * 1024) : load_stream16(lp + p * 1024);
       kq[2 * p] = (u32x2_t){w.x, w.y};
       kq[2 * p + 1] = (u32x2_t){w.z, w.w};
     }
     const uint8_t* sc = kt + (uint64_t)B * D + (uint64_t)ln.col * NG * 2;
     if constexpr (NG == 4) {
-      const u32x2_t w = load_stream8(sc);
+      const u32x2_t w = LDS ? *(const u32x2_t*)sc : load_stream8(sc);
       ks[0] = w.x;
       ks[1] = w.y;
     } else {
-      ks[0] = __builtin_nontemporal_load((const uint32_t*)sc);
+      ks[0] = LDS ? *(const uint32_t*)sc : __builtin_nontemporal_load((const uint32_t*)sc);
     }
   }
+  template <bool LDS = false>
   __device__ __forceinline__ void load_v_tile(const uint8_t* vt, const Lane& ln) {
     const uint8_t* lp = vt + (uint64_t)ln.lane * 16;
 #pragma unroll
     for (int p = 0; p < D / 64; p++) {  // dim tiles 4p .. 4p + 3
-      const uint4 w = load_stream16(lp + p * 1024);
+      const uint4 w = LDS ? *(const uint4*)(lp + p * 1024) : load_stream16(lp + p * 1024);
       vq[4 * p] = w.x;
       vq[4 * p + 1] = w.y;
       vq[4 * p + 2] = w.z;
@@ -392,7 +395,7 @@ struct BlockRegs<kDtypeQ8, D> {
     const uint8_t* sc = vt + (uint64_t)B * D + (uint64_t)ln.grp * 4 * NG * 2;
 #pragma unroll
     for (int i = 0; i < NG / 2; i++) {
-      const uint4 w = load_stream16(sc + i * 16);
+      const uint4 w = LDS ? *(const uint4*)(sc + i * 16) : load_stream16(sc + i * 16);
       vs[4 * i] = w.x;
       vs[4 * i + 1] = w.y;
       vs[4 * i + 2] = w.z;
@@ -1181,7 +1184,11 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
           mark_wide(g.fault);
       } else {
         s_app[0][dd] = (uint16_t)encode_f16(kv, g.rounding);
-        s_app[1][dd] = (uint16_t)encode_f16(vv, g.rounding);
+        const uint32_t ve = encode_f16(vv, g.rounding);
+        s_app[1][dd] = (uint16_t)ve;
+        // an Inf/NaN V marks the pool (chunked prefill's leak-safe instance)
+        if (__builtin_amdgcn_ballot_w64(f16_nonfinite(ve)) != 0 && ln.lane == 0)
+          mark_nonfinite_v(g.fault);
       }
     }
   };
@@ -1431,10 +1438,18 @@ __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16
   }
 }
 
-template <int D>
-__device__ __forceinline__ f16x4 softmax_block_pf(const float (&s)[4], const Lane& ln,
-                                                  Accum<D>& st) {
-  const float lmax = __builtin_fmaxf(__builtin_fmaxf(s[0], s[1]), __builtin_fmaxf(s[2], s[3]));
+// Lazy online softmax of NB blocks at once (prefill): one max test, one rescale of the
+// accumulators and one rare-path ballot per NB blocks instead of per block. ef gets the
+// f32 weights (the exact Q8_0 P.V forms scale x weight from them), pw their binary16.
+template <int D, int NB>
+__device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], const Lane& ln,
+                                                Accum<D>& st, f16x4 (&pw)[NB],
+                                                float (&ef)[NB][4]) {
+  float lmax = s[0][0];
+#pragma unroll
+  for (int b = 0; b < NB; b++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) lmax = __builtin_fmaxf(lmax, s[b][r]);
   const bool bad =
       ln.real && (!(lmax <= st.m_ref + kRescaleLog2) || !__builtin_isfinite(st.m_ref));
   float ar[4] = {1.0f, 1.0f, 1.0f, 1.0f};
@@ -1453,25 +1468,50 @@ __device__ __forceinline__ f16x4 softmax_block_pf(const float (&s)[4], const Lan
   for (int m = 0; m < D / 16; m++)
 #pragma unroll
     for (int r = 0; r < 4; r++) st.acc[m][r] *= ar[r];
-  f16x4 pw;
   if (__builtin_amdgcn_ballot_w64(ln.real && st.m_ref == -__builtin_inff()) == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float e = __builtin_amdgcn_exp2f(s[r] - st.m_ref);
-      st.l_part += e;
-      pw[r] = (_Float16)e;
-    }
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float e = __builtin_amdgcn_exp2f(s[b][r] - st.m_ref);
+        st.l_part += e;
+        ef[b][r] = e;
+        pw[b][r] = (_Float16)e;
+      }
   } else {
     const bool dead = (st.m_ref == -__builtin_inff());
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const float sv = s[r];
-      const float e = dead ? (sv != sv ? sv : 0.0f) : __builtin_amdgcn_exp2f(sv - st.m_ref);
-      st.l_part += e;
-      pw[r] = (_Float16)e;
-    }
+    for (int b = 0; b < NB; b++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float sv = s[b][r];
+        const float e = dead ? (sv != sv ? sv : 0.0f) : __builtin_amdgcn_exp2f(sv - st.m_ref);
+        st.l_part += e;
+        ef[b][r] = e;
+        pw[b][r] = (_Float16)e;
+      }
   }
-  return pw;
+}
+
+// Whether an F16 V operand (tokens t0 + grp*4 + r of dims 16m + col) holds an Inf or
+// NaN at a token in [lo, hi).
+template <int D>
+__device__ __forceinline__ bool v_nonfinite_in(const u32x2_t (&vr)[D / 16], const Lane& ln,
+                                               int32_t t0, int32_t lo, int32_t hi) {
+  uint32_t ex = 0;  // bit r: token r's values with all-ones exponents
+#pragma unroll
+  for (int m = 0; m < D / 16; m++) {
+    const uint32_t a = ~vr[m].x & 0x7c007c00u, b = ~vr[m].y & 0x7c007c00u;
+    ex |= ((a & 0xffffu) == 0 ? 1u : 0u) | ((a >> 16) == 0 ? 2u : 0u) |
+          ((b & 0xffffu) == 0 ? 4u : 0u) | ((b >> 16) == 0 ? 8u : 0u);
+  }
+  uint32_t in = 0;
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const int32_t t = t0 + ln.grp * 4 + r;
+    in |= (t >= lo && t < hi) ? (1u << r) : 0u;
+  }
+  return (ex & in) != 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -1484,27 +1524,66 @@ __device__ __forceinline__ f16x4 softmax_block_pf(const float (&s)[4], const Lan
 // query rows instead of heads: column c of a wave's tile is (token c / G, head
 // c % G) for 16 / G consecutive query tokens, each with its own causal end. QK,
 // the softmax reductions (over the 4 lanes of a column) and PV are the decode
-// step unchanged.
+// block step.
 //
 // A workgroup holds 4 consecutive tiles (4 waves) of one (sequence, KV head) and
-// streams the blocks up to its furthest causal end once: the 256 threads load
-// block j + 1 (K and V tiles, 16 bytes per thread per load) into registers while
-// the waves compute block j from LDS, then store it to the other half of a
-// double buffer. Every K/V byte is read from memory once per 4 tiles instead of
-// once per tile; the operand reads come from LDS in the same orders as the
-// decode kernel's global loads.
-template <int D, int NS>
+// streams the blocks up to its furthest causal end once, two blocks per step: the
+// 256 threads stage the next step's blocks into the other half of an LDS double
+// buffer (one block in registers at a time, stored at the middle and at the end of
+// the step) while the waves compute the current step. Per step a wave does both
+// blocks' QK, one softmax update over their 32 keys, then both P.V products.
+//
+// Storage: F16 tiles are staged as loaded except V, whose 8-byte chunks are
+// XOR-swizzled by row so the P.V operand reads hit distinct banks. Q8_0 tiles are
+// staged as loaded (their operand order reads conflict-free) and converted by the
+// decode kernel's BlockRegs; over a pool marked as holding scales of 512 or more
+// (the sticky word), the fast instance exits and the EXACT instance, launched after
+// it, computes with qk_block_q8x / pv_block_q8x.
+//
+// Tokens past a column's causal end carry weight 0 in the P.V product, but an
+// Inf/NaN V there would still reach the column through 0 * NaN. F16 pools that have
+// stored such a value carry a sticky mark (pool_has_nonfinite_v) and run the
+// leak-safe instance: on a block that crosses the tile's nearest causal end, a
+// wave-uniform check for non-finite V values past that end sends the block down a
+// masked path, one P.V per query token of the tile with P restricted to that token's
+// columns and V zeroed from its end, so no column reads a position past its own (as
+// the reference's token loop never does). Q8_0 V values are finite unless a scale
+// is, and a pool holding an inf or NaN scale is marked wide, so the fast Q8_0
+// instance needs no check; the exact one masks P x scale per lane at the lane's own
+// column end.
+template <int DT, int D>
+constexpr int prefill_tile_bytes() {
+  return DT == kDtypeF16 ? B * D * 2 : B * D + B * D / 32 * 2;
+}
+
+enum : int { kPfFast = 0, kPfExact = 1, kPfLeakSafe = 2 };
+
+template <int DT, int D, int MODE>
 __global__ void __launch_bounds__(256) attn_prefill_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
     const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ q_lens,
-    const int64_t* __restrict__ q_offsets, float scale) {
+    const int64_t* __restrict__ q_offsets, uint32_t max_q_len, float scale) {
   constexpr int NC = D / 32, NM = D / 16;
-  constexpr int kTileBytes = B * D * 2;             // one f16 K or V tile
-  constexpr int kLoads = 2 * kTileBytes / (256 * 16);  // 16-byte loads per thread per block
-  static_assert(kLoads >= 1 && kLoads * 256 * 16 == 2 * kTileBytes, "block staging");
-  __shared__ __align__(16) uint8_t s_kv[2][2 * kTileBytes];  // [buffer][K tile | V tile]
+  constexpr int kStep = 2;  // blocks per softmax step
+  constexpr int kTile = prefill_tile_bytes<DT, D>();
+  static_assert(kTile % 16 == 0, "tiles are whole 16-byte chunks");
+  constexpr int kBlk = 2 * kTile;               // K tile | V tile
+  constexpr int kChunks = kBlk / 16;
+  constexpr int kLoads = (kChunks + 255) / 256;  // 16-byte loads per thread per block
+  __shared__ __align__(16) uint8_t s_kv[2][kStep][kBlk];
+  constexpr bool EXACT = MODE == kPfExact;
 
+  if constexpr (DT == kDtypeQ8) {
+    // The word cannot change during a prefill launch (only appends set it), so every
+    // wave reads the same value and the workgroup leaves as a whole.
+    if (pool_has_wide_scales(g.fault) != EXACT) return;
+  }
+  if constexpr (DT == kDtypeF16) {
+    // Likewise the pool's mark of a stored Inf/NaN V (appends, fill and write set it):
+    // without one the fast instance computes, with one the leak-safe instance.
+    if (pool_has_nonfinite_v(g.fault) != (MODE == kPfLeakSafe)) return;
+  }
   const uint32_t sk = blockIdx.x;
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1512,15 +1591,23 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   const int32_t cap = (int32_t)(max_blocks * B);
   int32_t ctx = ctx_lens[seq];
   int32_t ql = q_lens[seq];
-  if (ctx < 0 || ctx > cap || ql < 0 || ql > (ctx < 0 ? 0 : (ctx > cap ? cap : ctx))) {
-    if (blockIdx.y == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
-    ctx = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-    ql = ql < 0 ? 0 : (ql > ctx ? ctx : ql);
+  int32_t p0;  // position of query 0
+  {
+    const int32_t c = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+    const int32_t qc = ql < 0 ? 0 : (ql > c ? c : ql);
+    p0 = c - qc;
+    // The grid holds max_q_len queries a sequence: past that the first max_q_len are
+    // computed, at the positions the caller gave them, and the fault is raised.
+    const int32_t nq = qc < (int32_t)max_q_len ? qc : (int32_t)max_q_len;
+    if (ctx != c || ql != nq) {
+      if (blockIdx.y == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
+      ctx = c;
+      ql = nq;  // from here: the number of queries computed
+    }
   }
   const int32_t tile0 = (int32_t)blockIdx.y * kAttnWaves;  // first tile of the workgroup
   if (tile0 * T >= ql) return;                              // uniform over the workgroup
   const int32_t tile = tile0 + wave;
-  const int32_t p0 = ctx - ql;  // position of query 0
   const bool wave_on = tile * T < ql;
 
   Lane ln;
@@ -1546,60 +1633,58 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   };
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
-  // Physical block j (uniform); an entry outside the pool raises the fault flag,
-  // stages block 0 instead and is skipped.
-  auto phys = [&](int32_t j, bool& ok) {
+  // Thread t stages 16-byte chunks t, t + 256, ... of a block's K | V pair; a table
+  // entry outside the pool raises the fault flag, stages block 0 and is skipped.
+  uint4 stg[kLoads];
+  auto load_block = [&](int32_t j) {
     const int32_t p = __builtin_amdgcn_readfirstlane(table[j]);
-    ok = p >= 0 && (uint64_t)p < g.num_blocks;
+    const bool ok = p >= 0 && (uint64_t)p < g.num_blocks;
     if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
-    return ok ? (uint64_t)p : 0;
-  };
-  // Thread t stages bytes [t*16, t*16 + 16) of every 4 KiB of the block's K|V pair.
-  // Pipeline: block j is computed from LDS buffer j & 1 while blocks j+1 .. j+NS
-  // are in flight in a ring of NS register stages (block b >= 1 in stage
-  // (b - 1) % NS). At the end of step j, block j+1 goes from its stage to the other
-  // LDS buffer (its loads were issued NS steps earlier), the barrier publishes it,
-  // and the freed stage takes block j+1+NS.
-  uint4 stage[NS][kLoads];
-  bool slive[NS];
-  auto load_block = [&](uint4 (&st_)[kLoads], uint64_t p) {
-    const uint8_t* kt = tile_ptr(g, p, layer, 0, kvh);
-    const uint8_t* vt = tile_ptr(g, p, layer, 1, kvh);
+    const uint8_t* kt = tile_ptr(g, ok ? (uint64_t)p : 0, layer, 0, kvh);
+    const uint8_t* vt = tile_ptr(g, ok ? (uint64_t)p : 0, layer, 1, kvh);
 #pragma unroll
     for (int i = 0; i < kLoads; i++) {
-      const uint32_t off = (uint32_t)(i * 256 + threadIdx.x) * 16u;
-      st_[i] = load_stream16(off < (uint32_t)kTileBytes ? kt + off : vt + (off - kTileBytes));
+      const uint32_t c = (uint32_t)(i * 256) + threadIdx.x;
+      if (c < (uint32_t)kChunks) {
+        const uint32_t off = c * 16u;
+        stg[i] = load_stream16(off < (uint32_t)kTile ? kt + off : vt + (off - kTile));
+      }
     }
+    return ok;
   };
-  // K is staged as loaded. V rows (one dim, 16 tokens = four 8-byte chunks) are
-  // stored with chunk c at c ^ ((dim >> 2) & 3), so the P.V operand reads (lanes
-  // 16 dims x 4 chunks) hit distinct banks; a 16-byte pair of chunks stays one
-  // aligned 16-byte unit, its halves swapped when the swizzle is odd.
-  auto store_block = [&](const uint4 (&st_)[kLoads], int buf) {
+  auto store_block = [&](int buf, int slot) {
 #pragma unroll
     for (int i = 0; i < kLoads; i++) {
-      const uint32_t off = (uint32_t)(i * 256 + threadIdx.x) * 16u;
-      if (off < (uint32_t)kTileBytes) {
-        *(uint4*)&s_kv[buf][off] = st_[i];
-      } else {
-        const uint32_t v = off - kTileBytes, dim = v / 32u, unit = (v % 32u) / 16u;
-        const uint32_t sw = (dim >> 2) & 3u;
-        const uint4 x = st_[i];
-        *(uint4*)&s_kv[buf][kTileBytes + dim * 32u + ((unit ^ (sw >> 1)) * 16u)] =
-            (sw & 1u) ? make_uint4(x.z, x.w, x.x, x.y) : x;
+      const uint32_t c = (uint32_t)(i * 256) + threadIdx.x;
+      if (c < (uint32_t)kChunks) {
+        const uint32_t off = c * 16u;
+        uint8_t* dst = s_kv[buf][slot];
+        if (DT == kDtypeF16 && off >= (uint32_t)kTile) {
+          // V rows (one dim, 16 tokens = four 8-byte chunks) with chunk c at
+          // c ^ ((dim >> 2) & 3); a 16-byte pair of chunks stays one aligned unit,
+          // its halves swapped when the swizzle is odd.
+          const uint32_t v = off - kTile, dim = v / 32u, unit = (v % 32u) / 16u;
+          const uint32_t sw = (dim >> 2) & 3u;
+          const uint4 x = stg[i];
+          *(uint4*)&dst[kTile + dim * 32u + ((unit ^ (sw >> 1)) * 16u)] =
+              (sw & 1u) ? make_uint4(x.z, x.w, x.x, x.y) : x;
+        } else {
+          *(uint4*)&dst[off] = stg[i];
+        }
       }
     }
   };
 
-  bool live = false;  // block in the LDS buffer being computed
-  {
-    uint4 st0[kLoads];
-    load_block(st0, nblk > 0 ? phys(0, live) : 0);
+  bool lv[kStep] = {false, false};   // blocks of the step being computed: in the pool
+  bool nlv[kStep] = {false, false};  // and of the next step
 #pragma unroll
-    for (int sl = 0; sl < NS; sl++)
-      if (1 + sl < nblk) load_block(stage[sl], phys(1 + sl, slive[sl]));
-    store_block(st0, 0);
+  for (int bb = 0; bb < kStep; bb++) {
+    if (bb < nblk) {
+      lv[bb] = load_block(bb);
+      store_block(0, bb);
+    }
   }
+  if (kStep < nblk) nlv[0] = load_block(kStep);
   f16x8 qh[NC], qlo[NC];
   float hscale;
   prep_q<D>(q + row_of(ln.real ? ln.col : 0), ln, scale * kLog2e, qh, qlo, hscale);
@@ -1607,39 +1692,107 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   st.reset();
   __syncthreads();
 
-  for (int32_t j0 = 0; j0 < nblk; j0 += NS) {
+  for (int32_t j0 = 0, buf = 0; j0 < nblk; j0 += kStep, buf ^= 1) {
+    const bool more = j0 + kStep < nblk;      // the workgroup has a next step
+    const bool more2 = j0 + kStep + 1 < nblk;  // with a second block
+    float sc[kStep][4];
 #pragma unroll
-    for (int sl = 0; sl < NS; sl++) {
-      const int32_t j = j0 + sl;
-      if (j < nblk) {
-        const int buf = j & 1;
-        if (j < nblk_w) {  // wave-uniform: blocks past the wave's tile are skipped
-          const uint8_t* ks = s_kv[buf];
-          const uint8_t* vs = s_kv[buf] + kTileBytes;
+    for (int bb = 0; bb < kStep; bb++) {
+      const int32_t j = j0 + bb;
+      const int32_t t0 = j * B;
+      const uint8_t* ks = s_kv[buf][bb];
+      if (j < nblk_w) {  // wave-uniform: blocks past the wave's tile are skipped
+        if constexpr (DT == kDtypeF16) {
           uint4 kr[NC];
-          u32x2_t vr[NM];
 #pragma unroll
           for (int c = 0; c < NC; c++)
             kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
-          const int32_t t0 = j * B;
-          float sc[4];
-          qk_block_pf<D>(kr, qh, qlo, hscale, ln, live, t0 + B <= end_min, t0, end_col, sc);
+          qk_block_pf<D>(kr, qh, qlo, hscale, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
+        } else {
+          BlockRegs<kDtypeQ8, D> rg;
+          rg.template load_k_tile<true>(ks, ln);
+          if constexpr (EXACT) {
+            qk_block_q8x<D>(rg, qh, qlo, hscale, ln, lv[bb], t0, end_col, sc[bb]);
+          } else {
+            uint4 kr[NC];
+            rg.k_operand(kr);
+            qk_block_pf<D>(kr, qh, qlo, hscale, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) sc[bb][r] = -__builtin_inff();
+      }
+      if (bb == 0 && more) {  // the next step's first block to the other buffer
+        store_block(buf ^ 1, 0);
+        if (more2) nlv[1] = load_block(j0 + kStep + 1);
+      }
+    }
+    f16x4 pw[kStep];
+    float ef[kStep][4];
+    softmax_step_pf<D, kStep>(sc, ln, st, pw, ef);
+#pragma unroll
+    for (int bb = 0; bb < kStep; bb++) {
+      const int32_t j = j0 + bb;
+      const int32_t t0 = j * B;
+      if (j < nblk_w && lv[bb]) {
+        const uint8_t* vs = s_kv[buf][bb] + kTile;
+        if constexpr (DT == kDtypeF16) {
+          u32x2_t vr[NM];
 #pragma unroll
           for (int m = 0; m < NM; m++) {
             const uint32_t dim = (uint32_t)(m * 16 + ln.col);
             vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((uint32_t)ln.grp ^ ((dim >> 2) & 3u)) * 8u));
           }
-          const f16x4 pw = softmax_block_pf<D>(sc, ln, st);
-          if (live) pv_block<D>(vr, pw, ln, t0, end_max, st);
-        }
-        if (j + 1 < nblk) {
-          // the other buffer was last read before the previous barrier
-          store_block(stage[sl], buf ^ 1);
-          live = slive[sl];
-          __syncthreads();
-          if (j + 1 + NS < nblk) load_block(stage[sl], phys(j + 1 + NS, slive[sl]));
+          // Leak-safe instance: a block where a non-finite V lies past the tile's
+          // nearest causal end takes one P.V per query token jt of the tile, V cut at
+          // that token's causal end, into a zeroed temporary; only the rows (columns)
+          // of token jt are added to the accumulators (a shared V operand would give
+          // every other row 0 * NaN). The check costs the fast instance a wave per
+          // SIMD, which is why it has none and the pool mark picks the instance.
+          bool leak = false;
+          if constexpr (MODE == kPfLeakSafe)
+            leak = t0 + B > end_min &&
+                   __builtin_amdgcn_ballot_w64(v_nonfinite_in<D>(vr, ln, t0, end_min, end_max)) != 0;
+          if (!leak) {
+            pv_block<D>(vr, pw[bb], ln, t0, end_max, st);
+          } else if constexpr (MODE == kPfLeakSafe) {
+            for (int32_t jt = 0; jt < T; jt++) {
+#pragma unroll
+              for (int m = 0; m < NM; m++) {
+                const uint32_t dim = (uint32_t)(m * 16 + ln.col);
+                vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((uint32_t)ln.grp ^ ((dim >> 2) & 3u)) * 8u));
+              }
+              mask_v_tail<D>(vr, ln, t0, p0 + tile * T + jt + 1);
+#pragma unroll
+              for (int m = 0; m < NM; m++) {
+                const f32x4 t = __builtin_amdgcn_mfma_f32_16x16x16f16(
+                    pw[bb], __builtin_bit_cast(f16x4, vr[m]), (f32x4){0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                  if ((ln.grp * 4 + r) / (int32_t)G == jt) st.acc[m][r] += t[r];
+              }
+            }
+          }
+        } else {
+          BlockRegs<kDtypeQ8, D> rg;
+          rg.template load_v_tile<true>(vs, ln);
+          if constexpr (EXACT) {
+            pv_block_q8x<D>(rg, ef[bb], ln, t0, end_col, st);
+          } else {
+            u32x2_t vr[NM];
+            rg.v_operand(vr);
+            pv_block<D>(vr, pw[bb], ln, t0, end_max, st);
+          }
         }
       }
+    }
+    if (more) {
+      if (more2) store_block(buf ^ 1, 1);
+      __syncthreads();
+      lv[0] = nlv[0];
+      lv[1] = more2 ? nlv[1] : false;
+      if (j0 + 2 * kStep < nblk) nlv[0] = load_block(j0 + 2 * kStep);
     }
   }
   if (!wave_on) return;
@@ -1728,12 +1881,31 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
   const uint32_t T = 16 / G;
   const uint32_t tiles = (max_q_len + T - 1) / T;
   dim3 grid(n_seqs * g.n_kv_heads, (tiles + kAttnWaves - 1) / kAttnWaves);
-  if (g.head_dim == 128)
-    attn_prefill_kernel<128, FKV_PREFILL_STAGES><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
-                                                  ctx_lens, q_lens, q_offsets, scale);
-  else
-    attn_prefill_kernel<64, FKV_PREFILL_STAGES><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, max_blocks,
-                                                 ctx_lens, q_lens, q_offsets, scale);
+#define FKV_LAUNCH_PF(DT_, D_, X_)                                                          \
+  attn_prefill_kernel<DT_, D_, X_><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
+                                                        max_blocks, ctx_lens, q_lens,         \
+                                                        q_offsets, max_q_len, scale)
+  // The fast instance, then the one for pools whose marks say the fast one cannot
+  // compute them: Q8_0 the exact instance (a scale of 512 or more was stored), F16 the
+  // leak-safe one (an Inf/NaN V was stored). Each exits at once where the other works.
+  const int dt = g.dtype == kDtypeQ8 ? kDtypeQ8 : kDtypeF16;
+  if (dt == kDtypeQ8) {
+    if (g.head_dim == 128) FKV_LAUNCH_PF(kDtypeQ8, 128, kPfFast);
+    else FKV_LAUNCH_PF(kDtypeQ8, 64, kPfFast);
+  } else {
+    if (g.head_dim == 128) FKV_LAUNCH_PF(kDtypeF16, 128, kPfFast);
+    else FKV_LAUNCH_PF(kDtypeF16, 64, kPfFast);
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (dt == kDtypeQ8) {
+    if (g.head_dim == 128) FKV_LAUNCH_PF(kDtypeQ8, 128, kPfExact);
+    else FKV_LAUNCH_PF(kDtypeQ8, 64, kPfExact);
+  } else {
+    if (g.head_dim == 128) FKV_LAUNCH_PF(kDtypeF16, 128, kPfLeakSafe);
+    else FKV_LAUNCH_PF(kDtypeF16, 64, kPfLeakSafe);
+  }
+#undef FKV_LAUNCH_PF
   return hipGetLastError();
 }
 

@@ -44,6 +44,18 @@ __device__ __forceinline__ bool pool_has_wide_scales(const uint32_t* fault) {
   return __builtin_amdgcn_readfirstlane(__atomic_load_n(fault + 1, __ATOMIC_RELAXED)) != 0;
 }
 
+// F16 pools: the third fault word records, sticky, that an Inf or NaN V value was
+// stored (append, fused step, fill, write). Chunked prefill over such a pool takes
+// its leak-safe instance, which keeps those values from queries whose causal end
+// lies before them.
+__device__ __forceinline__ bool f16_nonfinite(uint32_t bits) { return (bits & 0x7c00u) == 0x7c00u; }
+__device__ __forceinline__ void mark_nonfinite_v(uint32_t* fault) {
+  if (__atomic_load_n(fault + 2, __ATOMIC_RELAXED) == 0u) atomicOr(fault + 2, 1u);
+}
+__device__ __forceinline__ bool pool_has_nonfinite_v(const uint32_t* fault) {
+  return __builtin_amdgcn_readfirstlane(__atomic_load_n(fault + 2, __ATOMIC_RELAXED)) != 0;
+}
+
 // 16-byte load of K/V bytes that are read once per launch: the nontemporal hint
 // keeps the stream from evicting reusable lines (block tables, q) and measured
 // 7.1 TB/s against 6.3 TB/s for plain loads in a read-only sweep on MI355X.

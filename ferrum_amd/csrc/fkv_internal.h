@@ -41,7 +41,8 @@ struct Geom {
   int32_t dtype;     // 0 f32, 1 f16, 8 q8_0
   int32_t rounding;  // 0 nearest-even, 1 ties away
   uint32_t* fault;   // device words: [0] FKV_FAULT_* bits; [1] nonzero once a Q8_0
-                     // scale of 512 or more was stored (sticky; q8_wide_scale)
+                     // scale of 512 or more was stored (sticky; q8_wide_scale);
+                     // [2], [3] chunked prefill's non-finite-V mark and its count
 };
 
 constexpr int kDtypeF32 = 0;

@@ -130,10 +130,14 @@ __global__ void __launch_bounds__(256) append_f16_kernel(Geom g, uint32_t layer,
   const float4 x = *(const float4*)(v + (token * g.n_kv_heads + h) * D + d0);
   uint16_t* vt = (uint16_t*)tile_ptr(g, (uint64_t)slot / Bs, layer, 1, h) + (uint64_t)d0 * Bs +
                  (uint64_t)slot % Bs;
-  vt[0] = (uint16_t)encode_f16(x.x, g.rounding);
-  vt[Bs] = (uint16_t)encode_f16(x.y, g.rounding);
-  vt[2 * Bs] = (uint16_t)encode_f16(x.z, g.rounding);
-  vt[3 * Bs] = (uint16_t)encode_f16(x.w, g.rounding);
+  const uint32_t e0 = encode_f16(x.x, g.rounding), e1 = encode_f16(x.y, g.rounding);
+  const uint32_t e2 = encode_f16(x.z, g.rounding), e3 = encode_f16(x.w, g.rounding);
+  vt[0] = (uint16_t)e0;
+  vt[Bs] = (uint16_t)e1;
+  vt[2 * Bs] = (uint16_t)e2;
+  vt[3 * Bs] = (uint16_t)e3;
+  if (f16_nonfinite(e0) || f16_nonfinite(e1) || f16_nonfinite(e2) || f16_nonfinite(e3))
+    mark_nonfinite_v(g.fault);  // chunked prefill then takes its leak-safe instance
 }
 
 // Any head_dim, F32/F16 storage: one element per thread.
@@ -160,11 +164,12 @@ __global__ void __launch_bounds__(256) append_scalar_kernel(Geom g, uint32_t lay
     float x = (kv ? v : k)[(uint64_t)token * per_kv + e];
     uint8_t* tile = tile_ptr(g, (uint64_t)slot / g.block_size, layer, kv, h);
     const uint64_t off = (uint64_t)slot % g.block_size;
-    if (g.dtype == kDtypeF16)
+    if (g.dtype == kDtypeF16) {
+      const uint32_t e = encode_f16(x, g.rounding);
       ((uint16_t*)tile)[kv ? (uint64_t)d * g.block_size + off
-                           : ((uint64_t)(d / 8) * g.block_size + off) * 8 + d % 8] =
-          (uint16_t)encode_f16(x, g.rounding);
-    else
+                           : ((uint64_t)(d / 8) * g.block_size + off) * 8 + d % 8] = (uint16_t)e;
+      if (kv && f16_nonfinite(e)) mark_nonfinite_v(g.fault);
+    } else
       ((float*)tile)[off * D + d] = x;
   }
 }

@@ -350,18 +350,21 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
                                          uint32_t max_ctx_len, float scale, void* workspace,
                                          uint64_t workspace_bytes, void* stream);
 
-/* Chunked-prefill attention over F16 storage: the reference's token-by-token
- * prefill (crates/model/src/llama.rs:363-378, each token running the attention
- * loop of :220-247 over positions 0 ..= its own) for a chunk whose K/V are
- * already appended. Sequence s has q_lens[s] new tokens at the end of its
- * ctx_lens[s]-token context: query i sits at position ctx_lens[s] - q_lens[s] + i
- * and attends to positions 0 ..= that position. q, out: device f32
- * [rows][n_heads][head_dim]; sequence s's queries are rows q_offsets[s] ..
- * q_offsets[s] + q_lens[s] - 1 (q_offsets: device int64). q_lens[s] = 1 is
- * decode. Needs f16 KV, block_size 16, head_dim 64 or 128, g <= 16. K/V values
- * of tokens that some queries of a 16-column tile must not see still enter the
- * matrix product with weight 0, so a NaN/Inf V value inside the chunk reaches
- * earlier queries of its tile. No workspace. */
+/* Chunked-prefill attention over F16 or Q8_0 storage: the reference's token-by-token
+ * prefill (crates/model/src/llama.rs:363-378, each token running the attention loop
+ * of :220-247 over positions 0 ..= its own) for a chunk whose K/V are already
+ * appended. Sequence s has q_lens[s] new tokens at the end of its ctx_lens[s]-token
+ * context: query i sits at position ctx_lens[s] - q_lens[s] + i and attends to
+ * positions 0 ..= that position. q, out: device f32 [rows][n_heads][head_dim];
+ * sequence s's queries are rows q_offsets[s] .. q_offsets[s] + q_lens[s] - 1
+ * (q_offsets: device int64). q_lens[s] = 1 is decode. Needs block_size 16, head_dim
+ * 64 or 128, g <= 16. The launch holds max_q_len queries a sequence: a q_lens[s]
+ * above it (or above ctx_lens[s]) raises FKV_FAULT_CTX_RANGE, and only its first
+ * max_q_len queries are computed, at the positions q_lens[s] gives them. No query
+ * reads a position past its own, Inf/NaN values included: an F16 pool that has
+ * stored an Inf/NaN V runs a slower instance that keeps them from earlier queries
+ * of the same tile. Q8_0 follows fkv_decode_attention's rule for scales of 512 or
+ * more. No workspace. */
 int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,
                               float* out, const int32_t* block_tables,
                               uint32_t max_blocks_per_seq, const int32_t* ctx_lens,

@@ -1,8 +1,17 @@
-"""GPU parity: chunked-prefill attention (f16 KV, matrix cores) against the CPU
+"""GPU parity: chunked-prefill attention (F16 and Q8_0 KV, matrix cores) against the CPU
 oracle's token-by-token restatement of crates/model/src/llama.rs:363-378.
 
-Bar: |got - want| <= 2e-3 + 1e-2 * |want| elementwise; q_len = 1 agrees with
-decode attention; output rows outside the chunk are never written."""
+Bar: |got - want| <= 2e-3 + 1e-2 * |want| elementwise on finite values, the same Inf
+and NaN positions and values elsewhere; q_len = 1 agrees with decode attention;
+output rows outside the chunk are never written. Also:
+- an Inf or NaN V inside a chunk reaches exactly the queries whose causal range holds
+  it (the reference's token loop never reads a later position), through the
+  leak-safe instance that a pool which stored such a value runs, which also meets
+  the bar on finite data;
+- a sequence whose q_len exceeds the call's max_q_len (the grid holds no more) is
+  clamped to it and raises FKV_FAULT_CTX_RANGE;
+- Q8_0 pools, with ordinary values and with values up to +-1e6 (the exact instance).
+"""
 import numpy as np
 import pytest
 
@@ -11,11 +20,11 @@ from tests.helpers import assert_close, make_pools, slots_for, to_dev
 pytestmark = pytest.mark.gpu
 
 
-def _pool(d, hkv, ctxs, seed, layers=1):
+def _pool(d, hkv, ctxs, seed, layers=1, dtype=1, kv=None):
     rng = np.random.default_rng(seed)
     nb = [(c + 15) // 16 for c in ctxs]
     nblk = sum(nb) + 4
-    pool, layout = make_pools(layers, hkv, d, nblk, dtype=1)
+    pool, layout = make_pools(layers, hkv, d, nblk, dtype=dtype)
     pool.fill(0)
     perm = rng.permutation(nblk).astype(np.int32)
     tab = np.zeros((len(ctxs), max(nb)), np.int32)
@@ -23,41 +32,67 @@ def _pool(d, hkv, ctxs, seed, layers=1):
     for i, n in enumerate(nb):
         tab[i, :n] = perm[off:off + n]
         off += n
-    k = rng.standard_normal((sum(ctxs), hkv, d), dtype=np.float32)
-    v = rng.standard_normal((sum(ctxs), hkv, d), dtype=np.float32)
+    if kv is None:
+        k = rng.standard_normal((sum(ctxs), hkv, d), dtype=np.float32)
+        v = rng.standard_normal((sum(ctxs), hkv, d), dtype=np.float32)
+    else:
+        k, v = kv(rng, sum(ctxs))
     slots = np.concatenate([slots_for(tab[i], c) for i, c in enumerate(ctxs)])
     for layer in range(layers):
         pool.append(layer, to_dev(k), to_dev(v), to_dev(slots))
     return pool, layout, tab
 
 
-def _prefill(pool, layer, q, tab, ctxs, qls, offs, fill=5.0):
+def _prefill(pool, layer, q, tab, ctxs, qls, offs, fill=5.0, max_q_len=None):
     import torch
     out = torch.full(q.shape, fill, dtype=torch.float32, device="cuda")
     pool.prefill_attention(layer, to_dev(q), out, to_dev(tab), to_dev(np.array(ctxs, np.int32)),
-                           to_dev(np.array(qls, np.int32)), to_dev(offs), max(qls), max(ctxs))
+                           to_dev(np.array(qls, np.int32)), to_dev(offs),
+                           max(qls) if max_q_len is None else max_q_len, max(ctxs))
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("d,g", [(128, 4), (64, 8), (128, 1), (64, 16), (128, 3), (128, 8)])
-def test_prefill_matches_oracle(d, g):
+def _want(pool, layout, q, tab, ctxs, qls, offs, d):
     import ferrum_amd as fa
     from oracle import ref
+    return ref.prefill_attention(layout, pool.read(), 0, q, tab, np.array(ctxs, np.int32),
+                                 np.array(qls, np.int32), offs, fa.default_scale(d))
+
+
+def _used(rows, offs, qls):
+    used = np.zeros(rows, bool)
+    for o, n in zip(offs, qls):
+        used[o:o + n] = True
+    return used
+
+
+def assert_close_nonfinite(got, want, what="prefill"):
+    """The attention bar on finite values; Inf and NaN where, and as, the oracle has them."""
+    fin = np.isfinite(want)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), f"{what}: NaN positions differ"
+    inf = np.isinf(want)
+    assert np.array_equal(got[inf], want[inf]), f"{what}: infinities differ"
+    assert_close(got[fin], want[fin], what=what)
+
+
+SHAPES = [(1, 128, 4), (1, 64, 8), (1, 128, 1), (1, 64, 16), (1, 128, 3), (1, 128, 8),
+          (8, 128, 4), (8, 64, 8), (8, 128, 1)]
+
+
+@pytest.mark.parametrize("dtype,d,g", SHAPES)
+def test_prefill_matches_oracle(dtype, d, g):
     hkv = 2
     ctxs = [1, 17, 64, 300, 777]
     qls = [1, 17, 5, 300, 129]  # fresh chunks and chunks after history
-    pool, layout, tab = _pool(d, hkv, ctxs, seed=d + g)
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=d + g, dtype=dtype)
     rows = sum(qls) + 3
     offs = np.concatenate([[2], 2 + np.cumsum(qls)[:-1]]).astype(np.int64)
     q = np.random.default_rng(g).standard_normal((rows, hkv * g, d), dtype=np.float32)
     got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
     assert pool.take_fault_flags() == 0
-    want = ref.prefill_attention(layout, pool.read(), 0, q, tab, np.array(ctxs, np.int32),
-                                 np.array(qls, np.int32), offs, fa.default_scale(d))
-    used = np.zeros(rows, bool)
-    for o, n in zip(offs, qls):
-        used[o:o + n] = True
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    used = _used(rows, offs, qls)
     assert_close(got[used], want[used], what="prefill")
     assert np.all(got[~used] == 5.0)  # rows outside every chunk are untouched
 
@@ -78,36 +113,118 @@ def test_prefill_with_one_query_is_decode():
     assert_close(got, dec.cpu().numpy(), what="prefill vs decode")
 
 
-def test_prefill_c3_chunk_shape():
+@pytest.mark.parametrize("dtype", [1, 8])
+def test_prefill_c3_chunk_shape(dtype):
     """BASELINE configs[2]'s prefill part at full size: 4 sequences appending 512-token
-    chunks behind 0 / 700 / 1500 / 3000 tokens of history, Llama-3-8B heads."""
-    import ferrum_amd as fa
-    from oracle import ref
+    chunks behind 0 / 700 / 1500 / 3000 tokens of history, Llama-3-8B heads; every row
+    of every chunk against the oracle."""
     hkv, g, d = 8, 4, 128
     hist = [0, 700, 1500, 3000]
     ctxs = [h + 512 for h in hist]
     qls = [512] * 4
-    pool, layout, tab = _pool(d, hkv, ctxs, seed=21)
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=21, dtype=dtype)
     offs = (np.arange(4) * 512).astype(np.int64)
     q = np.random.default_rng(2).standard_normal((2048, hkv * g, d), dtype=np.float32)
     got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
-    # the scalar oracle checks the shortest and the longest history (rows 0..511, 1536..2047)
-    pick = [0, 3]
-    want = ref.prefill_attention(layout, pool.read(), 0, q, tab[pick],
-                                 np.array(ctxs, np.int32)[pick], np.array(qls, np.int32)[pick],
-                                 offs[pick], fa.default_scale(d))
-    rows = np.r_[0:512, 1536:2048]
-    assert_close(got[rows], want[rows], what="c3 prefill")
+    assert pool.take_fault_flags() == 0
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    assert_close(got, want, what="c3 prefill")
 
 
-def test_prefill_rejects_non_f16_pools():
+@pytest.mark.parametrize("g", [4, 1, 16])
+@pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
+def test_nonfinite_v_reaches_only_later_queries(bad, g):
+    """V of position p0 + 9 of a fresh 40-token chunk (and of position 3 of a chunk after
+    100 tokens of history) holds an Inf/NaN in a few dims: queries before it must be
+    finite, the ones at or after it what the oracle gives."""
+    hkv, d = 2, 128
+    ctxs, qls = [40, 140], [40, 40]
+    marks = [(0, 9), (1, 100 + 3)]
+
+    def kv(rng, n):
+        k = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        v = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        base = [0, ctxs[0]]
+        for s, pos in marks:
+            v[base[s] + pos, 1, [3, 70, 127]] = bad
+        return k, v
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=31, kv=kv)
+    offs = np.array([0, 40], np.int64)
+    q = np.random.default_rng(4).standard_normal((80, hkv * g, d), dtype=np.float32)
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    assert pool.take_fault_flags() == 0
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    assert np.all(np.isfinite(want[:9])) and np.all(np.isfinite(want[40:43]))
+    assert not np.all(np.isfinite(want[9:40]))
+    assert_close_nonfinite(got, want)
+
+
+def test_leak_safe_instance_on_finite_data():
+    """A pool that once stored a NaN V (elsewhere) runs the leak-safe instance for every
+    later prefill: on finite chunks it meets the same bar."""
+    hkv, g, d = 8, 4, 128
+    ctxs, qls = [600, 1300], [600, 256]
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=41)
+    import torch
+    spare = int(np.setdiff1d(np.arange(pool.config.num_blocks), tab.ravel())[0])
+    bad = np.full((1, hkv, d), np.nan, np.float32)
+    pool.append(0, to_dev(bad), to_dev(bad), to_dev(np.array([spare * 16], np.int64)))
+    torch.cuda.synchronize()
+    offs = np.array([0, 600], np.int64)
+    q = np.random.default_rng(5).standard_normal((856, hkv * g, d), dtype=np.float32)
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    assert pool.take_fault_flags() == 0
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    assert_close(got, want, what="leak-safe prefill")
+
+
+def test_q_len_past_max_q_len_is_clamped_and_flagged():
+    """Sequence 1 says 300 queries but the call's max_q_len is 200: its first 200 rows are
+    computed, the rest untouched, FKV_FAULT_CTX_RANGE raised; sequence 0 is unaffected."""
+    import ferrum_amd as fa
+    hkv, g, d = 2, 4, 128
+    ctxs, qls = [150, 500], [150, 300]
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=51)
+    offs = np.array([0, 150], np.int64)
+    q = np.random.default_rng(6).standard_normal((450, hkv * g, d), dtype=np.float32)
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs, max_q_len=200)
+    assert pool.take_fault_flags() == fa.FAULT_CTX_RANGE
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    assert_close(got[:350], want[:350], what="clamped prefill")
+    assert np.all(got[350:] == 5.0)
+
+
+def test_q8_prefill_with_wide_values():
+    """Q8_0 K and V with +-1e6 values (scales ~7,874): the pool is marked and the exact
+    instance computes; q is small enough that the scores stay O(1)."""
+    hkv, g, d = 2, 4, 128
+    ctxs, qls = [300, 700], [300, 200]
+
+    def kv(rng, n):
+        k = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        v = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        for x in (k, v):
+            idx = rng.integers(0, d, size=(n, hkv))
+            np.put_along_axis(x, idx[..., None], rng.choice([-1e6, 1e6], size=(n, hkv, 1)), -1)
+        return k, v
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=61, dtype=8, kv=kv)
+    offs = np.array([0, 300], np.int64)
+    q = np.random.default_rng(7).standard_normal((500, hkv * g, d), dtype=np.float32) * 2e-6
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    assert pool.take_fault_flags() == 0
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    assert np.abs(want).max() > 1e3
+    assert_close(got, want, what="q8 wide prefill")
+
+
+def test_prefill_rejects_f32_pools():
     import torch
 
     import ferrum_amd as fa
     pool, _ = make_pools(1, 2, 64, 4, dtype=0)
     q = torch.zeros((1, 8, 64), dtype=torch.float32, device="cuda")
     z = torch.zeros(1, dtype=torch.int32, device="cuda")
-    with pytest.raises(fa.KernelError, match="prefill attention needs f16 kv"):
+    with pytest.raises(fa.KernelError, match="prefill attention needs f16 or q8_0 kv"):
         pool.prefill_attention(0, q, q.clone(), torch.zeros((1, 1), dtype=torch.int32,
                                                             device="cuda"),
                                z + 1, z + 1, torch.zeros(1, dtype=torch.int64, device="cuda"), 1,
