@@ -140,6 +140,113 @@ __global__ void __launch_bounds__(256) append_f16_kernel(Geom g, uint32_t layer,
     mark_nonfinite_v(g.fault);  // chunked prefill then takes its leak-safe instance
 }
 
+// F16 storage, block_size 16, head_dim 64 or 128, 16-byte aligned k/v: one workgroup
+// per 16 consecutive input tokens (a window) x 256 / (2 D) KV heads; thread (c, o)
+// of a head holds dims 8c .. 8c+7 of window token o, tokens fastest, so a wave's
+// loads cover whole 128-byte lines of four token rows.
+// - K: the thread's 16-byte run goes to run c of its token's [D/8][16][8] tile;
+//   tokens at consecutive slots of one block make a wave's stores contiguous.
+// - V: the window's rows are transposed through LDS ([dim][token]); thread (d, hh)
+//   then stores tokens 8hh .. 8hh+7 of dim d: one 16-byte store when they sit at
+//   offsets 0..7 or 8..15 of one block (the whole half of the tile's row d), else one
+//   2-byte store per token (any slot mapping, slots < 0 skipped).
+// Encoding and fault rules are append_f16_kernel's, bit for bit.
+template <int D>
+__global__ void __launch_bounds__(256) append_f16_tile_kernel(Geom g, uint32_t layer,
+                                                              const float* __restrict__ k,
+                                                              const float* __restrict__ v,
+                                                              const int64_t* __restrict__ slots,
+                                                              uint32_t n_tokens) {
+  constexpr int kRuns = D / 8;           // 8-dim runs of a row
+  constexpr int kTph = 16 * kRuns;       // threads per (window, head)
+  constexpr int kHpw = 256 / kTph;       // heads per workgroup
+  static_assert(kHpw * kTph == 256, "head_dim 64 or 128");
+  __shared__ int64_t s_slot[16];
+  __shared__ __align__(16) uint16_t s_v[kHpw][D][16];
+
+  const uint32_t hgroups = (g.n_kv_heads + kHpw - 1) / kHpw;
+  const uint32_t win = blockIdx.x / hgroups, hg = blockIdx.x % hgroups;
+  const uint32_t hl = threadIdx.x / kTph, u = threadIdx.x % kTph;
+  const uint32_t h = hg * kHpw + hl;
+  const bool head_ok = h < g.n_kv_heads;
+  const uint64_t cap = g.num_blocks * 16u;
+  if (threadIdx.x < 16) {
+    const uint64_t t = (uint64_t)win * 16u + threadIdx.x;
+    int64_t sl = t < n_tokens ? slots[t] : -1;
+    if (sl >= 0 && (uint64_t)sl >= cap) {
+      raise_fault(g.fault, kFaultSlot);
+      sl = -1;
+    }
+    s_slot[threadIdx.x] = sl;
+  }
+  __syncthreads();
+
+  const uint32_t c = u / 16u, o = u % 16u;
+  const int64_t slot = s_slot[o];
+  uint32_t ve[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (slot >= 0 && head_ok) {
+    const uint64_t row = ((uint64_t)win * 16u + o) * g.n_kv_heads + h;
+    const float* ks = k + row * D + c * 8u;
+    const float* vs = v + row * D + c * 8u;
+    const float4 a = *(const float4*)ks, b = *(const float4*)(ks + 4);
+    const float4 x = *(const float4*)vs, y = *(const float4*)(vs + 4);
+    uint8_t* kt = tile_ptr(g, (uint64_t)slot / 16u, layer, 0, h);
+    *(uint4*)(kt + ((uint64_t)c * 16u + (uint64_t)slot % 16u) * 16u) =
+        make_uint4(encode_f16(a.x, g.rounding) | (encode_f16(a.y, g.rounding) << 16),
+                   encode_f16(a.z, g.rounding) | (encode_f16(a.w, g.rounding) << 16),
+                   encode_f16(b.x, g.rounding) | (encode_f16(b.y, g.rounding) << 16),
+                   encode_f16(b.z, g.rounding) | (encode_f16(b.w, g.rounding) << 16));
+    ve[0] = encode_f16(x.x, g.rounding); ve[1] = encode_f16(x.y, g.rounding);
+    ve[2] = encode_f16(x.z, g.rounding); ve[3] = encode_f16(x.w, g.rounding);
+    ve[4] = encode_f16(y.x, g.rounding); ve[5] = encode_f16(y.y, g.rounding);
+    ve[6] = encode_f16(y.z, g.rounding); ve[7] = encode_f16(y.w, g.rounding);
+    bool nf = false;
+#pragma unroll
+    for (int e = 0; e < 8; e++) nf = nf || f16_nonfinite(ve[e]);
+    if (nf) mark_nonfinite_v(g.fault);  // chunked prefill then takes its leak-safe instance
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) s_v[hl][c * 8u + e][o] = (uint16_t)ve[e];
+  __syncthreads();
+
+  if (!head_ok) return;
+  // V row d of each destination tile. The window's tokens split into segments: maximal
+  // runs of consecutive slots inside one 8-aligned group of a block (a whole group when
+  // the window is aligned with the blocks, else two or three per group where a sequence
+  // begins mid-window). Thread (d, hh) stores the segments that start at its tokens
+  // hh*8 .. hh*8+7 with the widest aligned stores the run allows.
+  const uint32_t d = u / 2u, hh = u % 2u;
+  const uint16_t* vrow = s_v[hl][d];
+  for (uint32_t i = hh * 8u; i < hh * 8u + 8u; i++) {
+    const int64_t s0 = s_slot[i];
+    if (s0 < 0 || (i > 0 && s0 % 8 != 0 && s_slot[i - 1] == s0 - 1)) continue;
+    uint32_t len = 1;
+    while (i + len < 16u && (s0 + len) % 8 != 0 && s_slot[i + len] == s0 + (int64_t)len) len++;
+    uint8_t* row = tile_ptr(g, (uint64_t)s0 / 16u, layer, 1, h) + (uint64_t)d * 32u;
+    uint32_t p = (uint32_t)(s0 % 16), j = i;
+    const uint32_t end = p + len;
+    while (p < end) {
+      const uint32_t n = end - p;
+      if (p % 8 == 0 && n >= 8) {
+        *(uint4*)(row + p * 2u) =
+            make_uint4(vrow[j] | ((uint32_t)vrow[j + 1] << 16), vrow[j + 2] | ((uint32_t)vrow[j + 3] << 16),
+                       vrow[j + 4] | ((uint32_t)vrow[j + 5] << 16), vrow[j + 6] | ((uint32_t)vrow[j + 7] << 16));
+        p += 8; j += 8;
+      } else if (p % 4 == 0 && n >= 4) {
+        *(uint2*)(row + p * 2u) =
+            make_uint2(vrow[j] | ((uint32_t)vrow[j + 1] << 16), vrow[j + 2] | ((uint32_t)vrow[j + 3] << 16));
+        p += 4; j += 4;
+      } else if (p % 2 == 0 && n >= 2) {
+        *(uint32_t*)(row + p * 2u) = vrow[j] | ((uint32_t)vrow[j + 1] << 16);
+        p += 2; j += 2;
+      } else {
+        *(uint16_t*)(row + p * 2u) = vrow[j];
+        p += 1; j += 1;
+      }
+    }
+  }
+}
+
 // Any head_dim, F32/F16 storage: one element per thread.
 __global__ void __launch_bounds__(256) append_scalar_kernel(Geom g, uint32_t layer,
                                                             const float* __restrict__ k,
@@ -469,6 +576,15 @@ hipError_t launch_append(const Geom& g, uint32_t layer, const float* k, const fl
       append_q8_kernel<true><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
     else
       append_q8_kernel<false><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
+  } else if (g.dtype == kDtypeF16 && g.block_size == 16 && (g.head_dim == 64 || g.head_dim == 128) &&
+             aligned) {
+    const uint32_t hpw = g.head_dim == 128 ? 1u : 2u;
+    const uint64_t wgs = ((uint64_t)n_tokens + 15u) / 16u * ((g.n_kv_heads + hpw - 1) / hpw);
+    if (wgs > 0x7fffffffull) return hipErrorInvalidValue;
+    if (g.head_dim == 128)
+      append_f16_tile_kernel<128><<<(uint32_t)wgs, 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
+    else
+      append_f16_tile_kernel<64><<<(uint32_t)wgs, 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
   } else if (g.dtype == kDtypeF16 && g.head_dim % 16 == 0 && aligned) {
     const uint64_t k_threads = (uint64_t)n_tokens * g.n_kv_heads * (g.head_dim / 8u);
     const uint64_t v_waves =

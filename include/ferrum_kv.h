@@ -213,8 +213,9 @@ int32_t fkv_block_refcount(const fkv_pool* pool, int32_t id, uint32_t* out);
 
 /* Append: the paged form of KvPool::append_layer (pool.rs:122-153).
  * k, v: device f32 [n_tokens][n_kv_heads][head_dim] (post-RoPE K, kv.rs:30-31).
- * slot_mapping: device int64 [n_tokens]; slot < 0 skips the token (padding).
- * F16 storage rounds with the pool's f16_rounding; Q8_0 quantises each 32-value
+ * slot_mapping: device int64 [n_tokens]; slot < 0 skips the token (padding). The
+ * slots of one call are distinct (a slot named twice ends up holding one of its
+ * tokens, which one unspecified). F16 storage rounds with the pool's f16_rounding; Q8_0 quantises each 32-value
  * run like Q8Activation::quantize_into (q8_dot.rs:35-61). */
 int32_t fkv_append(fkv_pool* pool, uint32_t layer, const float* k, const float* v,
                    const int64_t* slot_mapping, uint32_t n_tokens, void* stream);

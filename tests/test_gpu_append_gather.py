@@ -165,6 +165,49 @@ def test_append_gather_roundtrip_scattered(dtype, d):
             assert np.array_equal(ov.cpu().numpy().view(np.uint8), tv.view(np.uint8))
 
 
+@pytest.mark.parametrize("d,hkv", [(128, 2), (64, 3), (64, 2)])
+@pytest.mark.parametrize("rounding", [0, 1])
+def test_append_f16_runs_at_every_alignment(d, hkv, rounding):
+    """F16 append of slot mappings whose runs of consecutive slots start at every offset
+    of a block and at every position of a 16-token window: chunks of 1..40 tokens
+    continuing 0..15 tokens into a block, a descending run, random single slots, -1
+    padding, and a token count that leaves the last window partial. Bytes no token
+    names keep the fill pattern; all bit-exact against the oracle."""
+    from oracle import ref
+    rng = np.random.default_rng(d + hkv + rounding)
+    nblk = 160
+    pool, layout = make_pools(2, hkv, d, nblk, dtype=1, rounding=rounding)
+    pool.fill(0x5a)
+    want = np.full(layout.pool_bytes, 0x5a, np.uint8)
+    perm = rng.permutation(nblk)
+    parts, b = [], 0
+    for start in range(16):
+        n = int(rng.integers(1, 41))
+        nb = (start + n + 15) // 16
+        blocks = perm[b: b + nb]
+        b += nb
+        pos = np.arange(start, start + n)
+        parts.append(blocks[pos // 16].astype(np.int64) * 16 + pos % 16)
+        if start % 5 == 0:
+            parts.append(np.array([-1], np.int64))
+    rest = perm[b: b + 4].astype(np.int64)
+    parts.append((rest[0] * 16 + np.arange(16))[::-1])      # descending run
+    parts.append(rng.permutation(np.concatenate([rest[1] * 16 + np.arange(16),
+                                                 rest[2] * 16 + np.arange(16)]))[:23])
+    parts.append(rest[3] * 16 + np.array([3, 4, 5, 9, 10, 15]))
+    slots = np.concatenate(parts)
+    assert slots.size % 16 != 0 and np.unique(slots[slots >= 0]).size == (slots >= 0).sum()
+    for layer in range(2):
+        k = rng.standard_normal((slots.size, hkv, d), dtype=np.float32)
+        v = rng.standard_normal((slots.size, hkv, d), dtype=np.float32)
+        pool.append(layer, to_dev(k), to_dev(v), to_dev(slots))
+        ref.append(layout, want, layer, k, v, slots)
+    got = pool.read()
+    mism = np.flatnonzero(got != want)
+    assert mism.size == 0, f"{mism.size} bytes differ, first at {mism[:4]}"
+    assert pool.take_fault_flags() == 0
+
+
 def test_append_out_of_range_slot_is_skipped_and_flagged():
     from oracle import ref
     pool, layout = make_pools(1, 1, 64, 4)
