@@ -578,6 +578,15 @@ def run_c3(args, torch, fa, lib, dev):
     max_pre_ctx = int(pre_prior.max() + chunk * (W + K))
     h = ctypes.c_void_p(pool.handle)
     scale = fa.default_scale(d)
+    pre_ws_bytes = pool.prefill_workspace_bytes(hq, n_pre, chunk, max_pre_ctx)
+    pre_ws = torch.empty(max(pre_ws_bytes, 1), dtype=torch.uint8, device=dev)
+
+    def prefill(t, l, sp):
+        fa.errors.check(lib.fkv_prefill_attention(
+            h, l, hq, qp[l].data_ptr(), op[l].data_ptr(), tab_pre.data_ptr(),
+            tab_pre.shape[1], pre_ctx[t].data_ptr(), q_lens.data_ptr(), q_offs.data_ptr(),
+            n_pre, chunk, max_pre_ctx, scale, pre_ws.data_ptr() if pre_ws_bytes else None,
+            pre_ws_bytes, sp))
 
     def step(t, sp):
         cl = dl.ctx_step_d[t].data_ptr()
@@ -588,10 +597,7 @@ def run_c3(args, torch, fa, lib, dev):
                 dl.max_ctx, scale, dl.ws.data_ptr(), dl.ws_bytes, sp))
             fa.errors.check(lib.fkv_append(h, l, kp[l].data_ptr(), vp[l].data_ptr(),
                                            pre_slots[t].data_ptr(), n_pre * chunk, sp))
-            fa.errors.check(lib.fkv_prefill_attention(
-                h, l, hq, qp[l].data_ptr(), op[l].data_ptr(), tab_pre.data_ptr(),
-                tab_pre.shape[1], pre_ctx[t].data_ptr(), q_lens.data_ptr(), q_offs.data_ptr(),
-                n_pre, chunk, max_pre_ctx, scale, sp))
+            prefill(t, l, sp)
 
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
@@ -607,6 +613,20 @@ def run_c3(args, torch, fa, lib, dev):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     assert pool.take_fault_flags() == 0
+    # chunked-prefill attention alone over the timed steps' chunks (it reads the pool
+    # only, so the calls can run again): 4 * D * Hq flops per (query, key) pair
+    p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    p0.record(stream)
+    for i in range(K):
+        for l in range(L):
+            prefill(W + i, l, sp)
+    p1.record(stream)
+    torch.cuda.synchronize()
+    assert pool.take_fault_flags() == 0
+    pre_us = p0.elapsed_time(p1) * 1e3 / (K * L)
+    pairs = sum(int((pre_prior + (W + i) * chunk).sum()) * chunk + n_pre * chunk * (chunk + 1) // 2
+                for i in range(K)) / K
+    pre_flop = 4.0 * d * hq * pairs
     # decode-only rate from a separate region of back-to-back fused decode calls
     dw, dms = dl.run(0, K)
     e = 2.0
@@ -629,6 +649,12 @@ def run_c3(args, torch, fa, lib, dev):
     res["pct_of_hbm_peak"] = round(100 * res["value"] / HBM_PEAK_GBS, 2)
     res["decode_only_ms_per_step"] = round(dw * 1e3 / K, 4)
     res["append_tokens_per_s"] = round((n_dec + n_pre * chunk) * K / wall, 1)
+    res["prefill_attention"] = {
+        "kernel": "attn_prefill_kernel (+ attn_prefill_combine_kernel for split key ranges)",
+        "us_per_call": round(pre_us, 2), "gflop_per_call": round(pre_flop / 1e9, 3),
+        "tflops": round(pre_flop / (pre_us * 1e-6) / 1e12, 1),
+        "flop_count": "4 * head_dim * n_heads per (query, key) pair",
+        "workspace_bytes": int(pre_ws_bytes)}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args, pool, dl.tables, dl.ctx_step[K - 1],
                                            dl.q[L - 1].cpu().numpy(), dl.out[L - 1].cpu().numpy(),

@@ -121,8 +121,10 @@ SIGNATURES = {
     "fkv_rope_append_decode_attention": (i32, [c_void_p, u32, u32, u32, f32, c_void_p, c_void_p,
                                                c_void_p, c_void_p, c_void_p, u32, c_void_p, u32,
                                                u32, f32, c_void_p, u64, c_void_p]),
+    "fkv_prefill_attention_workspace_size": (i32, [c_void_p, u32, u32, u32, u32, P(u64)]),
     "fkv_prefill_attention": (i32, [c_void_p, u32, u32, c_void_p, c_void_p, c_void_p, u32,
-                                    c_void_p, c_void_p, c_void_p, u32, u32, u32, f32, c_void_p]),
+                                    c_void_p, c_void_p, c_void_p, u32, u32, u32, f32, c_void_p,
+                                    u64, c_void_p]),
     "fkv_device_copy": (i32, [c_void_p, c_void_p, u64, c_void_p]),
     "fkv_seqs_create": (i32, [c_void_p, P(c_void_p)]),
     "fkv_seqs_destroy": (i32, [c_void_p]),

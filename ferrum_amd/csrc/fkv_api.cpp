@@ -629,34 +629,63 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
                           workspace_bytes, stream, &rope);
 }
 
+// Argument checks shared by the prefill workspace query and the call.
+static int32_t check_prefill(const fkv_pool* pool, uint32_t n_heads, uint32_t n_seqs,
+                             uint32_t max_blocks_per_seq, uint32_t max_q_len,
+                             uint32_t max_ctx_len) {
+  int32_t st = check_attention(pool, n_heads, max_ctx_len);
+  if (st) return st;
+  if (pool->cfg.kv_dtype != FKV_DTYPE_F16 && pool->cfg.kv_dtype != FKV_DTYPE_Q8_0)
+    return fail(FKV_ERR_KERNEL, "prefill attention needs f16 or q8_0 kv");
+  if ((uint64_t)n_seqs * pool->cfg.n_kv_heads > 0x7fffffffull)
+    return fail(FKV_ERR_INVALID, "too many sequences");
+  if (max_q_len > max_ctx_len) return fail(FKV_ERR_INVALID, "max_q_len exceeds max_ctx_len");
+  const uint32_t tokens_per_tile = 16u / (n_heads / pool->cfg.n_kv_heads);
+  if (((uint64_t)max_q_len + tokens_per_tile - 1) / tokens_per_tile > 65535ull * 4u)
+    return fail(FKV_ERR_KERNEL, "prefill chunk too long");
+  (void)max_blocks_per_seq;
+  return FKV_OK;
+}
+
+int32_t fkv_prefill_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                             uint32_t n_seqs, uint32_t max_q_len,
+                                             uint32_t max_ctx_len, uint64_t* bytes_out) {
+  if (!pool || !bytes_out) return fail(FKV_ERR_INVALID, "null argument");
+  int32_t st = check_prefill(pool, n_heads, n_seqs, 0, max_q_len, max_ctx_len);
+  if (st) return st;
+  *bytes_out = (n_seqs == 0 || max_q_len == 0)
+                   ? 0
+                   : fkv::prefill_plan(pool->geom, n_heads, n_seqs, max_q_len, max_ctx_len).ws_bytes;
+  return ok();
+}
+
 int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,
                               float* out, const int32_t* block_tables,
                               uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
                               const int32_t* q_lens, const int64_t* q_offsets, uint32_t n_seqs,
                               uint32_t max_q_len, uint32_t max_ctx_len, float scale,
-                              void* stream) {
+                              void* workspace, uint64_t workspace_bytes, void* stream) {
   if (!pool) return fail(FKV_ERR_INVALID, "null argument");
   if (layer >= pool->cfg.n_layers) return fail(FKV_ERR_CACHE, "layer out of range");
-  int32_t st = check_attention(pool, n_heads, max_ctx_len);
+  int32_t st = check_prefill(pool, n_heads, n_seqs, max_blocks_per_seq, max_q_len, max_ctx_len);
   if (st) return st;
-  if (pool->cfg.kv_dtype != FKV_DTYPE_F16 && pool->cfg.kv_dtype != FKV_DTYPE_Q8_0)
-    return fail(FKV_ERR_KERNEL, "prefill attention needs f16 or q8_0 kv");
   if (n_seqs == 0 || max_q_len == 0) return ok();
   if (!q || !out || !block_tables || !ctx_lens || !q_lens || !q_offsets)
     return fail(FKV_ERR_INVALID, "null argument");
   if ((uintptr_t)q % 16 != 0) return fail(FKV_ERR_INVALID, "q must be 16-byte aligned");
-  if ((uint64_t)n_seqs * pool->cfg.n_kv_heads > 0x7fffffffull)
-    return fail(FKV_ERR_INVALID, "too many sequences");
   if ((uint64_t)max_ctx_len > (uint64_t)max_blocks_per_seq * pool->cfg.block_size)
     return fail(FKV_ERR_INVALID, "max_ctx_len exceeds the block table");
-  if (max_q_len > max_ctx_len) return fail(FKV_ERR_INVALID, "max_q_len exceeds max_ctx_len");
-  const uint32_t tokens_per_tile = 16u / (n_heads / pool->cfg.n_kv_heads);
-  if (((uint64_t)max_q_len + tokens_per_tile - 1) / tokens_per_tile > 65535ull * 4u)
-    return fail(FKV_ERR_KERNEL, "prefill chunk too long");
+  const fkv::PrefillPlan plan =
+      fkv::prefill_plan(pool->geom, n_heads, n_seqs, max_q_len, max_ctx_len);
+  if (workspace && workspace_bytes < plan.ws_bytes)
+    return fail(FKV_ERR_INVALID, "prefill workspace too small");
+  if ((uintptr_t)workspace % 16 != 0)
+    return fail(FKV_ERR_INVALID, "workspace must be 16-byte aligned");
   DeviceGuard dg(pool->cfg.device);
   FKV_HIP(fkv::launch_prefill_attention(pool->geom, layer, n_heads, q, out, block_tables,
                                         max_blocks_per_seq, ctx_lens, q_lens, q_offsets, n_seqs,
-                                        max_q_len, scale, (hipStream_t)stream),
+                                        max_q_len, scale, plan,
+                                        plan.ws_bytes ? workspace : nullptr, (hipStream_t)stream),
           "prefill_attention");
   return ok();
 }

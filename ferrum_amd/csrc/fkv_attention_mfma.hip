@@ -49,6 +49,8 @@
 #include <stdint.h>
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "fkv_device.h"
 #include "fkv_internal.h"
 
@@ -1393,7 +1395,10 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
   }
 }
 
-// Prefill versions of qk_block and softmax_block. The prefill kernel is bound by
+// Prefill versions of qk_block and softmax_block; qk_block_pf leaves the scores
+// without q's power-of-two scale (hscale), which softmax_step_pf applies inside its
+// exponent's fma (x * hscale is exact, so the sum is the one a separate product
+// would give). The prefill kernel is bound by
 // the VALU work around its MFMAs, so the work that is rare per block sits behind
 // wave-uniform branches: the lo-chain NaN repair (only when a score is NaN), the
 // causal mask (only on a block that crosses some column's causal end) and the
@@ -1405,7 +1410,7 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
 // and never written.
 template <int D>
 __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
-                                            const f16x8 (&ql)[D / 32], float hscale,
+                                            const f16x8 (&ql)[D / 32],
                                             const Lane& ln, bool live, bool full, int32_t t0,
                                             int32_t end, float (&s)[4]) {
   f32x4 ah = {0.0f, 0.0f, 0.0f, 0.0f}, al = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1428,12 +1433,12 @@ __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16
   }
   if (live && full) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) s[r] = x[r] * hscale;
+    for (int r = 0; r < 4; r++) s[r] = x[r];
   } else {
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const bool ok = ln.real && live && t0 + ln.grp * 4 + r < end;
-      s[r] = ok ? x[r] * hscale : -__builtin_inff();
+      s[r] = ok ? x[r] : -__builtin_inff();
     }
   }
 }
@@ -1442,18 +1447,18 @@ __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16
 // accumulators and one rare-path ballot per NB blocks instead of per block. ef gets the
 // f32 weights (the exact Q8_0 P.V forms scale x weight from them), pw their binary16.
 template <int D, int NB>
-__device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], const Lane& ln,
-                                                Accum<D>& st, f16x4 (&pw)[NB],
+__device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], float hscale,
+                                                const Lane& ln, Accum<D>& st, f16x4 (&pw)[NB],
                                                 float (&ef)[NB][4]) {
   float lmax = s[0][0];
 #pragma unroll
   for (int b = 0; b < NB; b++)
 #pragma unroll
     for (int r = 0; r < 4; r++) lmax = __builtin_fmaxf(lmax, s[b][r]);
+  lmax *= hscale;
   const bool bad =
       ln.real && (!(lmax <= st.m_ref + kRescaleLog2) || !__builtin_isfinite(st.m_ref));
-  float ar[4] = {1.0f, 1.0f, 1.0f, 1.0f};
-  if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+  if (__builtin_amdgcn_ballot_w64(bad) != 0) {  // some column's max moved: rescale
     float x = lmax;
     x = __builtin_fmaxf(x, __shfl_xor(x, 16));
     x = __builtin_fmaxf(x, __shfl_xor(x, 32));
@@ -1461,19 +1466,20 @@ __device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], const L
     const float alpha = (mn == -__builtin_inff()) ? 1.0f : __builtin_amdgcn_exp2f(st.m_ref - mn);
     st.l_part *= alpha;
     st.m_ref = mn;
+    float ar[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) ar[r] = __shfl(alpha, ln.grp * 4 + r);
+#pragma unroll
+    for (int m = 0; m < D / 16; m++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) st.acc[m][r] *= ar[r];
   }
-#pragma unroll
-  for (int m = 0; m < D / 16; m++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) st.acc[m][r] *= ar[r];
   if (__builtin_amdgcn_ballot_w64(ln.real && st.m_ref == -__builtin_inff()) == 0) {
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const float e = __builtin_amdgcn_exp2f(s[b][r] - st.m_ref);
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[b][r], hscale, -st.m_ref));
         st.l_part += e;
         ef[b][r] = e;
         pw[b][r] = (_Float16)e;
@@ -1485,7 +1491,8 @@ __device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], const L
 #pragma unroll
       for (int r = 0; r < 4; r++) {
         const float sv = s[b][r];
-        const float e = dead ? (sv != sv ? sv : 0.0f) : __builtin_amdgcn_exp2f(sv - st.m_ref);
+        const float e = dead ? (sv != sv ? sv : 0.0f)
+                             : __builtin_amdgcn_exp2f(__builtin_fmaf(sv, hscale, -st.m_ref));
         st.l_part += e;
         ef[b][r] = e;
         pw[b][r] = (_Float16)e;
@@ -1533,7 +1540,7 @@ __device__ __forceinline__ bool v_nonfinite_in(const u32x2_t (&vr)[D / 16], cons
 // the step) while the waves compute the current step. Per step a wave does both
 // blocks' QK, one softmax update over their 32 keys, then both P.V products.
 //
-// Storage: F16 tiles are staged as loaded except V, whose 8-byte chunks are
+// Storage: F16 tiles are staged as loaded except V, whose 16-byte units are
 // XOR-swizzled by row so the P.V operand reads hit distinct banks. Q8_0 tiles are
 // staged as loaded (their operand order reads conflict-free) and converted by the
 // decode kernel's BlockRegs; over a pool marked as holding scales of 512 or more
@@ -1558,12 +1565,48 @@ constexpr int prefill_tile_bytes() {
 
 enum : int { kPfFast = 0, kPfExact = 1, kPfLeakSafe = 2 };
 
+// One sequence of a prefill launch: the context clamped to the block table, the
+// number of queries computed (q_lens[s] clamped to the context and to max_q_len) and
+// the position of query 0 (from the stated q_len). The kernel and its combine agree
+// on these through this function.
+struct PfSeq {
+  int32_t ctx, ql, p0;
+  bool clamped;  // ctx or q_len was out of range: FKV_FAULT_CTX_RANGE
+};
+__device__ __forceinline__ PfSeq pf_seq(const int32_t* ctx_lens, const int32_t* q_lens,
+                                        uint32_t seq, int32_t cap, uint32_t max_q_len) {
+  const int32_t ctx = ctx_lens[seq], ql = q_lens[seq];
+  const int32_t c = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
+  const int32_t qc = ql < 0 ? 0 : (ql > c ? c : ql);
+  const int32_t nq = qc < (int32_t)max_q_len ? qc : (int32_t)max_q_len;
+  return PfSeq{c, nq, c - qc, ctx != c || ql != nq};
+}
+
+// Blocks the workgroup of tiles tile0 .. tile0 + 3 streams (up to its furthest causal
+// end), and the number of key-range pieces it is cut into: pieces of about
+// split_blocks blocks (split_blocks 0: one piece), at most max_splits.
+__device__ __forceinline__ int32_t pf_wg_blocks(const PfSeq& sq, int32_t tile0, int32_t T) {
+  const int32_t last = (tile0 + kAttnWaves) * T - 1 < sq.ql - 1 ? (tile0 + kAttnWaves) * T - 1 : sq.ql - 1;
+  return (sq.p0 + last + 1 + B - 1) / B;
+}
+__device__ __forceinline__ int32_t pf_pieces(int32_t nblk, uint32_t split_blocks,
+                                             uint32_t max_splits) {
+  if (split_blocks == 0) return 1;
+  const int32_t n = (nblk + (int32_t)split_blocks - 1) / (int32_t)split_blocks;
+  return n < 1 ? 1 : (n > (int32_t)max_splits ? (int32_t)max_splits : n);
+}
+
 template <int DT, int D, int MODE>
-__global__ void __launch_bounds__(256) attn_prefill_kernel(
+// The fast instances hold 4 waves per SIMD (at most 128 VGPRs): the kernel is bound by
+// instruction issue, and the fourth wave fills the others' dependency stalls.
+__global__ void __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
     const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ q_lens,
-    const int64_t* __restrict__ q_offsets, uint32_t max_q_len, float scale) {
+    const int64_t* __restrict__ q_offsets, uint32_t max_q_len, float scale,
+    uint32_t split_blocks, uint32_t max_splits, float* __restrict__ ws_o,
+    float* __restrict__ ws_ml) {
   constexpr int NC = D / 32, NM = D / 16;
   constexpr int kStep = 2;  // blocks per softmax step
   constexpr int kTile = prefill_tile_bytes<DT, D>();
@@ -1588,25 +1631,21 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int32_t T = 16 / (int32_t)G;  // query tokens per wave tile
-  const int32_t cap = (int32_t)(max_blocks * B);
-  int32_t ctx = ctx_lens[seq];
-  int32_t ql = q_lens[seq];
-  int32_t p0;  // position of query 0
-  {
-    const int32_t c = ctx < 0 ? 0 : (ctx > cap ? cap : ctx);
-    const int32_t qc = ql < 0 ? 0 : (ql > c ? c : ql);
-    p0 = c - qc;
-    // The grid holds max_q_len queries a sequence: past that the first max_q_len are
-    // computed, at the positions the caller gave them, and the fault is raised.
-    const int32_t nq = qc < (int32_t)max_q_len ? qc : (int32_t)max_q_len;
-    if (ctx != c || ql != nq) {
-      if (blockIdx.y == 0 && threadIdx.x == 0 && kvh == 0) raise_fault(g.fault, kFaultCtx);
-      ctx = c;
-      ql = nq;  // from here: the number of queries computed
-    }
-  }
+  const PfSeq sq = pf_seq(ctx_lens, q_lens, seq, (int32_t)(max_blocks * B), max_q_len);
+  // The grid holds max_q_len queries a sequence: past that the first max_q_len are
+  // computed, at the positions the caller gave them, and the fault is raised.
+  if (sq.clamped && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0 && kvh == 0)
+    raise_fault(g.fault, kFaultCtx);
+  const int32_t ql = sq.ql, p0 = sq.p0;  // queries computed; position of query 0
   const int32_t tile0 = (int32_t)blockIdx.y * kAttnWaves;  // first tile of the workgroup
   if (tile0 * T >= ql) return;                              // uniform over the workgroup
+  // Key blocks [jbeg, jend): piece blockIdx.z of the workgroup's range, whose length
+  // follows its furthest causal end (pieces of a range differ by at most one block).
+  const int32_t nblk = pf_wg_blocks(sq, tile0, T);
+  const int32_t npiece = pf_pieces(nblk, split_blocks, max_splits);
+  if ((int32_t)blockIdx.z >= npiece) return;
+  const int32_t jbeg = (int32_t)blockIdx.z * nblk / npiece;
+  const int32_t jend = ((int32_t)blockIdx.z + 1) * nblk / npiece;
   const int32_t tile = tile0 + wave;
   const bool wave_on = tile * T < ql;
 
@@ -1622,9 +1661,6 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   const int32_t end_min = p0 + tile * T + 1;             // nearest end: blocks before it
                                                          // need no causal mask
   const int32_t nblk_w = (end_max + B - 1) / B;
-  // the workgroup's furthest end: its last tile's last query (or the chunk's last)
-  const int32_t wg_last = (tile0 + kAttnWaves) * T - 1 < ql - 1 ? (tile0 + kAttnWaves) * T - 1 : ql - 1;
-  const int32_t nblk = (p0 + wg_last + 1 + B - 1) / B;
   const int64_t qrow0 = q_offsets[seq];
   auto row_of = [&](int32_t colv) {  // q/out row of column colv (clamped for padding)
     const int32_t j = tile * T + colv / (int32_t)G;
@@ -1660,14 +1696,11 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
         const uint32_t off = c * 16u;
         uint8_t* dst = s_kv[buf][slot];
         if (DT == kDtypeF16 && off >= (uint32_t)kTile) {
-          // V rows (one dim, 16 tokens = four 8-byte chunks) with chunk c at
-          // c ^ ((dim >> 2) & 3); a 16-byte pair of chunks stays one aligned unit,
-          // its halves swapped when the swizzle is odd.
+          // V rows (one dim, 16 tokens = two 16-byte units) with unit u at
+          // u ^ ((dim >> 3) & 1): the P.V operand reads (8 bytes a lane, 16 dims a
+          // lane group) then hit 16 distinct bank pairs, and a staged unit stays whole.
           const uint32_t v = off - kTile, dim = v / 32u, unit = (v % 32u) / 16u;
-          const uint32_t sw = (dim >> 2) & 3u;
-          const uint4 x = stg[i];
-          *(uint4*)&dst[kTile + dim * 32u + ((unit ^ (sw >> 1)) * 16u)] =
-              (sw & 1u) ? make_uint4(x.z, x.w, x.x, x.y) : x;
+          *(uint4*)&dst[kTile + dim * 32u + ((unit ^ ((dim >> 3) & 1u)) * 16u)] = stg[i];
         } else {
           *(uint4*)&dst[off] = stg[i];
         }
@@ -1679,12 +1712,14 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   bool nlv[kStep] = {false, false};  // and of the next step
 #pragma unroll
   for (int bb = 0; bb < kStep; bb++) {
-    if (bb < nblk) {
-      lv[bb] = load_block(bb);
+    if (jbeg + bb < jend) {
+      lv[bb] = load_block(jbeg + bb);
       store_block(0, bb);
     }
   }
-  if (kStep < nblk) nlv[0] = load_block(kStep);
+  if (jbeg + kStep < jend) nlv[0] = load_block(jbeg + kStep);
+  // blocks this wave computes: the piece's, up to the wave's furthest causal end
+  const int32_t jw_end = nblk_w < jend ? nblk_w : jend;
   f16x8 qh[NC], qlo[NC];
   float hscale;
   prep_q<D>(q + row_of(ln.real ? ln.col : 0), ln, scale * kLog2e, qh, qlo, hscale);
@@ -1692,31 +1727,31 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   st.reset();
   __syncthreads();
 
-  for (int32_t j0 = 0, buf = 0; j0 < nblk; j0 += kStep, buf ^= 1) {
-    const bool more = j0 + kStep < nblk;      // the workgroup has a next step
-    const bool more2 = j0 + kStep + 1 < nblk;  // with a second block
+  for (int32_t j0 = jbeg, buf = 0; j0 < jend; j0 += kStep, buf ^= 1) {
+    const bool more = j0 + kStep < jend;      // the workgroup has a next step
+    const bool more2 = j0 + kStep + 1 < jend;  // with a second block
     float sc[kStep][4];
 #pragma unroll
     for (int bb = 0; bb < kStep; bb++) {
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
       const uint8_t* ks = s_kv[buf][bb];
-      if (j < nblk_w) {  // wave-uniform: blocks past the wave's tile are skipped
+      if (j < jw_end) {  // wave-uniform: blocks past the wave's tile are skipped
         if constexpr (DT == kDtypeF16) {
           uint4 kr[NC];
 #pragma unroll
           for (int c = 0; c < NC; c++)
             kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
-          qk_block_pf<D>(kr, qh, qlo, hscale, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
+          qk_block_pf<D>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
         } else {
           BlockRegs<kDtypeQ8, D> rg;
           rg.template load_k_tile<true>(ks, ln);
           if constexpr (EXACT) {
-            qk_block_q8x<D>(rg, qh, qlo, hscale, ln, lv[bb], t0, end_col, sc[bb]);
+            qk_block_q8x<D>(rg, qh, qlo, 1.0f, ln, lv[bb], t0, end_col, sc[bb]);
           } else {
             uint4 kr[NC];
             rg.k_operand(kr);
-            qk_block_pf<D>(kr, qh, qlo, hscale, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
+            qk_block_pf<D>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
           }
         }
       } else {
@@ -1730,19 +1765,19 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
     }
     f16x4 pw[kStep];
     float ef[kStep][4];
-    softmax_step_pf<D, kStep>(sc, ln, st, pw, ef);
+    softmax_step_pf<D, kStep>(sc, hscale, ln, st, pw, ef);
 #pragma unroll
     for (int bb = 0; bb < kStep; bb++) {
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
-      if (j < nblk_w && lv[bb]) {
+      if (j < jw_end && lv[bb]) {
         const uint8_t* vs = s_kv[buf][bb] + kTile;
         if constexpr (DT == kDtypeF16) {
           u32x2_t vr[NM];
 #pragma unroll
           for (int m = 0; m < NM; m++) {
             const uint32_t dim = (uint32_t)(m * 16 + ln.col);
-            vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((uint32_t)ln.grp ^ ((dim >> 2) & 3u)) * 8u));
+            vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((((uint32_t)ln.grp >> 1) ^ ((dim >> 3) & 1u)) * 16u) + ((uint32_t)ln.grp & 1u) * 8u));
           }
           // Leak-safe instance: a block where a non-finite V lies past the tile's
           // nearest causal end takes one P.V per query token jt of the tile, V cut at
@@ -1761,7 +1796,7 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
 #pragma unroll
               for (int m = 0; m < NM; m++) {
                 const uint32_t dim = (uint32_t)(m * 16 + ln.col);
-                vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((uint32_t)ln.grp ^ ((dim >> 2) & 3u)) * 8u));
+                vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((((uint32_t)ln.grp >> 1) ^ ((dim >> 3) & 1u)) * 16u) + ((uint32_t)ln.grp & 1u) * 8u));
               }
               mask_v_tail<D>(vr, ln, t0, p0 + tile * T + jt + 1);
 #pragma unroll
@@ -1792,7 +1827,7 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
       __syncthreads();
       lv[0] = nlv[0];
       lv[1] = more2 ? nlv[1] : false;
-      if (j0 + 2 * kStep < nblk) nlv[0] = load_block(j0 + 2 * kStep);
+      if (j0 + 2 * kStep < jend) nlv[0] = load_block(j0 + 2 * kStep);
     }
   }
   if (!wave_on) return;
@@ -1800,19 +1835,78 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(
   float lsum = st.l_part;
   lsum += __shfl_xor(lsum, 16);
   lsum += __shfl_xor(lsum, 32);
+  // Piece partials: slot ((sk * gridDim.y + y) * max_splits + z) holds the workgroup's
+  // 64 columns (wave * 16 + column) x (unnormalised output [D], then max and sum in
+  // the log2 domain).
+  const uint64_t pslot = (((uint64_t)sk * gridDim.y + blockIdx.y) * max_splits + blockIdx.z) *
+                             (uint64_t)(kAttnWaves * 16) + (uint64_t)wave * 16u;
   // accumulator row r of this lane is column grp*4 + r; its M and L live in lane grp*4 + r
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const int c = ln.grp * 4 + r;
     const float M = __shfl(st.m_ref, c);
-    const float inv = 1.0f / __shfl(lsum, c);
+    const float L = __shfl(lsum, c);
     const int32_t jc = tile * T + c / (int32_t)G;
     if (c < T * (int32_t)G && jc < ql) {
-      float* o = out + row_of(c);
+      // one piece: the normalised output; several: this piece's partial (the same
+      // stores, selected, so the accumulators need no second path)
+      const bool whole = npiece == 1;
+      const float inv = 1.0f / L;
+      float* o = whole ? out + row_of(c) : ws_o + (pslot + (uint64_t)c) * D;
 #pragma unroll
       for (int m = 0; m < NM; m++)
-        o[m * 16 + ln.col] = __builtin_isfinite(M) ? st.acc[m][r] * inv : 0.0f;
+        o[m * 16 + ln.col] =
+            whole ? (__builtin_isfinite(M) ? st.acc[m][r] * inv : 0.0f) : st.acc[m][r];
+      if (!whole && ln.col == 0) {
+        ws_ml[(pslot + (uint64_t)c) * 2] = M;
+        ws_ml[(pslot + (uint64_t)c) * 2 + 1] = L;
+      }
     }
+  }
+}
+
+// Merges the key-range pieces of every prefill workgroup cut into more than one:
+// out = sum_z 2^(m_z - M) o_z / sum_z 2^(m_z - M) l_z with M = max_z m_z (0 where M is
+// not finite, as the single-piece path writes). Grid (n_seqs * n_kv_heads, tile
+// groups): one workgroup per prefill workgroup, thread t on dim t % D of columns
+// t / D, t / D + 256 / D, ...
+template <int D>
+__global__ void __launch_bounds__(256) attn_prefill_combine_kernel(
+    uint32_t n_kv_heads, uint32_t n_heads, uint32_t G, uint32_t max_blocks,
+    const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ q_lens,
+    const int64_t* __restrict__ q_offsets, uint32_t max_q_len, uint32_t split_blocks,
+    uint32_t max_splits, const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
+    float* __restrict__ out) {
+  const uint32_t sk = blockIdx.x;
+  const uint32_t seq = sk / n_kv_heads, kvh = sk % n_kv_heads;
+  const int32_t T = 16 / (int32_t)G;
+  const PfSeq sq = pf_seq(ctx_lens, q_lens, seq, (int32_t)(max_blocks * B), max_q_len);
+  const int32_t tile0 = (int32_t)blockIdx.y * kAttnWaves;
+  if (tile0 * T >= sq.ql) return;
+  const int32_t npiece = pf_pieces(pf_wg_blocks(sq, tile0, T), split_blocks, max_splits);
+  if (npiece <= 1) return;
+  const uint64_t slot0 = ((uint64_t)sk * gridDim.y + blockIdx.y) * max_splits;
+  constexpr uint32_t kCols = kAttnWaves * 16, kStride = 256 / D;
+  const uint32_t d = threadIdx.x % D;
+  const int64_t qrow0 = q_offsets[seq];
+  for (uint32_t cc = threadIdx.x / D; cc < kCols; cc += kStride) {
+    const int32_t c = (int32_t)(cc % 16u);
+    const int32_t jc = (tile0 + (int32_t)(cc / 16u)) * T + c / (int32_t)G;
+    if (c >= T * (int32_t)G || jc >= sq.ql) continue;
+    float M = -__builtin_inff();
+    for (int32_t z = 0; z < npiece; z++)
+      M = __builtin_fmaxf(M, ws_ml[((slot0 + z) * kCols + cc) * 2]);
+    float o = 0.0f, L = 0.0f;
+    if (__builtin_isfinite(M)) {
+      for (int32_t z = 0; z < npiece; z++) {
+        const uint64_t i = (slot0 + z) * kCols + cc;
+        const float w = __builtin_amdgcn_exp2f(ws_ml[i * 2] - M);
+        o = __builtin_fmaf(w, ws_o[i * D + d], o);
+        L = __builtin_fmaf(w, ws_ml[i * 2 + 1], L);
+      }
+    }
+    const uint64_t row = ((uint64_t)(qrow0 + jc) * n_heads + (uint64_t)kvh * G + (uint64_t)(c % (int32_t)G)) * D;
+    out[row + d] = __builtin_isfinite(M) ? o * (1.0f / L) : 0.0f;
   }
 }
 
@@ -1871,20 +1965,62 @@ hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_hea
   return hipGetLastError();
 }
 
+PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_q_len,
+                         uint32_t max_ctx_len) {
+  PrefillPlan p{};
+  const uint32_t G = n_heads / g.n_kv_heads;
+  const uint32_t T = 16 / G;
+  const uint64_t tiles = ((uint64_t)max_q_len + T - 1) / T;
+  p.tile_groups = (uint32_t)((tiles + kAttnWaves - 1) / kAttnWaves);
+  const uint64_t max_nblk = ((uint64_t)max_ctx_len + B - 1) / B;
+  // Pieces pay only where the grid leaves workgroup slots idle (each piece restages q
+  // and writes a partial): split so that about twice the slots have work, into pieces
+  // of at least kPrefillMinPieceBlocks. FKV_PREFILL_SPLIT_BLOCKS sets the piece length
+  // (0: no split).
+  uint64_t split = 0;
+  if (const char* e = getenv("FKV_PREFILL_SPLIT_BLOCKS")) {
+    split = strtoull(e, nullptr, 10);
+  } else {
+    int dev = 0, cus = 0;
+    const uint64_t wgs = (uint64_t)n_seqs * g.n_kv_heads * p.tile_groups;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        cus > 0 && wgs < (uint64_t)cus * kPrefillWgsPerCu) {
+      const uint64_t want = ((uint64_t)cus * kPrefillWgsPerCu * 2 + wgs - 1) / wgs;
+      split = std::max<uint64_t>(kPrefillMinPieceBlocks, (max_nblk + want - 1) / want);
+    }
+  }
+  if (split == 0 || max_nblk <= split) return p;  // one piece per workgroup
+  split = std::max<uint64_t>(split, (max_nblk + kPrefillMaxSplits - 1) / kPrefillMaxSplits);
+  if (max_nblk <= split) return p;
+  p.split_blocks = (uint32_t)split;
+  p.max_splits = (uint32_t)((max_nblk + split - 1) / split);
+  const uint64_t slots = (uint64_t)n_seqs * g.n_kv_heads * p.tile_groups * p.max_splits *
+                         (uint64_t)(kAttnWaves * 16);
+  p.ws_o_floats = slots * g.head_dim;
+  p.ws_bytes = (p.ws_o_floats + slots * 2) * sizeof(float);
+  return p;
+}
+
 hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
                                     const float* q, float* out, const int32_t* tables,
                                     uint32_t max_blocks, const int32_t* ctx_lens,
                                     const int32_t* q_lens, const int64_t* q_offsets,
                                     uint32_t n_seqs, uint32_t max_q_len, float scale,
-                                    hipStream_t s) {
+                                    const PrefillPlan& plan, void* workspace, hipStream_t s) {
   const uint32_t G = n_heads / g.n_kv_heads;
-  const uint32_t T = 16 / G;
-  const uint32_t tiles = (max_q_len + T - 1) / T;
-  dim3 grid(n_seqs * g.n_kv_heads, (tiles + kAttnWaves - 1) / kAttnWaves);
+  // Without a workspace every workgroup is one piece.
+  const bool split = plan.split_blocks != 0 && workspace != nullptr;
+  const uint32_t split_blocks = split ? plan.split_blocks : 0u;
+  const uint32_t max_splits = split ? plan.max_splits : 1u;
+  float* ws_o = split ? (float*)workspace : nullptr;
+  float* ws_ml = split ? ws_o + plan.ws_o_floats : nullptr;
+  dim3 grid(n_seqs * g.n_kv_heads, plan.tile_groups, max_splits);
 #define FKV_LAUNCH_PF(DT_, D_, X_)                                                          \
   attn_prefill_kernel<DT_, D_, X_><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
                                                         max_blocks, ctx_lens, q_lens,         \
-                                                        q_offsets, max_q_len, scale)
+                                                        q_offsets, max_q_len, scale,          \
+                                                        split_blocks, max_splits, ws_o, ws_ml)
   // The fast instance, then the one for pools whose marks say the fast one cannot
   // compute them: Q8_0 the exact instance (a scale of 512 or more was stored), F16 the
   // leak-safe one (an Inf/NaN V was stored). Each exits at once where the other works.
@@ -1906,6 +2042,19 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
     else FKV_LAUNCH_PF(kDtypeF16, 64, kPfLeakSafe);
   }
 #undef FKV_LAUNCH_PF
+  e = hipGetLastError();
+  if (e != hipSuccess || !split) return e;
+  const dim3 cgrid(n_seqs * g.n_kv_heads, plan.tile_groups);
+  if (g.head_dim == 128)
+    attn_prefill_combine_kernel<128><<<cgrid, 256, 0, s>>>(g.n_kv_heads, n_heads, G, max_blocks,
+                                                           ctx_lens, q_lens, q_offsets, max_q_len,
+                                                           split_blocks, max_splits, ws_o, ws_ml,
+                                                           out);
+  else
+    attn_prefill_combine_kernel<64><<<cgrid, 256, 0, s>>>(g.n_kv_heads, n_heads, G, max_blocks,
+                                                          ctx_lens, q_lens, q_offsets, max_q_len,
+                                                          split_blocks, max_splits, ws_o, ws_ml,
+                                                          out);
   return hipGetLastError();
 }
 

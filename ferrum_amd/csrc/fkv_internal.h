@@ -42,7 +42,8 @@ struct Geom {
   int32_t rounding;  // 0 nearest-even, 1 ties away
   uint32_t* fault;   // device words: [0] FKV_FAULT_* bits; [1] nonzero once a Q8_0
                      // scale of 512 or more was stored (sticky; q8_wide_scale);
-                     // [2], [3] chunked prefill's non-finite-V mark and its count
+                     // [2] nonzero once an F16 pool stored an Inf/NaN V (sticky;
+                     // f16_nonfinite); [3] unused
 };
 
 constexpr int kDtypeF32 = 0;
@@ -122,15 +123,33 @@ hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_hea
                                    uint32_t max_blocks, const int32_t* ctx_lens,
                                    uint32_t n_seqs, float scale, uint32_t n_waves,
                                    uint32_t* ws_pre, float* ws_o, float* ws_ml, hipStream_t s);
-// F16 chunked-prefill attention (fkv_attention_mfma.hip): query i of sequence s
-// is at position ctx_lens[s] - q_lens[s] + i and attends causally; q/out rows of
-// sequence s start at q_offsets[s]. Needs G <= 16.
+// Chunked-prefill attention (fkv_attention_mfma.hip), F16 or Q8_0 storage: query i
+// of sequence s is at position ctx_lens[s] - q_lens[s] + i and attends causally;
+// q/out rows of sequence s start at q_offsets[s]. Needs G <= 16.
+// A workgroup (16 / G queries per wave, 4 waves) whose key range is longer than
+// split_blocks blocks is cut into pieces of about equal length (at most max_splits),
+// each its own workgroup, whose partials a combine kernel merges; the plan splits
+// only grids smaller than the device's workgroup slots and sizes the workspace for
+// the longest context the call allows. With split_blocks 0 or no workspace, every
+// workgroup is one piece.
+constexpr uint64_t kPrefillWgsPerCu = 4;         // resident prefill workgroups per CU
+constexpr uint64_t kPrefillMinPieceBlocks = 64;  // shortest piece the plan makes
+constexpr uint64_t kPrefillMaxSplits = 32;
+struct PrefillPlan {
+  uint32_t tile_groups;   // grid.y: groups of 4 query tiles
+  uint32_t split_blocks;  // 0: no split
+  uint32_t max_splits;
+  uint64_t ws_o_floats;   // partial outputs, then (max, sum) pairs
+  uint64_t ws_bytes;
+};
+PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_q_len,
+                         uint32_t max_ctx_len);
 hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
                                     const float* q, float* out, const int32_t* tables,
                                     uint32_t max_blocks, const int32_t* ctx_lens,
                                     const int32_t* q_lens, const int64_t* q_offsets,
                                     uint32_t n_seqs, uint32_t max_q_len, float scale,
-                                    hipStream_t s);
+                                    const PrefillPlan& plan, void* workspace, hipStream_t s);
 // Merges split partials (m, l, o) per (sequence, query head) into out.
 hipError_t launch_attention_combine(uint32_t head_dim, const int32_t* ctx_lens,
                                     uint32_t n_seqs, uint32_t n_heads, uint32_t max_blocks,

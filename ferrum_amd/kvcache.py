@@ -409,12 +409,22 @@ class PagedKvPool:
             block_tables.shape[1], _dev(ctx_lens, torch.int32, "ctx_lens"), n_seqs, max_ctx_len,
             scale, ws_ptr, ws_bytes, _stream_ptr(stream)))
 
+    def prefill_workspace_bytes(self, n_heads: int, n_seqs: int, max_q_len: int,
+                                max_ctx_len: int) -> int:
+        """Bytes of the partials workspace of a prefill call (0: no workgroup splits)."""
+        n = ctypes.c_uint64(0)
+        check(self._lib.fkv_prefill_attention_workspace_size(self._h, n_heads, n_seqs, max_q_len,
+                                                             max_ctx_len, ctypes.byref(n)))
+        return n.value
+
     def prefill_attention(self, layer: int, q, out, block_tables, ctx_lens, q_lens, q_offsets,
                           max_q_len: int, max_ctx_len: int, scale: Optional[float] = None,
-                          stream=None) -> None:
-        """Chunked prefill (f16 KV): q, out float32 [rows, n_heads, head_dim]; sequence s's
-        q_lens[s] queries are rows q_offsets[s].. and sit at the end of its ctx_lens[s]
-        context, each attending causally (crates/model/src/llama.rs:363-378)."""
+                          workspace=None, split: bool = True, stream=None) -> None:
+        """Chunked prefill (F16 or Q8_0 KV): q, out float32 [rows, n_heads, head_dim];
+        sequence s's q_lens[s] queries are rows q_offsets[s].. and sit at the end of its
+        ctx_lens[s] context, each attending causally (crates/model/src/llama.rs:363-378).
+        workspace: device scratch for the key-range pieces (allocated here when None);
+        split=False passes none, so every workgroup reads its whole key range."""
         import torch
         rows, n_heads, d = q.shape
         if d != self.config.head_dim or tuple(out.shape) != tuple(q.shape):
@@ -424,12 +434,19 @@ class PagedKvPool:
             raise ValueError("ctx_lens/q_lens/q_offsets must have one entry per sequence")
         if scale is None:
             scale = default_scale(d)
+        ws_ptr, ws_bytes = 0, 0
+        if split:
+            need = self.prefill_workspace_bytes(n_heads, n_seqs, max_q_len, max_ctx_len)
+            if need:
+                if workspace is None:
+                    workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+                ws_ptr, ws_bytes = workspace.data_ptr(), workspace.numel() * workspace.element_size()
         check(self._lib.fkv_prefill_attention(
             self._h, layer, n_heads, _dev(q, torch.float32, "q"), _dev(out, torch.float32, "out"),
             _dev(block_tables, torch.int32, "block_tables"), block_tables.shape[1],
             _dev(ctx_lens, torch.int32, "ctx_lens"), _dev(q_lens, torch.int32, "q_lens"),
             _dev(q_offsets, torch.int64, "q_offsets"), n_seqs, max_q_len, max_ctx_len, scale,
-            _stream_ptr(stream)))
+            ws_ptr, ws_bytes, _stream_ptr(stream)))
 
 
 class SequenceManager:

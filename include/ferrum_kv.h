@@ -365,13 +365,22 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
  * reads a position past its own, Inf/NaN values included: an F16 pool that has
  * stored an Inf/NaN V runs a slower instance that keeps them from earlier queries
  * of the same tile. Q8_0 follows fkv_decode_attention's rule for scales of 512 or
- * more. No workspace. */
+ * more.
+ * workspace: NULL, or device scratch of fkv_prefill_attention_workspace_size()
+ * bytes (16-byte aligned; no initialisation) in which workgroups over long
+ * contexts leave the partial results of pieces of their key range for a merge
+ * pass. With NULL every workgroup reads its whole key range itself (same results
+ * within the attention tolerance; slower when contexts differ in length). Calls
+ * that share one workspace must not overlap. */
+int32_t fkv_prefill_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
+                                             uint32_t n_seqs, uint32_t max_q_len,
+                                             uint32_t max_ctx_len, uint64_t* bytes_out);
 int32_t fkv_prefill_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads, const float* q,
                               float* out, const int32_t* block_tables,
                               uint32_t max_blocks_per_seq, const int32_t* ctx_lens,
                               const int32_t* q_lens, const int64_t* q_offsets, uint32_t n_seqs,
                               uint32_t max_q_len, uint32_t max_ctx_len, float scale,
-                              void* stream);
+                              void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* Device-to-device byte copy with the same 16-byte vector kernel style as the
  * pool kernels; used to calibrate HBM counters and to measure copy bandwidth. */

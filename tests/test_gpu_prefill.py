@@ -10,7 +10,10 @@ output rows outside the chunk are never written. Also:
   the bar on finite data;
 - a sequence whose q_len exceeds the call's max_q_len (the grid holds no more) is
   clamped to it and raises FKV_FAULT_CTX_RANGE;
-- Q8_0 pools, with ordinary values and with values up to +-1e6 (the exact instance).
+- Q8_0 pools, with ordinary values and with values up to +-1e6 (the exact instance);
+- key ranges cut into pieces (the workspace path, down to one-block pieces through
+  FKV_PREFILL_SPLIT_BLOCKS) and read whole (no workspace): both meet the bar, every
+  instance.
 """
 import numpy as np
 import pytest
@@ -43,12 +46,12 @@ def _pool(d, hkv, ctxs, seed, layers=1, dtype=1, kv=None):
     return pool, layout, tab
 
 
-def _prefill(pool, layer, q, tab, ctxs, qls, offs, fill=5.0, max_q_len=None):
+def _prefill(pool, layer, q, tab, ctxs, qls, offs, fill=5.0, max_q_len=None, split=True):
     import torch
     out = torch.full(q.shape, fill, dtype=torch.float32, device="cuda")
     pool.prefill_attention(layer, to_dev(q), out, to_dev(tab), to_dev(np.array(ctxs, np.int32)),
                            to_dev(np.array(qls, np.int32)), to_dev(offs),
-                           max(qls) if max_q_len is None else max_q_len, max(ctxs))
+                           max(qls) if max_q_len is None else max_q_len, max(ctxs), split=split)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
@@ -80,16 +83,19 @@ SHAPES = [(1, 128, 4), (1, 64, 8), (1, 128, 1), (1, 64, 16), (1, 128, 3), (1, 12
           (8, 128, 4), (8, 64, 8), (8, 128, 1)]
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("dtype,d,g", SHAPES)
-def test_prefill_matches_oracle(dtype, d, g):
+def test_prefill_matches_oracle(dtype, d, g, split):
     hkv = 2
-    ctxs = [1, 17, 64, 300, 777]
-    qls = [1, 17, 5, 300, 129]  # fresh chunks and chunks after history
+    ctxs = [1, 17, 64, 300, 777, 1100]
+    qls = [1, 17, 5, 300, 129, 40]  # fresh chunks and chunks after history
     pool, layout, tab = _pool(d, hkv, ctxs, seed=d + g, dtype=dtype)
+    if split:  # max_ctx 1,100 = 69 blocks: pieces of 34-35 blocks
+        assert pool.prefill_workspace_bytes(hkv * g, len(ctxs), max(qls), max(ctxs)) > 0
     rows = sum(qls) + 3
     offs = np.concatenate([[2], 2 + np.cumsum(qls)[:-1]]).astype(np.int64)
     q = np.random.default_rng(g).standard_normal((rows, hkv * g, d), dtype=np.float32)
-    got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs, split=split)
     assert pool.take_fault_flags() == 0
     want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
     used = _used(rows, offs, qls)
@@ -113,6 +119,43 @@ def test_prefill_with_one_query_is_decode():
     assert_close(got, dec.cpu().numpy(), what="prefill vs decode")
 
 
+@pytest.mark.parametrize("pieces", [1, 3, 7])
+@pytest.mark.parametrize("dtype,g", [(1, 4), (8, 4), (1, 16), (1, 1)])
+def test_prefill_small_pieces(dtype, g, pieces, monkeypatch):
+    """Key ranges cut into pieces of `pieces` blocks (at most 32 a workgroup, so longer
+    ranges get longer pieces): odd and one-block pieces, pieces past a wave's own
+    causal end, ranges shorter than one piece; against the oracle."""
+    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
+    hkv, d = 2, 128
+    ctxs = [3, 16, 33, 190, 520, 1029]
+    qls = [3, 9, 33, 61, 200, 17]
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=71 + g, dtype=dtype)
+    assert pool.prefill_workspace_bytes(hkv * g, len(ctxs), max(qls), max(ctxs)) > 0
+    offs = np.concatenate([[0], np.cumsum(qls)[:-1]]).astype(np.int64)
+    q = np.random.default_rng(8).standard_normal((sum(qls), hkv * g, d), dtype=np.float32)
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    assert pool.take_fault_flags() == 0
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    assert_close(got, want, what=f"prefill, {pieces}-block pieces")
+
+
+def test_prefill_workspace_too_small_is_rejected():
+    import torch
+
+    import ferrum_amd as fa
+    hkv, g, d = 2, 4, 128
+    ctxs, qls = [3000], [100]  # 188 blocks over a 14-workgroup grid: split
+    pool, _, tab = _pool(d, hkv, ctxs, seed=81)
+    need = pool.prefill_workspace_bytes(hkv * g, 1, 100, 3000)
+    assert need > 0
+    q = torch.zeros((100, hkv * g, d), dtype=torch.float32, device="cuda")
+    ws = torch.empty(need - 16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(fa.InvalidRequest, match="prefill workspace too small"):
+        pool.prefill_attention(0, q, q.clone(), to_dev(tab), to_dev(np.array(ctxs, np.int32)),
+                               to_dev(np.array(qls, np.int32)), to_dev(np.zeros(1, np.int64)),
+                               100, 3000, workspace=ws)
+
+
 @pytest.mark.parametrize("dtype", [1, 8])
 def test_prefill_c3_chunk_shape(dtype):
     """BASELINE configs[2]'s prefill part at full size: 4 sequences appending 512-token
@@ -126,17 +169,22 @@ def test_prefill_c3_chunk_shape(dtype):
     offs = (np.arange(4) * 512).astype(np.int64)
     q = np.random.default_rng(2).standard_normal((2048, hkv * g, d), dtype=np.float32)
     got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    whole = _prefill(pool, 0, q, tab, ctxs, qls, offs, split=False)
     assert pool.take_fault_flags() == 0
     want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
     assert_close(got, want, what="c3 prefill")
+    assert_close(whole, want, what="c3 prefill, whole key ranges")
 
 
+@pytest.mark.parametrize("pieces", [0, 1, 2])
 @pytest.mark.parametrize("g", [4, 1, 16])
 @pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
-def test_nonfinite_v_reaches_only_later_queries(bad, g):
+def test_nonfinite_v_reaches_only_later_queries(bad, g, pieces, monkeypatch):
     """V of position p0 + 9 of a fresh 40-token chunk (and of position 3 of a chunk after
     100 tokens of history) holds an Inf/NaN in a few dims: queries before it must be
-    finite, the ones at or after it what the oracle gives."""
+    finite, the ones at or after it what the oracle gives; with whole key ranges (0)
+    and with pieces of 1 and 2 blocks."""
+    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
     hkv, d = 2, 128
     ctxs, qls = [40, 140], [40, 40]
     marks = [(0, 9), (1, 100 + 3)]
@@ -178,10 +226,13 @@ def test_leak_safe_instance_on_finite_data():
     assert_close(got, want, what="leak-safe prefill")
 
 
-def test_q_len_past_max_q_len_is_clamped_and_flagged():
+@pytest.mark.parametrize("pieces", [0, 3])
+def test_q_len_past_max_q_len_is_clamped_and_flagged(pieces, monkeypatch):
     """Sequence 1 says 300 queries but the call's max_q_len is 200: its first 200 rows are
-    computed, the rest untouched, FKV_FAULT_CTX_RANGE raised; sequence 0 is unaffected."""
+    computed, the rest untouched, FKV_FAULT_CTX_RANGE raised; sequence 0 is unaffected
+    (whole key ranges, and 3-block pieces merged under the same clamp)."""
     import ferrum_amd as fa
+    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
     hkv, g, d = 2, 4, 128
     ctxs, qls = [150, 500], [150, 300]
     pool, layout, tab = _pool(d, hkv, ctxs, seed=51)
@@ -194,9 +245,12 @@ def test_q_len_past_max_q_len_is_clamped_and_flagged():
     assert np.all(got[350:] == 5.0)
 
 
-def test_q8_prefill_with_wide_values():
+@pytest.mark.parametrize("pieces", [0, 5])
+def test_q8_prefill_with_wide_values(pieces, monkeypatch):
     """Q8_0 K and V with +-1e6 values (scales ~7,874): the pool is marked and the exact
-    instance computes; q is small enough that the scores stay O(1)."""
+    instance computes, with whole key ranges and with 5-block pieces; q is small enough
+    that the scores stay O(1)."""
+    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
     hkv, g, d = 2, 4, 128
     ctxs, qls = [300, 700], [300, 200]
 
