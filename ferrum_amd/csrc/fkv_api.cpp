@@ -80,6 +80,7 @@ struct fkv_pool {
   uint8_t* dev = nullptr;
   uint8_t* host = nullptr;
   uint32_t* fault = nullptr;
+  uint32_t* fault_host = nullptr;  // pinned: the fault read's copy lands here
   std::vector<int32_t> free_list;  // stack; LIFO reuse, as a fragmented pool would see
   std::vector<uint32_t> refcount;
   std::vector<fkv_seqs*> managers;  // detached when the pool is destroyed
@@ -152,15 +153,18 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
     return fail(FKV_ERR_UNAVAILABLE, "no device memory for kv pool");
   }
   // Four device words: the FKV_FAULT_* bits; the sticky mark of a Q8_0 scale of 512 or
-  // more (read by the attention kernels to pick their exact instance); the chunked
-  // prefill's mark of a non-finite V past a causal end and its workgroup count (the
-  // leak-safe instance clears both).
+  // more (read by the attention kernels to pick their exact instance); the sticky mark
+  // of an Inf/NaN V stored in an F16 pool (read by chunked prefill to pick its
+  // leak-safe instance); the staging word of fkv_paged_take_fault_flags.
   e = hipMalloc((void**)&p->fault, 4 * sizeof(uint32_t));
   if (e == hipSuccess) e = hipMemset(p->fault, 0, 4 * sizeof(uint32_t));
+  if (e == hipSuccess)
+    e = hipHostMalloc((void**)&p->fault_host, 64, hipHostMallocDefault);
   if (e == hipSuccess && host_total) e = hipHostMalloc((void**)&p->host, host_total, hipHostMallocDefault);
   if (e != hipSuccess) {
     (void)hipFree(p->dev);
     if (p->fault) (void)hipFree(p->fault);
+    if (p->fault_host) (void)hipHostFree(p->fault_host);
     delete p;
     return hip_fail(e, "pool allocation");
   }
@@ -191,6 +195,7 @@ int32_t fkv_paged_destroy(fkv_pool* pool) {
   (void)hipDeviceSynchronize();
   if (pool->dev) (void)hipFree(pool->dev);
   if (pool->fault) (void)hipFree(pool->fault);
+  if (pool->fault_host) (void)hipHostFree(pool->fault_host);
   if (pool->host) (void)hipHostFree(pool->host);
   delete pool;
   return ok();
@@ -207,14 +212,16 @@ int32_t fkv_paged_get_info(const fkv_pool* pool, fkv_paged_info* out) {
   return ok();
 }
 
-int32_t fkv_paged_take_fault_flags(fkv_pool* pool, uint32_t* flags_out) {
+int32_t fkv_paged_take_fault_flags(fkv_pool* pool, void* stream, uint32_t* flags_out) {
   if (!pool || !flags_out) return fail(FKV_ERR_INVALID, "null argument");
   DeviceGuard dg(pool->cfg.device);
-  FKV_HIP(hipDeviceSynchronize(), "synchronize");
-  uint32_t f = 0;
-  FKV_HIP(hipMemcpy(&f, pool->fault, sizeof f, hipMemcpyDeviceToHost), "read fault flags");
-  FKV_HIP(hipMemset(pool->fault, 0, sizeof f), "clear fault flags");
-  *flags_out = f;
+  const hipStream_t s = (hipStream_t)stream;
+  FKV_HIP(fkv::launch_take_fault(pool->fault, s), "take fault flags");
+  FKV_HIP(hipMemcpyAsync(pool->fault_host, pool->fault + 3, sizeof(uint32_t),
+                         hipMemcpyDeviceToHost, s),
+          "read fault flags");
+  FKV_HIP(hipStreamSynchronize(s), "synchronize");
+  *flags_out = *(volatile uint32_t*)pool->fault_host;
   return ok();
 }
 
@@ -277,31 +284,36 @@ static int32_t check_range(const fkv_pool* pool, uint64_t offset, uint64_t bytes
   return FKV_OK;
 }
 
-int32_t fkv_paged_read(fkv_pool* pool, uint64_t offset, uint64_t bytes, void* host_dst) {
+int32_t fkv_paged_read(fkv_pool* pool, uint64_t offset, uint64_t bytes, void* host_dst,
+                       void* stream) {
   if (!pool || (bytes && !host_dst)) return fail(FKV_ERR_INVALID, "null argument");
   if (check_range(pool, offset, bytes)) return FKV_ERR_INVALID;
   DeviceGuard dg(pool->cfg.device);
-  FKV_HIP(hipDeviceSynchronize(), "synchronize");
-  FKV_HIP(hipMemcpy(host_dst, pool->dev + offset, bytes, hipMemcpyDeviceToHost), "pool read");
+  const hipStream_t s = (hipStream_t)stream;
+  if (bytes)
+    FKV_HIP(hipMemcpyAsync(host_dst, pool->dev + offset, bytes, hipMemcpyDeviceToHost, s),
+            "pool read");
+  FKV_HIP(hipStreamSynchronize(s), "synchronize");
   return ok();
 }
 
-int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const void* host_src) {
+int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const void* host_src,
+                        void* stream) {
   if (!pool || (bytes && !host_src)) return fail(FKV_ERR_INVALID, "null argument");
   if (check_range(pool, offset, bytes)) return FKV_ERR_INVALID;
   DeviceGuard dg(pool->cfg.device);
-  FKV_HIP(hipDeviceSynchronize(), "synchronize");
-  FKV_HIP(hipMemcpy(pool->dev + offset, host_src, bytes, hipMemcpyHostToDevice), "pool write");
+  const hipStream_t s = (hipStream_t)stream;
+  if (bytes)
+    FKV_HIP(hipMemcpyAsync(pool->dev + offset, host_src, bytes, hipMemcpyHostToDevice, s),
+            "pool write");
   const uint8_t* img = (const uint8_t*)host_src;
   const int word = pool->cfg.kv_dtype == FKV_DTYPE_Q8_0 &&
                            q8_image_has_wide_scale(pool, offset, bytes, img) ? 1
                    : pool->cfg.kv_dtype == FKV_DTYPE_F16 &&
                            f16_image_has_nonfinite_v(pool, offset, bytes, img) ? 2
                                                                                 : 0;
-  if (word) {
-    const uint32_t one = 1;
-    FKV_HIP(hipMemcpy(pool->fault + word, &one, sizeof one, hipMemcpyHostToDevice), "pool write");
-  }
+  if (word) FKV_HIP(fkv::launch_fill(pool->fault + word, 1, sizeof(uint32_t), s), "pool write");
+  FKV_HIP(hipStreamSynchronize(s), "synchronize");
   return ok();
 }
 

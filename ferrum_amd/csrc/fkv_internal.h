@@ -43,7 +43,7 @@ struct Geom {
   uint32_t* fault;   // device words: [0] FKV_FAULT_* bits; [1] nonzero once a Q8_0
                      // scale of 512 or more was stored (sticky; q8_wide_scale);
                      // [2] nonzero once an F16 pool stored an Inf/NaN V (sticky;
-                     // f16_nonfinite); [3] unused
+                     // f16_nonfinite); [3] staging word of the fault read
 };
 
 constexpr int kDtypeF32 = 0;
@@ -95,6 +95,8 @@ hipError_t launch_gather_tables(const Geom& g, uint32_t layer, const int32_t* ta
 hipError_t launch_copy_blocks(const Geom& g, const int64_t* pairs, uint32_t n_pairs,
                               hipStream_t s);
 hipError_t launch_fill(void* dst, uint8_t byte, uint64_t bytes, hipStream_t s);
+// fault[3] = fault[0], fault[0] = 0, atomically (fkv_paged_take_fault_flags).
+hipError_t launch_take_fault(uint32_t* fault, hipStream_t s);
 hipError_t launch_device_copy(void* dst, const void* src, uint64_t bytes, hipStream_t s);
 
 // Returns hipErrorInvalidValue when no kernel is instantiated for the shape.

@@ -683,6 +683,18 @@ hipError_t launch_copy_blocks(const Geom& g, const int64_t* pairs, uint32_t n_pa
   return hipGetLastError();
 }
 
+// Moves the FKV_FAULT_* word into the staging word fault[3] and clears it in one
+// atomic exchange, so a bit that a kernel on another stream raises meanwhile is kept
+// for the next read.
+__global__ void take_fault_kernel(uint32_t* fault) {
+  if (threadIdx.x == 0) fault[3] = atomicExch(fault, 0u);
+}
+
+hipError_t launch_take_fault(uint32_t* fault, hipStream_t s) {
+  take_fault_kernel<<<1, 64, 0, s>>>(fault);
+  return hipGetLastError();
+}
+
 hipError_t launch_fill(void* dst, uint8_t byte, uint64_t bytes, hipStream_t s) {
   if (bytes == 0) return hipSuccess;
   uint32_t word = 0x01010101u * byte;

@@ -223,23 +223,29 @@ class PagedKvPool:
         return n.value
 
     # -- raw image ---------------------------------------------------------
-    def read(self, offset: int = 0, nbytes: Optional[int] = None) -> np.ndarray:
+    def read(self, offset: int = 0, nbytes: Optional[int] = None, stream=None) -> np.ndarray:
+        """Bytes of the pool image, after the work enqueued on `stream` (default: the
+        current stream)."""
         if nbytes is None:
             nbytes = self.pool_bytes - offset
         out = np.empty(nbytes, dtype=np.uint8)
-        check(self._lib.fkv_paged_read(self._h, offset, nbytes, out.ctypes.data))
+        check(self._lib.fkv_paged_read(self._h, offset, nbytes, out.ctypes.data,
+                                       _stream_ptr(stream)))
         return out
 
-    def write(self, data: np.ndarray, offset: int = 0) -> None:
+    def write(self, data: np.ndarray, offset: int = 0, stream=None) -> None:
         data = np.ascontiguousarray(data).view(np.uint8)
-        check(self._lib.fkv_paged_write(self._h, offset, data.size, data.ctypes.data))
+        check(self._lib.fkv_paged_write(self._h, offset, data.size, data.ctypes.data,
+                                        _stream_ptr(stream)))
 
     def fill(self, byte: int, stream=None) -> None:
         check(self._lib.fkv_paged_fill(self._h, byte, _stream_ptr(stream)))
 
-    def take_fault_flags(self) -> int:
+    def take_fault_flags(self, stream=None) -> int:
+        """FKV_FAULT_* bits raised by the work enqueued on `stream` (default: the current
+        stream) and by work already finished elsewhere; clears them."""
         f = ctypes.c_uint32()
-        check(self._lib.fkv_paged_take_fault_flags(self._h, ctypes.byref(f)))
+        check(self._lib.fkv_paged_take_fault_flags(self._h, _stream_ptr(stream), ctypes.byref(f)))
         return f.value
 
     # -- device operations --------------------------------------------------

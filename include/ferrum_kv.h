@@ -190,14 +190,21 @@ typedef struct fkv_pool fkv_pool;
 int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out);
 int32_t fkv_paged_destroy(fkv_pool* pool);
 int32_t fkv_paged_get_info(const fkv_pool* pool, fkv_paged_info* out);
-/* Reads and clears the FKV_FAULT_* bits the kernels raised (synchronises the device). */
-int32_t fkv_paged_take_fault_flags(fkv_pool* pool, uint32_t* flags_out);
+/* Reads and clears the FKV_FAULT_* bits the kernels raised, in stream order: the
+ * bits of every call enqueued on `stream` before this one (and of any other work
+ * already finished), then synchronises that stream only. The read and the clear
+ * are one atomic exchange on the device, so a bit raised meanwhile by work on
+ * another stream is reported by the next call. */
+int32_t fkv_paged_take_fault_flags(fkv_pool* pool, void* stream, uint32_t* flags_out);
 /* Fill every byte of device storage with `byte` (async on stream). */
 int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream);
-/* Synchronous raw copies between device storage and host memory (byte offsets
- * into the pool). Used to persist or inspect the pool image. */
-int32_t fkv_paged_read(fkv_pool* pool, uint64_t offset, uint64_t bytes, void* host_dst);
-int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const void* host_src);
+/* Raw copies between device storage and host memory (byte offsets into the pool),
+ * ordered on `stream` after the work enqueued there, which is then synchronised (the
+ * host buffer may be reused on return). Used to persist or inspect the pool image. */
+int32_t fkv_paged_read(fkv_pool* pool, uint64_t offset, uint64_t bytes, void* host_dst,
+                       void* stream);
+int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const void* host_src,
+                        void* stream);
 
 /* Host-side block allocator (free list with refcounts). Replaces the slot scan
  * of pool.rs:83-101; exhaustion is FKV_ERR_UNAVAILABLE "no free kv blocks", the
