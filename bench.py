@@ -13,8 +13,10 @@ N(0,1), synthetic (no checkpoint).
 --workload picks another BASELINE config (c1 TinyLlama prefill + 64 decode steps,
 c3 continuous batching with chunked prefill in a fragmented 60%-of-HBM pool, c4
 Q8_0 KV, c5 70B long context plus copy_blocks and swap), q8gemv, the decode layer's
-Q8_0 weight projections (fkv_gemm_q8_0 over Llama-3-8B's 32 layers), or gguf, the
-GGUF open + weight upload to HBM; each prints its own line.
+Q8_0 weight projections (fkv_gemm_q8_0 over Llama-3-8B's 32 layers), gguf, the
+GGUF open + weight upload to HBM, or layer, the attention half of the decode layer
+GPU-resident (q/k/v projections, RoPE + append + attention, attn_output, C2's batch);
+each prints its own line.
 
 Printed JSON line: value = algorithmic HBM bytes of the step's calls (attention +
 append) / wall time per step, timed over K steps bracketed by synchronisation.
@@ -59,7 +61,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c5", "q8gemv", "gguf"])
+                    choices=["c1", "c2", "c3", "c4", "c5", "q8gemv", "gguf", "layer"])
     ap.add_argument("--gguf-layers", type=int, default=4,
                     help="gguf: Llama-3-8B layers in the synthetic file (232 MB of Q8_0 each)")
     ap.add_argument("--gguf-threads", type=int, default=0, help="gguf: host threads (0 = 4, fewer on fewer CPUs)")
@@ -861,6 +863,147 @@ def run_q8gemv(args, torch, fa, lib, dev):
     return res
 
 
+def run_layer(args, torch, fa, lib, dev):
+    """The attention half of Llama-3-8B's decode layer, GPU-resident (DecodeAttentionLayer,
+    llama.rs:185-255): per layer, q/k/v from the normed rows (one fkv_gemm_q8_0_multi
+    launch), RoPE + KV append + decode attention (fkv_rope_append_decode_attention), and
+    attn_output (fkv_gemm_q8_0), for C2's batch: 64 sequences, contexts uniform in
+    [128, 4096], 32 layers with distinct synthetic Q8_0 weights (44.6 MB a layer), f16 KV.
+    value = algorithmic bytes a step (weights, KV read and appended, activations) / wall
+    time a step."""
+    from oracle import ref
+
+    K, W = args.steps, args.warmup
+    rng = np.random.default_rng(args.seed)
+    L, hq, hkv, d, n_embd, n_seqs = 32, 32, 8, 128, 4096, 64
+    rope_dim, theta = 128, 500000.0
+    ctx0 = rng.integers(128, 4097, n_seqs).astype(np.int64)
+    nblk_seq = (ctx0 + W + K + 15) // 16
+    pool = fa.PagedKvPool(fa.PagedConfig(n_layers=L, n_kv_heads=hkv, head_dim=d,
+                                         num_blocks=int(nblk_seq.sum()) + 64, block_size=16,
+                                         kv_dtype=1))
+    tables = make_tables(pool, nblk_seq, rng)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    fill_context(torch, pool, range(L), tables, ctx0, hkv, d, gen, dev)
+    ctx_step = np.stack([ctx0 + t + 1 for t in range(W + K)]).astype(np.int32)
+    ctx_d = torch.from_numpy(ctx_step).to(dev)
+    tab_d = torch.from_numpy(tables).to(dev)
+    max_ctx = int(ctx_step.max())
+    shapes = [(hq * d, n_embd), (hkv * d, n_embd), (hkv * d, n_embd), (n_embd, hq * d)]
+    layers, w_bytes = [], 0
+    for l in range(L):
+        w = [q8_weights(torch, r, c, gen, dev) for r, c in shapes]
+        w_bytes += sum(x.numel() for x in w)
+        layers.append(fa.DecodeAttentionLayer(pool, l, *w, hq, n_embd, rope_dim, theta,
+                                              max_seqs=n_seqs, max_ctx_len=max_ctx))
+    x = torch.randn((L, n_seqs, n_embd), generator=gen, device=dev)
+    y = torch.empty_like(x)
+    stream = torch.cuda.current_stream()
+
+    def step(t):
+        for l in range(L):
+            layers[l].forward(x[l], tab_d, ctx_d[t], max_ctx, y[l], stream=stream)
+
+    for t in range(W):
+        step(t)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(K):
+        step(W + i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    region_ms = e0.elapsed_time(e1)
+    assert pool.take_fault_flags() == 0
+    # activations: x read, q/k/v written and read, attention rows written and read, y written
+    act = n_seqs * 4 * (n_embd + 2 * (hq + 2 * hkv) * d + 2 * hq * d + n_embd)
+    kv = [attn_bytes(ctx_step[W + i], hq, hkv, d, 2.0) + append_bytes(n_seqs, hkv, d, 2.0, 0)
+          for i in range(K)]
+    step_bytes = [float(k) * L + w_bytes + act * L for k in kv]
+    value = sum(step_bytes) / wall / 1e9
+    res = {
+        "metric": METRIC + " (decode layer leg: attention half of the layer)",
+        "value": round(value, 2), "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": round(wall * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f16",
+        "data": "synthetic: N(0,1) normed rows and K/V, random Q8_0 weights, seeded",
+        "config": {"workload": "llama3-8b decode layer, attention half (q/k/v gemm, RoPE + "
+                               "append + attention, attn_output gemm), C2 batch",
+                   "n_seqs": n_seqs, "n_layers": L, "n_heads": hq, "n_kv_heads": hkv,
+                   "head_dim": d, "n_embd": n_embd, "weights": "q8_0", "kv_dtype": "f16",
+                   "rope_dim": rope_dim, "rope_theta": theta,
+                   "mean_ctx": float(ctx_step[W:W + K].mean()), "parallelism": "single GPU"},
+        "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "tokens_per_s": round(n_seqs * K / wall, 1),
+        "us_per_layer": round(region_ms * 1e3 / (K * L), 2),
+        "bytes_per_step": {"weights": int(w_bytes), "kv": int(np.mean(kv) * L),
+                           "activations": int(act * L)},
+        "roofline": {"bound": "hbm", "kernel": "whole layer (3 launches: gemm_q8_kernel, "
+                     "attn_mfma_kernel + attn_combine_kernel, gemm_q8_kernel)",
+                     "achieved": round(sum(step_bytes) / K / (region_ms * 1e-3 / K) / 1e9, 2),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(sum(step_bytes) / (region_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = layer_cpu_baseline(args, torch, fa, pool, layers[L - 1], x[L - 1],
+                                                 tables, ctx_step[W + K - 1], shapes)
+    return res
+
+
+def layer_cpu_baseline(args, torch, fa, pool, lay, x, tables, ctx, shapes):
+    """The oracle chain of the same layer (fo_q8_gemm for q/k/v, fo_rope, the AVX2
+    attention restatement, fo_q8_gemm for attn_output) on a bounded sample of the batch,
+    at 16 threads (GEMMs and attention), in the leg's unit."""
+    from oracle import ref
+    if not ref.avx2_available():
+        return None
+    hq, hkv, d, n_embd = lay.n_heads, lay.hkv, lay.d, lay.n_embd
+    seqs = np.arange(4)
+    ctx = np.asarray(ctx, np.int64)[seqs]
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    w = [t.cpu().numpy() for t in (lay.wq, lay.wk, lay.wv, lay.wo)]
+    xs = x[seqs].cpu().numpy()
+    bs = 16
+    nb = (ctx + bs - 1) // bs
+    used = [int(b) for s, n in zip(seqs, nb) for b in tables[s, :n]]
+    remap = {b: i for i, b in enumerate(used)}
+    lay1 = ref.Layout(1, hkv, d, bs, len(used), dtype=1)
+    region = lay1.block_bytes
+    image = np.empty(lay1.pool_bytes, np.uint8)
+    for b, i in remap.items():
+        image[i * region:(i + 1) * region] = pool.read(b * pool.block_bytes + lay.layer * region,
+                                                       region)
+    tab = np.zeros((len(seqs), int(nb.max())), np.int32)
+    for j, (s, n) in enumerate(zip(seqs, nb)):
+        tab[j, :n] = [remap[int(b)] for b in tables[s, :n]]
+    scale = fa.default_scale(d)
+    ctx32 = ctx.astype(np.int32)
+
+    def chain():
+        q = ref.q8_gemm(w[0], shapes[0][0], n_embd, xs, threads).reshape(len(seqs), hq, d)
+        k = ref.q8_gemm(w[1], shapes[1][0], n_embd, xs, threads).reshape(len(seqs), hkv, d)
+        ref.q8_gemm(w[2], shapes[2][0], n_embd, xs, threads)
+        qr, _ = ref.rope_step(q, k, ctx32, lay.rope_dim, lay.theta)
+        o = ref.avx2_attention(lay1, image, 0, qr, tab, ctx32, scale, threads)
+        return ref.q8_gemm(w[3], n_embd, hq * d, o.reshape(len(seqs), hq * d), threads)
+
+    sec, reps = cpu_timed(chain, args.cpu_seconds)
+    wb = sum(a.size for a in w)
+    nbytes = wb + attn_bytes(ctx, hq, hkv, d, 2.0)
+    return {"value": round(nbytes / sec / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"layer {lay.layer}, {len(seqs)} of the batch's sequences "
+                       f"({int(ctx.sum())} tokens): the oracle chain fo_q8_gemm x3, fo_rope, "
+                       f"AVX2 attention, fo_q8_gemm; {reps} reps at {threads} threads "
+                       "(the K/V append is not timed)"),
+            "seconds_per_chain": round(sec, 4)}
+
+
 def run_gguf(args, torch, fa, lib, dev):
     """gguf::load + weight upload to HBM: a synthetic Llama-3-8B-shaped Q8_0 GGUF
     (--gguf-layers layers of the 7 projections, alignment 32) is written to a temporary
@@ -969,7 +1112,7 @@ def main():
     dev = torch.device("cuda:0")
     lib = _lib.load()
     run = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5,
-           "q8gemv": run_q8gemv, "gguf": run_gguf}[args.workload]
+           "q8gemv": run_q8gemv, "gguf": run_gguf, "layer": run_layer}[args.workload]
     result = run(args, torch, fa, lib, dev)
     print(json.dumps(result), flush=True)
 

@@ -13,12 +13,13 @@ from .errors import (CacheError, FerrumError, GgufError, InternalError, InvalidR
 from .gguf import GgufFile
 from .kvcache import (KvPoolConfig, PagedConfig, PagedKvPool, PreallocatedKvPool,
                       SequenceManager, default_scale, device_copy)
+from .layer import DecodeAttentionLayer
 from .q8 import gemm_q8_0, gemm_q8_0_multi, gemv_q8_0, q8_0_row_bytes
 
 __all__ = [
     "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "FAULT_BLOCK_RANGE", "FAULT_CTX_RANGE",
     "FAULT_SLOT_RANGE", "FAULT_VALUE_RANGE", "GATHER_F32", "GATHER_RAW", "ROUND_HALF_AWAY",
-    "ROUND_NEAREST_EVEN", "STATIC_SCRATCH_BYTES", "CacheError", "FerrumError", "GgufError", "GgufFile", "InternalError",
+    "ROUND_NEAREST_EVEN", "STATIC_SCRATCH_BYTES", "CacheError", "DecodeAttentionLayer", "FerrumError", "GgufError", "GgufFile", "InternalError",
     "InvalidRequest",
     "KernelError", "Unavailable", "KvPoolConfig", "PagedConfig", "PagedKvPool",
     "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "gemm_q8_0", "gemm_q8_0_multi",

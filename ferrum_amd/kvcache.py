@@ -298,6 +298,13 @@ class PagedKvPool:
                                                             max_ctx_len, ctypes.byref(n)))
         return n.value
 
+    def rope_attention_workspace_bytes(self, n_heads: int, n_seqs: int, max_ctx_len: int) -> int:
+        """Bytes of the workspace of a rope_append_decode_attention call."""
+        n = ctypes.c_uint64()
+        check(self._lib.fkv_rope_append_decode_attention_workspace_size(
+            self._h, n_heads, n_seqs, max_ctx_len, ctypes.byref(n)))
+        return n.value
+
     def decode_attention(self, layer: int, q, out, block_tables, ctx_lens, max_ctx_len: int,
                          scale: Optional[float] = None, workspace=None, stream=None) -> None:
         """q, out: float32 [n_seqs, n_heads, head_dim]; block_tables int32 [n_seqs, max_blocks];
