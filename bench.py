@@ -77,6 +77,10 @@ def parse():
     ap.add_argument("--rope-dim", type=int, default=0,
                     help="> 0: time fkv_rope_append_decode_attention (q and k before RoPE)")
     ap.add_argument("--rope-theta", type=float, default=500000.0)
+    ap.add_argument("--kv-dtype", default="f16", choices=["f16", "f32", "q8_0"],
+                    help="c2: KV storage (f32 runs the VALU attention kernel)")
+    ap.add_argument("--n-heads", type=int, default=32,
+                    help="c2: query heads over the 8 KV heads (64: GQA group 8)")
     return ap.parse_args()
 
 
@@ -419,8 +423,11 @@ def decode_workload(args, torch, fa, lib, dev, *, name, L, n_seqs, hq, hkv, d, d
     if args.rope_dim:
         extra_cfg = dict(extra_cfg or {}, rope_dim=args.rope_dim, rope_theta=args.rope_theta)
     e = elem_bytes(dtype)
-    kname = ("fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)" if dtype == 1
-             else "fkv_append_decode_attention (tail slots + append + attn_mfma_kernel<q8_0> + combine)")
+    kname = {1: "fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)",
+             8: "fkv_append_decode_attention (attn_mfma_kernel<q8_0>, its exact instance "
+                "(exits at once unless the pool holds a scale >= 512), attn_combine_kernel)",
+             0: "fkv_append_decode_attention (tail slots + append_f32_kernel + "
+                "attn_partition_kernel + attn_combine_kernel)"}[dtype]
     res = decode_result(args, dl, W, K, wall, region_ms, e, name, dict(extra_cfg or {}), kname,
                         None)
     if fill_ms:
@@ -442,12 +449,18 @@ def run_c2(args, torch, fa, lib, dev):
     n_seqs = 64
     ctx0 = rng.integers(128, 4097, n_seqs).astype(np.int64)
     nb = int(((ctx0 + args.warmup + args.steps + 15) // 16).sum()) + 64
+    dtype = {"f16": 1, "f32": 0, "q8_0": 8}[args.kv_dtype]
+    variant = args.kv_dtype != "f16" or args.n_heads != 32
+    name = "llama3-8b decode step (BASELINE configs[1])"
+    if variant:  # a counter-study variant of the config, not the headline line
+        name += f", variant: {args.kv_dtype} KV, {args.n_heads} query heads"
     res, pool, dl = decode_workload(
-        args, torch, fa, lib, dev, name="llama3-8b decode step (BASELINE configs[1])", L=32,
-        n_seqs=n_seqs, hq=32, hkv=8, d=128, dtype=1, ctx0=ctx0, num_blocks=nb,
-        extra_cfg={"kv_dtype": "f16", "ctx": f"uniform[128,4096] seed {args.seed}"})
-    res["roofline"]["traffic"] = read_traffic(
-        os.path.join(ROOT, "profiles", "decode_attention_llama3_8b_c2_hbm_traffic.md"))
+        args, torch, fa, lib, dev, name=name, L=32, n_seqs=n_seqs, hq=args.n_heads, hkv=8,
+        d=128, dtype=dtype, ctx0=ctx0, num_blocks=nb,
+        extra_cfg={"kv_dtype": args.kv_dtype, "ctx": f"uniform[128,4096] seed {args.seed}"})
+    if not variant:
+        res["roofline"]["traffic"] = read_traffic(
+            os.path.join(ROOT, "profiles", "decode_attention_llama3_8b_c2_hbm_traffic.md"))
     res["device_copy_gbs"] = round(calibrate_copy(torch, fa, dev), 1)
     return res
 

@@ -6,9 +6,13 @@
 // out_h = sum_p w_p V[p][h / g], with f32 accumulation.
 //
 // Decode attention is a GEMV over HBM, but with a GQA group of G query heads it
-// is G GEMVs over the same K/V bytes. Done on the VALU (v_fma_mix) that work
-// capped the stream at 47% of HBM peak for G = 8; on MFMA it is a few percent
-// of the matrix-core rate, and the VALU only runs the softmax.
+// is G GEMVs over the same K/V bytes. On the VALU that work grows with G: the
+// F32-storage VALU kernel (fkv_attention.hip) issues 677 VALU instructions per
+// 16-token block and KV head at G = 4 and 1,214 at G = 8, where it streams at
+// 3.7 TB/s (46% of HBM peak), and F16 storage would bring half the bytes for the
+// same FMAs. Here the G heads are MFMA columns: ~200 VALU instructions and 16
+// MFMAs per block at any G (the matrix cores busy ~7% of the time), 5.7-5.9 TB/s
+// at G = 4 and 8 (C2, measured with rocprof counters).
 //
 // One wave processes one 16-token block at a time:
 //
