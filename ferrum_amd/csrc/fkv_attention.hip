@@ -12,6 +12,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <mutex>
 #include <type_traits>
 
@@ -690,11 +691,11 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(RopeTable rope, const in
 __global__ void __launch_bounds__(256) tail_slots_kernel(Geom g, const int32_t* __restrict__ tables,
                                                          uint32_t max_blocks,
                                                          const int32_t* __restrict__ ctx_lens,
-                                                         uint32_t n_seqs, int64_t* __restrict__ slots) {
+                                                         uint32_t n_seqs, int64_t cap,
+                                                         int64_t* __restrict__ slots) {
   const uint32_t s = blockIdx.x * 256u + threadIdx.x;
   if (s >= n_seqs) return;
   const int32_t ctx = ctx_lens[s];
-  const int64_t cap = (int64_t)max_blocks * g.block_size;
   int64_t slot = -1;
   if (ctx > 0 && ctx <= cap) {
     const int32_t pos = ctx - 1;
@@ -711,9 +712,11 @@ __global__ void __launch_bounds__(256) tail_slots_kernel(Geom g, const int32_t* 
 
 hipError_t launch_tail_slots(const Geom& g, const int32_t* tables, uint32_t max_blocks,
                              const int32_t* ctx_lens, uint32_t n_seqs, int64_t* slots,
-                             hipStream_t s) {
+                             hipStream_t s, uint64_t ctx_cap) {
+  const uint64_t rows = (uint64_t)max_blocks * g.block_size;
+  const uint64_t cap = ctx_cap < rows ? ctx_cap : rows;
   tail_slots_kernel<<<(n_seqs + 255) / 256, 256, 0, s>>>(g, tables, max_blocks, ctx_lens, n_seqs,
-                                                          slots);
+                                                          (int64_t)cap, slots);
   return hipGetLastError();
 }
 
@@ -727,13 +730,19 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
   const uint32_t G = n_heads / g.n_kv_heads;
   const AttnPlan p = plan_attention(g, n_heads, n_seqs, max_ctx_len);
   uint8_t* ws = (uint8_t*)workspace;
+  // The context a launch holds: the table row, and what its splits cover. A longer one
+  // is clamped to it by every kernel (FKV_FAULT_CTX_RANGE), which then stores no token
+  // for the sequence and rotates at the clamped position.
+  const uint64_t split_cap = (uint64_t)p.max_splits * p.split_tokens;
+  const uint64_t row_cap = (uint64_t)max_blocks * g.block_size;
+  const int32_t ctx_cap = (int32_t)std::min<uint64_t>(std::min(split_cap, row_cap), 0x7fffffffull);
   if (rope != nullptr && rope->rope_dim > 0 && !p.mfma_path) {
     // Rotate q and the new K rows into the workspace, then run the unrotated step.
     float* q_rot = (float*)(ws + append_attention_workspace_bytes(g, n_heads, n_seqs, max_ctx_len));
     float* k_rot = q_rot + (uint64_t)n_seqs * n_heads * g.head_dim;
     const uint64_t pairs = (uint64_t)n_seqs * (n_heads + g.n_kv_heads) * (g.head_dim / 2);
     rope_rows_kernel<<<(uint32_t)((pairs + 255) / 256), 256, 0, s>>>(
-        *rope, ctx_lens, (int32_t)(max_blocks * g.block_size), n_seqs, n_heads, g.n_kv_heads,
+        *rope, ctx_lens, ctx_cap, n_seqs, n_heads, g.n_kv_heads,
         g.head_dim, q, k_new, q_rot, k_rot);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -744,7 +753,8 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
   if (k_new != nullptr && !p.mfma_path) {
     // Separate append launch: slots derived from the block tables first.
     int64_t* slots = (int64_t*)(ws + p.total);
-    hipError_t e = launch_tail_slots(g, tables, max_blocks, ctx_lens, n_seqs, slots, s);
+    hipError_t e = launch_tail_slots(g, tables, max_blocks, ctx_lens, n_seqs, slots, s,
+                                     (uint64_t)ctx_cap);
     if (e == hipSuccess) e = launch_append(g, layer, k_new, v_new, slots, n_seqs, s);
     if (e != hipSuccess) return e;
     k_new = v_new = nullptr;

@@ -173,11 +173,12 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
 // the rotated q and k rows when the storage is not F16.
 uint64_t rope_attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
                                         uint32_t max_ctx_len);
-// Slot of position ctx_lens[s] - 1 through the block table (-1 for an empty
-// context or an entry outside the pool, which raises kFaultBlock).
+// Slot of position ctx_lens[s] - 1 through the block table (-1 for an empty context,
+// a context past min(ctx_cap, the table row) or an entry outside the pool, which
+// raises kFaultBlock).
 hipError_t launch_tail_slots(const Geom& g, const int32_t* tables, uint32_t max_blocks,
                              const int32_t* ctx_lens, uint32_t n_seqs, int64_t* slots,
-                             hipStream_t s);
+                             hipStream_t s, uint64_t ctx_cap = ~0ull);
 // Device scratch one call needs (0 when every sequence fits one split): the
 // split partials, which need no initialisation.
 uint64_t attention_workspace_bytes(const Geom& g, uint32_t n_heads, uint32_t n_seqs,

@@ -93,7 +93,9 @@ extern "C" {
 #define FKV_FAULT_CTX_RANGE 4u    /* ctx_len < 0, > max_blocks_per_seq * block_size, or
                                      (decode attention) longer than the call's splits
                                      hold, which max_ctx_len sized: the context is
-                                     clamped to that bound */
+                                     clamped to that bound, and a fused decode step
+                                     (every storage type) stores no token for that
+                                     sequence and rotates it at the clamped position */
 #define FKV_FAULT_VALUE_RANGE 8u  /* Q8_0 append stored a block scale past the binary16
                                      range (a 32-value run with |x| >= 65520 * 127): the
                                      scale is +-inf, as the reference's encoder stores it,

@@ -263,3 +263,36 @@ def test_attention_non_finite_scores(ctx, dtype):
     q2[0, :, 0] = -1.0
     got2 = _run(pool, 0, q2, tab, [ctx])
     assert np.all(got2 == 0.0)
+
+
+@pytest.mark.parametrize("dtype", [1, 8, 0])
+def test_fused_step_past_max_ctx_len_stores_no_token(dtype):
+    """The fused step under the same rule on every storage type: sequence 2's context
+    (1,100) is past what max_ctx_len = 512 sized, so FKV_FAULT_CTX_RANGE is raised, its
+    token is not stored and it attends over 512 positions; sequences 0 and 1 store their
+    tokens and attend normally. Pool bytes against the oracle's append of the two
+    tokens only, outputs at the attention bar."""
+    import torch
+
+    import ferrum_amd as fa
+    from oracle import ref
+    ctxs = [40, 300, 1100]
+    pool, layout, tab = _build(dtype, 128, 2, ctxs, seed=12, layers=1)
+    before = pool.read()
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((3, 8, 128), dtype=np.float32)
+    knew = rng.standard_normal((3, 2, 128), dtype=np.float32)
+    vnew = rng.standard_normal((3, 2, 128), dtype=np.float32)
+    out = torch.full(q.shape, 123.0, dtype=torch.float32, device="cuda")
+    pool.append_decode_attention(0, to_dev(knew), to_dev(vnew), to_dev(q), out, to_dev(tab),
+                                 to_dev(np.array(ctxs, np.int32)), 512)
+    torch.cuda.synchronize()
+    assert pool.take_fault_flags() & fa.FAULT_CTX_RANGE
+    tail = np.array([slots_for(tab[i], c)[-1] for i, c in enumerate(ctxs[:2])], np.int64)
+    want_image = before.copy()
+    ref.append(layout, want_image, 0, knew[:2], vnew[:2], tail)
+    assert np.array_equal(pool.read(), want_image)
+    want = ref.attention(layout, want_image, 0, q, tab, np.array([40, 300, 512]),
+                         fa.default_scale(128))
+    assert_close(out.cpu().numpy(), want)
+    pool.close()
