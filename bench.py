@@ -143,7 +143,9 @@ def slots_of(tables, seqs, pos, bs=16):
 def fill_context(torch, pool, layers, tables, ctx, hkv, d, gen, dev, outlier_frac=0.0,
                  chunk=1 << 18, timer=None):
     """Append N(0,1) K/V (optionally with a fraction of +-20 outliers) for positions
-    0 .. ctx[s]-1 of every sequence into every layer, in chunks of tokens."""
+    0 .. ctx[s]-1 of every sequence into every layer, in launches of `chunk` tokens.
+    With `timer`, the HIP-event time of every full-size launch (or of the single launch
+    of a smaller fill) goes to it; returns the tokens of one timed launch."""
     ctx = np.asarray(ctx, np.int64)
     seq_of = np.repeat(np.arange(ctx.size), ctx)
     pos = np.concatenate([np.arange(c) for c in ctx]) if ctx.sum() else np.zeros(0, np.int64)
@@ -161,7 +163,7 @@ def fill_context(torch, pool, layers, tables, ctx, hkv, d, gen, dev, outlier_fra
                     sgn = torch.where(torch.rand(x.shape, generator=gen, device=dev) < 0.5, -20.0, 20.0)
                     x[m] = sgn[m]
             e0 = e1 = None
-            if timer is not None and a == 0 and b == n:
+            if timer is not None and (b - a == chunk or (a == 0 and b == n)):
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
             pool.append(layer, k, v, slots_all[a:b])
@@ -172,7 +174,7 @@ def fill_context(torch, pool, layers, tables, ctx, hkv, d, gen, dev, outlier_fra
     torch.cuda.synchronize()
     if timer is not None and times:
         timer.extend(a.elapsed_time(b) for a, b in times)
-    return n
+    return min(n, chunk)  # tokens of each timed launch
 
 
 def calibrate_copy(torch, fa, dev, nbytes=4 << 30):

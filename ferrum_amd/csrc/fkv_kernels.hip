@@ -341,6 +341,119 @@ __global__ void __launch_bounds__(256) append_q8_kernel(Geom g, uint32_t layer,
   }
 }
 
+// Q8_0 storage, head_dim 64 or 128, 16-byte aligned k/v: one workgroup per 16
+// consecutive tokens x 256 / (32 * D / 64) KV heads. Thread (token o, kv, pair i)
+// quantises dims 64i .. 64i+63 of one row (two Q8_0 blocks, each as append_q8_kernel
+// does). K: the two blocks' 8-dim runs g of one token share a 16-byte unit of the
+// operand order, so K goes out as four 16-byte stores; the two scales as one 4-byte
+// store. V: a 16-byte unit holds dims j, j+16, j+32, j+48 of 4 consecutive tokens, so
+// the quants go through LDS and thread (head, pair i, dim j) stores, for each segment of
+// the window (a maximal run of consecutive slots inside one 4-aligned token group), a
+// whole unit when the segment is the whole group and single bytes otherwise.
+template <int D>
+__global__ void __launch_bounds__(256) append_q8_tile_kernel(Geom g, uint32_t layer,
+                                                             const float* __restrict__ k,
+                                                             const float* __restrict__ v,
+                                                             const int64_t* __restrict__ slots,
+                                                             uint32_t n_tokens) {
+  constexpr int kPairs = D / 64;           // 64-dim pairs of Q8_0 blocks per row
+  constexpr int kTph = 16 * 2 * kPairs;    // quantising threads per head
+  constexpr int kHpw = 256 / kTph;         // heads per workgroup
+  static_assert(kHpw * kTph == 256, "head_dim 64 or 128");
+  constexpr uint32_t cpr = D / 32;
+  __shared__ int64_t s_slot[16];
+  __shared__ __align__(16) uint8_t s_vq[kHpw][kPairs][16][64];
+
+  const uint32_t hgroups = (g.n_kv_heads + kHpw - 1) / kHpw;
+  const uint32_t win = blockIdx.x / hgroups, hg = blockIdx.x % hgroups;
+  const uint32_t hl = threadIdx.x / kTph, u = threadIdx.x % kTph;
+  const uint32_t h = hg * kHpw + hl;
+  const bool head_ok = h < g.n_kv_heads;
+  const uint32_t B = g.block_size;
+  const uint64_t cap = g.num_blocks * B;
+  if (threadIdx.x < 16) {
+    const uint64_t t = (uint64_t)win * 16u + threadIdx.x;
+    int64_t sl = t < n_tokens ? slots[t] : -1;
+    if (sl >= 0 && (uint64_t)sl >= cap) {
+      raise_fault(g.fault, kFaultSlot);
+      sl = -1;
+    }
+    s_slot[threadIdx.x] = sl;
+  }
+  __syncthreads();
+
+  const uint32_t o = u % 16u, kv = (u / 16u) % 2u, i = u / 32u;
+  const int64_t slot = s_slot[o];
+  if (slot >= 0 && head_ok) {
+    const float* src = (kv ? v : k) + (((uint64_t)win * 16u + o) * g.n_kv_heads + h) * D + i * 64u;
+    uint32_t q[2][8], sc[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      float x[32];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float4 t = ((const float4*)(src + b * 32))[j];
+        x[4 * j] = t.x; x[4 * j + 1] = t.y; x[4 * j + 2] = t.z; x[4 * j + 3] = t.w;
+      }
+      sc[b] = q8_quantize(x, g.rounding, q[b]);
+      // A scale of 512 or more sends later attention over the pool to its exact loop;
+      // one past the binary16 range is stored as +-inf, as the reference's encoder
+      // stores it, and flagged.
+      if (q8_wide_scale(sc[b])) {
+        mark_wide(g.fault);
+        if ((sc[b] & 0x7c00u) == 0x7c00u) raise_fault(g.fault, kFaultRange);
+      }
+    }
+    const uint32_t off = (uint32_t)((uint64_t)slot % B);
+    uint8_t* tile = tile_ptr(g, (uint64_t)slot / B, layer, kv, h);
+    *(uint32_t*)(tile + (uint64_t)B * D + ((uint64_t)off * cpr + 2u * i) * 2u) = sc[0] | (sc[1] << 16);
+    if (kv == 0) {
+#pragma unroll
+      for (uint32_t gg = 0; gg < 4; gg++)
+        *(uint4*)(tile + q8_quant_offset(0, off, i * 64u + gg * 8u, D)) =
+            make_uint4(q[0][2 * gg], q[0][2 * gg + 1], q[1][2 * gg], q[1][2 * gg + 1]);
+    } else {
+      uint32_t* dst = (uint32_t*)s_vq[hl][i][o];
+#pragma unroll
+      for (int w = 0; w < 8; w++) {
+        dst[w] = q[0][w];
+        dst[8 + w] = q[1][w];
+      }
+    }
+  }
+  __syncthreads();
+
+  if (threadIdx.x >= (uint32_t)(kHpw * kPairs * 16)) return;
+  const uint32_t vh = threadIdx.x / (kPairs * 16u), vi = (threadIdx.x / 16u) % kPairs,
+                 j = threadIdx.x % 16u;
+  const uint32_t hv = hg * kHpw + vh;
+  if (hv >= g.n_kv_heads) return;
+  for (uint32_t e0 = 0; e0 < 16u; e0++) {
+    const int64_t s0 = s_slot[e0];
+    if (s0 < 0 || (e0 > 0 && s0 % 4 != 0 && s_slot[e0 - 1] == s0 - 1)) continue;
+    uint32_t len = 1;
+    while (e0 + len < 16u && (s0 + len) % 4 != 0 && s_slot[e0 + len] == s0 + (int64_t)len) len++;
+    const uint32_t off = (uint32_t)((uint64_t)s0 % B);
+    uint8_t* unit = tile_ptr(g, (uint64_t)s0 / B, layer, 1, hv) +
+                    (q8_quant_offset(1, off, vi * 64u + j, D) & ~(uint64_t)15);
+    if (len == 4) {  // the whole 4-token group: bytes mm*4 + e = token e0+e, dim j + 16mm
+      uint32_t w[4];
+#pragma unroll
+      for (uint32_t mm = 0; mm < 4; mm++)
+        w[mm] = (uint32_t)s_vq[vh][vi][e0][16 * mm + j] |
+                ((uint32_t)s_vq[vh][vi][e0 + 1][16 * mm + j] << 8) |
+                ((uint32_t)s_vq[vh][vi][e0 + 2][16 * mm + j] << 16) |
+                ((uint32_t)s_vq[vh][vi][e0 + 3][16 * mm + j] << 24);
+      *(uint4*)unit = make_uint4(w[0], w[1], w[2], w[3]);
+    } else {
+      for (uint32_t e = 0; e < len; e++)
+#pragma unroll
+        for (uint32_t mm = 0; mm < 4; mm++)
+          unit[mm * 4u + (off + e) % 4u] = s_vq[vh][vi][e0 + e][16 * mm + j];
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Gather (paged KvPool::k / v): one unit = one (row, kv, head, chunk)
 // ---------------------------------------------------------------------------
@@ -570,7 +683,15 @@ hipError_t launch_append(const Geom& g, uint32_t layer, const float* k, const fl
                          const int64_t* slots, uint32_t n_tokens, hipStream_t s) {
   if (n_tokens == 0) return hipSuccess;
   const bool aligned = ((uintptr_t)k % 16 == 0) && ((uintptr_t)v % 16 == 0);
-  if (g.dtype == kDtypeQ8) {
+  if (g.dtype == kDtypeQ8 && (g.head_dim == 64 || g.head_dim == 128) && aligned) {
+    const uint32_t hpw = g.head_dim == 128 ? 4u : 8u;
+    const uint64_t wgs = ((uint64_t)n_tokens + 15u) / 16u * ((g.n_kv_heads + hpw - 1) / hpw);
+    if (wgs > 0x7fffffffull) return hipErrorInvalidValue;
+    if (g.head_dim == 128)
+      append_q8_tile_kernel<128><<<(uint32_t)wgs, 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
+    else
+      append_q8_tile_kernel<64><<<(uint32_t)wgs, 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
+  } else if (g.dtype == kDtypeQ8) {
     uint64_t units = (uint64_t)n_tokens * 2u * g.n_kv_heads * (g.head_dim / 32u);
     if (aligned)
       append_q8_kernel<true><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);

@@ -165,18 +165,20 @@ def test_append_gather_roundtrip_scattered(dtype, d):
             assert np.array_equal(ov.cpu().numpy().view(np.uint8), tv.view(np.uint8))
 
 
-@pytest.mark.parametrize("d,hkv", [(128, 2), (64, 3), (64, 2)])
+@pytest.mark.parametrize("dtype", [1, 8])
+@pytest.mark.parametrize("d,hkv", [(128, 2), (64, 3), (64, 2), (128, 5)])
 @pytest.mark.parametrize("rounding", [0, 1])
-def test_append_f16_runs_at_every_alignment(d, hkv, rounding):
-    """F16 append of slot mappings whose runs of consecutive slots start at every offset
-    of a block and at every position of a 16-token window: chunks of 1..40 tokens
-    continuing 0..15 tokens into a block, a descending run, random single slots, -1
-    padding, and a token count that leaves the last window partial. Bytes no token
-    names keep the fill pattern; all bit-exact against the oracle."""
+def test_append_runs_at_every_alignment(dtype, d, hkv, rounding):
+    """F16 and Q8_0 append (the 16-token window kernels) of slot mappings whose runs of
+    consecutive slots start at every offset of a block and at every position of a
+    16-token window: chunks of 1..40 tokens continuing 0..15 tokens into a block, a
+    descending run, random single slots, -1 padding, and a token count that leaves the
+    last window partial; head counts that leave a workgroup's last heads empty. Bytes no
+    token names keep the fill pattern; all bit-exact against the oracle."""
     from oracle import ref
-    rng = np.random.default_rng(d + hkv + rounding)
+    rng = np.random.default_rng(d + hkv + rounding + dtype)
     nblk = 160
-    pool, layout = make_pools(2, hkv, d, nblk, dtype=1, rounding=rounding)
+    pool, layout = make_pools(2, hkv, d, nblk, dtype=dtype, rounding=rounding)
     pool.fill(0x5a)
     want = np.full(layout.pool_bytes, 0x5a, np.uint8)
     perm = rng.permutation(nblk)
@@ -196,7 +198,9 @@ def test_append_f16_runs_at_every_alignment(d, hkv, rounding):
                                                  rest[2] * 16 + np.arange(16)]))[:23])
     parts.append(rest[3] * 16 + np.array([3, 4, 5, 9, 10, 15]))
     slots = np.concatenate(parts)
-    assert slots.size % 16 != 0 and np.unique(slots[slots >= 0]).size == (slots >= 0).sum()
+    if slots.size % 16 == 0:  # keep the last window partial
+        slots = np.append(slots, rest[3] * 16 + 7)
+    assert np.unique(slots[slots >= 0]).size == (slots >= 0).sum()
     for layer in range(2):
         k = rng.standard_normal((slots.size, hkv, d), dtype=np.float32)
         v = rng.standard_normal((slots.size, hkv, d), dtype=np.float32)
