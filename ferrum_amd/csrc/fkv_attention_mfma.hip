@@ -1425,15 +1425,14 @@ __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16
     al = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], al, 0, 0, 0);
   }
   float x[4];
-  bool nan = false;
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    x[r] = ah[r] + al[r];
-    nan = nan || x[r] != x[r];
-  }
-  if (__builtin_amdgcn_ballot_w64(nan) != 0) {  // see qk_block: the inf * 0 case
+  for (int r = 0; r < 4; r++) x[r] = ah[r] + al[r];
+  // One test for the four: a NaN score makes the sum NaN (as does inf - inf, which only
+  // sends the block through the repair below, where it changes nothing).
+  const float xs = (x[0] + x[1]) + (x[2] + x[3]);
+  if (__builtin_amdgcn_ballot_w64(xs != xs) != 0) {  // see qk_block: the inf * 0 case
 #pragma unroll
-    for (int r = 0; r < 4; r++) x[r] = (al[r] != al[r] && ah[r] == ah[r]) ? ah[r] : x[r];
+    for (int r = 0; r < 4; r++) x[r] = ((al[r] != al[r]) & (ah[r] == ah[r])) ? ah[r] : x[r];
   }
   if (live && full) {
 #pragma unroll
@@ -1461,7 +1460,7 @@ __device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], float h
     for (int r = 0; r < 4; r++) lmax = __builtin_fmaxf(lmax, s[b][r]);
   lmax *= hscale;
   const bool bad =
-      ln.real && (!(lmax <= st.m_ref + kRescaleLog2) || !__builtin_isfinite(st.m_ref));
+      ln.real & (!(lmax <= st.m_ref + kRescaleLog2) | !__builtin_isfinite(st.m_ref));
   if (__builtin_amdgcn_ballot_w64(bad) != 0) {  // some column's max moved: rescale
     float x = lmax;
     x = __builtin_fmaxf(x, __shfl_xor(x, 16));
@@ -1478,7 +1477,7 @@ __device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], float h
 #pragma unroll
       for (int r = 0; r < 4; r++) st.acc[m][r] *= ar[r];
   }
-  if (__builtin_amdgcn_ballot_w64(ln.real && st.m_ref == -__builtin_inff()) == 0) {
+  if (__builtin_amdgcn_ballot_w64(ln.real & (st.m_ref == -__builtin_inff())) == 0) {
 #pragma unroll
     for (int b = 0; b < NB; b++)
 #pragma unroll
@@ -1674,42 +1673,69 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
   // Thread t stages 16-byte chunks t, t + 256, ... of a block's K | V pair; a table
-  // entry outside the pool raises the fault flag, stages block 0 and is skipped.
+  // entry outside the pool raises the fault flag, stages block 0 and is skipped. The
+  // chunk's source (relative to the K tile: the V tile of the same head is n_kv_heads
+  // tiles on) and its LDS destination (V rows with their two 16-byte units swapped on
+  // rows with bit 3 of the dim set, so the P.V operand reads hit 16 distinct bank
+  // pairs) are the thread's own, worked out once.
+  const uint8_t* kbase = tile_ptr(g, 0, layer, 0, kvh);
+  // (n_kv_heads tiles of one layer's K fit in 32 bits: a block of every layer does not)
+  const uint32_t v_skip = (uint32_t)(g.n_kv_heads * g.tile_bytes) - (uint32_t)kTile;
   uint4 stg[kLoads];
-  auto load_block = [&](int32_t j) {
-    const int32_t p = __builtin_amdgcn_readfirstlane(table[j]);
-    const bool ok = p >= 0 && (uint64_t)p < g.num_blocks;
-    if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
-    const uint8_t* kt = tile_ptr(g, ok ? (uint64_t)p : 0, layer, 0, kvh);
-    const uint8_t* vt = tile_ptr(g, ok ? (uint64_t)p : 0, layer, 1, kvh);
+  auto chunk_off = [&](int i) {
+    const uint32_t c = (uint32_t)(i * 256) + threadIdx.x;
+    return (c < (uint32_t)kChunks ? c : 0u) * 16u;
+  };
+  // F16 keeps the swizzled destinations in registers; Q8_0 (no swizzle, one register
+  // short of spilling) works its offsets out at each use.
+  constexpr int kPre = DT == kDtypeF16 ? kLoads : 1;
+  uint32_t src_pre[kPre], dst_pre[kPre];
+  if constexpr (DT == kDtypeF16) {
 #pragma unroll
     for (int i = 0; i < kLoads; i++) {
-      const uint32_t c = (uint32_t)(i * 256) + threadIdx.x;
-      if (c < (uint32_t)kChunks) {
-        const uint32_t off = c * 16u;
-        stg[i] = load_stream16(off < (uint32_t)kTile ? kt + off : vt + (off - kTile));
+      const uint32_t off = chunk_off(i);
+      const bool is_v = off >= (uint32_t)kTile;
+      src_pre[i] = off + (is_v ? v_skip : 0u);
+      if (is_v) {
+        const uint32_t v = off - kTile, dim = v / 32u, unit = (v % 32u) / 16u;
+        dst_pre[i] = kTile + dim * 32u + ((unit ^ ((dim >> 3) & 1u)) * 16u);
+      } else {
+        dst_pre[i] = off;
       }
     }
+  }
+  auto src_off = [&](int i) -> uint32_t {
+    if constexpr (DT == kDtypeF16) {
+      return src_pre[i];
+    } else {
+      const uint32_t off = chunk_off(i);
+      return off + (off >= (uint32_t)kTile ? v_skip : 0u);
+    }
+  };
+  auto dst_off = [&](int i) -> uint32_t {
+    if constexpr (DT == kDtypeF16) return dst_pre[i];
+    else return chunk_off(i);
+  };
+  // every thread holds chunk i unless the block's last 256-chunk row is partial
+  auto has_chunk = [&](int i) {
+    return (i + 1) * 256 <= kChunks || (uint32_t)(i * 256) + threadIdx.x < (uint32_t)kChunks;
+  };
+  auto load_block_at = [&](int32_t p) {
+    p = __builtin_amdgcn_readfirstlane(p);
+    const bool ok = (p >= 0) & ((uint64_t)p < g.num_blocks);
+    if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
+    const uint8_t* kt = kbase + (ok ? (uint64_t)p : 0u) * g.block_bytes;
+#pragma unroll
+    for (int i = 0; i < kLoads; i++)
+      if (has_chunk(i)) stg[i] = load_stream16(kt + src_off(i));
     return ok;
   };
+  auto load_block = [&](int32_t j) { return load_block_at(table[j]); };
   auto store_block = [&](int buf, int slot) {
+    uint8_t* dst = s_kv[buf][slot];
 #pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-      const uint32_t c = (uint32_t)(i * 256) + threadIdx.x;
-      if (c < (uint32_t)kChunks) {
-        const uint32_t off = c * 16u;
-        uint8_t* dst = s_kv[buf][slot];
-        if (DT == kDtypeF16 && off >= (uint32_t)kTile) {
-          // V rows (one dim, 16 tokens = two 16-byte units) with unit u at
-          // u ^ ((dim >> 3) & 1): the P.V operand reads (8 bytes a lane, 16 dims a
-          // lane group) then hit 16 distinct bank pairs, and a staged unit stays whole.
-          const uint32_t v = off - kTile, dim = v / 32u, unit = (v % 32u) / 16u;
-          *(uint4*)&dst[kTile + dim * 32u + ((unit ^ ((dim >> 3) & 1u)) * 16u)] = stg[i];
-        } else {
-          *(uint4*)&dst[off] = stg[i];
-        }
-      }
-    }
+    for (int i = 0; i < kLoads; i++)
+      if (has_chunk(i)) *(uint4*)&dst[dst_off(i)] = stg[i];
   };
 
   bool lv[kStep] = {false, false};   // blocks of the step being computed: in the pool
@@ -1734,6 +1760,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   for (int32_t j0 = jbeg, buf = 0; j0 < jend; j0 += kStep, buf ^= 1) {
     const bool more = j0 + kStep < jend;      // the workgroup has a next step
     const bool more2 = j0 + kStep + 1 < jend;  // with a second block
+    // the table entry of the block staged in the middle of the step, read up front
+    const int32_t p_mid = more2 ? table[j0 + kStep + 1] : 0;
     float sc[kStep][4];
 #pragma unroll
     for (int bb = 0; bb < kStep; bb++) {
@@ -1764,7 +1792,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       }
       if (bb == 0 && more) {  // the next step's first block to the other buffer
         store_block(buf ^ 1, 0);
-        if (more2) nlv[1] = load_block(j0 + kStep + 1);
+        if (more2) nlv[1] = load_block_at(p_mid);
       }
     }
     f16x4 pw[kStep];
