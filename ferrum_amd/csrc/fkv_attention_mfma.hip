@@ -1630,7 +1630,18 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     // without one the fast instance computes, with one the leak-safe instance.
     if (pool_has_nonfinite_v(g.fault) != (MODE == kPfLeakSafe)) return;
   }
-  const uint32_t sk = blockIdx.x;
+  // Which sequence this workgroup takes: its grid column's, moved on by a quarter of
+  // the batch per step of q(y) = (y + y / 8) % 4. The hardware deals workgroups
+  // w = x + gridDim.x * y to the 8 XCDs and their 4 shader engines in rotation, so
+  // with gridDim.x dividing 256 the four that share a CU (w 32 apart, or 256 apart,
+  // depending on how the engine fills its CUs) all had the same x, hence the same
+  // sequence: the CUs holding the longest history carried 3x the others' blocks and
+  // the kernel ended on them. q differs between the four under either fill, so a CU
+  // now gets one workgroup from each quarter of the batch (C3: 194.8 -> 173.2 us).
+  const uint32_t ns = gridDim.x / g.n_kv_heads;
+  const uint32_t q4 = (blockIdx.y + blockIdx.y / 8u) % 4u;
+  const uint32_t sk = ((blockIdx.x / g.n_kv_heads + q4 * ns / 4u) % ns) * g.n_kv_heads +
+                      blockIdx.x % g.n_kv_heads;
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int32_t T = 16 / (int32_t)G;  // query tokens per wave tile
