@@ -70,6 +70,9 @@ def parse():
                     help="q8gemv: activation rows a call (1 = Kernels::gemv, more = gemm)")
     ap.add_argument("--gemv-fused", action="store_true",
                     help="q8gemv: q/k/v and gate/up each in one fkv_gemm_q8_0_multi launch")
+    ap.add_argument("--gemm-batched", action="store_true",
+                    help="q8gemv: the same groups through fkv_gemm_q8_0_batched (the matrix "
+                         "cores from 8 tokens)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
@@ -751,8 +754,13 @@ def run_q8gemv(args, torch, fa, lib, dev):
     ys_of = {name: torch.empty(T, rows, device=dev) for name, rows, _ in LLAMA3_8B_PROJ}
     calls, weights = [], []
     step_bytes = 0.0
+    fused = args.gemv_fused or args.gemm_batched
     groups = ([["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"],
-               ["ffn_down"]] if args.gemv_fused else [[n] for n, _, _ in LLAMA3_8B_PROJ])
+               ["ffn_down"]] if fused else [[n] for n, _, _ in LLAMA3_8B_PROJ])
+    gws = None
+    if args.gemm_batched:  # one workspace for every call (they are stream-ordered)
+        need = max(fa.gemm_q8_0_batched_workspace_bytes(c, T) for c in (4096, 14336))
+        gws = torch.empty(max(need, 16), dtype=torch.uint8, device=dev)
     shape = {n: (r, c) for n, r, c in LLAMA3_8B_PROJ}
     stream = torch.cuda.current_stream()
     sp = stream.cuda_stream
@@ -766,7 +774,18 @@ def run_q8gemv(args, torch, fa, lib, dev):
             step_bytes += w.numel() + T * cols * 4 + T * rows * 4
         for g in groups:
             cols = shape[g[0]][1]
-            if len(g) == 1:
+            if args.gemm_batched:
+                n = len(g)
+                arr_p, arr_u = ctypes.c_void_p * n, ctypes.c_uint64 * n
+                a = (arr_p(*[layer_w[m].data_ptr() for m in g]),
+                     arr_u(*[layer_w[m].numel() for m in g]), arr_u(*[shape[m][0] for m in g]),
+                     arr_p(*[ys_of[m].data_ptr() for m in g]),
+                     arr_u(*[T * shape[m][0] for m in g]))
+                keep.append(a)
+                calls.append((lib.fkv_gemm_q8_0_batched,
+                              (n, a[0], a[1], a[2], cols, xs[cols].data_ptr(), T * cols, T, a[3],
+                               a[4], gws.data_ptr(), gws.numel(), sp)))
+            elif len(g) == 1:
                 r = shape[g[0]][0]
                 w = layer_w[g[0]]
                 calls.append((lib.fkv_gemm_q8_0, (w.data_ptr(), w.numel(), r, cols,
@@ -807,6 +826,8 @@ def run_q8gemv(args, torch, fa, lib, dev):
     value = step_bytes * K / wall / 1e9
     achieved = step_bytes / len(calls) / (region_ms * 1e-3 / n_launch) / 1e9
     kname = "gemv_q8_kernel<%d>" % (4 if T >= 3 else T)
+    if args.gemm_batched and T >= 8:
+        kname = "q8_act_kernel + gemm_q8_mfma_kernel (fkv_gemm_q8_0_batched)"
     res = {
         "metric": "Q8_0 weight GEMV HBM GB/s (Llama-3-8B decode projections), 1xMI355X",
         "value": round(value, 2),
@@ -822,7 +843,8 @@ def run_q8gemv(args, torch, fa, lib, dev):
         "data": "synthetic: random int8 quants, f16 scales in [2^-10, 2^-6); x ~ N(0,1)",
         "config": {"workload": "q8gemv", "model_shapes": "Llama-3-8B", "n_layers": L,
                    "tokens": T, "calls_per_step": len(calls),
-                   "fused": "q/k/v and gate/up one launch each" if args.gemv_fused else "none",
+                   "fused": "q/k/v and gate/up one launch each" if fused else "none",
+                   "batched_gemm": bool(args.gemm_batched),
                    "weight_bytes_per_step": int(sum(w[3].numel() for w in weights)),
                    "parallelism": "single GPU"},
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
@@ -835,7 +857,7 @@ def run_q8gemv(args, torch, fa, lib, dev):
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": read_traffic(os.path.join(ROOT, "profiles",
                                                  "q8_gemv_llama3_8b_decode_kernel_stats.md"))
-            if T == 1 and not args.gemv_fused else None,
+            if T == 1 and not fused else None,
             "bytes_per_launch": int(step_bytes / len(calls)),
             "ms_per_launch": round(region_ms / n_launch, 5),
         },
@@ -880,9 +902,9 @@ def run_q8gemv(args, torch, fa, lib, dev):
 
 def run_layer(args, torch, fa, lib, dev):
     """The attention half of Llama-3-8B's decode layer, GPU-resident (DecodeAttentionLayer,
-    llama.rs:185-255): per layer, q/k/v from the normed rows (one fkv_gemm_q8_0_multi
-    launch), RoPE + KV append + decode attention (fkv_rope_append_decode_attention), and
-    attn_output (fkv_gemm_q8_0), for C2's batch: 64 sequences, contexts uniform in
+    llama.rs:185-255): per layer, q/k/v from the normed rows (one fkv_gemm_q8_0_batched
+    call), RoPE + KV append + decode attention (fkv_rope_append_decode_attention), and
+    attn_output (fkv_gemm_q8_0_batched), for C2's batch: 64 sequences, contexts uniform in
     [128, 4096], 32 layers with distinct synthetic Q8_0 weights (44.6 MB a layer), f16 KV.
     value = algorithmic bytes a step (weights, KV read and appended, activations) / wall
     time a step."""
@@ -956,8 +978,9 @@ def run_layer(args, torch, fa, lib, dev):
         "us_per_layer": round(region_ms * 1e3 / (K * L), 2),
         "bytes_per_step": {"weights": int(w_bytes), "kv": int(np.mean(kv) * L),
                            "activations": int(act * L)},
-        "roofline": {"bound": "hbm", "kernel": "whole layer (3 launches: gemm_q8_kernel, "
-                     "attn_mfma_kernel + attn_combine_kernel, gemm_q8_kernel)",
+        "roofline": {"bound": "hbm", "kernel": "whole layer (q8_act_kernel + "
+                     "gemm_q8_mfma_kernel, attn_mfma_kernel + attn_combine_kernel, "
+                     "q8_act_kernel + gemm_q8_mfma_kernel)",
                      "achieved": round(sum(step_bytes) / K / (region_ms * 1e-3 / K) / 1e9, 2),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(sum(step_bytes) / (region_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

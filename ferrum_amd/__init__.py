@@ -14,7 +14,8 @@ from .gguf import GgufFile
 from .kvcache import (KvPoolConfig, PagedConfig, PagedKvPool, PreallocatedKvPool,
                       SequenceManager, default_scale, device_copy)
 from .layer import DecodeAttentionLayer
-from .q8 import gemm_q8_0, gemm_q8_0_multi, gemv_q8_0, q8_0_row_bytes
+from .q8 import (gemm_q8_0, gemm_q8_0_batched, gemm_q8_0_batched_workspace_bytes, gemm_q8_0_multi,
+                 gemv_q8_0, q8_0_row_bytes)
 
 __all__ = [
     "DTYPE_F16", "DTYPE_F32", "DTYPE_Q8_0", "FAULT_BLOCK_RANGE", "FAULT_CTX_RANGE",
@@ -22,7 +23,8 @@ __all__ = [
     "ROUND_NEAREST_EVEN", "STATIC_SCRATCH_BYTES", "CacheError", "DecodeAttentionLayer", "FerrumError", "GgufError", "GgufFile", "InternalError",
     "InvalidRequest",
     "KernelError", "Unavailable", "KvPoolConfig", "PagedConfig", "PagedKvPool",
-    "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "gemm_q8_0", "gemm_q8_0_multi",
+    "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "gemm_q8_0", "gemm_q8_0_batched",
+    "gemm_q8_0_batched_workspace_bytes", "gemm_q8_0_multi",
     "gemv_q8_0", "load_library", "q8_0_row_bytes",
 ]
 

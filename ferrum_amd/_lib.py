@@ -144,6 +144,9 @@ SIGNATURES = {
                             c_void_p]),
     "fkv_gemm_q8_0_multi": (i32, [u32, c_void_p, c_void_p, c_void_p, u64, c_void_p, u64, u64,
                                   c_void_p, c_void_p, c_void_p]),
+    "fkv_gemm_q8_0_batched_workspace_size": (i32, [u64, u64, P(u64)]),
+    "fkv_gemm_q8_0_batched": (i32, [u32, c_void_p, c_void_p, c_void_p, u64, c_void_p, u64, u64,
+                                    c_void_p, c_void_p, c_void_p, u64, c_void_p]),
     "fkv_gguf_open": (i32, [ctypes.c_char_p, P(c_void_p)]),
     "fkv_gguf_close": (i32, [c_void_p]),
     "fkv_gguf_info": (i32, [c_void_p, P(u32), P(u64), P(u64), P(u64), P(u64), P(u64)]),

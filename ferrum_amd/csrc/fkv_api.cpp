@@ -1283,27 +1283,74 @@ int32_t fkv_gemm_q8_0(const void* w, uint64_t w_len, uint64_t rows, uint64_t col
   return gemm_q8(w, w_len, rows, cols, x, x_len, n_tokens, y, y_len, stream);
 }
 
-int32_t fkv_gemm_q8_0_multi(uint32_t n_mats, const void* const* w, const uint64_t* w_len,
-                            const uint64_t* rows, uint64_t cols, const float* x,
-                            uint64_t x_len, uint64_t n_tokens, float* const* y,
-                            const uint64_t* y_len, void* stream) {
+// The multi-matrix checks (fkv_gemm_q8_0_multi) into b; FKV_OK with b.n == 0 when
+// nothing is to be launched.
+static int32_t gemm_q8_batch(uint32_t n_mats, const void* const* w, const uint64_t* w_len,
+                             const uint64_t* rows, uint64_t cols, const float* x, uint64_t x_len,
+                             uint64_t n_tokens, float* const* y, const uint64_t* y_len,
+                             fkv::GemvBatch* b) {
+  *b = fkv::GemvBatch{};
   if (n_mats == 0 || n_mats > (uint32_t)fkv::kGemvMaxMats)
     return fail(FKV_ERR_INVALID, "n_mats must be 1..4");
   if (!w || !w_len || !rows || !y || !y_len) return fail(FKV_ERR_INVALID, "null argument");
-  if (n_tokens == 0) return ok();
-  fkv::GemvBatch b{};
+  if (n_tokens == 0) return FKV_OK;
   for (uint32_t m = 0; m < n_mats; ++m) {
     int32_t st = check_gemm_q8(w[m], w_len[m], rows[m], cols, x, x_len, n_tokens, y[m], y_len[m]);
     if (st) return st;
     if (rows[m] == 0) continue;
-    b.m[b.n].w = (const uint8_t*)w[m];
-    b.m[b.n].y = y[m];
-    b.m[b.n].rows = (uint32_t)rows[m];
-    b.n++;
+    b->m[b->n].w = (const uint8_t*)w[m];
+    b->m[b->n].y = y[m];
+    b->m[b->n].rows = (uint32_t)rows[m];
+    b->n++;
   }
+  return FKV_OK;
+}
+
+int32_t fkv_gemm_q8_0_multi(uint32_t n_mats, const void* const* w, const uint64_t* w_len,
+                            const uint64_t* rows, uint64_t cols, const float* x,
+                            uint64_t x_len, uint64_t n_tokens, float* const* y,
+                            const uint64_t* y_len, void* stream) {
+  fkv::GemvBatch b;
+  int32_t st = gemm_q8_batch(n_mats, w, w_len, rows, cols, x, x_len, n_tokens, y, y_len, &b);
+  if (st) return st;
   if (b.n == 0) return ok();
   FKV_HIP(fkv::launch_gemv_q8(b, (uint32_t)cols, x, (uint32_t)n_tokens, (hipStream_t)stream),
           "gemv launch");
+  return ok();
+}
+
+int32_t fkv_gemm_q8_0_batched_workspace_size(uint64_t cols, uint64_t n_tokens,
+                                             uint64_t* bytes_out) {
+  if (!bytes_out) return fail(FKV_ERR_INVALID, "null argument");
+  *bytes_out = 0;
+  if (cols == 0 || cols % 1024 != 0 || cols > 0xffffffffull || n_tokens > 0x7fff0000ull ||
+      n_tokens < fkv::kGemmMfmaMinTokens)
+    return ok();  // such calls run the GEMV and need no workspace
+  *bytes_out = fkv::gemm_mfma_workspace_bytes((uint32_t)cols, (uint32_t)n_tokens);
+  return ok();
+}
+
+int32_t fkv_gemm_q8_0_batched(uint32_t n_mats, const void* const* w, const uint64_t* w_len,
+                              const uint64_t* rows, uint64_t cols, const float* x,
+                              uint64_t x_len, uint64_t n_tokens, float* const* y,
+                              const uint64_t* y_len, void* workspace, uint64_t workspace_bytes,
+                              void* stream) {
+  fkv::GemvBatch b;
+  int32_t st = gemm_q8_batch(n_mats, w, w_len, rows, cols, x, x_len, n_tokens, y, y_len, &b);
+  if (st) return st;
+  if (b.n == 0) return ok();
+  if (!fkv::gemm_mfma_eligible(b, (uint32_t)cols, (uint32_t)n_tokens)) {
+    FKV_HIP(fkv::launch_gemv_q8(b, (uint32_t)cols, x, (uint32_t)n_tokens, (hipStream_t)stream),
+            "gemv launch");
+    return ok();
+  }
+  const uint64_t need = fkv::gemm_mfma_workspace_bytes((uint32_t)cols, (uint32_t)n_tokens);
+  if (!workspace || workspace_bytes < need) return fail(FKV_ERR_INVALID, "gemm workspace too small");
+  if ((uintptr_t)workspace % 16 != 0)
+    return fail(FKV_ERR_INVALID, "gemm workspace must be 16-byte aligned");
+  FKV_HIP(fkv::launch_gemm_q8_mfma(b, (uint32_t)cols, x, (uint32_t)n_tokens, workspace,
+                                   (hipStream_t)stream),
+          "gemm launch");
   return ok();
 }
 

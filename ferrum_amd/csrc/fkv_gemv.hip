@@ -43,6 +43,7 @@ namespace fkv {
 namespace {
 
 typedef float f32x4a __attribute__((ext_vector_type(4), aligned(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kQ8Bytes = 34;
 constexpr int kGemvWaves = 4;
@@ -360,7 +361,257 @@ hipError_t launch_t(const GemvBatch& b, uint32_t n_wg, uint32_t cols, const floa
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Batched Q8_0 GEMM on the matrix cores
+// ---------------------------------------------------------------------------
+//
+// For a batch of activation rows (a decode step's sequences, a prefill chunk) the GEMV
+// above takes 4 tokens a launch row, so a 64-token batch reads every weight 16 times.
+// Here the activation is quantized once, into a workspace (q8_act_kernel, the same
+// arithmetic as quantize_x), and gemm_q8_mfma_kernel takes each 32-value block's
+// integer dots of 16 weight rows x 16 tokens from one v_mfma_i32_16x16x32_i8: the int32
+// sums are exact, so they are the reference's sumi whatever the order inside the
+// instruction. Each output then takes acc = acc + f32(sumi) * (w_scale * x_scale) block
+// by block in order from +0, which is dot_q8_row_q8_act (q8_dot.rs:72-109) bit for bit.
+//
+// Workspace, per 16-token tile tt of the batch (tokens past n_tokens quantize to zeros):
+//   quants: 16-byte unit (tt, block pair p, lane) at ((tt * nb/2 + p) * 64 + lane) * 16;
+//           lane = grp*16 + c holds quants grp*8 .. +7 of token tt*16 + c of block 2p
+//           (bytes 0..7) and of block 2p + 1 (bytes 8..15): the MFMA B operand order,
+//           1 KiB per load instruction.
+//   scales: f32 (the binary16 scale's value); token c's scales of blocks 4u .. 4u + 3
+//           in the 16-byte unit (tt * nb/4 + u) * 16 + c after the quants.
+// Needs cols % 1024 == 0 (whole pairs of 16-block chunks) and 16-byte aligned weights.
+
+constexpr uint32_t kMmChunk = 16;       // blocks staged a step (544 bytes a row)
+constexpr uint32_t kMmRowStride = 552;  // LDS bytes a staged row: 138 dwords, so the 16
+                                        // rows' reads start in 16 distinct even banks
+constexpr uint32_t kMmUnits = 16u * 34u;  // 16-byte units of a staged chunk
+
+__host__ __device__ constexpr uint64_t mm_quant_bytes(uint32_t n_tiles, uint32_t nb) {
+  return (uint64_t)n_tiles * nb * 16u * 32u;  // 16 tokens x 32 quants a block
+}
+
+__global__ __launch_bounds__(256) void q8_act_kernel(const float* __restrict__ x, uint32_t cols,
+                                                     uint32_t n_tokens, uint32_t n_tiles,
+                                                     uint8_t* __restrict__ ws) {
+  // Item i: token t = i / (cols/8), values 8j .. 8j + 7 with j = i % (cols/8): piece
+  // grp = j % 4 of block j / 4. The four pieces of a block are a quad of lanes (the
+  // item count per token is a multiple of 4), which exits or stays as a whole.
+  const uint32_t per = cols / 8u, nb = cols / 32u;
+  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= (uint64_t)n_tiles * 16u * per) return;
+  const uint32_t t = (uint32_t)(i / per), j = (uint32_t)(i % per);
+  f32x4a a = {0.0f, 0.0f, 0.0f, 0.0f}, b = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (t < n_tokens) {
+    const float* src = x + (uint64_t)t * cols + 8u * j;
+    a = *(const f32x4a*)src;
+    b = *(const f32x4a*)(src + 4);
+  }
+  float m = __builtin_fmaxf(__builtin_fabsf(a.x), __builtin_fabsf(a.y));
+  m = __builtin_fmaxf(m, __builtin_fabsf(a.z));
+  m = __builtin_fmaxf(m, __builtin_fabsf(a.w));
+  m = __builtin_fmaxf(m, __builtin_fabsf(b.x));
+  m = __builtin_fmaxf(m, __builtin_fabsf(b.y));
+  m = __builtin_fmaxf(m, __builtin_fabsf(b.z));
+  m = __builtin_fmaxf(m, __builtin_fabsf(b.w));
+  m = __builtin_fmaxf(m, 0.0f);  // all NaN: 0, as the reference's amax = 0 start
+  m = __builtin_fmaxf(m, dev::dpp<0xB1>(m));
+  m = __builtin_fmaxf(m, dev::dpp<0x4E>(m));
+  const float d = div127(m);
+  const float id = (d != 0.0f) ? 1.0f / d : 0.0f;
+  const uint32_t qa = q8_byte(a.x * id) | (q8_byte(a.y * id) << 8) |
+                      (q8_byte(a.z * id) << 16) | (q8_byte(a.w * id) << 24);
+  const uint32_t qb = q8_byte(b.x * id) | (q8_byte(b.y * id) << 8) |
+                      (q8_byte(b.z * id) << 16) | (q8_byte(b.w * id) << 24);
+  const uint32_t tt = t / 16u, c = t % 16u, blk = j / 4u, grp = j % 4u;
+  const uint64_t unit = ((uint64_t)tt * (nb / 2u) + blk / 2u) * 64u + grp * 16u + c;
+  *(uint2*)(ws + unit * 16u + (blk % 2u) * 8u) = make_uint2(qa, qb);
+  if (grp == 0u) {
+    float* xs = (float*)(ws + mm_quant_bytes(n_tiles, nb));
+    xs[(((uint64_t)tt * (nb / 4u) + blk / 4u) * 16u + c) * 4u + blk % 4u] =
+        dev::f16_bits_to_f32(f16_bits_away(d));
+  }
+}
+
+// A workgroup: 16 weight rows of one of the launch's matrices x 4 token tiles (wave w:
+// tile blockIdx.y * 4 + w). The 16 rows' Q8_0 bytes are staged chunk by chunk (16
+// blocks) into LDS as stored, with their scales as f32 [block][row]; a lane (c, grp)
+// reads its A operand, quants grp*8 .. +7 of row c, from there (one 16-bit realignment
+// for blocks at 2 mod 4). Chunk k + 1's weights and B operands load while chunk k is
+// computed.
+struct MmB {
+  uint4 q[kMmChunk / 2];  // block pairs
+  uint4 s[kMmChunk / 4];  // scales of 4 blocks
+};
+
+__global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const GemvBatch bat, uint32_t cols,
+                                                           uint32_t n_tokens, uint32_t n_tiles,
+                                                           const uint8_t* __restrict__ ws) {
+  uint32_t mi = 0;
+#pragma unroll
+  for (int j = 1; j < kGemvMaxMats; ++j)
+    if ((uint32_t)j < bat.n && blockIdx.x >= bat.m[j].wg0) mi = (uint32_t)j;
+  const GemvMat M = mi == 0u ? bat.m[0] : mi == 1u ? bat.m[1] : mi == 2u ? bat.m[2] : bat.m[3];
+  const uint32_t rows = M.rows;
+  const uint32_t row0 = (blockIdx.x - M.wg0) * 16u;
+  const uint32_t nb = cols / 32u;
+  const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t c = lane & 15u, grp = lane >> 4;
+  const uint32_t tt = blockIdx.y * 4u + wave;
+  const bool on = tt < n_tiles;  // wave-uniform; an idle wave still stages
+  const uint32_t ttc = on ? tt : n_tiles - 1u;
+
+  __shared__ __align__(16) uint8_t s_w[2][16 * kMmRowStride];
+  __shared__ __align__(16) float s_ws[2][kMmChunk][16];
+
+  // Staging: thread t moves units t, t + 256, t + 512 (< 544) of the chunk's 16 rows
+  // (row u / 34, 16 bytes at u % 34) and the scale of (row t / 16, block t % 16). A
+  // row past the matrix stages its last row (never stored).
+  const uint8_t* wrow[3];
+  uint32_t ldst[3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const uint32_t u = tid + 256u * (uint32_t)i;
+    const uint32_t r = (u < kMmUnits ? u : 0u) / 34u, q = (u < kMmUnits ? u : 0u) % 34u;
+    const uint32_t rr = row0 + r < rows ? row0 + r : rows - 1u;
+    wrow[i] = M.w + (uint64_t)rr * row_bytes + q * 16u;
+    ldst[i] = r * kMmRowStride + q * 16u;
+  }
+  const uint32_t sr = tid / 16u, sb = tid % 16u;
+  const uint8_t* srow = M.w + (uint64_t)(row0 + sr < rows ? row0 + sr : rows - 1u) * row_bytes +
+                        sb * kQ8Bytes;
+  uint4 stg[3];
+  uint32_t sbits = 0;
+  auto stage_load = [&](uint32_t k) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (tid + 256u * (uint32_t)i < kMmUnits)
+        stg[i] = *(const uint4*)(wrow[i] + (uint64_t)k * (kMmChunk * kQ8Bytes));
+    sbits = *(const uint16_t*)(srow + (uint64_t)k * (kMmChunk * kQ8Bytes));
+  };
+  auto stage_store = [&](uint32_t buf) {
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+      if (tid + 256u * (uint32_t)i < kMmUnits) {
+        uint2* dst = (uint2*)&s_w[buf][ldst[i]];  // 8-byte aligned rows
+        dst[0] = make_uint2(stg[i].x, stg[i].y);
+        dst[1] = make_uint2(stg[i].z, stg[i].w);
+      }
+    s_ws[buf][sb][sr] = dev::f16_bits_to_f32(sbits);
+  };
+  // B operands and x scales of chunk k for this wave's token tile.
+  const uint8_t* bq = ws + (((uint64_t)ttc * (nb / 2u)) * 64u + lane) * 16u;
+  const uint8_t* bs = ws + mm_quant_bytes(n_tiles, nb) + (((uint64_t)ttc * (nb / 4u)) * 16u + c) * 16u;
+  auto b_load = [&](uint32_t k, MmB& o) {
+#pragma unroll
+    for (int p = 0; p < (int)kMmChunk / 2; ++p)
+      o.q[p] = *(const uint4*)(bq + ((uint64_t)k * (kMmChunk / 2u) + p) * 1024u);
+#pragma unroll
+    for (int u = 0; u < (int)kMmChunk / 4; ++u)
+      o.s[u] = *(const uint4*)(bs + ((uint64_t)k * (kMmChunk / 4u) + u) * 256u);
+  };
+
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // Chunk k from LDS buffer `buf` with B operands o; block order within the chunk.
+  auto compute = [&](uint32_t buf, const MmB& o) {
+    const uint8_t* wl = &s_w[buf][c * kMmRowStride + grp * 8u];
+#pragma unroll
+    for (int b = 0; b < (int)kMmChunk; ++b) {
+      uint32_t lo, hi;
+      if (b % 2 == 0) {  // quants at 34b + 2 + 8grp: 2 mod 4
+        const uint32_t* p = (const uint32_t*)(wl + 34 * b);
+        const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+        lo = __builtin_amdgcn_alignbit(d1, d0, 16);
+        hi = __builtin_amdgcn_alignbit(d2, d1, 16);
+      } else {  // 0 mod 4
+        const uint32_t* p = (const uint32_t*)(wl + 34 * b + 2);
+        lo = p[0];
+        hi = p[1];
+      }
+      const uint4 u = o.q[b / 2];
+      const long av = (long)(((uint64_t)hi << 32) | lo);
+      const long bv = (b % 2 == 0) ? (long)(((uint64_t)u.y << 32) | u.x)
+                                   : (long)(((uint64_t)u.w << 32) | u.z);
+      const v4i zero = {0, 0, 0, 0};
+      const v4i si = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
+      const float4 w4 = *(const float4*)&s_ws[buf][b][grp * 4u];
+      const uint4 s4 = o.s[b / 4];
+      const float xs = __uint_as_float((b % 4 == 0) ? s4.x : (b % 4 == 1) ? s4.y
+                                       : (b % 4 == 2) ? s4.z : s4.w);
+      acc[0] = acc[0] + (float)si[0] * (w4.x * xs);
+      acc[1] = acc[1] + (float)si[1] * (w4.y * xs);
+      acc[2] = acc[2] + (float)si[2] * (w4.z * xs);
+      acc[3] = acc[3] + (float)si[3] * (w4.w * xs);
+    }
+  };
+
+  const uint32_t nc = nb / kMmChunk;  // even
+  MmB b0, b1;
+  b_load(0, b0);
+  stage_load(0);
+  stage_store(0);
+  __syncthreads();
+  for (uint32_t k = 0; k < nc; k += 2) {
+    // chunk k (buffer 0, b0) while chunk k + 1 loads; then chunk k + 1 (buffer 1, b1)
+    b_load(k + 1, b1);
+    stage_load(k + 1);
+    if (on) compute(0, b0);
+    stage_store(1);
+    __syncthreads();
+    if (k + 2 < nc) {
+      b_load(k + 2, b0);
+      stage_load(k + 2);
+    }
+    if (on) compute(1, b1);
+    if (k + 2 < nc) stage_store(0);
+    __syncthreads();
+  }
+
+  if (!on) return;
+  const uint32_t tok = tt * 16u + c;
+  if (tok < n_tokens) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t row = row0 + grp * 4u + (uint32_t)r;
+      if (row < rows) M.y[(uint64_t)tok * rows + row] = acc[r];
+    }
+  }
+}
+
 }  // namespace
+
+bool gemm_mfma_eligible(const GemvBatch& b, uint32_t cols, uint32_t n_tokens) {
+  if (n_tokens < kGemmMfmaMinTokens || cols % 1024u != 0u) return false;
+  for (uint32_t m = 0; m < b.n; ++m)
+    if ((uintptr_t)b.m[m].w % 16u != 0u) return false;
+  return true;
+}
+
+uint64_t gemm_mfma_workspace_bytes(uint32_t cols, uint32_t n_tokens) {
+  const uint32_t n_tiles = (n_tokens + 15u) / 16u, nb = cols / 32u;
+  return mm_quant_bytes(n_tiles, nb) + (uint64_t)n_tiles * nb * 16u * 4u;
+}
+
+hipError_t launch_gemm_q8_mfma(GemvBatch b, uint32_t cols, const float* x, uint32_t n_tokens,
+                               void* workspace, hipStream_t s) {
+  uint32_t n_wg = 0;
+  for (uint32_t m = 0; m < b.n; ++m) {
+    b.m[m].wg0 = n_wg;
+    n_wg += (b.m[m].rows + 15u) / 16u;
+  }
+  for (uint32_t m = b.n; m < (uint32_t)kGemvMaxMats; ++m) b.m[m] = b.m[0];
+  const uint32_t n_tiles = (n_tokens + 15u) / 16u;
+  const uint64_t items = (uint64_t)n_tiles * 16u * (cols / 8u);
+  q8_act_kernel<<<(uint32_t)((items + 255u) / 256u), 256, 0, s>>>(x, cols, n_tokens, n_tiles,
+                                                                   (uint8_t*)workspace);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  gemm_q8_mfma_kernel<<<dim3(n_wg, (n_tiles + 3u) / 4u), 256, 0, s>>>(b, cols, n_tokens, n_tiles,
+                                                                      (const uint8_t*)workspace);
+  return hipGetLastError();
+}
 
 size_t gemv_lds_bytes(uint32_t tokens, uint32_t cols) {
   return (size_t)tokens * gemv_padded_blocks(cols / 32u) * kXDw * 4u;

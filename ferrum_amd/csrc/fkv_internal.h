@@ -218,5 +218,14 @@ struct GemvBatch {
 };
 hipError_t launch_gemv_q8(GemvBatch b, uint32_t cols, const float* x, uint32_t n_tokens,
                           hipStream_t s);
+// Batched form on the matrix cores (same results bit for bit): the activation quantized
+// once into a workspace of gemm_mfma_workspace_bytes, then one i8 MFMA per 32-value
+// block of 16 rows x 16 tokens. Eligible for n_tokens >= kGemmMfmaMinTokens, cols a
+// multiple of 1024 and 16-byte aligned weights.
+constexpr uint32_t kGemmMfmaMinTokens = 8;
+bool gemm_mfma_eligible(const GemvBatch& b, uint32_t cols, uint32_t n_tokens);
+uint64_t gemm_mfma_workspace_bytes(uint32_t cols, uint32_t n_tokens);
+hipError_t launch_gemm_q8_mfma(GemvBatch b, uint32_t cols, const float* x, uint32_t n_tokens,
+                               void* workspace, hipStream_t s);
 
 }  // namespace fkv

@@ -7,21 +7,23 @@ attention loop over the sequence's positions (:220-247) and linear attn_output
 (:249-255). Here that span is three launches on one stream for a batch of sequences,
 each with its own position:
 
-1. fkv_gemm_q8_0_multi: q, k and v from the normed rows, one launch (Q8_0 weights);
+1. fkv_gemm_q8_0_batched: q, k and v from the normed rows, one launch (Q8_0 weights; on
+   the matrix cores for batches of 8 sequences or more, the GEMV below that);
 2. fkv_rope_append_decode_attention: RoPE of q and k at position ctx_lens[s] - 1, the
    append of k and v through the block tables, decode attention;
-3. fkv_gemm_q8_0: attn_output of the attention rows.
+3. fkv_gemm_q8_0_batched: attn_output of the attention rows.
 
-Nothing crosses to the host. The activation buffers are allocated once, for the largest
-batch the layer was built for; the attention workspace grows when a call's plan needs more
-than it holds (the split plan depends on the batch and context, not monotonically).
+Nothing crosses to the host. The activation buffers and the GEMM workspace are allocated
+once, for the largest batch the layer was built for; the attention workspace grows when a
+call's plan needs more than it holds (the split plan depends on the batch and context, not
+monotonically).
 """
 from __future__ import annotations
 
 from typing import Optional
 
 from .kvcache import PagedKvPool, default_scale
-from .q8 import gemm_q8_0, gemm_q8_0_multi, q8_0_row_bytes
+from .q8 import gemm_q8_0_batched, gemm_q8_0_batched_workspace_bytes, q8_0_row_bytes
 
 
 class DecodeAttentionLayer:
@@ -56,6 +58,11 @@ class DecodeAttentionLayer:
         self.attn = torch.empty_like(self.q)
         need = pool.rope_attention_workspace_bytes(n_heads, max_seqs, max_ctx_len)
         self.ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        # the quantized activation rows of either GEMM (the launches are stream-ordered)
+        # (the size grows with the batch: the largest is the one for max_seqs rows)
+        gneed = max(gemm_q8_0_batched_workspace_bytes(n_embd, max_seqs),
+                    gemm_q8_0_batched_workspace_bytes(self.q_rows, max_seqs))
+        self.gws = torch.empty(max(gneed, 16), dtype=torch.uint8, device=dev)
 
     def _workspace(self, n: int, max_ctx_len: int):
         import torch
@@ -74,11 +81,12 @@ class DecodeAttentionLayer:
         if n == 0:
             return
         q, k, v, attn = self.q[:n], self.k[:n], self.v[:n], self.attn[:n]
-        gemm_q8_0_multi([self.wq, self.wk, self.wv], [self.q_rows, self.kv_rows, self.kv_rows],
-                        self.n_embd, x, n, [q, k, v], stream=stream)
+        gemm_q8_0_batched([self.wq, self.wk, self.wv], [self.q_rows, self.kv_rows, self.kv_rows],
+                          self.n_embd, x, n, [q, k, v], workspace=self.gws, stream=stream)
         self.pool.rope_append_decode_attention(self.layer, k, v, q, attn, block_tables, ctx_lens,
                                                max_ctx_len, self.rope_dim, self.theta,
                                                scale=self.scale,
                                                workspace=self._workspace(n, max_ctx_len),
                                                stream=stream)
-        gemm_q8_0(self.wo, self.n_embd, self.q_rows, attn, n, y, stream=stream)
+        gemm_q8_0_batched([self.wo], [self.n_embd], self.q_rows, attn, n, [y],
+                          workspace=self.gws, stream=stream)

@@ -22,7 +22,7 @@ from .errors import check
 from .kvcache import _stream_ptr
 
 __all__ = ["Q8_0_BLOCK", "Q8_0_BLOCK_BYTES", "gemv_q8_0", "gemm_q8_0", "gemm_q8_0_multi",
-           "q8_0_row_bytes"]
+           "gemm_q8_0_batched", "gemm_q8_0_batched_workspace_bytes", "q8_0_row_bytes"]
 
 Q8_0_BLOCK = 32        # crates/core-types/src/dtype.rs:19-21
 Q8_0_BLOCK_BYTES = 34
@@ -79,3 +79,34 @@ def gemm_q8_0_multi(ws, rows, cols: int, x, n_tokens: int, ys, stream=None) -> N
     check(_lib.load().fkv_gemm_q8_0_multi(
         n, arr_p(*[p for p, _ in wp]), arr_u(*[k for _, k in wp]), arr_u(*rows), cols, xp, xn,
         n_tokens, arr_p(*[p for p, _ in yp]), arr_u(*[k for _, k in yp]), _stream_ptr(stream)))
+
+
+def gemm_q8_0_batched_workspace_bytes(cols: int, n_tokens: int) -> int:
+    """Workspace bytes of gemm_q8_0_batched (0 where the call runs the GEMV)."""
+    n = ctypes.c_uint64()
+    check(_lib.load().fkv_gemm_q8_0_batched_workspace_size(cols, n_tokens, ctypes.byref(n)))
+    return n.value
+
+
+def gemm_q8_0_batched(ws, rows, cols: int, x, n_tokens: int, ys, workspace=None,
+                      stream=None) -> None:
+    """gemm_q8_0_multi on the matrix cores for batches (n_tokens >= 8, cols a multiple of
+    1024, 16-byte aligned weights; otherwise the GEMV), bit-identical. `workspace`: a
+    device uint8 tensor of gemm_q8_0_batched_workspace_bytes (allocated here when None)."""
+    import torch
+    n = len(ws)
+    if len(rows) != n or len(ys) != n:
+        raise ValueError("ws, rows and ys must have one entry per matrix")
+    wp = [_dev_any(w, torch.uint8, "w") for w in ws]
+    yp = [_dev_any(y, torch.float32, "y") for y in ys]
+    xp, xn = _dev_any(x, torch.float32, "x")
+    need = gemm_q8_0_batched_workspace_bytes(cols, n_tokens)
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    wsp, wsn = (workspace.data_ptr(), workspace.numel()) if workspace is not None else (0, 0)
+    arr_p = ctypes.c_void_p * max(n, 1)
+    arr_u = ctypes.c_uint64 * max(n, 1)
+    check(_lib.load().fkv_gemm_q8_0_batched(
+        n, arr_p(*[p for p, _ in wp]), arr_u(*[k for _, k in wp]), arr_u(*rows), cols, xp, xn,
+        n_tokens, arr_p(*[p for p, _ in yp]), arr_u(*[k for _, k in yp]), wsp, wsn,
+        _stream_ptr(stream)))

@@ -73,6 +73,28 @@ int32_t fkv_gemm_q8_0_multi(uint32_t n_mats, const void* const* w, const uint64_
                             uint64_t x_len, uint64_t n_tokens, float* const* y,
                             const uint64_t* y_len, void* stream);
 
+/* fkv_gemm_q8_0_multi for batches of activation rows (a decode step's sequences, a
+ * prefill chunk) on the matrix cores, with the same results bit for bit. No counterpart
+ * in the reference, which loops over tokens (scalar.rs:98-116); the entry points above
+ * read every weight once per 4 tokens. Here each activation row is quantized once into
+ * `workspace`, and one v_mfma_i32_16x16x32_i8 gives a 32-value block's exact integer
+ * dots for 16 weight rows x 16 tokens; each output then accumulates
+ * f32(sumi) * (w_scale * x_scale) block by block in order, as dot_q8_row_q8_act does.
+ * That path runs when n_tokens >= 8, cols is a multiple of 1024 and every w is 16-byte
+ * aligned; other calls run the GEMV kernel (workspace unused). Same checks, strings
+ * and order as fkv_gemm_q8_0_multi; then, for a call that takes the matrix-core path,
+ * a workspace that is NULL, smaller than fkv_gemm_q8_0_batched_workspace_size() or not
+ * 16-byte aligned is FKV_ERR_INVALID "gemm workspace too small" / "gemm workspace must
+ * be 16-byte aligned". The workspace needs no initialisation; calls that share one
+ * must not overlap. */
+int32_t fkv_gemm_q8_0_batched_workspace_size(uint64_t cols, uint64_t n_tokens,
+                                             uint64_t* bytes_out);
+int32_t fkv_gemm_q8_0_batched(uint32_t n_mats, const void* const* w, const uint64_t* w_len,
+                              const uint64_t* rows, uint64_t cols, const float* x,
+                              uint64_t x_len, uint64_t n_tokens, float* const* y,
+                              const uint64_t* y_len, void* workspace, uint64_t workspace_bytes,
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif
