@@ -514,54 +514,63 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const GemvBatch bat, 
   };
 
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  // Chunk k from LDS buffer `buf` with B operands o; block order within the chunk.
+  // Chunk k from LDS buffer `buf` with B operands o. Four blocks' integer dots are
+  // issued before their epilogues, which then run in block order.
   auto compute = [&](uint32_t buf, const MmB& o) {
     const uint8_t* wl = &s_w[buf][c * kMmRowStride + grp * 8u];
 #pragma unroll
-    for (int b = 0; b < (int)kMmChunk; ++b) {
-      uint32_t lo, hi;
-      if (b % 2 == 0) {  // quants at 34b + 2 + 8grp: 2 mod 4
-        const uint32_t* p = (const uint32_t*)(wl + 34 * b);
-        const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
-        lo = __builtin_amdgcn_alignbit(d1, d0, 16);
-        hi = __builtin_amdgcn_alignbit(d2, d1, 16);
-      } else {  // 0 mod 4
-        const uint32_t* p = (const uint32_t*)(wl + 34 * b + 2);
-        lo = p[0];
-        hi = p[1];
+    for (int b0 = 0; b0 < (int)kMmChunk; b0 += 4) {
+      v4i si[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = b0 + i;
+        uint32_t lo, hi;
+        if (b % 2 == 0) {  // quants at 34b + 2 + 8grp: 2 mod 4
+          const uint32_t* p = (const uint32_t*)(wl + 34 * b);
+          const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
+          lo = __builtin_amdgcn_alignbit(d1, d0, 16);
+          hi = __builtin_amdgcn_alignbit(d2, d1, 16);
+        } else {  // 0 mod 4
+          const uint32_t* p = (const uint32_t*)(wl + 34 * b + 2);
+          lo = p[0];
+          hi = p[1];
+        }
+        const uint4 u = o.q[b / 2];
+        const long av = (long)(((uint64_t)hi << 32) | lo);
+        const long bv = (b % 2 == 0) ? (long)(((uint64_t)u.y << 32) | u.x)
+                                     : (long)(((uint64_t)u.w << 32) | u.z);
+        const v4i zero = {0, 0, 0, 0};
+        si[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
       }
-      const uint4 u = o.q[b / 2];
-      const long av = (long)(((uint64_t)hi << 32) | lo);
-      const long bv = (b % 2 == 0) ? (long)(((uint64_t)u.y << 32) | u.x)
-                                   : (long)(((uint64_t)u.w << 32) | u.z);
-      const v4i zero = {0, 0, 0, 0};
-      const v4i si = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
-      const float4 w4 = *(const float4*)&s_ws[buf][b][grp * 4u];
-      const uint4 s4 = o.s[b / 4];
-      const float xs = __uint_as_float((b % 4 == 0) ? s4.x : (b % 4 == 1) ? s4.y
-                                       : (b % 4 == 2) ? s4.z : s4.w);
-      acc[0] = acc[0] + (float)si[0] * (w4.x * xs);
-      acc[1] = acc[1] + (float)si[1] * (w4.y * xs);
-      acc[2] = acc[2] + (float)si[2] * (w4.z * xs);
-      acc[3] = acc[3] + (float)si[3] * (w4.w * xs);
+      const uint4 s4 = o.s[b0 / 4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = b0 + i;
+        const float4 w4 = *(const float4*)&s_ws[buf][b][grp * 4u];
+        const float xs = __uint_as_float(i == 0 ? s4.x : i == 1 ? s4.y : i == 2 ? s4.z : s4.w);
+        acc[0] = acc[0] + (float)si[i][0] * (w4.x * xs);
+        acc[1] = acc[1] + (float)si[i][1] * (w4.y * xs);
+        acc[2] = acc[2] + (float)si[i][2] * (w4.z * xs);
+        acc[3] = acc[3] + (float)si[i][3] * (w4.w * xs);
+      }
     }
   };
 
   const uint32_t nc = nb / kMmChunk;  // even
   MmB b0, b1;
-  b_load(0, b0);
+  if (on) b_load(0, b0);
   stage_load(0);
   stage_store(0);
   __syncthreads();
   for (uint32_t k = 0; k < nc; k += 2) {
     // chunk k (buffer 0, b0) while chunk k + 1 loads; then chunk k + 1 (buffer 1, b1)
-    b_load(k + 1, b1);
+    if (on) b_load(k + 1, b1);
     stage_load(k + 1);
     if (on) compute(0, b0);
     stage_store(1);
     __syncthreads();
     if (k + 2 < nc) {
-      b_load(k + 2, b0);
+      if (on) b_load(k + 2, b0);
       stage_load(k + 2);
     }
     if (on) compute(1, b1);
