@@ -154,7 +154,7 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
   }
   // Four device words: the FKV_FAULT_* bits; the sticky mark of a Q8_0 scale of 512 or
   // more (read by the attention kernels to pick their exact instance); the sticky mark
-  // of an Inf/NaN V stored in an F16 pool (read by chunked prefill to pick its
+  // of an Inf/NaN K or V stored in an F16 pool (read by chunked prefill to pick its
   // leak-safe instance); the staging word of fkv_paged_take_fault_flags.
   e = hipMalloc((void**)&p->fault, 4 * sizeof(uint32_t));
   if (e == hipSuccess) e = hipMemset(p->fault, 0, 4 * sizeof(uint32_t));
@@ -237,7 +237,7 @@ int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream) {
     const uint8_t wide = (byte & 0x60u) == 0x60u ? 1 : 0;
     FKV_HIP(fkv::launch_fill(pool->fault + 1, wide, sizeof(uint32_t), (hipStream_t)stream), "fill");
   } else if (pool->cfg.kv_dtype == FKV_DTYPE_F16) {
-    // Every V value is now (byte << 8 | byte): Inf/NaN exactly when its exponent bits are.
+    // Every K and V value is now (byte << 8 | byte): Inf/NaN exactly when its exponent bits are.
     const uint8_t nonfinite = (byte & 0x7cu) == 0x7cu ? 1 : 0;
     FKV_HIP(fkv::launch_fill(pool->fault + 2, nonfinite, sizeof(uint32_t), (hipStream_t)stream),
             "fill");
@@ -246,18 +246,13 @@ int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream) {
 }
 
 // Whether bytes [offset, offset + bytes) of an F16 pool image (src) write an Inf or NaN
-// into a V tile (tile i of the pool is V when (i / n_kv_heads) is odd; every 16-bit
-// word of it is a value, little-endian, so its high byte decides).
-static bool f16_image_has_nonfinite_v(const fkv_pool* pool, uint64_t offset, uint64_t bytes,
-                                      const uint8_t* src) {
-  const uint64_t tile = pool->geom.tile_bytes, hkv = pool->cfg.n_kv_heads;
-  const uint64_t end = offset + bytes;
-  for (uint64_t t = offset / tile; t * tile < end; t++) {
-    if ((t / hkv) % 2 == 0) continue;  // a K tile
-    const uint64_t a = std::max(t * tile, offset), b = std::min((t + 1) * tile, end);
-    for (uint64_t x = a + ((a - t * tile) % 2 == 0 ? 1 : 0); x < b; x += 2)
-      if ((src[x - offset] & 0x7cu) == 0x7cu) return true;
-  }
+// K or V value (every 16-bit word of a K or V tile is a value, little-endian, so its high
+// byte decides; tiles start at even offsets, so the high bytes are the odd offsets).
+static bool f16_image_has_nonfinite_kv(const fkv_pool* pool, uint64_t offset, uint64_t bytes,
+                                       const uint8_t* src) {
+  (void)pool;
+  for (uint64_t x = offset + (offset % 2 == 0 ? 1 : 0); x < offset + bytes; x += 2)
+    if ((src[x - offset] & 0x7cu) == 0x7cu) return true;
   return false;
 }
 
@@ -310,7 +305,7 @@ int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const v
   const int word = pool->cfg.kv_dtype == FKV_DTYPE_Q8_0 &&
                            q8_image_has_wide_scale(pool, offset, bytes, img) ? 1
                    : pool->cfg.kv_dtype == FKV_DTYPE_F16 &&
-                           f16_image_has_nonfinite_v(pool, offset, bytes, img) ? 2
+                           f16_image_has_nonfinite_kv(pool, offset, bytes, img) ? 2
                                                                                 : 0;
   if (word) FKV_HIP(fkv::launch_fill(pool->fault + word, 1, sizeof(uint32_t), s), "pool write");
   FKV_HIP(hipStreamSynchronize(s), "synchronize");

@@ -205,9 +205,11 @@ __device__ __forceinline__ void qk_block(const uint4 (&kr)[D / 32], const f16x8 
                                          const f16x8 (&ql)[D / 32], float hscale,
                                          const Lane& ln, bool live, int32_t t0, int32_t end,
                                          float (&s)[4]) {
-  // hi and lo parts in separate chains: a K value of +-inf times a zero lo part
-  // is NaN, where the f32 dot of the reference gives +-inf. A NaN that only the lo
-  // chain has is that case, and the hi chain alone is the right score.
+  // hi and lo parts in separate chains. An infinite K value meets q's hi part with
+  // the sign of q (its hi part is q rounded), so the hi chain holds every infinity of
+  // the reference's f32 dot with the right sign; the lo part can be zero (inf * 0 =
+  // NaN) or of the other sign (+inf + -inf = NaN in the sum). So a NaN sum whose hi
+  // chain is not NaN takes the hi chain alone.
   f32x4 ah = {0.0f, 0.0f, 0.0f, 0.0f}, al = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int c = 0; c < D / 32; c++) {
@@ -218,7 +220,8 @@ __device__ __forceinline__ void qk_block(const uint4 (&kr)[D / 32], const f16x8 
 #pragma unroll
   for (int r = 0; r < 4; r++) {
     const bool ok = ln.real && live && t0 + ln.grp * 4 + r < end;
-    const float x = (al[r] != al[r] && ah[r] == ah[r]) ? ah[r] : ah[r] + al[r];
+    const float sum = ah[r] + al[r];
+    const float x = (sum != sum && ah[r] == ah[r]) ? ah[r] : sum;
     s[r] = ok ? x * hscale : -__builtin_inff();
   }
 }
@@ -523,7 +526,8 @@ __device__ __forceinline__ void qk_block_q8x(const BlockRegs<kDtypeQ8, D>& rg,
     const f32x4 tl = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], zero, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-      const float x = (tl[r] != tl[r] && th[r] == th[r]) ? th[r] : th[r] + tl[r];
+      const float sum = th[r] + tl[r];  // see qk_block: a NaN sum, hi chain not NaN
+      const float x = (sum != sum && th[r] == th[r]) ? th[r] : sum;
       const float d = f16_bits_to_f32((sc[r][c / 2] >> (16 * (c & 1))) & 0xffffu);
       acc[r] = __builtin_fmaf(d, x, acc[r]);
     }
@@ -1189,12 +1193,14 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
             ln.lane == 0)
           mark_wide(g.fault);
       } else {
-        s_app[0][dd] = (uint16_t)encode_f16(kv, g.rounding);
+        const uint32_t ke = encode_f16(kv, g.rounding);
+        s_app[0][dd] = (uint16_t)ke;
         const uint32_t ve = encode_f16(vv, g.rounding);
         s_app[1][dd] = (uint16_t)ve;
-        // an Inf/NaN V marks the pool (chunked prefill's leak-safe instance)
-        if (__builtin_amdgcn_ballot_w64(f16_nonfinite(ve)) != 0 && ln.lane == 0)
-          mark_nonfinite_v(g.fault);
+        // an Inf/NaN K or V marks the pool (chunked prefill's leak-safe instance)
+        if (__builtin_amdgcn_ballot_w64(f16_nonfinite(ke) || f16_nonfinite(ve)) != 0 &&
+            ln.lane == 0)
+          mark_nonfinite_kv(g.fault);
       }
     }
   };
@@ -1412,7 +1418,7 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
 // layer. Padding columns (ln.real false) are not masked: their q is zero, their
 // accumulator rows are their own (an MFMA output row depends on its A row only)
 // and never written.
-template <int D>
+template <int D, bool REPAIR = true>
 __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
                                             const f16x8 (&ql)[D / 32],
                                             const Lane& ln, bool live, bool full, int32_t t0,
@@ -1427,12 +1433,15 @@ __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16
   float x[4];
 #pragma unroll
   for (int r = 0; r < 4; r++) x[r] = ah[r] + al[r];
-  // One test for the four: a NaN score makes the sum NaN (as does inf - inf, which only
-  // sends the block through the repair below, where it changes nothing).
-  const float xs = (x[0] + x[1]) + (x[2] + x[3]);
-  if (__builtin_amdgcn_ballot_w64(xs != xs) != 0) {  // see qk_block: the inf * 0 case
+  // One test for the four: a NaN score makes the sum NaN. Only an infinite K makes the
+  // sum NaN with a hi chain that is not (see qk_block); the fast F16 instance runs over
+  // pools that never stored one (the non-finite mark) and skips the test.
+  if constexpr (REPAIR) {
+    const float xs = (x[0] + x[1]) + (x[2] + x[3]);
+    if (__builtin_amdgcn_ballot_w64(xs != xs) != 0) {  // see qk_block
 #pragma unroll
-    for (int r = 0; r < 4; r++) x[r] = ((al[r] != al[r]) & (ah[r] == ah[r])) ? ah[r] : x[r];
+      for (int r = 0; r < 4; r++) x[r] = ((x[r] != x[r]) & (ah[r] == ah[r])) ? ah[r] : x[r];
+    }
   }
   if (live && full) {
 #pragma unroll
@@ -1552,7 +1561,7 @@ __device__ __forceinline__ bool v_nonfinite_in(const u32x2_t (&vr)[D / 16], cons
 //
 // Tokens past a column's causal end carry weight 0 in the P.V product, but an
 // Inf/NaN V there would still reach the column through 0 * NaN. F16 pools that have
-// stored such a value carry a sticky mark (pool_has_nonfinite_v) and run the
+// stored a non-finite K or V carry a sticky mark (pool_has_nonfinite_kv) and run the
 // leak-safe instance: on a block that crosses the tile's nearest causal end, a
 // wave-uniform check for non-finite V values past that end sends the block down a
 // masked path, one P.V per query token of the tile with P restricted to that token's
@@ -1626,9 +1635,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     if (pool_has_wide_scales(g.fault) != EXACT) return;
   }
   if constexpr (DT == kDtypeF16) {
-    // Likewise the pool's mark of a stored Inf/NaN V (appends, fill and write set it):
-    // without one the fast instance computes, with one the leak-safe instance.
-    if (pool_has_nonfinite_v(g.fault) != (MODE == kPfLeakSafe)) return;
+    // Likewise the pool's mark of a stored Inf/NaN K or V (appends, fill and write set
+    // it): without one the fast instance computes, with one the leak-safe instance.
+    if (pool_has_nonfinite_kv(g.fault) != (MODE == kPfLeakSafe)) return;
   }
   // Which sequence this workgroup takes: its grid column's, moved on by a quarter of
   // the batch per step of q(y) = (y + y / 8) % 4. The hardware deals workgroups
@@ -1779,13 +1788,19 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
       const uint8_t* ks = s_kv[buf][bb];
-      if (j < jw_end) {  // wave-uniform: blocks past the wave's tile are skipped
+      // F16: every wave scores both blocks. One past the wave's tile (at most the last of
+      // the workgroup's range, or a slot holding an earlier step's block) lies past every
+      // column's causal end, so the causal mask gives it -inf throughout; skipping it
+      // instead cost a -inf store of the four scores on every step. Q8_0 skips it (its
+      // operand conversion for such a block would spill inside the loop).
+      if (DT == kDtypeF16 || j < jw_end) {  // wave-uniform
         if constexpr (DT == kDtypeF16) {
           uint4 kr[NC];
 #pragma unroll
           for (int c = 0; c < NC; c++)
             kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
-          qk_block_pf<D>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
+          qk_block_pf<D, MODE != kPfFast>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0,
+                                          end_col, sc[bb]);
         } else {
           BlockRegs<kDtypeQ8, D> rg;
           rg.template load_k_tile<true>(ks, ln);
@@ -1794,7 +1809,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
           } else {
             uint4 kr[NC];
             rg.k_operand(kr);
-            qk_block_pf<D>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0, end_col, sc[bb]);
+            // (the repair kept: without it the register allocation spills 12 bytes)
+            qk_block_pf<D, true>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0, end_col,
+                                 sc[bb]);
           }
         }
       } else {
@@ -2066,7 +2083,7 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
                                                         split_blocks, max_splits, ws_o, ws_ml)
   // The fast instance, then the one for pools whose marks say the fast one cannot
   // compute them: Q8_0 the exact instance (a scale of 512 or more was stored), F16 the
-  // leak-safe one (an Inf/NaN V was stored). Each exits at once where the other works.
+  // leak-safe one (an Inf/NaN K or V was stored). Each exits at once where the other works.
   const int dt = g.dtype == kDtypeQ8 ? kDtypeQ8 : kDtypeF16;
   if (dt == kDtypeQ8) {
     if (g.head_dim == 128) FKV_LAUNCH_PF(kDtypeQ8, 128, kPfFast);

@@ -44,15 +44,20 @@ __device__ __forceinline__ bool pool_has_wide_scales(const uint32_t* fault) {
   return __builtin_amdgcn_readfirstlane(__atomic_load_n(fault + 1, __ATOMIC_RELAXED)) != 0;
 }
 
-// F16 pools: the third fault word records, sticky, that an Inf or NaN V value was
-// stored (append, fused step, fill, write). Chunked prefill over such a pool takes
-// its leak-safe instance, which keeps those values from queries whose causal end
-// lies before them.
+// F16 pools: the third fault word records, sticky, that an Inf or NaN K or V value
+// was stored (append, fused step, fill, write). Chunked prefill over such a pool takes
+// its leak-safe instance, which keeps such V values from queries whose causal end lies
+// before them and repairs the scores an infinite K gives (inf x 0 in the q lo part);
+// without one, the fast instance does neither.
 __device__ __forceinline__ bool f16_nonfinite(uint32_t bits) { return (bits & 0x7c00u) == 0x7c00u; }
-__device__ __forceinline__ void mark_nonfinite_v(uint32_t* fault) {
+// either binary16 of a packed pair
+__device__ __forceinline__ bool f16x2_nonfinite(uint32_t w) {
+  return f16_nonfinite(w & 0xffffu) || f16_nonfinite(w >> 16);
+}
+__device__ __forceinline__ void mark_nonfinite_kv(uint32_t* fault) {
   if (__atomic_load_n(fault + 2, __ATOMIC_RELAXED) == 0u) atomicOr(fault + 2, 1u);
 }
-__device__ __forceinline__ bool pool_has_nonfinite_v(const uint32_t* fault) {
+__device__ __forceinline__ bool pool_has_nonfinite_kv(const uint32_t* fault) {
   return __builtin_amdgcn_readfirstlane(__atomic_load_n(fault + 2, __ATOMIC_RELAXED)) != 0;
 }
 

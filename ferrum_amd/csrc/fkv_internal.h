@@ -42,7 +42,7 @@ struct Geom {
   int32_t rounding;  // 0 nearest-even, 1 ties away
   uint32_t* fault;   // device words: [0] FKV_FAULT_* bits; [1] nonzero once a Q8_0
                      // scale of 512 or more was stored (sticky; q8_wide_scale);
-                     // [2] nonzero once an F16 pool stored an Inf/NaN V (sticky;
+                     // [2] nonzero once an F16 pool stored an Inf/NaN K or V (sticky;
                      // f16_nonfinite); [3] staging word of the fault read
 };
 

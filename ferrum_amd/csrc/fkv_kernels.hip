@@ -105,11 +105,14 @@ __global__ void __launch_bounds__(256) append_f16_kernel(Geom g, uint32_t layer,
     const float* src = k + ((uint64_t)token * g.n_kv_heads + h) * D + c * 8u;
     const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
     uint8_t* tile = tile_ptr(g, (uint64_t)slot / Bs, layer, 0, h);
-    *(uint4*)(tile + ((uint64_t)c * Bs + (uint64_t)slot % Bs) * 16u) =
-        make_uint4(encode_f16(a.x, g.rounding) | (encode_f16(a.y, g.rounding) << 16),
-                   encode_f16(a.z, g.rounding) | (encode_f16(a.w, g.rounding) << 16),
-                   encode_f16(b.x, g.rounding) | (encode_f16(b.y, g.rounding) << 16),
-                   encode_f16(b.z, g.rounding) | (encode_f16(b.w, g.rounding) << 16));
+    const uint4 w = make_uint4(encode_f16(a.x, g.rounding) | (encode_f16(a.y, g.rounding) << 16),
+                               encode_f16(a.z, g.rounding) | (encode_f16(a.w, g.rounding) << 16),
+                               encode_f16(b.x, g.rounding) | (encode_f16(b.y, g.rounding) << 16),
+                               encode_f16(b.z, g.rounding) | (encode_f16(b.w, g.rounding) << 16));
+    *(uint4*)(tile + ((uint64_t)c * Bs + (uint64_t)slot % Bs) * 16u) = w;
+    if (f16x2_nonfinite(w.x) || f16x2_nonfinite(w.y) || f16x2_nonfinite(w.z) ||
+        f16x2_nonfinite(w.w))
+      mark_nonfinite_kv(g.fault);  // chunked prefill then takes its leak-safe instance
     return;
   }
   const uint32_t dgs = D / 16;  // 16-dim groups per head
@@ -137,7 +140,7 @@ __global__ void __launch_bounds__(256) append_f16_kernel(Geom g, uint32_t layer,
   vt[2 * Bs] = (uint16_t)e2;
   vt[3 * Bs] = (uint16_t)e3;
   if (f16_nonfinite(e0) || f16_nonfinite(e1) || f16_nonfinite(e2) || f16_nonfinite(e3))
-    mark_nonfinite_v(g.fault);  // chunked prefill then takes its leak-safe instance
+    mark_nonfinite_kv(g.fault);  // chunked prefill then takes its leak-safe instance
 }
 
 // F16 storage, block_size 16, head_dim 64 or 128, 16-byte aligned k/v: one workgroup
@@ -191,19 +194,20 @@ __global__ void __launch_bounds__(256) append_f16_tile_kernel(Geom g, uint32_t l
     const float4 a = *(const float4*)ks, b = *(const float4*)(ks + 4);
     const float4 x = *(const float4*)vs, y = *(const float4*)(vs + 4);
     uint8_t* kt = tile_ptr(g, (uint64_t)slot / 16u, layer, 0, h);
-    *(uint4*)(kt + ((uint64_t)c * 16u + (uint64_t)slot % 16u) * 16u) =
-        make_uint4(encode_f16(a.x, g.rounding) | (encode_f16(a.y, g.rounding) << 16),
-                   encode_f16(a.z, g.rounding) | (encode_f16(a.w, g.rounding) << 16),
-                   encode_f16(b.x, g.rounding) | (encode_f16(b.y, g.rounding) << 16),
-                   encode_f16(b.z, g.rounding) | (encode_f16(b.w, g.rounding) << 16));
+    const uint4 kw = make_uint4(encode_f16(a.x, g.rounding) | (encode_f16(a.y, g.rounding) << 16),
+                                encode_f16(a.z, g.rounding) | (encode_f16(a.w, g.rounding) << 16),
+                                encode_f16(b.x, g.rounding) | (encode_f16(b.y, g.rounding) << 16),
+                                encode_f16(b.z, g.rounding) | (encode_f16(b.w, g.rounding) << 16));
+    *(uint4*)(kt + ((uint64_t)c * 16u + (uint64_t)slot % 16u) * 16u) = kw;
     ve[0] = encode_f16(x.x, g.rounding); ve[1] = encode_f16(x.y, g.rounding);
     ve[2] = encode_f16(x.z, g.rounding); ve[3] = encode_f16(x.w, g.rounding);
     ve[4] = encode_f16(y.x, g.rounding); ve[5] = encode_f16(y.y, g.rounding);
     ve[6] = encode_f16(y.z, g.rounding); ve[7] = encode_f16(y.w, g.rounding);
-    bool nf = false;
+    bool nf = f16x2_nonfinite(kw.x) || f16x2_nonfinite(kw.y) || f16x2_nonfinite(kw.z) ||
+              f16x2_nonfinite(kw.w);
 #pragma unroll
     for (int e = 0; e < 8; e++) nf = nf || f16_nonfinite(ve[e]);
-    if (nf) mark_nonfinite_v(g.fault);  // chunked prefill then takes its leak-safe instance
+    if (nf) mark_nonfinite_kv(g.fault);  // chunked prefill then takes its leak-safe instance
   }
 #pragma unroll
   for (int e = 0; e < 8; e++) s_v[hl][c * 8u + e][o] = (uint16_t)ve[e];
@@ -275,7 +279,7 @@ __global__ void __launch_bounds__(256) append_scalar_kernel(Geom g, uint32_t lay
       const uint32_t e = encode_f16(x, g.rounding);
       ((uint16_t*)tile)[kv ? (uint64_t)d * g.block_size + off
                            : ((uint64_t)(d / 8) * g.block_size + off) * 8 + d % 8] = (uint16_t)e;
-      if (kv && f16_nonfinite(e)) mark_nonfinite_v(g.fault);
+      if (f16_nonfinite(e)) mark_nonfinite_kv(g.fault);
     } else
       ((float*)tile)[off * D + d] = x;
   }

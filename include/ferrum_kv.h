@@ -372,8 +372,8 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
  * above it (or above ctx_lens[s]) raises FKV_FAULT_CTX_RANGE, and only its first
  * max_q_len queries are computed, at the positions q_lens[s] gives them. No query
  * reads a position past its own, Inf/NaN values included: an F16 pool that has
- * stored an Inf/NaN V runs a slower instance that keeps them from earlier queries
- * of the same tile. Q8_0 follows fkv_decode_attention's rule for scales of 512 or
+ * stored an Inf/NaN K or V runs a slower instance that keeps such V values from
+ * earlier queries of the same tile and gives an infinite K's scores exactly. Q8_0 follows fkv_decode_attention's rule for scales of 512 or
  * more.
  * workspace: NULL, or device scratch of fkv_prefill_attention_workspace_size()
  * bytes (16-byte aligned; no initialisation) in which workgroups over long

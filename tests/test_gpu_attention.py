@@ -265,6 +265,37 @@ def test_attention_non_finite_scores(ctx, dtype):
     assert np.all(got2 == 0.0)
 
 
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("bad", [np.inf, -np.inf])
+def test_attention_infinite_k_with_any_q(bad, dtype):
+    """One K row holds +-Inf at two dims; 16 query heads see it with random q there. On
+    the matrix cores q is split into f16 hi + lo parts after a scaling, so the lo part
+    at those dims is zero or of either sign: the score must still be the reference's
+    dot (+-Inf, or NaN where the two infinities meet with opposite signs), giving zeros,
+    a dropped token or NaN as the oracle does."""
+    import ferrum_amd as fa
+    from oracle import ref
+    d, hkv, g, ctx = 128, 1, 16, 300
+    nb = (ctx + 15) // 16
+    pool, layout = make_pools(1, hkv, d, nb + 2, dtype=dtype)
+    pool.fill(0)
+    rng = np.random.default_rng(12)
+    k = rng.standard_normal((ctx, hkv, d), dtype=np.float32)
+    v = rng.standard_normal((ctx, hkv, d), dtype=np.float32)
+    k[ctx // 2, 0, [7, 90]] = bad
+    tab = np.arange(nb, dtype=np.int32)[None, :]
+    pool.append(0, to_dev(k), to_dev(v), to_dev(slots_for(tab[0], ctx)))
+    q = rng.standard_normal((1, g, d), dtype=np.float32)
+    q[0, :8, 7] = rng.uniform(0.3, 3.0, 8)        # same sign at both dims
+    q[0, :8, 90] = rng.uniform(0.3, 3.0, 8)
+    q[0, 8:12, 7] = rng.uniform(0.3, 3.0, 4)      # opposite signs: NaN
+    q[0, 8:12, 90] = -rng.uniform(0.3, 3.0, 4)
+    got = _run(pool, 0, q, tab, [ctx])
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array([ctx]), fa.default_scale(d))
+    assert np.isnan(want[0, 8:12]).all()
+    assert_close(got, want)
+
+
 @pytest.mark.parametrize("dtype", [1, 8, 0])
 def test_fused_step_past_max_ctx_len_stores_no_token(dtype):
     """The fused step under the same rule on every storage type: sequence 2's context

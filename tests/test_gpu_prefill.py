@@ -7,7 +7,9 @@ output rows outside the chunk are never written. Also:
 - an Inf or NaN V inside a chunk reaches exactly the queries whose causal range holds
   it (the reference's token loop never reads a later position), through the
   leak-safe instance that a pool which stored such a value runs, which also meets
-  the bar on finite data;
+  the bar on finite data; an infinite K (stored by the bulk append or the fused
+  decode step) marks the pool the same way, and its +-Inf scores come out as the
+  reference's dot gives them;
 - a sequence whose q_len exceeds the call's max_q_len (the grid holds no more) is
   clamped to it and raises FKV_FAULT_CTX_RANGE;
 - Q8_0 pools, with ordinary values and with values up to +-1e6 (the exact instance);
@@ -204,6 +206,48 @@ def test_nonfinite_v_reaches_only_later_queries(bad, g, pieces, monkeypatch):
     want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
     assert np.all(np.isfinite(want[:9])) and np.all(np.isfinite(want[40:43]))
     assert not np.all(np.isfinite(want[9:40]))
+    assert_close_nonfinite(got, want)
+
+
+@pytest.mark.parametrize("append", ["bulk", "fused"])
+@pytest.mark.parametrize("bad", [np.inf, -np.inf])
+def test_infinite_k_marks_the_pool_and_matches_the_oracle(bad, append):
+    """K (V finite) holds +-Inf at dims 5 and 77 of some positions the chunks read. q is
+    1.0 on dim 77, exact in f16, so q's lo part there is 0: the f16 hi + lo split gives
+    inf * 0 = NaN in the lo chain where the reference's dot gives +-Inf. Only a pool
+    marked as holding a non-finite K runs the instance that repairs it, and the store
+    must mark the pool: by the bulk append (positions inside and before the chunks) and
+    by the fused decode step (the last position of sequence 1)."""
+    import torch
+    hkv, g, d = 2, 4, 128
+    ctxs, qls = [60, 160], [40, 40]
+    marks = [(0, 30), (1, 100 + 15), (1, 20)] if append == "bulk" else []
+    base = [0, ctxs[0]]
+
+    def kv(rng, n):
+        k = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        v = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        for s, pos in marks:
+            k[base[s] + pos, 1, [5, 77]] = bad
+        return k, v
+    pool_ctxs = ctxs if append == "bulk" else [60, 159]
+    pool, layout, tab = _pool(d, hkv, pool_ctxs, seed=33, kv=kv)
+    if append == "fused":  # sequence 1's position 159 through the fused step
+        kn = np.random.default_rng(3).standard_normal((1, hkv, d)).astype(np.float32)
+        kn[0, 1, [5, 77]] = bad
+        vn = np.ones((1, hkv, d), np.float32)
+        qd = np.ones((1, hkv * g, d), np.float32)
+        out = torch.zeros(qd.shape, dtype=torch.float32, device="cuda")
+        pool.append_decode_attention(0, to_dev(kn), to_dev(vn), to_dev(qd), out,
+                                     to_dev(tab[1:2]), to_dev(np.array([160], np.int32)), 160)
+        torch.cuda.synchronize()
+    offs = np.array([0, 40], np.int64)
+    q = np.random.default_rng(9).standard_normal((80, hkv * g, d), dtype=np.float32)
+    q[:, :, 77] = 1.0
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    assert pool.take_fault_flags() == 0
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    assert not np.all(np.isfinite(want))
     assert_close_nonfinite(got, want)
 
 
