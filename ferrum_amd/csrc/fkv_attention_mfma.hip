@@ -1418,18 +1418,26 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
 // layer. Padding columns (ln.real false) are not masked: their q is zero, their
 // accumulator rows are their own (an MFMA output row depends on its A row only)
 // and never written.
-template <int D, bool REPAIR = true>
-__device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
-                                            const f16x8 (&ql)[D / 32],
-                                            const Lane& ln, bool live, bool full, int32_t t0,
-                                            int32_t end, float (&s)[4]) {
-  f32x4 ah = {0.0f, 0.0f, 0.0f, 0.0f}, al = {0.0f, 0.0f, 0.0f, 0.0f};
+template <int D>
+__device__ __forceinline__ void qk_mfma_pf(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
+                                           const f16x8 (&ql)[D / 32], f32x4& ah, f32x4& al) {
+  ah = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+  al = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int c = 0; c < D / 32; c++) {
     const f16x8 kv = __builtin_bit_cast(f16x8, kr[c]);
     ah = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qh[c], ah, 0, 0, 0);
     al = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], al, 0, 0, 0);
   }
+}
+
+template <int D, bool REPAIR = true>
+__device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
+                                            const f16x8 (&ql)[D / 32],
+                                            const Lane& ln, bool live, bool full, int32_t t0,
+                                            int32_t end, float (&s)[4]) {
+  f32x4 ah, al;
+  qk_mfma_pf<D>(kr, qh, ql, ah, al);
   float x[4];
 #pragma unroll
   for (int r = 0; r < 4; r++) x[r] = ah[r] + al[r];
@@ -1783,6 +1791,43 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     // the table entry of the block staged in the middle of the step, read up front
     const int32_t p_mid = more2 ? table[j0 + kStep + 1] : 0;
     float sc[kStep][4];
+    if constexpr (DT == kDtypeF16 && MODE == kPfFast) {
+      // Both blocks' QK chains issued back to back (the second block's LDS reads and
+      // MFMAs overlap the first's latency), then the staging of the next step, then
+      // the scores: one wave-uniform test for the causal mask of the step.
+      f32x4 ah[kStep], al[kStep];
+#pragma unroll
+      for (int bb = 0; bb < kStep; bb++) {
+        const uint8_t* ks = s_kv[buf][bb];
+        uint4 kr[NC];
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+          kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
+        qk_mfma_pf<D>(kr, qh, qlo, ah[bb], al[bb]);
+      }
+      if (more) {  // the next step's first block to the other buffer
+        store_block(buf ^ 1, 0);
+        if (more2) nlv[1] = load_block_at(p_mid);
+      }
+      // a block past a column's causal end (or past the wave's tile, or not in the
+      // pool) is masked; the step's blocks both lie before every end in the common case
+      const bool full2 = lv[0] & lv[1] & ((j0 + kStep) * B <= end_min);
+#pragma unroll
+      for (int bb = 0; bb < kStep; bb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sc[bb][r] = ah[bb][r] + al[bb][r];
+      if (!full2) {
+#pragma unroll
+        for (int bb = 0; bb < kStep; bb++) {
+          const int32_t t0 = (j0 + bb) * B;
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const bool ok = ln.real && lv[bb] && t0 + ln.grp * 4 + r < end_col;
+            sc[bb][r] = ok ? sc[bb][r] : -__builtin_inff();
+          }
+        }
+      }
+    } else {
 #pragma unroll
     for (int bb = 0; bb < kStep; bb++) {
       const int32_t j = j0 + bb;
@@ -1823,6 +1868,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         if (more2) nlv[1] = load_block_at(p_mid);
       }
     }
+    }  // DT != kDtypeF16 || MODE != kPfFast
     f16x4 pw[kStep];
     float ef[kStep][4];
     softmax_step_pf<D, kStep>(sc, hscale, ln, st, pw, ef);
