@@ -1431,6 +1431,21 @@ __device__ __forceinline__ void qk_mfma_pf(const uint4 (&kr)[D / 32], const f16x
   }
 }
 
+// The same dot in one chain (hi then lo part of each 32-dim run into one accumulator):
+// for pools without an infinite K, where no score needs the hi chain alone.
+template <int D>
+__device__ __forceinline__ f32x4 qk_mfma_pf1(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
+                                             const f16x8 (&ql)[D / 32]) {
+  f32x4 a = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int c = 0; c < D / 32; c++) {
+    const f16x8 kv = __builtin_bit_cast(f16x8, kr[c]);
+    a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qh[c], a, 0, 0, 0);
+    a = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], a, 0, 0, 0);
+  }
+  return a;
+}
+
 template <int D, bool REPAIR = true>
 __device__ __forceinline__ void qk_block_pf(const uint4 (&kr)[D / 32], const f16x8 (&qh)[D / 32],
                                             const f16x8 (&ql)[D / 32],
@@ -1520,6 +1535,15 @@ __device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], float h
   }
 }
 
+// Byte offset, in a staged F16 V tile of the prefill kernel, of the 8 bytes (tokens
+// grp*4 .. grp*4 + 3) of dim `dim`: rows of 32 bytes, the row's four 8-byte slots
+// permuted by bits 2-3 of the dim. The LDS serves a 64-bit read 16 lanes a clock over
+// 32 banks; the lanes of one token group read dims col = 0..15, 4 rows to 128 bytes,
+// and the permutation puts cols c, c+4, c+8 and c+12 on different slots.
+__device__ __forceinline__ uint32_t pf_v_off(uint32_t dim, uint32_t grp) {
+  return dim * 32u + ((grp ^ ((dim >> 2) & 3u)) * 8u);
+}
+
 // Whether an F16 V operand (tokens t0 + grp*4 + r of dims 16m + col) holds an Inf or
 // NaN at a token in [lo, hi).
 template <int D>
@@ -1584,6 +1608,10 @@ constexpr int prefill_tile_bytes() {
 }
 
 enum : int { kPfFast = 0, kPfExact = 1, kPfLeakSafe = 2 };
+template <int N>
+struct PfBuf {  // a staging buffer index as a type
+  static constexpr int value = N;
+};
 
 // One sequence of a prefill launch: the context clamped to the block table, the
 // number of queries computed (q_lens[s] clamped to the context and to max_q_len) and
@@ -1634,7 +1662,12 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   constexpr int kBlk = 2 * kTile;               // K tile | V tile
   constexpr int kChunks = kBlk / 16;
   constexpr int kLoads = (kChunks + 255) / 256;  // 16-byte loads per thread per block
-  __shared__ __align__(16) uint8_t s_kv[2][kStep][kBlk];
+  // Two staging buffers (steps alternate), as two arrays: the loop runs two steps an
+  // iteration, each with its buffer known at compile time, so the compiler sees that a
+  // step's LDS reads do not touch the loads landing in the other buffer and does not
+  // wait for them.
+  __shared__ __align__(16) uint8_t s_kv0[kStep][kBlk];
+  __shared__ __align__(16) uint8_t s_kv1[kStep][kBlk];
   constexpr bool EXACT = MODE == kPfExact;
 
   if constexpr (DT == kDtypeQ8) {
@@ -1703,9 +1736,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // Thread t stages 16-byte chunks t, t + 256, ... of a block's K | V pair; a table
   // entry outside the pool raises the fault flag, stages block 0 and is skipped. The
   // chunk's source (relative to the K tile: the V tile of the same head is n_kv_heads
-  // tiles on) and its LDS destination (V rows with their two 16-byte units swapped on
-  // rows with bit 3 of the dim set, so the P.V operand reads hit 16 distinct bank
-  // pairs) are the thread's own, worked out once.
+  // tiles on) and its LDS destination are the thread's own, worked out once. A V chunk
+  // (8 tokens of one dim: slots 2u and 2u + 1 of the row in pf_v_off's terms) lands as
+  // two 8-byte stores: slot 2u at dst_pre, slot 2u + 1 at dst_pre ^ 8.
   const uint8_t* kbase = tile_ptr(g, 0, layer, 0, kvh);
   // (n_kv_heads tiles of one layer's K fit in 32 bits: a block of every layer does not)
   const uint32_t v_skip = (uint32_t)(g.n_kv_heads * g.tile_bytes) - (uint32_t)kTile;
@@ -1718,6 +1751,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // short of spilling) works its offsets out at each use.
   constexpr int kPre = DT == kDtypeF16 ? kLoads : 1;
   uint32_t src_pre[kPre], dst_pre[kPre];
+  // F16 chunks that are all K or all V for every thread (the case of head_dim 128) need
+  // no test at the store.
+  constexpr bool kSplitV = DT == kDtypeF16 && kTile % 4096 == 0;
   if constexpr (DT == kDtypeF16) {
 #pragma unroll
     for (int i = 0; i < kLoads; i++) {
@@ -1726,7 +1762,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       src_pre[i] = off + (is_v ? v_skip : 0u);
       if (is_v) {
         const uint32_t v = off - kTile, dim = v / 32u, unit = (v % 32u) / 16u;
-        dst_pre[i] = kTile + dim * 32u + ((unit ^ ((dim >> 3) & 1u)) * 16u);
+        dst_pre[i] = kTile + pf_v_off(dim, 2u * unit);
       } else {
         dst_pre[i] = off;
       }
@@ -1759,23 +1795,81 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     return ok;
   };
   auto load_block = [&](int32_t j) { return load_block_at(table[j]); };
-  auto store_block = [&](int buf, int slot) {
-    uint8_t* dst = s_kv[buf][slot];
+  auto store_block = [&](uint8_t* dst) {
 #pragma unroll
-    for (int i = 0; i < kLoads; i++)
-      if (has_chunk(i)) *(uint4*)&dst[dst_off(i)] = stg[i];
+    for (int i = 0; i < kLoads; i++) {
+      if (!has_chunk(i)) continue;
+      const uint4 w = stg[i];
+      if constexpr (DT == kDtypeF16) {
+        // chunk i is V for every thread when its 256 chunks start at or past the K tile
+        const bool v_all = kSplitV && i * 256 * 16 >= kTile;
+        const bool v_any = v_all || (!kSplitV && i * 256 * 16 + 4096 > kTile);
+        if (v_all || (v_any && dst_pre[i] >= (uint32_t)kTile)) {
+          *(uint2*)&dst[dst_pre[i]] = make_uint2(w.x, w.y);
+          *(uint2*)&dst[dst_pre[i] ^ 8u] = make_uint2(w.z, w.w);
+          continue;
+        }
+      }
+      *(uint4*)&dst[dst_off(i)] = w;
+    }
   };
+  // F16 stages with loads straight into LDS: no staging registers, and a block's data
+  // lands while the step computes. An instruction writes 64 lanes' data contiguously;
+  // the lanes' sources give the layout: K as stored (16 bytes a lane, instruction n
+  // of the block = bytes n*1024 ..), V in pf_v_off's slot order (4 bytes a lane,
+  // instruction n = dims 8n .. 8n + 7). Wave w issues instructions w, w + 4, ...; its
+  // lanes' V sources differ between them by a constant, as the slot permutation of
+  // dims 8(w + 4k) + l/8 does not depend on k.
+  constexpr bool kDma = DT == kDtypeF16;
+  constexpr int kKIns = kTile / 1024, kVIns = kTile / 256;
+  uint32_t dma_k = 0, dma_v = 0;
+  if constexpr (kDma) {
+    const uint32_t l = ln.lane, w = (uint32_t)wave;
+    dma_k = (w * 64u + l) * 16u;
+    const uint32_t sl = (l % 8u) / 2u, perm = (2u * w + (l >> 5)) & 3u;
+    dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + w * 256u + (l >> 3) * 32u +
+            (sl ^ perm) * 8u + (l % 2u) * 4u;
+  }
+  auto dma_block_at = [&](int32_t p, uint8_t* dst) {
+    p = __builtin_amdgcn_readfirstlane(p);
+    const bool ok = (p >= 0) & ((uint64_t)p < g.num_blocks);
+    if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
+    const uint8_t* kt = kbase + (ok ? (uint64_t)p : 0u) * g.block_bytes;
+#pragma unroll
+    for (int k = 0; k < (kKIns + 3) / 4; k++)
+      if (k * 4 + wave < kKIns)
+        __builtin_amdgcn_global_load_lds(
+            kt + dma_k + k * 4096u,
+            (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int k = 0; k < kVIns / 4; k++)
+      __builtin_amdgcn_global_load_lds(
+          kt + dma_v + k * 1024u,
+          (__attribute__((address_space(3))) void*)(dst + kTile + (k * 4 + wave) * 256), 4, 0, 0);
+    return ok;
+  };
+  // every load this wave issued has landed (vmcnt 0; expcnt and lgkmcnt left alone)
+  auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
   bool lv[kStep] = {false, false};   // blocks of the step being computed: in the pool
   bool nlv[kStep] = {false, false};  // and of the next step
+  int32_t pn[kStep] = {0, 0};        // (DMA) table entries of the next step's blocks
+  if constexpr (kDma) {
 #pragma unroll
-  for (int bb = 0; bb < kStep; bb++) {
-    if (jbeg + bb < jend) {
-      lv[bb] = load_block(jbeg + bb);
-      store_block(0, bb);
+    for (int bb = 0; bb < kStep; bb++) {
+      if (jbeg + bb < jend) lv[bb] = dma_block_at(table[jbeg + bb], s_kv0[bb]);
+      if (jbeg + kStep + bb < jend) pn[bb] = table[jbeg + kStep + bb];
     }
+  } else {
+#pragma unroll
+    for (int bb = 0; bb < kStep; bb++) {
+      if (jbeg + bb < jend) {
+        lv[bb] = load_block(jbeg + bb);
+        store_block(s_kv0[bb]);
+      }
+    }
+    if (jbeg + kStep < jend) nlv[0] = load_block(jbeg + kStep);
   }
-  if (jbeg + kStep < jend) nlv[0] = load_block(jbeg + kStep);
   // blocks this wave computes: the piece's, up to the wave's furthest causal end
   const int32_t jw_end = nblk_w < jend ? nblk_w : jend;
   f16x8 qh[NC], qlo[NC];
@@ -1783,30 +1877,45 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   prep_q<D>(q + row_of(ln.real ? ln.col : 0), ln, scale * kLog2e, qh, qlo, hscale);
   Accum<D> st;
   st.reset();
+  if constexpr (kDma) dma_wait();
   __syncthreads();
 
-  for (int32_t j0 = jbeg, buf = 0; j0 < jend; j0 += kStep, buf ^= 1) {
+  int32_t j0 = jbeg;
+  // One step: blocks j0, j0 + 1 from buffer BUF; the next step's go to the other.
+  auto step = [&](auto bufc) __attribute__((always_inline)) {
+    constexpr int BUF = decltype(bufc)::value;
+    uint8_t(*const cur)[kBlk] = BUF == 0 ? s_kv0 : s_kv1;
+    uint8_t(*const nxt)[kBlk] = BUF == 0 ? s_kv1 : s_kv0;
     const bool more = j0 + kStep < jend;      // the workgroup has a next step
     const bool more2 = j0 + kStep + 1 < jend;  // with a second block
     // the table entry of the block staged in the middle of the step, read up front
-    const int32_t p_mid = more2 ? table[j0 + kStep + 1] : 0;
+    const int32_t p_mid = (!kDma && more2) ? table[j0 + kStep + 1] : 0;
+    if constexpr (kDma) {
+      // the next step's blocks into the other buffer (its readers passed the barrier
+      // that ended the last step), and the table entries of the step after
+      if (more) nlv[0] = dma_block_at(pn[0], nxt[0]);
+      if (more2) nlv[1] = dma_block_at(pn[1], nxt[1]);
+#pragma unroll
+      for (int bb = 0; bb < kStep; bb++)
+        pn[bb] = j0 + 2 * kStep + bb < jend ? table[j0 + 2 * kStep + bb] : 0;
+    }
     float sc[kStep][4];
     if constexpr (DT == kDtypeF16 && MODE == kPfFast) {
       // Both blocks' QK chains issued back to back (the second block's LDS reads and
       // MFMAs overlap the first's latency), then the staging of the next step, then
       // the scores: one wave-uniform test for the causal mask of the step.
-      f32x4 ah[kStep], al[kStep];
+      f32x4 a[kStep];
 #pragma unroll
       for (int bb = 0; bb < kStep; bb++) {
-        const uint8_t* ks = s_kv[buf][bb];
+        const uint8_t* ks = cur[bb];
         uint4 kr[NC];
 #pragma unroll
         for (int c = 0; c < NC; c++)
           kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
-        qk_mfma_pf<D>(kr, qh, qlo, ah[bb], al[bb]);
+        a[bb] = qk_mfma_pf1<D>(kr, qh, qlo);
       }
-      if (more) {  // the next step's first block to the other buffer
-        store_block(buf ^ 1, 0);
+      if (!kDma && more) {  // the next step's first block to the other buffer
+        store_block(nxt[0]);
         if (more2) nlv[1] = load_block_at(p_mid);
       }
       // a block past a column's causal end (or past the wave's tile, or not in the
@@ -1815,7 +1924,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 #pragma unroll
       for (int bb = 0; bb < kStep; bb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) sc[bb][r] = ah[bb][r] + al[bb][r];
+        for (int r = 0; r < 4; r++) sc[bb][r] = a[bb][r];
       if (!full2) {
 #pragma unroll
         for (int bb = 0; bb < kStep; bb++) {
@@ -1832,7 +1941,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     for (int bb = 0; bb < kStep; bb++) {
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
-      const uint8_t* ks = s_kv[buf][bb];
+      const uint8_t* ks = cur[bb];
       // F16: every wave scores both blocks. One past the wave's tile (at most the last of
       // the workgroup's range, or a slot holding an earlier step's block) lies past every
       // column's causal end, so the causal mask gives it -inf throughout; skipping it
@@ -1863,8 +1972,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 #pragma unroll
         for (int r = 0; r < 4; r++) sc[bb][r] = -__builtin_inff();
       }
-      if (bb == 0 && more) {  // the next step's first block to the other buffer
-        store_block(buf ^ 1, 0);
+      if (!kDma && bb == 0 && more) {  // the next step's first block to the other buffer
+        store_block(nxt[0]);
         if (more2) nlv[1] = load_block_at(p_mid);
       }
     }
@@ -1877,13 +1986,13 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
       if (j < jw_end && lv[bb]) {
-        const uint8_t* vs = s_kv[buf][bb] + kTile;
+        const uint8_t* vs = cur[bb] + kTile;
         if constexpr (DT == kDtypeF16) {
           u32x2_t vr[NM];
 #pragma unroll
           for (int m = 0; m < NM; m++) {
             const uint32_t dim = (uint32_t)(m * 16 + ln.col);
-            vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((((uint32_t)ln.grp >> 1) ^ ((dim >> 3) & 1u)) * 16u) + ((uint32_t)ln.grp & 1u) * 8u));
+            vr[m] = *(const u32x2_t*)(vs + pf_v_off(dim, (uint32_t)ln.grp));
           }
           // Leak-safe instance: a block where a non-finite V lies past the tile's
           // nearest causal end takes one P.V per query token jt of the tile, V cut at
@@ -1902,7 +2011,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 #pragma unroll
               for (int m = 0; m < NM; m++) {
                 const uint32_t dim = (uint32_t)(m * 16 + ln.col);
-                vr[m] = *(const u32x2_t*)(vs + dim * 32u + (((((uint32_t)ln.grp >> 1) ^ ((dim >> 3) & 1u)) * 16u) + ((uint32_t)ln.grp & 1u) * 8u));
+                vr[m] = *(const u32x2_t*)(vs + pf_v_off(dim, (uint32_t)ln.grp));
               }
               mask_v_tail<D>(vr, ln, t0, p0 + tile * T + jt + 1);
 #pragma unroll
@@ -1929,12 +2038,23 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       }
     }
     if (more) {
-      if (more2) store_block(buf ^ 1, 1);
+      if constexpr (kDma) {
+        dma_wait();
+      } else {
+        if (more2) store_block(nxt[1]);
+      }
       __syncthreads();
       lv[0] = nlv[0];
       lv[1] = more2 ? nlv[1] : false;
-      if (j0 + 2 * kStep < jend) nlv[0] = load_block(j0 + 2 * kStep);
+      if (!kDma && j0 + 2 * kStep < jend) nlv[0] = load_block(j0 + 2 * kStep);
     }
+  };
+  while (j0 < jend) {
+    step(PfBuf<0>{});
+    j0 += kStep;
+    if (j0 >= jend) break;
+    step(PfBuf<1>{});
+    j0 += kStep;
   }
   if (!wave_on) return;
 
