@@ -1733,12 +1733,10 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   };
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
-  // Thread t stages 16-byte chunks t, t + 256, ... of a block's K | V pair; a table
-  // entry outside the pool raises the fault flag, stages block 0 and is skipped. The
-  // chunk's source (relative to the K tile: the V tile of the same head is n_kv_heads
-  // tiles on) and its LDS destination are the thread's own, worked out once. A V chunk
-  // (8 tokens of one dim: slots 2u and 2u + 1 of the row in pf_v_off's terms) lands as
-  // two 8-byte stores: slot 2u at dst_pre, slot 2u + 1 at dst_pre ^ 8.
+  // A table entry outside the pool raises the fault flag, stages block 0 and is
+  // skipped. Q8_0 (load_block / store_block): thread t moves 16-byte chunks t, t + 256,
+  // ... of a block's K | V pair through registers, stored as loaded (the V tile of the
+  // same head is n_kv_heads tiles past its K tile). F16: dma_block_at below.
   const uint8_t* kbase = tile_ptr(g, 0, layer, 0, kvh);
   // (n_kv_heads tiles of one layer's K fit in 32 bits: a block of every layer does not)
   const uint32_t v_skip = (uint32_t)(g.n_kv_heads * g.tile_bytes) - (uint32_t)kTile;
@@ -1746,39 +1744,6 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   auto chunk_off = [&](int i) {
     const uint32_t c = (uint32_t)(i * 256) + threadIdx.x;
     return (c < (uint32_t)kChunks ? c : 0u) * 16u;
-  };
-  // F16 keeps the swizzled destinations in registers; Q8_0 (no swizzle, one register
-  // short of spilling) works its offsets out at each use.
-  constexpr int kPre = DT == kDtypeF16 ? kLoads : 1;
-  uint32_t src_pre[kPre], dst_pre[kPre];
-  // F16 chunks that are all K or all V for every thread (the case of head_dim 128) need
-  // no test at the store.
-  constexpr bool kSplitV = DT == kDtypeF16 && kTile % 4096 == 0;
-  if constexpr (DT == kDtypeF16) {
-#pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-      const uint32_t off = chunk_off(i);
-      const bool is_v = off >= (uint32_t)kTile;
-      src_pre[i] = off + (is_v ? v_skip : 0u);
-      if (is_v) {
-        const uint32_t v = off - kTile, dim = v / 32u, unit = (v % 32u) / 16u;
-        dst_pre[i] = kTile + pf_v_off(dim, 2u * unit);
-      } else {
-        dst_pre[i] = off;
-      }
-    }
-  }
-  auto src_off = [&](int i) -> uint32_t {
-    if constexpr (DT == kDtypeF16) {
-      return src_pre[i];
-    } else {
-      const uint32_t off = chunk_off(i);
-      return off + (off >= (uint32_t)kTile ? v_skip : 0u);
-    }
-  };
-  auto dst_off = [&](int i) -> uint32_t {
-    if constexpr (DT == kDtypeF16) return dst_pre[i];
-    else return chunk_off(i);
   };
   // every thread holds chunk i unless the block's last 256-chunk row is partial
   auto has_chunk = [&](int i) {
@@ -1790,28 +1755,17 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
     const uint8_t* kt = kbase + (ok ? (uint64_t)p : 0u) * g.block_bytes;
 #pragma unroll
-    for (int i = 0; i < kLoads; i++)
-      if (has_chunk(i)) stg[i] = load_stream16(kt + src_off(i));
+    for (int i = 0; i < kLoads; i++) {
+      const uint32_t off = chunk_off(i);
+      if (has_chunk(i)) stg[i] = load_stream16(kt + off + (off >= (uint32_t)kTile ? v_skip : 0u));
+    }
     return ok;
   };
   auto load_block = [&](int32_t j) { return load_block_at(table[j]); };
   auto store_block = [&](uint8_t* dst) {
 #pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-      if (!has_chunk(i)) continue;
-      const uint4 w = stg[i];
-      if constexpr (DT == kDtypeF16) {
-        // chunk i is V for every thread when its 256 chunks start at or past the K tile
-        const bool v_all = kSplitV && i * 256 * 16 >= kTile;
-        const bool v_any = v_all || (!kSplitV && i * 256 * 16 + 4096 > kTile);
-        if (v_all || (v_any && dst_pre[i] >= (uint32_t)kTile)) {
-          *(uint2*)&dst[dst_pre[i]] = make_uint2(w.x, w.y);
-          *(uint2*)&dst[dst_pre[i] ^ 8u] = make_uint2(w.z, w.w);
-          continue;
-        }
-      }
-      *(uint4*)&dst[dst_off(i)] = w;
-    }
+    for (int i = 0; i < kLoads; i++)
+      if (has_chunk(i)) *(uint4*)&dst[chunk_off(i)] = stg[i];
   };
   // F16 stages with loads straight into LDS: no staging registers, and a block's data
   // lands while the step computes. An instruction writes 64 lanes' data contiguously;
@@ -1902,8 +1856,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     float sc[kStep][4];
     if constexpr (DT == kDtypeF16 && MODE == kPfFast) {
       // Both blocks' QK chains issued back to back (the second block's LDS reads and
-      // MFMAs overlap the first's latency), then the staging of the next step, then
-      // the scores: one wave-uniform test for the causal mask of the step.
+      // MFMAs overlap the first's latency), then the scores: one wave-uniform test for
+      // the causal mask of the step.
       f32x4 a[kStep];
 #pragma unroll
       for (int bb = 0; bb < kStep; bb++) {
@@ -1913,10 +1867,6 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         for (int c = 0; c < NC; c++)
           kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
         a[bb] = qk_mfma_pf1<D>(kr, qh, qlo);
-      }
-      if (!kDma && more) {  // the next step's first block to the other buffer
-        store_block(nxt[0]);
-        if (more2) nlv[1] = load_block_at(p_mid);
       }
       // a block past a column's causal end (or past the wave's tile, or not in the
       // pool) is masked; the step's blocks both lie before every end in the common case
