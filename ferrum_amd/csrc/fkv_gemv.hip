@@ -63,10 +63,11 @@ __device__ __forceinline__ uint32_t tail_dw(bool aligned, uint32_t block) {
 }
 constexpr int kXRegs = 2;  // activation passes (8 values a lane) loaded up front
 
-// LDS blocks a token: the step count rounded up to whole groups of kPipe steps, so
-// every step a group runs reads inside the array.
-__host__ __device__ constexpr uint32_t gemv_padded_blocks(uint32_t nb) {
-  return (nb + 16u * kPipe - 1u) / (16u * kPipe) * (16u * kPipe);
+// LDS blocks a token: the step count rounded up to whole groups of kPipe iterations
+// (an iteration is S steps of 16 blocks), so every step a group runs reads inside the
+// array.
+__host__ __device__ constexpr uint32_t gemv_padded_blocks(uint32_t nb, uint32_t S = 1) {
+  return (nb + 16u * S * kPipe - 1u) / (16u * S * kPipe) * (16u * S * kPipe);
 }
 
 struct RawBlock {
@@ -212,7 +213,12 @@ __device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, const XP
 
 // Four waves a SIMD (at most 128 VGPRs) keep every wave of a 14336-row matrix
 // resident at once, so its weight stream never pauses between rounds of waves.
-template <int T>
+// S = 2 (launches with few rows): a weight row takes two 16-lane DPP rows, h = 0 the
+// even 16-block steps and h = 1 the odd ones, so a wave holds 2 weight rows and the
+// launch twice the waves. Each iteration's two steps are added in order by both DPP
+// rows (the products of the other one brought over by a lane swap), so the sum is
+// the same as S = 1's, bit for bit.
+template <int T, int S>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch bat, uint32_t cols,
                                                                const float* x, uint32_t n_tokens) {
   // This workgroup's matrix (uniform: scalar selects over the launch's few matrices).
@@ -232,25 +238,27 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
 
   const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
   const uint32_t l = lane & 15u;
-  const uint32_t row = wg * kRowsPerWg + wave * kRowsPerWave + (lane >> 4);
+  const uint32_t h = (lane >> 4) % (uint32_t)S;  // which steps of its row this DPP row takes
+  constexpr uint32_t kRowsWg = kRowsPerWg / S;
+  const uint32_t row = wg * kRowsWg + wave * (kRowsPerWave / S) + (lane >> 4) / S;
   const bool row_ok = row < rows;
-  const uint32_t n_it = (nb + 15u) / 16u;      // 16-block steps a row
-  const uint32_t nbp = gemv_padded_blocks(nb);  // LDS blocks a token (whole groups)
+  const uint32_t n_it = (nb + 16u * S - 1u) / (16u * S);  // iterations (S steps) a row
+  const uint32_t nbp = gemv_padded_blocks(nb, S);         // LDS blocks a token (whole groups)
 
   // Weights through a buffer resource based at this workgroup's first row: a lane
   // whose block lies past its row's end asks for an offset beyond the resource, which
   // reads zeros without touching memory. So no load is clamped or branched around,
   // and every step's loads are a lane offset plus an immediate.
   const uint64_t row_bytes = (uint64_t)nb * kQ8Bytes;
-  const uint32_t row0 = wg * kRowsPerWg;
+  const uint32_t row0 = wg * kRowsWg;
   const uint64_t base = (uint64_t)(uintptr_t)w + row0 * row_bytes;
   const uint64_t left = (uint64_t)rows * row_bytes - row0 * row_bytes;
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       (void*)(uintptr_t)base, (short)0, (int)(left < kOobOffset ? left : kOobOffset - 1u),
       kBufferWord3);
   // A row past the end reads the last row (its results are not stored).
-  const uint32_t lane_off =
-      (uint32_t)((uint64_t)((row_ok ? row : rows - 1u) - row0) * row_bytes) + l * kQ8Bytes;
+  const uint32_t lane_off = (uint32_t)((uint64_t)((row_ok ? row : rows - 1u) - row0) * row_bytes) +
+                            (h * 16u + l) * kQ8Bytes;
   // Which activation copy this lane's blocks pair with (the parity of a lane's block
   // addresses is the same at every step), as LDS dword offsets of its 8 quant dwords
   // and of its (9th dword, scale) pair; and its byte offsets of the 8 dwords and of
@@ -271,10 +279,11 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
   // statement that may touch memory (x is not __restrict__, so that covers it).
   __asm__ volatile("" ::: "memory");
 
-  // Step it's loads: blocks it*16 + l; beyond the row (or the step count) none.
+  // Iteration it's loads: blocks (it*S + h)*16 + l; beyond the row (or the step count)
+  // none.
   auto load_step = [&](uint32_t it, RawBlock& rb) {
-    const bool in = it * 16u + l < nb;
-    const uint32_t o = it * (16u * kQ8Bytes);
+    const bool in = (it * S + h) * 16u + l < nb;
+    const uint32_t o = it * (16u * S * kQ8Bytes);
     const uint32_t od = in ? dw_off + o : kOobOffset;
     const uint32_t ot = in ? tail_off + o : kOobOffset;
     const v4u a = __builtin_amdgcn_raw_buffer_load_b128(rsrc, od, 0, 0);
@@ -302,13 +311,13 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
   // Step it into acc: lane L's block is the L-th added. Blocks past the row's end
   // (loaded as zeros, paired with LDS padding) add +0: acc starts at +0 and a zero
   // sum is +0 under round-to-nearest, so acc is never -0 and acc + 0 == acc.
-  const uint32_t* lane_x = lds + (uint64_t)l * kXDw;
+  const uint32_t* lane_x = lds + (uint64_t)(h * 16u + l) * kXDw;
   auto consume = [&](uint32_t it, const RawBlock& rb) {
-    const bool ok = it * 16u + l < nb;
+    const bool ok = (it * S + h) * 16u + l < nb;
     const float ws = dev::f16_bits_to_f32(aligned ? rb.tail : rb.d[0]);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const uint32_t* xb = lane_x + ((uint64_t)t * nbp + it * 16u) * kXDw;
+      const uint32_t* xb = lane_x + ((uint64_t)t * nbp + it * 16u * S) * kXDw;
       const uint4 x0 = *(const uint4*)(xb + q_dw);
       const uint4 x1 = *(const uint4*)(xb + q_dw + 4u);
       const uint2 xt = *(const uint2*)(xb + t_dw);
@@ -324,7 +333,16 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
       s = __builtin_amdgcn_sdot4((int)rb.tail, (int)xt.x, s, false);
       float p = (float)s * (ws * __uint_as_float(xt.y));
       p = ok ? p : 0.0f;
-      acc[t] = chain16(acc[t], p, std::make_integer_sequence<int, 16>{});
+      if constexpr (S == 1) {
+        acc[t] = chain16(acc[t], p, std::make_integer_sequence<int, 16>{});
+      } else {
+        // this lane's product and the other DPP row's for the same lane index: step
+        // it*2 (h = 0's) first, then step it*2 + 1 (h = 1's)
+        const float o = __shfl_xor(p, 16);
+        const float first = h == 0u ? p : o, second = h == 0u ? o : p;
+        acc[t] = chain16(acc[t], first, std::make_integer_sequence<int, 16>{});
+        acc[t] = chain16(acc[t], second, std::make_integer_sequence<int, 16>{});
+      }
     }
   };
 
@@ -338,25 +356,25 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
     }
   }
 
-  if (row_ok && l == 0u) {
+  if (row_ok && l == 0u && h == 0u) {
 #pragma unroll
     for (int t = 0; t < T; ++t)
       if ((uint32_t)t < nt) y[(uint64_t)(t0 + t) * rows + row] = acc[t];
   }
 }
 
-template <int T>
+template <int T, int S>
 hipError_t launch_t(const GemvBatch& b, uint32_t n_wg, uint32_t cols, const float* x,
                     uint32_t n_tokens, hipStream_t s) {
   const dim3 grid(n_wg, (n_tokens + T - 1u) / T);
-  const size_t lds = gemv_lds_bytes(T, cols);
+  const size_t lds = (size_t)T * gemv_padded_blocks(cols / 32u, S) * kXDw * 4u;
   if (lds > 65536u) {
-    const hipError_t e = hipFuncSetAttribute((const void*)gemv_q8_kernel<T>,
+    const hipError_t e = hipFuncSetAttribute((const void*)gemv_q8_kernel<T, S>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(gemv_q8_kernel<T>, grid, dim3(kGemvThreads), lds, s, b, cols, x,
+  hipLaunchKernelGGL((gemv_q8_kernel<T, S>), grid, dim3(kGemvThreads), lds, s, b, cols, x,
                      n_tokens);
   return hipGetLastError();
 }
@@ -626,6 +644,10 @@ size_t gemv_lds_bytes(uint32_t tokens, uint32_t cols) {
   return (size_t)tokens * gemv_padded_blocks(cols / 32u) * kXDw * 4u;
 }
 
+// Launches of one token whose S = 1 grid would leave SIMDs with fewer than two waves
+// (under 512 workgroups of 4 waves on 256 CUs) take S = 2, when its LDS fits as well.
+constexpr uint32_t kGemvSplitBelowWgs = 512;
+
 uint32_t gemv_tokens_per_launch(uint32_t n_tokens, uint32_t cols) {
   uint32_t t = n_tokens >= 3u ? 4u : (n_tokens == 2u ? 2u : 1u);
   while (t > 1u && gemv_lds_bytes(t, cols) > 65536u) t /= 2u;
@@ -635,15 +657,24 @@ uint32_t gemv_tokens_per_launch(uint32_t n_tokens, uint32_t cols) {
 hipError_t launch_gemv_q8(GemvBatch b, uint32_t cols, const float* x, uint32_t n_tokens,
                           hipStream_t s) {
   uint32_t n_wg = 0;
+  for (uint32_t m = 0; m < b.n; ++m) n_wg += (b.m[m].rows + kRowsPerWg - 1u) / kRowsPerWg;
+  const uint32_t tpl = gemv_tokens_per_launch(n_tokens, cols);
+  const uint32_t S = (tpl == 1u && n_wg < kGemvSplitBelowWgs &&
+                      (size_t)gemv_padded_blocks(cols / 32u, 2) * kXDw * 4u <= 65536u)
+                         ? 2u
+                         : 1u;
+  n_wg = 0;
   for (uint32_t m = 0; m < b.n; ++m) {
     b.m[m].wg0 = n_wg;
-    n_wg += (b.m[m].rows + kRowsPerWg - 1u) / kRowsPerWg;
+    n_wg += (b.m[m].rows + kRowsPerWg / S - 1u) / (kRowsPerWg / S);
   }
   for (uint32_t m = b.n; m < (uint32_t)kGemvMaxMats; ++m) b.m[m] = b.m[0];
-  switch (gemv_tokens_per_launch(n_tokens, cols)) {
-    case 4: return launch_t<4>(b, n_wg, cols, x, n_tokens, s);
-    case 2: return launch_t<2>(b, n_wg, cols, x, n_tokens, s);
-    default: return launch_t<1>(b, n_wg, cols, x, n_tokens, s);
+  switch (tpl) {
+    case 4: return launch_t<4, 1>(b, n_wg, cols, x, n_tokens, s);
+    case 2: return launch_t<2, 1>(b, n_wg, cols, x, n_tokens, s);
+    default:
+      return S == 2u ? launch_t<1, 2>(b, n_wg, cols, x, n_tokens, s)
+                     : launch_t<1, 1>(b, n_wg, cols, x, n_tokens, s);
   }
 }
 
