@@ -1544,17 +1544,6 @@ __device__ __forceinline__ uint32_t pf_v_off(uint32_t dim, uint32_t grp) {
   return dim * 32u + ((grp ^ ((dim >> 2) & 3u)) * 8u);
 }
 
-// Byte offset of lane (col, grp)'s 16-byte P.V operand unit for the dims 16m + col of a
-// prefill step whose two blocks' V tiles are interleaved (fast F16 instance): the unit
-// holds tokens grp*4 .. +3 of the step's first block, then the same of its second.
-// Dims D/2 a staging slot (its V area), 64 bytes a dim, the four units of a dim permuted
-// by bits 1-2 of the dim: a 128-bit LDS read is served 8 lanes a clock over 32 banks,
-// and cols c .. c + 7 of one token group then take 8 distinct 16-byte bank groups. The
-// offset is from the first slot's V area; the second slot's is kBlk further.
-__device__ __forceinline__ uint32_t pf_vc_lane_off(uint32_t col, uint32_t grp) {
-  return col * 64u + ((grp ^ ((col >> 1) & 3u)) * 16u);
-}
-
 // Whether an F16 V operand (tokens t0 + grp*4 + r of dims 16m + col) holds an Inf or
 // NaN at a token in [lo, hi).
 template <int D>
@@ -1619,6 +1608,17 @@ constexpr int prefill_tile_bytes() {
 }
 
 enum : int { kPfFast = 0, kPfExact = 1, kPfLeakSafe = 2 };
+// K direct loads of 4 bytes a lane into LDS at vdst + k*1024 from source offset voff +
+// k*1024, k < K: the instruction's immediate offset (a constant, hence the recursion)
+// is added to both addresses.
+template <int K>
+__device__ __forceinline__ void pf_v_dma(__amdgpu_buffer_rsrc_t rs, uint8_t* vdst, uint32_t voff) {
+  if constexpr (K > 0) {
+    pf_v_dma<K - 1>(rs, vdst, voff);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)vdst, 4,
+                                             voff, 0, (K - 1) * 1024, 0);
+  }
+}
 template <int N>
 struct PfBuf {  // a staging buffer index as a type
   static constexpr int value = N;
@@ -1795,86 +1795,43 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + w * 256u + (l >> 3) * 32u +
             (sl ^ perm) * 8u + (l % 2u) * 4u;
   }
+  // A block's loads go through a buffer resource based at its K tile: the lane's offset
+  // is a register worked out once, the instruction's a scalar, so issuing them costs no
+  // vector instruction.
   auto dma_block_at = [&](int32_t p, uint8_t* dst) {
     p = __builtin_amdgcn_readfirstlane(p);
     const bool ok = (p >= 0) & ((uint64_t)p < g.num_blocks);
+    // The tile address is wave-uniform; passed through readfirstlane (and worked out
+    // before the fault branch below) the compiler keeps the resource in scalar
+    // registers instead of looping over lanes.
+    const uint64_t ka = (uint64_t)(uintptr_t)kbase + (ok ? (uint64_t)p : 0u) * g.block_bytes;
+    const uint64_t kau = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(ka >> 32)) << 32) |
+                         (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ka);
+    const uint8_t* kt = (const uint8_t*)(uintptr_t)kau;
     if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
-    const uint8_t* kt = kbase + (ok ? (uint64_t)p : 0u) * g.block_bytes;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)kt, (short)0, 0x7fffffff, 0x00020000);
 #pragma unroll
     for (int k = 0; k < (kKIns + 3) / 4; k++)
       if (k * 4 + wave < kKIns)
-        __builtin_amdgcn_global_load_lds(
-            kt + dma_k + k * 4096u,
-            (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16, 0, 0);
-#pragma unroll
-    for (int k = 0; k < kVIns / 4; k++)
-      __builtin_amdgcn_global_load_lds(
-          kt + dma_v + k * 1024u,
-          (__attribute__((address_space(3))) void*)(dst + kTile + (k * 4 + wave) * 256), 4, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rs, (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16, dma_k,
+            k * 4096, 0, 0);
+    // V instruction k: LDS bytes (4k + wave)*256 of the V area and source bytes
+    // dma_v + k*1024, both 1024 apart per k, so one immediate offset (added to the LDS
+    // address as well as to the source) steps both and every k shares the M0 base.
+    pf_v_dma<kVIns / 4>(rs, dst + kTile + wave * 256, dma_v);
     return ok;
   };
-  // Fast F16 instance: a step's two V tiles interleaved (pf_vc_lane_off's layout), so
-  // that one 16-byte read gives a lane its operand of both blocks. Instruction n of the
-  // step writes LDS bytes 256n .. of the interleaved area (dims 4n .. 4n + 3, split
-  // between the two slots' V areas); lane l brings dword l % 4 of the 16-byte unit
-  // (l % 16) / 4 of dim 4n + l / 16: bytes 0-7 of a unit from the first block, 8-15 from
-  // the second. For wave w, n = w + 4k, and the unit permutation (bits 1-2 of the dim)
-  // does not depend on k.
+  // Fast F16 instance: P.V of a step's two blocks in one MFMA (below).
   constexpr bool kPair = kDma && MODE == kPfFast;
-  uint32_t dma_vc = 0;
-  if constexpr (kPair) {
-    const uint32_t l = ln.lane, w = (uint32_t)wave;
-    const uint32_t tg = ((l & 15u) >> 2) ^ ((2u * w + (l >> 5)) & 3u);  // token group
-    dma_vc = (uint32_t)(g.n_kv_heads * g.tile_bytes) + 128u * w + (l >> 4) * 32u + tg * 8u +
-             (l & 1u) * 4u;
-  }
-  // Both blocks of a step (the second only when has1; its lanes then read the first's
-  // V, finite, which the masked P.V path zeroes).
-  auto dma_pair_at = [&](int32_t p0, int32_t p1, bool has1, uint8_t(*dst)[kBlk], bool& ok0,
-                         bool& ok1) {
-    p0 = __builtin_amdgcn_readfirstlane(p0);
-    p1 = __builtin_amdgcn_readfirstlane(has1 ? p1 : p0);
-    ok0 = (p0 >= 0) & ((uint64_t)p0 < g.num_blocks);
-    const bool in1 = (p1 >= 0) & ((uint64_t)p1 < g.num_blocks);
-    ok1 = has1 & in1;
-    if ((!ok0 || (has1 && !in1)) && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
-    const uint8_t* kt0 = kbase + (ok0 ? (uint64_t)p0 : 0u) * g.block_bytes;
-    const uint8_t* kt1 = kbase + (in1 ? (uint64_t)p1 : 0u) * g.block_bytes;
-#pragma unroll
-    for (int k = 0; k < (kKIns + 3) / 4; k++)
-      if (k * 4 + wave < kKIns) {
-        __builtin_amdgcn_global_load_lds(
-            kt0 + dma_k + k * 4096u,
-            (__attribute__((address_space(3))) void*)(dst[0] + (k * 4 + wave) * 1024), 16, 0, 0);
-        if (has1)
-          __builtin_amdgcn_global_load_lds(
-              kt1 + dma_k + k * 4096u,
-              (__attribute__((address_space(3))) void*)(dst[1] + (k * 4 + wave) * 1024), 16, 0, 0);
-      }
-    const uint8_t* vb = (ln.lane & 2u) ? kt1 : kt0;
-#pragma unroll
-    for (int k = 0; k < kVIns / 2; k++) {
-      const int n = k * 4 + wave;  // slot n / kVIns, instruction n % kVIns of its V area
-      __builtin_amdgcn_global_load_lds(
-          vb + dma_vc + k * 512u,
-          (__attribute__((address_space(3))) void*)(dst[(k * 4) / kVIns] + kTile +
-                                                    (n % kVIns) * 256),
-          4, 0, 0);
-    }
-  };
   // every load this wave issued has landed (vmcnt 0; expcnt and lgkmcnt left alone)
   auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
   bool lv[kStep] = {false, false};   // blocks of the step being computed: in the pool
   bool nlv[kStep] = {false, false};  // and of the next step
   int32_t pn[kStep] = {0, 0};        // (DMA) table entries of the next step's blocks
-  if constexpr (kPair) {
-    dma_pair_at(table[jbeg], jbeg + 1 < jend ? table[jbeg + 1] : 0, jbeg + 1 < jend, s_kv0,
-                lv[0], lv[1]);
-#pragma unroll
-    for (int bb = 0; bb < kStep; bb++)
-      if (jbeg + kStep + bb < jend) pn[bb] = table[jbeg + kStep + bb];
-  } else if constexpr (kDma) {
+  if constexpr (kDma) {
 #pragma unroll
     for (int bb = 0; bb < kStep; bb++) {
       if (jbeg + bb < jend) lv[bb] = dma_block_at(table[jbeg + bb], s_kv0[bb]);
@@ -1913,12 +1870,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     if constexpr (kDma) {
       // the next step's blocks into the other buffer (its readers passed the barrier
       // that ended the last step), and the table entries of the step after
-      if constexpr (kPair) {
-        if (more) dma_pair_at(pn[0], pn[1], more2, nxt, nlv[0], nlv[1]);
-      } else {
-        if (more) nlv[0] = dma_block_at(pn[0], nxt[0]);
-        if (more2) nlv[1] = dma_block_at(pn[1], nxt[1]);
-      }
+      if (more) nlv[0] = dma_block_at(pn[0], nxt[0]);
+      if (more2) nlv[1] = dma_block_at(pn[1], nxt[1]);
 #pragma unroll
       for (int bb = 0; bb < kStep; bb++)
         pn[bb] = j0 + 2 * kStep + bb < jend ? table[j0 + 2 * kStep + bb] : 0;
@@ -2004,13 +1957,15 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     if constexpr (kPair) {
       // P.V of both blocks: one 16x16x32 MFMA per 16 dims, k-slots grp*8 .. +3 the first
       // block's tokens grp*4 .. +3 and grp*8 + 4 .. +7 the second's, in P (the lane's own
-      // weights) and in V (the interleaved unit) alike. The pool holds no Inf/NaN here, so
-      // V needs zeroing only where P's zeros could meet unwritten bytes: tokens at or past
-      // the wave's furthest causal end, and a block not in the pool or not staged.
+      // weights) and in V (8 bytes from each block's tile, one ds_read2st64_b64: the two
+      // slots' V areas are kBlk apart) alike. The pool holds no Inf/NaN here, so V needs
+      // zeroing only where P's zeros could meet unwritten bytes: tokens at or past the
+      // wave's furthest causal end, and a block not in the pool or not staged (a slot
+      // not staged this step holds an earlier block's bytes, or nothing written yet).
       if (j0 < jw_end) {  // wave-uniform
         const f16x8 pa = {pw[0][0], pw[0][1], pw[0][2], pw[0][3],
                           pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
-        const uint8_t* vc = cur[0] + kTile + pf_vc_lane_off((uint32_t)ln.col, (uint32_t)ln.grp);
+        const uint8_t* vc = cur[0] + kTile;
         // Masks (wave-uniform branch) change only the V operands: MFMAs in common code
         // keep the accumulators in place (MFMAs on both sides of a branch made the
         // compiler move them between registers, and spill). Operands half at a time.
@@ -2019,8 +1974,11 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         for (int h = 0; h < 2; h++) {
           uint4 v[NM / 2];
 #pragma unroll
-          for (int i = 0; i < NM / 2; i++)
-            v[i] = *(const uint4*)(vc + h * kBlk + i * 1024);
+          for (int i = 0; i < NM / 2; i++) {
+            const uint32_t vo = pf_v_off((uint32_t)((h * (NM / 2) + i) * 16 + ln.col), (uint32_t)ln.grp);
+            const u32x2_t a = *(const u32x2_t*)(vc + vo), b = *(const u32x2_t*)(vc + kBlk + vo);
+            v[i] = uint4{a.x, a.y, b.x, b.y};
+          }
           if (vmask) {
             const int32_t t0 = j0 * B + ln.grp * 4;
             const int32_t n0 = lv[0] ? end_max - t0 : 0, n1 = lv[1] ? end_max - t0 - B : 0;
