@@ -1535,15 +1535,6 @@ __device__ __forceinline__ void softmax_step_pf(const float (&s)[NB][4], float h
   }
 }
 
-// Byte offset, in a staged F16 V tile of the prefill kernel, of the 8 bytes (tokens
-// grp*4 .. grp*4 + 3) of dim `dim`: rows of 32 bytes, the row's four 8-byte slots
-// permuted by bits 2-3 of the dim. The LDS serves a 64-bit read 16 lanes a clock over
-// 32 banks; the lanes of one token group read dims col = 0..15, 4 rows to 128 bytes,
-// and the permutation puts cols c, c+4, c+8 and c+12 on different slots.
-__device__ __forceinline__ uint32_t pf_v_off(uint32_t dim, uint32_t grp) {
-  return dim * 32u + ((grp ^ ((dim >> 2) & 3u)) * 8u);
-}
-
 // Whether an F16 V operand (tokens t0 + grp*4 + r of dims 16m + col) holds an Inf or
 // NaN at a token in [lo, hi).
 template <int D>
@@ -1608,15 +1599,36 @@ constexpr int prefill_tile_bytes() {
 }
 
 enum : int { kPfFast = 0, kPfExact = 1, kPfLeakSafe = 2 };
-// K direct loads of 4 bytes a lane into LDS at vdst + k*1024 from source offset voff +
-// k*1024, k < K: the instruction's immediate offset (a constant, hence the recursion)
-// is added to both addresses.
-template <int K>
-__device__ __forceinline__ void pf_v_dma(__amdgpu_buffer_rsrc_t rs, uint8_t* vdst, uint32_t voff) {
+// F16 V tiles of a prefill step in LDS: the step's two blocks interleaved by 16-dim
+// chunks of 512 bytes, chunk m of block b at byte ((m % NMH) * 2 + b) * 512 of the V area
+// of staging slot m / NMH (NMH = D/32 chunks a slot). So the 8 bytes a lane takes from
+// each block for the paired P.V operand are 512 bytes apart, the pair a
+// ds_read2st64_b64 gives. In a chunk, dim 16m + col has 32 bytes (16 tokens) whose four
+// 8-byte slots (token groups) are permuted by bits 2-3 of col: the LDS serves a 64-bit
+// read 16 lanes a clock over 32 banks, the lanes of one token group read cols 0..15,
+// 4 to 128 bytes, and the permutation puts cols c, c+4, c+8 and c+12 on different
+// slots. Byte offset of (chunk m, block b, col, token group grp) from the first slot's
+// V area:
+template <int NMH, int KBLK>
+__device__ __forceinline__ uint32_t pf_vi_off(uint32_t m, uint32_t b, uint32_t col, uint32_t grp) {
+  return (m / NMH) * KBLK + ((m % NMH) * 2u + b) * 512u + col * 32u +
+         ((grp ^ ((col >> 2) & 3u)) * 8u);
+}
+// Block b's V direct loads of wave w, k < K: 4 bytes a lane, instruction k = dims
+// 8(4k + w) .. +7, i.e. half w % 2 of chunk 2k + w/2, from source offset voff + k*1024.
+// The instruction's immediate offset (a constant, hence the recursion) is added to the
+// LDS address as well, so the LDS base handed over is the destination less k*1024.
+template <int K, int NMH, int KBLK>
+__device__ __forceinline__ void pf_v_dma(__amdgpu_buffer_rsrc_t rs, uint8_t* varea0, uint32_t b,
+                                         uint32_t w, uint32_t voff) {
   if constexpr (K > 0) {
-    pf_v_dma<K - 1>(rs, vdst, voff);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)vdst, 4,
-                                             voff, 0, (K - 1) * 1024, 0);
+    pf_v_dma<K - 1, NMH, KBLK>(rs, varea0, b, w, voff);
+    constexpr uint32_t k = K - 1;
+    const uint32_t m = 2u * k + w / 2u;
+    uint8_t* lds = varea0 + (m / NMH) * KBLK + ((m % NMH) * 2u + b) * 512u + (w % 2u) * 256u -
+                   k * 1024u;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 4,
+                                             voff, 0, (int)(k * 1024u), 0);
   }
 }
 template <int N>
@@ -1781,7 +1793,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // F16 stages with loads straight into LDS: no staging registers, and a block's data
   // lands while the step computes. An instruction writes 64 lanes' data contiguously;
   // the lanes' sources give the layout: K as stored (16 bytes a lane, instruction n
-  // of the block = bytes n*1024 ..), V in pf_v_off's slot order (4 bytes a lane,
+  // of the block = bytes n*1024 ..), V in pf_vi_off's order (4 bytes a lane,
   // instruction n = dims 8n .. 8n + 7). Wave w issues instructions w, w + 4, ...; its
   // lanes' V sources differ between them by a constant, as the slot permutation of
   // dims 8(w + 4k) + l/8 does not depend on k.
@@ -1798,7 +1810,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // A block's loads go through a buffer resource based at its K tile: the lane's offset
   // is a register worked out once, the instruction's a scalar, so issuing them costs no
   // vector instruction.
-  auto dma_block_at = [&](int32_t p, uint8_t* dst) {
+  // Block p to staging buffer buf as its block b (K tile to slot b, V interleaved).
+  auto dma_block_at = [&](int32_t p, uint8_t(*buf)[kBlk], int b) {
+    uint8_t* const dst = buf[b];
     p = __builtin_amdgcn_readfirstlane(p);
     const bool ok = (p >= 0) & ((uint64_t)p < g.num_blocks);
     // The tile address is wave-uniform; passed through readfirstlane (and worked out
@@ -1817,10 +1831,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             rs, (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16, dma_k,
             k * 4096, 0, 0);
-    // V instruction k: LDS bytes (4k + wave)*256 of the V area and source bytes
-    // dma_v + k*1024, both 1024 apart per k, so one immediate offset (added to the LDS
-    // address as well as to the source) steps both and every k shares the M0 base.
-    pf_v_dma<kVIns / 4>(rs, dst + kTile + wave * 256, dma_v);
+    pf_v_dma<kVIns / 4, NM / 2, kBlk>(rs, buf[0] + kTile, (uint32_t)b, (uint32_t)wave, dma_v);
     return ok;
   };
   // Fast F16 instance: P.V of a step's two blocks in one MFMA (below).
@@ -1834,7 +1845,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   if constexpr (kDma) {
 #pragma unroll
     for (int bb = 0; bb < kStep; bb++) {
-      if (jbeg + bb < jend) lv[bb] = dma_block_at(table[jbeg + bb], s_kv0[bb]);
+      if (jbeg + bb < jend) lv[bb] = dma_block_at(table[jbeg + bb], s_kv0, bb);
       if (jbeg + kStep + bb < jend) pn[bb] = table[jbeg + kStep + bb];
     }
   } else {
@@ -1870,8 +1881,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     if constexpr (kDma) {
       // the next step's blocks into the other buffer (its readers passed the barrier
       // that ended the last step), and the table entries of the step after
-      if (more) nlv[0] = dma_block_at(pn[0], nxt[0]);
-      if (more2) nlv[1] = dma_block_at(pn[1], nxt[1]);
+      if (more) nlv[0] = dma_block_at(pn[0], nxt, 0);
+      if (more2) nlv[1] = dma_block_at(pn[1], nxt, 1);
 #pragma unroll
       for (int bb = 0; bb < kStep; bb++)
         pn[bb] = j0 + 2 * kStep + bb < jend ? table[j0 + 2 * kStep + bb] : 0;
@@ -1957,8 +1968,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     if constexpr (kPair) {
       // P.V of both blocks: one 16x16x32 MFMA per 16 dims, k-slots grp*8 .. +3 the first
       // block's tokens grp*4 .. +3 and grp*8 + 4 .. +7 the second's, in P (the lane's own
-      // weights) and in V (8 bytes from each block's tile, one ds_read2st64_b64: the two
-      // slots' V areas are kBlk apart) alike. The pool holds no Inf/NaN here, so V needs
+      // weights) and in V (8 bytes from each block's tile, 512 bytes apart in pf_vi_off's
+      // layout: one ds_read2st64_b64) alike. The pool holds no Inf/NaN here, so V needs
       // zeroing only where P's zeros could meet unwritten bytes: tokens at or past the
       // wave's furthest causal end, and a block not in the pool or not staged (a slot
       // not staged this step holds an earlier block's bytes, or nothing written yet).
@@ -1975,8 +1986,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
           uint4 v[NM / 2];
 #pragma unroll
           for (int i = 0; i < NM / 2; i++) {
-            const uint32_t vo = pf_v_off((uint32_t)((h * (NM / 2) + i) * 16 + ln.col), (uint32_t)ln.grp);
-            const u32x2_t a = *(const u32x2_t*)(vc + vo), b = *(const u32x2_t*)(vc + kBlk + vo);
+            const uint32_t vo = pf_vi_off<NM / 2, kBlk>((uint32_t)(h * (NM / 2) + i), 0u,
+                                                        (uint32_t)ln.col, (uint32_t)ln.grp);
+            const u32x2_t a = *(const u32x2_t*)(vc + vo), b = *(const u32x2_t*)(vc + vo + 512u);
             v[i] = uint4{a.x, a.y, b.x, b.y};
           }
           if (vmask) {
@@ -2006,13 +2018,14 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
       if (j < jw_end && lv[bb]) {
-        const uint8_t* vs = cur[bb] + kTile;
+        const uint8_t* vs = cur[bb] + kTile;  // (Q8_0; F16 V is interleaved: vi0)
+        const uint8_t* vi0 = cur[0] + kTile;
         if constexpr (DT == kDtypeF16) {
           u32x2_t vr[NM];
 #pragma unroll
           for (int m = 0; m < NM; m++) {
-            const uint32_t dim = (uint32_t)(m * 16 + ln.col);
-            vr[m] = *(const u32x2_t*)(vs + pf_v_off(dim, (uint32_t)ln.grp));
+            vr[m] = *(const u32x2_t*)(vi0 + pf_vi_off<NM / 2, kBlk>((uint32_t)m, (uint32_t)bb,
+                                                                    (uint32_t)ln.col, (uint32_t)ln.grp));
           }
           // Leak-safe instance: a block where a non-finite V lies past the tile's
           // nearest causal end takes one P.V per query token jt of the tile, V cut at
@@ -2030,8 +2043,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
             for (int32_t jt = 0; jt < T; jt++) {
 #pragma unroll
               for (int m = 0; m < NM; m++) {
-                const uint32_t dim = (uint32_t)(m * 16 + ln.col);
-                vr[m] = *(const u32x2_t*)(vs + pf_v_off(dim, (uint32_t)ln.grp));
+                vr[m] = *(const u32x2_t*)(vi0 + pf_vi_off<NM / 2, kBlk>((uint32_t)m, (uint32_t)bb,
+                                                                        (uint32_t)ln.col, (uint32_t)ln.grp));
               }
               mask_v_tail<D>(vr, ln, t0, p0 + tile * T + jt + 1);
 #pragma unroll
