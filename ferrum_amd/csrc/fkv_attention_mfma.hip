@@ -1811,10 +1811,13 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // is a register worked out once, the instruction's a scalar, so issuing them costs no
   // vector instruction.
   // Block p to staging buffer buf as its block b (K tile to slot b, V interleaved).
+  // (the pool's block count clamped to 32 bits: the same test for any int32 p >= 0,
+  // and a scalar compare)
+  const uint32_t nblk32 = g.num_blocks > 0xffffffffull ? 0xffffffffu : (uint32_t)g.num_blocks;
   auto dma_block_at = [&](int32_t p, uint8_t(*buf)[kBlk], int b) {
     uint8_t* const dst = buf[b];
     p = __builtin_amdgcn_readfirstlane(p);
-    const bool ok = (p >= 0) & ((uint64_t)p < g.num_blocks);
+    const bool ok = (p >= 0) & ((uint32_t)p < nblk32);
     // The tile address is wave-uniform; passed through readfirstlane (and worked out
     // before the fault branch below) the compiler keeps the resource in scalar
     // registers instead of looping over lanes.
