@@ -1807,13 +1807,13 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + w * 256u + (l >> 3) * 32u +
             (sl ^ perm) * 8u + (l % 2u) * 4u;
   }
-  // A block's loads go through a buffer resource based at its K tile: the lane's offset
-  // is a register worked out once, the instruction's a scalar, so issuing them costs no
-  // vector instruction.
-  // Block p to staging buffer buf as its block b (K tile to slot b, V interleaved).
   // (the pool's block count clamped to 32 bits: the same test for any int32 p >= 0,
   // and a scalar compare)
   const uint32_t nblk32 = g.num_blocks > 0xffffffffull ? 0xffffffffu : (uint32_t)g.num_blocks;
+  // Block p to staging buffer buf as its block b (K tile to slot b, V interleaved with
+  // the other block's). The loads go through a buffer resource based at the block's K
+  // tile: the lane's offset is a register worked out once, the instruction's a scalar or
+  // an immediate, so issuing them costs no vector instruction.
   auto dma_block_at = [&](int32_t p, uint8_t(*buf)[kBlk], int b) {
     uint8_t* const dst = buf[b];
     p = __builtin_amdgcn_readfirstlane(p);
