@@ -81,7 +81,8 @@ def parse():
                     help="> 0: time fkv_rope_append_decode_attention (q and k before RoPE)")
     ap.add_argument("--rope-theta", type=float, default=500000.0)
     ap.add_argument("--kv-dtype", default="f16", choices=["f16", "f32", "q8_0"],
-                    help="c2: KV storage (f32 runs the VALU attention kernel)")
+                    help="c2: KV storage (f32 runs the VALU attention kernel); c3: f16 "
+                         "(BASELINE's) or q8_0")
     ap.add_argument("--n-heads", type=int, default=32,
                     help="c2: query heads over the 8 KV heads (64: GQA group 8)")
     return ap.parse_args()
@@ -568,10 +569,13 @@ def run_c3(args, torch, fa, lib, dev):
     ctx_dec = np.minimum(np.round(np.exp(rng.normal(np.log(2048), 1.0, n_dec))), 32768 - W - K)
     ctx_dec = np.maximum(ctx_dec, 1).astype(np.int64)
     pre_prior = np.array([0, 512, 1024, 1536], np.int64)  # chunked prefill in progress
-    block_bytes = L * 2 * hkv * 16 * d * 2
+    if args.kv_dtype not in ("f16", "q8_0"):
+        raise SystemExit("c3: --kv-dtype f16 or q8_0")
+    dtype = {"f16": 1, "q8_0": 8}[args.kv_dtype]
+    block_bytes = int(L * 2 * hkv * 16 * d * elem_bytes(dtype))
     num_blocks = int(0.6 * 288e9 // block_bytes)
     pool = fa.PagedKvPool(fa.PagedConfig(n_layers=L, n_kv_heads=hkv, head_dim=d,
-                                         num_blocks=num_blocks, block_size=16, kv_dtype=1))
+                                         num_blocks=num_blocks, block_size=16, kv_dtype=dtype))
     nblk = np.concatenate([(ctx_dec + W + K + 15) // 16, (pre_prior + chunk * (W + K) + 15) // 16])
     tables = make_tables(pool, nblk, rng, fragment_cycles=10000)
     gen = torch.Generator(device=dev)
@@ -649,15 +653,15 @@ def run_c3(args, torch, fa, lib, dev):
     pre_flop = 4.0 * d * hq * pairs
     # decode-only rate from a separate region of back-to-back fused decode calls
     dw, dms = dl.run(0, K)
-    e = 2.0
+    e = elem_bytes(dtype)
     dec_bytes = [attn_bytes(dl.ctx_step[W + i], hq, hkv, d, e) * L for i in range(K)]
-    pre_attn = sum(attn_bytes_prefill(pre_prior + (W + i) * chunk + chunk, chunk, hq, hkv, d)
+    pre_attn = sum(attn_bytes_prefill(pre_prior + (W + i) * chunk + chunk, chunk, hq, hkv, d, e)
                    for i in range(K)) * L
     app = (append_bytes(n_dec, hkv, d, e, 0) + append_bytes(n_pre * chunk, hkv, d, e)) * L * K
     total = float(sum(dec_bytes)) + pre_attn + app
     res = decode_result(args, dl, 0, K, dw, dms, e, "llama3-8b continuous batching "
                         "(BASELINE configs[2])",
-                        {"kv_dtype": "f16", "ctx": "log-normal median 2048 sigma 1.0 cap 32768",
+                        {"kv_dtype": args.kv_dtype, "ctx": "log-normal median 2048 sigma 1.0 cap 32768",
                          "prefill": f"{n_pre} x {chunk}-token chunks",
                          "pool_blocks": num_blocks, "pool_gb": round(pool.pool_bytes / 1e9, 1),
                          "fragmented_by": "10000 seeded alloc/free cycles"},
@@ -682,11 +686,11 @@ def run_c3(args, torch, fa, lib, dev):
     return res
 
 
-def attn_bytes_prefill(ctx_end, q_len, hq, hkv, d):
+def attn_bytes_prefill(ctx_end, q_len, hq, hkv, d, e=2.0):
     """Chunked prefill of q_len queries ending at ctx_end per sequence: K/V of the
-    whole context once per KV head, q and out in f32."""
+    whole context once per KV head (e bytes a value), q and out in f32."""
     ctx_end = np.asarray(ctx_end, np.int64)
-    return float((ctx_end * hkv * d * 2 * 2 + q_len * hq * d * 8 + ((ctx_end + 15) // 16) * 4).sum())
+    return float((ctx_end * hkv * d * 2 * e + q_len * hq * d * 8 + ((ctx_end + 15) // 16) * 4).sum())
 
 
 def run_c1(args, torch, fa, lib, dev):

@@ -1757,9 +1757,10 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
   // A table entry outside the pool raises the fault flag, stages block 0 and is
-  // skipped. Q8_0 (load_block / store_block): thread t moves 16-byte chunks t, t + 256,
-  // ... of a block's K | V pair through registers, stored as loaded (the V tile of the
-  // same head is n_kv_heads tiles past its K tile). F16: dma_block_at below.
+  // skipped. Blocks are staged by direct loads into LDS (dma_block_at below); the
+  // register path (load_block / store_block: thread t moves 16-byte chunks t, t + 256,
+  // ... of a block's K | V pair, stored as loaded; the V tile of the same head is
+  // n_kv_heads tiles past its K tile) is kept for configurations without them.
   const uint8_t* kbase = tile_ptr(g, 0, layer, 0, kvh);
   // (n_kv_heads tiles of one layer's K fit in 32 bits: a block of every layer does not)
   const uint32_t v_skip = (uint32_t)(g.n_kv_heads * g.tile_bytes) - (uint32_t)kTile;
@@ -1797,7 +1798,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // instruction n = dims 8n .. 8n + 7). Wave w issues instructions w, w + 4, ...; its
   // lanes' V sources differ between them by a constant, as the slot permutation of
   // dims 8(w + 4k) + l/8 does not depend on k.
-  constexpr bool kDma = DT == kDtypeF16;
+  constexpr bool kDma = true;
   constexpr int kKIns = kTile / 1024, kVIns = kTile / 256;
   uint32_t dma_k = 0, dma_v = 0;
   if constexpr (kDma) {
@@ -1828,17 +1829,40 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)kt, (short)0, 0x7fffffff, 0x00020000);
+    if constexpr (DT == kDtypeF16) {
 #pragma unroll
-    for (int k = 0; k < (kKIns + 3) / 4; k++)
-      if (k * 4 + wave < kKIns)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            rs, (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16, dma_k,
-            k * 4096, 0, 0);
-    pf_v_dma<kVIns / 4, NM / 2, kBlk>(rs, buf[0] + kTile, (uint32_t)b, (uint32_t)wave, dma_v);
+      for (int k = 0; k < (kKIns + 3) / 4; k++)
+        if (k * 4 + wave < kKIns)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs, (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16,
+              dma_k + k * 4096u, 0, 0, 0);
+      pf_v_dma<kVIns / 4, NM / 2, kBlk>(rs, buf[0] + kTile, (uint32_t)b, (uint32_t)wave, dma_v);
+    } else {
+      // Q8_0 tiles as stored, K to dst and V to dst + kTile: 16-byte units, instruction
+      // i of the block (wave w takes i = w, w + 4, ...) = 64 units of the K tile (i' = i)
+      // or of the V tile (i' = i - kQIns) from unit min(64i', units - 64): every lane
+      // loads a unit of the tile, the last instruction overlapping the one before with
+      // the same bytes.
+      constexpr int kUnits = kTile / 16, kQIns = (kUnits + 63) / 64;
+      static_assert(kUnits >= 64, "a Q8_0 tile holds at least 64 units");
+      const uint32_t vsrc = (uint32_t)(g.n_kv_heads * g.tile_bytes);
+#pragma unroll
+      for (int k = 0; k < (2 * kQIns + 3) / 4; k++) {
+        const int i = wave + 4 * k;  // wave-uniform
+        if (i < 2 * kQIns) {
+          const bool isv = i >= kQIns;
+          const int ip = isv ? i - kQIns : i;
+          const int u0 = ip * 64 < kUnits - 64 ? ip * 64 : kUnits - 64;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              rs, (__attribute__((address_space(3))) void*)(dst + (isv ? kTile : 0) + u0 * 16),
+              16, (isv ? vsrc : 0u) + ((uint32_t)u0 + ln.lane) * 16u, 0, 0, 0);
+        }
+      }
+    }
     return ok;
   };
   // Fast F16 instance: P.V of a step's two blocks in one MFMA (below).
-  constexpr bool kPair = kDma && MODE == kPfFast;
+  constexpr bool kPair = DT == kDtypeF16 && MODE == kPfFast;
   // every load this wave issued has landed (vmcnt 0; expcnt and lgkmcnt left alone)
   auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
