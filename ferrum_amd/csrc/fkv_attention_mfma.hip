@@ -1683,8 +1683,6 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   constexpr int kTile = prefill_tile_bytes<DT, D>();
   static_assert(kTile % 16 == 0, "tiles are whole 16-byte chunks");
   constexpr int kBlk = 2 * kTile;               // K tile | V tile
-  constexpr int kChunks = kBlk / 16;
-  constexpr int kLoads = (kChunks + 255) / 256;  // 16-byte loads per thread per block
   // Two staging buffers (steps alternate), as two arrays: the loop runs two steps an
   // iteration, each with its buffer known at compile time, so the compiler sees that a
   // step's LDS reads do not touch the loads landing in the other buffer and does not
@@ -1757,40 +1755,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
   // A table entry outside the pool raises the fault flag, stages block 0 and is
-  // skipped. Blocks are staged by direct loads into LDS (dma_block_at below); the
-  // register path (load_block / store_block: thread t moves 16-byte chunks t, t + 256,
-  // ... of a block's K | V pair, stored as loaded; the V tile of the same head is
-  // n_kv_heads tiles past its K tile) is kept for configurations without them.
+  // skipped. Blocks are staged by direct loads into LDS (dma_block_at below).
   const uint8_t* kbase = tile_ptr(g, 0, layer, 0, kvh);
-  // (n_kv_heads tiles of one layer's K fit in 32 bits: a block of every layer does not)
-  const uint32_t v_skip = (uint32_t)(g.n_kv_heads * g.tile_bytes) - (uint32_t)kTile;
-  uint4 stg[kLoads];
-  auto chunk_off = [&](int i) {
-    const uint32_t c = (uint32_t)(i * 256) + threadIdx.x;
-    return (c < (uint32_t)kChunks ? c : 0u) * 16u;
-  };
-  // every thread holds chunk i unless the block's last 256-chunk row is partial
-  auto has_chunk = [&](int i) {
-    return (i + 1) * 256 <= kChunks || (uint32_t)(i * 256) + threadIdx.x < (uint32_t)kChunks;
-  };
-  auto load_block_at = [&](int32_t p) {
-    p = __builtin_amdgcn_readfirstlane(p);
-    const bool ok = (p >= 0) & ((uint64_t)p < g.num_blocks);
-    if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
-    const uint8_t* kt = kbase + (ok ? (uint64_t)p : 0u) * g.block_bytes;
-#pragma unroll
-    for (int i = 0; i < kLoads; i++) {
-      const uint32_t off = chunk_off(i);
-      if (has_chunk(i)) stg[i] = load_stream16(kt + off + (off >= (uint32_t)kTile ? v_skip : 0u));
-    }
-    return ok;
-  };
-  auto load_block = [&](int32_t j) { return load_block_at(table[j]); };
-  auto store_block = [&](uint8_t* dst) {
-#pragma unroll
-    for (int i = 0; i < kLoads; i++)
-      if (has_chunk(i)) *(uint4*)&dst[chunk_off(i)] = stg[i];
-  };
   // F16 stages with loads straight into LDS: no staging registers, and a block's data
   // lands while the step computes. An instruction writes 64 lanes' data contiguously;
   // the lanes' sources give the layout: K as stored (16 bytes a lane, instruction n
@@ -1798,10 +1764,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // instruction n = dims 8n .. 8n + 7). Wave w issues instructions w, w + 4, ...; its
   // lanes' V sources differ between them by a constant, as the slot permutation of
   // dims 8(w + 4k) + l/8 does not depend on k.
-  constexpr bool kDma = true;
   constexpr int kKIns = kTile / 1024, kVIns = kTile / 256;
   uint32_t dma_k = 0, dma_v = 0;
-  if constexpr (kDma) {
+  if constexpr (DT == kDtypeF16) {
     const uint32_t l = ln.lane, w = (uint32_t)wave;
     dma_k = (w * 64u + l) * 16u;
     const uint32_t sl = (l % 8u) / 2u, perm = (2u * w + (l >> 5)) & 3u;
@@ -1868,22 +1833,11 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 
   bool lv[kStep] = {false, false};   // blocks of the step being computed: in the pool
   bool nlv[kStep] = {false, false};  // and of the next step
-  int32_t pn[kStep] = {0, 0};        // (DMA) table entries of the next step's blocks
-  if constexpr (kDma) {
+  int32_t pn[kStep] = {0, 0};        // table entries of the next step's blocks
 #pragma unroll
-    for (int bb = 0; bb < kStep; bb++) {
-      if (jbeg + bb < jend) lv[bb] = dma_block_at(table[jbeg + bb], s_kv0, bb);
-      if (jbeg + kStep + bb < jend) pn[bb] = table[jbeg + kStep + bb];
-    }
-  } else {
-#pragma unroll
-    for (int bb = 0; bb < kStep; bb++) {
-      if (jbeg + bb < jend) {
-        lv[bb] = load_block(jbeg + bb);
-        store_block(s_kv0[bb]);
-      }
-    }
-    if (jbeg + kStep < jend) nlv[0] = load_block(jbeg + kStep);
+  for (int bb = 0; bb < kStep; bb++) {
+    if (jbeg + bb < jend) lv[bb] = dma_block_at(table[jbeg + bb], s_kv0, bb);
+    if (jbeg + kStep + bb < jend) pn[bb] = table[jbeg + kStep + bb];
   }
   // blocks this wave computes: the piece's, up to the wave's furthest causal end
   const int32_t jw_end = nblk_w < jend ? nblk_w : jend;
@@ -1892,7 +1846,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   prep_q<D>(q + row_of(ln.real ? ln.col : 0), ln, scale * kLog2e, qh, qlo, hscale);
   Accum<D> st;
   st.reset();
-  if constexpr (kDma) dma_wait();
+  dma_wait();
   __syncthreads();
 
   int32_t j0 = jbeg;
@@ -1903,17 +1857,13 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     uint8_t(*const nxt)[kBlk] = BUF == 0 ? s_kv1 : s_kv0;
     const bool more = j0 + kStep < jend;      // the workgroup has a next step
     const bool more2 = j0 + kStep + 1 < jend;  // with a second block
-    // the table entry of the block staged in the middle of the step, read up front
-    const int32_t p_mid = (!kDma && more2) ? table[j0 + kStep + 1] : 0;
-    if constexpr (kDma) {
-      // the next step's blocks into the other buffer (its readers passed the barrier
-      // that ended the last step), and the table entries of the step after
-      if (more) nlv[0] = dma_block_at(pn[0], nxt, 0);
-      if (more2) nlv[1] = dma_block_at(pn[1], nxt, 1);
+    // the next step's blocks into the other buffer (its readers passed the barrier that
+    // ended the last step), and the table entries of the step after
+    if (more) nlv[0] = dma_block_at(pn[0], nxt, 0);
+    if (more2) nlv[1] = dma_block_at(pn[1], nxt, 1);
 #pragma unroll
-      for (int bb = 0; bb < kStep; bb++)
-        pn[bb] = j0 + 2 * kStep + bb < jend ? table[j0 + 2 * kStep + bb] : 0;
-    }
+    for (int bb = 0; bb < kStep; bb++)
+      pn[bb] = j0 + 2 * kStep + bb < jend ? table[j0 + 2 * kStep + bb] : 0;
     float sc[kStep][4];
     if constexpr (DT == kDtypeF16 && MODE == kPfFast) {
       // Both blocks' QK chains issued back to back (the second block's LDS reads and
@@ -1982,10 +1932,6 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       } else {
 #pragma unroll
         for (int r = 0; r < 4; r++) sc[bb][r] = -__builtin_inff();
-      }
-      if (!kDma && bb == 0 && more) {  // the next step's first block to the other buffer
-        store_block(nxt[0]);
-        if (more2) nlv[1] = load_block_at(p_mid);
       }
     }
     }  // DT != kDtypeF16 || MODE != kPfFast
@@ -2099,15 +2045,10 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     }
     }  // !kPair
     if (more) {
-      if constexpr (kDma) {
-        dma_wait();
-      } else {
-        if (more2) store_block(nxt[1]);
-      }
+      dma_wait();
       __syncthreads();
       lv[0] = nlv[0];
       lv[1] = more2 ? nlv[1] : false;
-      if (!kDma && j0 + 2 * kStep < jend) nlv[0] = load_block(j0 + 2 * kStep);
     }
   };
   while (j0 < jend) {
