@@ -62,6 +62,7 @@ __device__ __forceinline__ uint32_t tail_dw(bool aligned, uint32_t block) {
   return aligned ? 16u + 2u * swap : 18u - 2u * swap;
 }
 constexpr int kXRegs = 2;  // activation passes (8 values a lane) loaded up front
+constexpr int kXRegsWide = 8;  // the same for one-token launches of more than 4096 columns
 
 // LDS blocks a token: the step count rounded up to whole groups of kPipe iterations
 // (an iteration is S steps of 16 blocks), so every step a group runs reads inside the
@@ -136,8 +137,9 @@ __device__ __forceinline__ uint32_t f16_bits_away(float d) {
 // (C = ceil((cols/8) / 256) passes a token), items j = (q % C) * 256 + thread:
 // values 8j .. 8j+8 of the token; four consecutive lanes (a quad) own one 32-value
 // block. Token and chunk are uniform, so no lane divides.
+template <int XR>
 struct XRegs {
-  f32x4a v[2 * kXRegs];
+  f32x4a v[2 * XR];
 };
 
 struct XPlan {
@@ -146,14 +148,15 @@ struct XPlan {
   uint32_t passes;   // nt * chunks
 };
 
-// Issues the loads of passes [q0, q0 + kXRegs). Items past a token's end read its
-// last item (in bounds; never stored), so no load sits under a branch.
+// Issues the loads of passes [q0, q0 + XR) (none past the last pass: a uniform
+// test). Items past a token's end read its last item (in bounds; never stored).
+template <int XR>
 __device__ __forceinline__ void load_x(const float* x, uint32_t cols, uint32_t t0,
-                                       const XPlan& pl, uint32_t q0, XRegs& r) {
+                                       const XPlan& pl, uint32_t q0, XRegs<XR>& r) {
 #pragma unroll
-  for (int k = 0; k < kXRegs; ++k) {
-    uint32_t q = q0 + (uint32_t)k;
-    q = q < pl.passes ? q : pl.passes - 1u;
+  for (int k = 0; k < XR; ++k) {
+    const uint32_t q = q0 + (uint32_t)k;
+    if (q >= pl.passes) break;  // uniform
     const uint32_t t = q / pl.chunks, c = q - t * pl.chunks;
     uint32_t j = c * kGemvThreads + threadIdx.x;
     j = j < pl.per_tok ? j : pl.per_tok - 1u;
@@ -163,10 +166,11 @@ __device__ __forceinline__ void load_x(const float* x, uint32_t cols, uint32_t t
   }
 }
 
-__device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, const XPlan& pl,
+template <int XR>
+__device__ __forceinline__ void quantize_x(const XRegs<XR>& r, uint32_t nb, const XPlan& pl,
                                            uint32_t q0, uint32_t* lds) {
 #pragma unroll
-  for (int k = 0; k < kXRegs; ++k) {
+  for (int k = 0; k < XR; ++k) {
     const uint32_t q = q0 + (uint32_t)k;
     if (q >= pl.passes) break;  // uniform
     const uint32_t t = q / pl.chunks, c = q - t * pl.chunks;
@@ -218,7 +222,7 @@ __device__ __forceinline__ void quantize_x(const XRegs& r, uint32_t nb, const XP
 // launch twice the waves. Each iteration's two steps are added in order by both DPP
 // rows (the products of the other one brought over by a lane swap), so the sum is
 // the same as S = 1's, bit for bit.
-template <int T, int S>
+template <int T, int S, int XR>
 __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch bat, uint32_t cols,
                                                                const float* x, uint32_t n_tokens) {
   // This workgroup's matrix (uniform: scalar selects over the launch's few matrices).
@@ -273,8 +277,8 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
   pl.per_tok = cols / 8u;
   pl.chunks = (pl.per_tok + kGemvThreads - 1u) / kGemvThreads;
   pl.passes = nt * pl.chunks;
-  XRegs xr;
-  load_x(x, cols, t0, pl, 0, xr);
+  XRegs<XR> xr;
+  load_x<XR>(x, cols, t0, pl, 0, xr);
   // Keep these loads ahead of the weight prefetch: no load moves across an asm
   // statement that may touch memory (x is not __restrict__, so that covers it).
   __asm__ volatile("" ::: "memory");
@@ -297,10 +301,10 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
 #pragma unroll
   for (int k = 0; k < kPipe; ++k) load_step((uint32_t)k, buf[k]);
 
-  quantize_x(xr, nbp, pl, 0, lds);
-  for (uint32_t q0 = kXRegs; q0 < pl.passes; q0 += kXRegs) {
-    load_x(x, cols, t0, pl, q0, xr);
-    quantize_x(xr, nbp, pl, q0, lds);
+  quantize_x<XR>(xr, nbp, pl, 0, lds);
+  for (uint32_t q0 = XR; q0 < pl.passes; q0 += XR) {
+    load_x<XR>(x, cols, t0, pl, q0, xr);
+    quantize_x<XR>(xr, nbp, pl, q0, lds);
   }
   __syncthreads();
 
@@ -363,18 +367,18 @@ __global__ __launch_bounds__(kGemvThreads) void gemv_q8_kernel(const GemvBatch b
   }
 }
 
-template <int T, int S>
+template <int T, int S, int XR = kXRegs>
 hipError_t launch_t(const GemvBatch& b, uint32_t n_wg, uint32_t cols, const float* x,
                     uint32_t n_tokens, hipStream_t s) {
   const dim3 grid(n_wg, (n_tokens + T - 1u) / T);
   const size_t lds = (size_t)T * gemv_padded_blocks(cols / 32u, S) * kXDw * 4u;
   if (lds > 65536u) {
-    const hipError_t e = hipFuncSetAttribute((const void*)gemv_q8_kernel<T, S>,
+    const hipError_t e = hipFuncSetAttribute((const void*)gemv_q8_kernel<T, S, XR>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize,
                                              (int)lds);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL((gemv_q8_kernel<T, S>), grid, dim3(kGemvThreads), lds, s, b, cols, x,
+  hipLaunchKernelGGL((gemv_q8_kernel<T, S, XR>), grid, dim3(kGemvThreads), lds, s, b, cols, x,
                      n_tokens);
   return hipGetLastError();
 }
@@ -673,6 +677,9 @@ hipError_t launch_gemv_q8(GemvBatch b, uint32_t cols, const float* x, uint32_t n
     case 4: return launch_t<4, 1>(b, n_wg, cols, x, n_tokens, s);
     case 2: return launch_t<2, 1>(b, n_wg, cols, x, n_tokens, s);
     default:
+      if (cols > 4096u)
+        return S == 2u ? launch_t<1, 2, kXRegsWide>(b, n_wg, cols, x, n_tokens, s)
+                       : launch_t<1, 1, kXRegsWide>(b, n_wg, cols, x, n_tokens, s);
       return S == 2u ? launch_t<1, 2>(b, n_wg, cols, x, n_tokens, s)
                      : launch_t<1, 1>(b, n_wg, cols, x, n_tokens, s);
   }

@@ -84,6 +84,9 @@ def test_reference_known_answer():
     (17, 96, 1), (33, 544, 3), (16, 512, 5), (100, 1056, 9), (1000, 4096, 1),
     (5, 8192, 7), (48, 2080, 8), (7, 57344, 2),
     (3, 65536, 2),   # the widest accepted: one token's activation copies fill 160 KB of LDS
+    # one token past 4096 columns: 3 activation passes a thread, and 32 (more than the
+    # 8 loaded up front, so the rest go through the loop)
+    (33, 4128, 1), (600, 4128, 1), (3, 65536, 1), (520, 65536, 1),
 ])
 def test_matches_oracle(rows, cols, n_tokens):
     rng = np.random.default_rng(rows * 7919 + cols + n_tokens)
