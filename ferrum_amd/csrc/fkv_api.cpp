@@ -644,6 +644,9 @@ static int32_t check_prefill(const fkv_pool* pool, uint32_t n_heads, uint32_t n_
   if (st) return st;
   if (pool->cfg.kv_dtype != FKV_DTYPE_F16 && pool->cfg.kv_dtype != FKV_DTYPE_Q8_0)
     return fail(FKV_ERR_KERNEL, "prefill attention needs f16 or q8_0 kv");
+  // the kernel offsets blocks by a 32 x 32-bit product
+  if (pool->geom.block_bytes > 0xffffffffull)
+    return fail(FKV_ERR_KERNEL, "prefill attention needs kv blocks under 4 GiB");
   if ((uint64_t)n_seqs * pool->cfg.n_kv_heads > 0x7fffffffull)
     return fail(FKV_ERR_INVALID, "too many sequences");
   if (max_q_len > max_ctx_len) return fail(FKV_ERR_INVALID, "max_q_len exceeds max_ctx_len");

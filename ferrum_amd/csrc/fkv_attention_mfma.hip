@@ -1773,9 +1773,10 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + w * 256u + (l >> 3) * 32u +
             (sl ^ perm) * 8u + (l % 2u) * 4u;
   }
-  // (the pool's block count clamped to 32 bits: the same test for any int32 p >= 0,
-  // and a scalar compare)
-  const uint32_t nblk32 = g.num_blocks > 0xffffffffull ? 0xffffffffu : (uint32_t)g.num_blocks;
+  // The pool's block count clamped to 2^31: one unsigned compare tests p >= 0 and
+  // p < num_blocks for any int32 p. A block's bytes fit 32 bits (the API checks), so
+  // its offset is one 32 x 32-bit product.
+  const uint32_t nblk32 = g.num_blocks > 0x80000000ull ? 0x80000000u : (uint32_t)g.num_blocks;
   // Block p to staging buffer buf as its block b (K tile to slot b, V interleaved with
   // the other block's). The loads go through a buffer resource based at the block's K
   // tile: the lane's offset is a register worked out once, the instruction's a scalar or
@@ -1783,21 +1784,23 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   auto dma_block_at = [&](int32_t p, uint8_t(*buf)[kBlk], int b) {
     uint8_t* const dst = buf[b];
     p = __builtin_amdgcn_readfirstlane(p);
-    const bool ok = (p >= 0) & ((uint32_t)p < nblk32);
+    const bool ok = (uint32_t)p < nblk32;
     // The tile address is wave-uniform; passed through readfirstlane (and worked out
     // before the fault branch below) the compiler keeps the resource in scalar
     // registers instead of looping over lanes.
-    const uint64_t ka = (uint64_t)(uintptr_t)kbase + (ok ? (uint64_t)p : 0u) * g.block_bytes;
+    const uint64_t ka = (uint64_t)(uintptr_t)kbase + (uint64_t)(ok ? (uint32_t)p : 0u) * (uint32_t)g.block_bytes;
     const uint64_t kau = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(ka >> 32)) << 32) |
                          (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ka);
     const uint8_t* kt = (const uint8_t*)(uintptr_t)kau;
-    if (!ok && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
+    if (__builtin_expect(!ok, 0)) {  // wave-uniform: the common path is one branch
+      if (threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
+    }
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc((void*)kt, (short)0, 0x7fffffff, 0x00020000);
     if constexpr (DT == kDtypeF16) {
 #pragma unroll
       for (int k = 0; k < (kKIns + 3) / 4; k++)
-        if (k * 4 + wave < kKIns)
+        if (kKIns % 4 == 0 || k * 4 + wave < kKIns)
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               rs, (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16,
               dma_k + k * 4096u, 0, 0, 0);
