@@ -368,7 +368,8 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
  * positions 0 ..= that position. q, out: device f32 [rows][n_heads][head_dim];
  * sequence s's queries are rows q_offsets[s] .. q_offsets[s] + q_lens[s] - 1
  * (q_offsets: device int64). q_lens[s] = 1 is decode. Needs block_size 16, head_dim
- * 64 or 128, g <= 16. The launch holds max_q_len queries a sequence: a q_lens[s]
+ * 64 or 128, g <= 16, and a pool block (all layers' K and V) under 4 GiB
+ * (FKV_ERR_KERNEL otherwise). The launch holds max_q_len queries a sequence: a q_lens[s]
  * above it (or above ctx_lens[s]) raises FKV_FAULT_CTX_RANGE, and only its first
  * max_q_len queries are computed, at the positions q_lens[s] gives them. No query
  * reads a position past its own, Inf/NaN values included: an F16 pool that has
