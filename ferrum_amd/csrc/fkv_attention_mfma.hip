@@ -1864,9 +1864,6 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     // ended the last step), and the table entries of the step after
     if (more) nlv[0] = dma_block_at(pn[0], nxt, 0);
     if (more2) nlv[1] = dma_block_at(pn[1], nxt, 1);
-#pragma unroll
-    for (int bb = 0; bb < kStep; bb++)
-      pn[bb] = j0 + 2 * kStep + bb < jend ? table[j0 + 2 * kStep + bb] : 0;
     float sc[kStep][4];
     if constexpr (DT == kDtypeF16 && MODE == kPfFast) {
       // Both blocks' QK chains issued back to back (the second block's LDS reads and
@@ -2047,6 +2044,13 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       }
     }
     }  // !kPair
+    // The table entries of the step after next, loaded after this step's last LDS read:
+    // a scalar load and an LDS read share one wait counter, so issued at the top it
+    // held up the step's first K operands; here its wait falls after the barrier.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int bb = 0; bb < kStep; bb++)
+      pn[bb] = j0 + 2 * kStep + bb < jend ? table[j0 + 2 * kStep + bb] : 0;
     if (more) {
       dma_wait();
       __syncthreads();
