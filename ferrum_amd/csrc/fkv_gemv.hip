@@ -61,8 +61,11 @@ __device__ __forceinline__ uint32_t tail_dw(bool aligned, uint32_t block) {
   const uint32_t swap = (block >> 3) & 1u;
   return aligned ? 16u + 2u * swap : 18u - 2u * swap;
 }
-constexpr int kXRegs = 2;  // activation passes (8 values a lane) loaded up front
-constexpr int kXRegsWide = 8;  // the same for one-token launches of more than 4096 columns
+// Activation passes (8 values a lane) loaded up front: 2 by default, 4 for two-token
+// launches and 8 for one-token launches of more than 4096 columns (measured: more
+// passes up front slowed the 3- and 4-token launches).
+constexpr int kXRegs = 2;
+constexpr int kXRegsWide = 8;
 
 // LDS blocks a token: the step count rounded up to whole groups of kPipe iterations
 // (an iteration is S steps of 16 blocks), so every step a group runs reads inside the
@@ -675,7 +678,7 @@ hipError_t launch_gemv_q8(GemvBatch b, uint32_t cols, const float* x, uint32_t n
   for (uint32_t m = b.n; m < (uint32_t)kGemvMaxMats; ++m) b.m[m] = b.m[0];
   switch (tpl) {
     case 4: return launch_t<4, 1>(b, n_wg, cols, x, n_tokens, s);
-    case 2: return launch_t<2, 1>(b, n_wg, cols, x, n_tokens, s);
+    case 2: return launch_t<2, 1, 4>(b, n_wg, cols, x, n_tokens, s);
     default:
       if (cols > 4096u)
         return S == 2u ? launch_t<1, 2, kXRegsWide>(b, n_wg, cols, x, n_tokens, s)
