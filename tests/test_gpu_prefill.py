@@ -11,7 +11,8 @@ output rows outside the chunk are never written. Also:
   decode step) marks the pool the same way, and its +-Inf scores come out as the
   reference's dot gives them;
 - a sequence whose q_len exceeds the call's max_q_len (the grid holds no more) is
-  clamped to it and raises FKV_FAULT_CTX_RANGE;
+  clamped to it and raises FKV_FAULT_CTX_RANGE; a table entry outside the pool raises
+  FKV_FAULT_BLOCK_RANGE and its block is skipped, other sequences unaffected;
 - Q8_0 pools, with ordinary values and with values up to +-1e6 (the exact instance);
 - key ranges cut into pieces (the workspace path, down to one-block pieces through
   FKV_PREFILL_SPLIT_BLOCKS) and read whole (no workspace): both meet the bar, every
@@ -289,6 +290,34 @@ def test_q_len_past_max_q_len_is_clamped_and_flagged(pieces, monkeypatch):
     want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
     assert_close(got[:350], want[:350], what="clamped prefill")
     assert np.all(got[350:] == 5.0)
+
+
+@pytest.mark.parametrize("dtype", [1, 8])
+@pytest.mark.parametrize("pieces", [0, 3])
+def test_table_entry_outside_the_pool_is_flagged_and_skipped(dtype, pieces, monkeypatch):
+    """Two of sequence 1's table entries point outside the pool (-1 and past the last
+    block): FKV_FAULT_BLOCK_RANGE is raised, those blocks are skipped (no read outside the
+    pool; the rows stay finite), sequence 0 still matches the oracle, and rows outside the
+    chunks are untouched. F16 and Q8_0, whole key ranges and 3-block pieces."""
+    import ferrum_amd as fa
+    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
+    hkv, g, d = 2, 4, 128
+    ctxs, qls = [100, 70], [20, 30]
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=61, dtype=dtype)
+    bad = tab.copy()
+    bad[1, 1] = -1
+    bad[1, 3] = int(tab.max()) + 40  # the pool holds sum(blocks) + 4
+    rows = sum(qls) + 2
+    offs = np.array([1, 1 + qls[0]], np.int64)
+    q = np.random.default_rng(7).standard_normal((rows, hkv * g, d), dtype=np.float32)
+    got = _prefill(pool, 0, q, bad, ctxs, qls, offs)
+    assert pool.take_fault_flags() & fa.FAULT_BLOCK_RANGE
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    s0 = slice(1, 1 + qls[0])
+    assert_close(got[s0], want[s0], what="prefill beside a bad table entry")
+    s1 = slice(1 + qls[0], 1 + qls[0] + qls[1])
+    assert np.all(np.isfinite(got[s1]))
+    assert np.all(got[0] == 5.0) and np.all(got[rows - 1] == 5.0)
 
 
 @pytest.mark.parametrize("d", [128, 64])
