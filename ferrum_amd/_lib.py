@@ -12,6 +12,10 @@ import threading
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libferrum_kv.so")
 
+# FKV_ABI_VERSION of include/ferrum_kv.h that these signatures follow; a library built
+# from another header revision is refused at load (C symbols carry no signature).
+ABI_VERSION = 2
+
 FKV_OK = 0
 FKV_ERR_CACHE = 1
 FKV_ERR_UNAVAILABLE = 2
@@ -185,5 +189,9 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        got = lib.fkv_abi_version()
+        if got != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {got}, these bindings need "
+                               f"{ABI_VERSION}: rebuild it with __graft_entry__.build()")
         _lib = lib
         return lib

@@ -9,6 +9,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -50,13 +51,19 @@ int32_t hip_fail(hipError_t e, const char* what) {
     if (e_ != hipSuccess) return hip_fail(e_, what); \
   } while (0)
 
-// Makes `device` current for the lifetime of the guard.
+// Makes `device` current for the lifetime of the guard (no runtime call beyond the
+// query when it already is, the usual case of a one-GPU process).
 struct DeviceGuard {
   int prev = -1;
   bool ok = false;
   explicit DeviceGuard(int device) {
     if (hipGetDevice(&prev) != hipSuccess) prev = -1;
-    ok = hipSetDevice(device) == hipSuccess;
+    if (prev == device) {
+      prev = -1;  // nothing to restore
+      ok = true;
+    } else {
+      ok = hipSetDevice(device) == hipSuccess;
+    }
   }
   ~DeviceGuard() {
     if (prev >= 0) (void)hipSetDevice(prev);
@@ -81,6 +88,7 @@ struct fkv_pool {
   uint8_t* host = nullptr;
   uint32_t* fault = nullptr;
   uint32_t* fault_host = nullptr;  // pinned: the fault read's copy lands here
+  std::mutex fault_mu;             // one fault read at a time owns fault[3] and fault_host
   std::vector<int32_t> free_list;  // stack; LIFO reuse, as a fragmented pool would see
   std::vector<uint32_t> refcount;
   std::vector<fkv_seqs*> managers;  // detached when the pool is destroyed
@@ -179,6 +187,10 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
   p->geom.dtype = c.kv_dtype;
   p->geom.rounding = c.f16_rounding;
   p->geom.fault = p->fault;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c.device) != hipSuccess)
+    cus = 0;
+  p->geom.n_cus = cus > 0 ? (uint32_t)cus : 0u;
   p->free_list.resize(c.num_blocks);
   for (uint64_t i = 0; i < c.num_blocks; i++)
     p->free_list[i] = (int32_t)(c.num_blocks - 1 - i);  // pop order 0, 1, 2, ...
@@ -214,6 +226,9 @@ int32_t fkv_paged_get_info(const fkv_pool* pool, fkv_paged_info* out) {
 
 int32_t fkv_paged_take_fault_flags(fkv_pool* pool, void* stream, uint32_t* flags_out) {
   if (!pool || !flags_out) return fail(FKV_ERR_INVALID, "null argument");
+  // The exchange's staging word and the pinned copy are per pool: a second thread's
+  // exchange between this one's and its copy would hand it the other's bits.
+  std::lock_guard<std::mutex> lock(pool->fault_mu);
   DeviceGuard dg(pool->cfg.device);
   const hipStream_t s = (hipStream_t)stream;
   FKV_HIP(fkv::launch_take_fault(pool->fault, s), "take fault flags");

@@ -13,6 +13,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -31,26 +32,46 @@ namespace fkv {
 
 namespace {
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch_addr[kMaxScratchDevices];
+std::mutex g_scratch_mu;  // serialises set-up; readers take the published address
+std::atomic<void*> g_scratch_addr[kMaxScratchDevices];
 }  // namespace
 
 hipError_t static_scratch_setup(int device) {
   if (device < 0 || device >= kMaxScratchDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch_addr[device] != nullptr) return hipSuccess;
+  if (g_scratch_addr[device].load(std::memory_order_acquire) != nullptr) return hipSuccess;
   void* p = nullptr;
   const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
   if (e != hipSuccess) return e;
   if (p == nullptr) return hipErrorInvalidSymbol;
-  g_scratch_addr[device] = p;
+  g_scratch_addr[device].store(p, std::memory_order_release);
   return hipSuccess;
 }
 
 void* static_scratch(int device) {
   if (device < 0 || device >= kMaxScratchDevices) return nullptr;
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  return g_scratch_addr[device];
+  return g_scratch_addr[device].load(std::memory_order_acquire);
+}
+
+const Tuning& tuning() {
+  static const Tuning t = [] {
+    Tuning r;
+    if (const char* e = getenv("FKV_ATTN_SPLIT_TOKENS")) {
+      const long v = strtol(e, nullptr, 10);
+      if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) r.split_tokens = (int32_t)v;
+    }
+    if (const char* e = getenv("FKV_ATTN_MODE")) r.stream_mode = strcmp(e, "stream") == 0;
+    if (const char* e = getenv("FKV_ATTN_ORDER")) {
+      const long v = strtol(e, nullptr, 10);
+      if (v >= 0 && v <= 2) r.attn_order = (int32_t)v;
+    }
+    if (const char* e = getenv("FKV_PREFILL_SPLIT_BLOCKS")) {
+      const long long v = strtoll(e, nullptr, 10);
+      if (v >= 0) r.prefill_split = v;
+    }
+    return r;
+  }();
+  return t;
 }
 
 namespace {
@@ -581,10 +602,7 @@ inline uint64_t align256(uint64_t x) { return (x + 255) / 256 * 256; }
 // 64 per head (1 x 576 tokens, 4 KV heads: 64 tokens, 9.7 us per call against
 // 13.8 us at 512). FKV_ATTN_SPLIT_TOKENS (a multiple of 16) overrides.
 uint32_t choose_split_tokens(uint32_t max_ctx_len, uint32_t n_seqs, uint32_t n_kv_heads) {
-  if (const char* e = getenv("FKV_ATTN_SPLIT_TOKENS")) {
-    long v = strtol(e, nullptr, 10);
-    if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) return (uint32_t)v;
-  }
+  if (tuning().split_tokens) return (uint32_t)tuning().split_tokens;
   const uint64_t segs = (uint64_t)n_seqs * (n_kv_heads ? n_kv_heads : 1);
   const uint64_t by_items = (uint64_t)max_ctx_len * segs / 2048;
   const uint64_t by_head = ((uint64_t)max_ctx_len + 63) / 64;
@@ -601,11 +619,10 @@ uint32_t choose_split_tokens(uint32_t max_ctx_len, uint32_t n_seqs, uint32_t n_k
 AttnPlan plan_attention(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_ctx_len) {
   AttnPlan p;
   const uint32_t G = g.n_kv_heads ? n_heads / g.n_kv_heads : 0;
-  const char* mode = getenv("FKV_ATTN_MODE");
   // F16: the split kernel by default; FKV_ATTN_MODE=stream selects the persistent one.
-  if (g.dtype == kDtypeF16 && G >= 1 && G <= 16 && stream_attention_supported(n_seqs) && mode &&
-      strcmp(mode, "stream") == 0) {
-    p.stream_waves = stream_attention_waves(g.head_dim, n_seqs);
+  if (g.dtype == kDtypeF16 && G >= 1 && G <= 16 && stream_attention_supported(n_seqs) &&
+      tuning().stream_mode) {
+    p.stream_waves = stream_attention_waves(g.head_dim, n_seqs, g.n_cus);
     if (p.stream_waves > 0) {
       p.stream_path = true;
       const uint64_t slots = (uint64_t)p.stream_waves + (uint64_t)n_seqs * g.n_kv_heads;

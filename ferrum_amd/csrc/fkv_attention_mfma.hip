@@ -2161,15 +2161,11 @@ bool stream_attention_supported(uint32_t n_seqs) {
   return n_seqs >= 1 && n_seqs <= kStreamMaxSeqs;
 }
 
-uint32_t stream_attention_waves(uint32_t head_dim, uint32_t n_seqs) {
+uint32_t stream_attention_waves(uint32_t head_dim, uint32_t n_seqs, uint32_t n_cus) {
   const size_t lds = ((size_t)n_seqs + 1) * 4;
   const int per_cu = head_dim == 128 ? stream_wgs_per_cu<128>(lds) : stream_wgs_per_cu<64>(lds);
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-    return 0;
-  if (per_cu <= 0 || cus <= 0) return 0;
-  return (uint32_t)(per_cu * cus) * kAttnWaves;
+  if (per_cu <= 0 || n_cus == 0) return 0;
+  return (uint32_t)per_cu * n_cus * kAttnWaves;
 }
 
 hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_heads,
@@ -2213,15 +2209,13 @@ PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint3
   // of at least kPrefillMinPieceBlocks. FKV_PREFILL_SPLIT_BLOCKS sets the piece length
   // (0: no split).
   uint64_t split = 0;
-  if (const char* e = getenv("FKV_PREFILL_SPLIT_BLOCKS")) {
-    split = strtoull(e, nullptr, 10);
+  if (tuning().prefill_split >= 0) {
+    split = (uint64_t)tuning().prefill_split;
   } else {
-    int dev = 0, cus = 0;
+    const uint64_t cus = g.n_cus;
     const uint64_t wgs = (uint64_t)n_seqs * g.n_kv_heads * p.tile_groups;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
-        cus > 0 && wgs < (uint64_t)cus * kPrefillWgsPerCu) {
-      const uint64_t want = ((uint64_t)cus * kPrefillWgsPerCu * 2 + wgs - 1) / wgs;
+    if (cus > 0 && wgs < cus * kPrefillWgsPerCu) {
+      const uint64_t want = (cus * kPrefillWgsPerCu * 2 + wgs - 1) / wgs;
       split = std::max<uint64_t>(kPrefillMinPieceBlocks, (max_nblk + want - 1) / want);
     }
   }
@@ -2308,8 +2302,7 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
   uint32_t order = n_seqs <= kOrderSortSeqs   ? kOrderLongestFirst
                    : n_seqs <= kOrderMaxSeqs ? kOrderFullFirst
                                              : kOrderGrid;
-  if (const char* e = getenv("FKV_ATTN_ORDER")) {
-    const long v = strtol(e, nullptr, 10);
+  if (const int32_t v = tuning().attn_order; v >= 0) {
     if (v == 0 || (v == 1 && n_seqs <= kOrderMaxSeqs) || (v == 2 && n_seqs <= kOrderSortSeqs))
       order = (uint32_t)v;
   }

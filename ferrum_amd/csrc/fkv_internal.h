@@ -44,7 +44,22 @@ struct Geom {
                      // scale of 512 or more was stored (sticky; q8_wide_scale);
                      // [2] nonzero once an F16 pool stored an Inf/NaN K or V (sticky;
                      // f16_nonfinite); [3] staging word of the fault read
+  uint32_t n_cus;    // compute units of the pool's device (read once, at creation)
 };
+
+// Overrides of the launch planners for measurements, read from the environment once per
+// process (the first call that plans a launch), not per call:
+//   FKV_ATTN_SPLIT_TOKENS   decode split length (a multiple of 16)
+//   FKV_ATTN_MODE=stream    F16 decode on the persistent kernel
+//   FKV_ATTN_ORDER          decode work order (0 grid, 1 full splits first, 2 longest first)
+//   FKV_PREFILL_SPLIT_BLOCKS  prefill key-range piece length in blocks (0: no pieces)
+struct Tuning {
+  int32_t split_tokens = 0;      // 0: the planner's rule
+  bool stream_mode = false;
+  int32_t attn_order = -1;       // -1: the planner's rule
+  int64_t prefill_split = -1;    // -1: the planner's rule
+};
+const Tuning& tuning();
 
 constexpr int kDtypeF32 = 0;
 constexpr int kDtypeF16 = 1;
@@ -119,7 +134,7 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
 constexpr uint32_t kStreamMaxSeqs = 8192;
 bool stream_attention_supported(uint32_t n_seqs);
 // Waves of a full-occupancy stream launch on the current device (0: unavailable).
-uint32_t stream_attention_waves(uint32_t head_dim, uint32_t n_seqs);
+uint32_t stream_attention_waves(uint32_t head_dim, uint32_t n_seqs, uint32_t n_cus);
 hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_heads,
                                    const float* q, float* out, const int32_t* tables,
                                    uint32_t max_blocks, const int32_t* ctx_lens,

@@ -16,7 +16,8 @@ each with its own position:
 Nothing crosses to the host. The activation buffers and the GEMM workspace are allocated
 once, for the largest batch the layer was built for; the attention workspace grows when a
 call's plan needs more than it holds (the split plan depends on the batch and context, not
-monotonically).
+monotonically). The buffer it replaces is recorded on every stream that used it, so the
+caching allocator hands it out again only after the kernels queued there are done.
 """
 from __future__ import annotations
 
@@ -58,17 +59,31 @@ class DecodeAttentionLayer:
         self.attn = torch.empty_like(self.q)
         need = pool.rope_attention_workspace_bytes(n_heads, max_seqs, max_ctx_len)
         self.ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
+        self._ws_streams = {}  # stream handle -> torch stream of each call that used self.ws
         # the quantized activation rows of either GEMM (the launches are stream-ordered)
         # (the size grows with the batch: the largest is the one for max_seqs rows)
         gneed = max(gemm_q8_0_batched_workspace_bytes(n_embd, max_seqs),
                     gemm_q8_0_batched_workspace_bytes(self.q_rows, max_seqs))
         self.gws = torch.empty(max(gneed, 16), dtype=torch.uint8, device=dev)
 
-    def _workspace(self, n: int, max_ctx_len: int):
+    def _workspace(self, n: int, max_ctx_len: int, stream):
         import torch
+        if stream is None:
+            ts = torch.cuda.current_stream(self.ws.device)
+        elif isinstance(stream, int):
+            ts = torch.cuda.ExternalStream(stream, device=self.ws.device)
+        else:
+            ts = stream
         need = self.pool.rope_attention_workspace_bytes(self.n_heads, n, max_ctx_len)
         if need > self.ws.numel():
-            self.ws = torch.empty(need, dtype=torch.uint8, device=self.ws.device)
+            old = self.ws
+            self.ws = torch.empty(need, dtype=torch.uint8, device=old.device)
+            # Kernels queued on the streams that used the old buffer may still read or
+            # write it: the allocator reuses it only once they have finished.
+            for s in self._ws_streams.values():
+                old.record_stream(s)
+            self._ws_streams = {}
+        self._ws_streams[ts.cuda_stream] = ts
         return self.ws
 
     def forward(self, x, block_tables, ctx_lens, max_ctx_len: int, y, stream=None) -> None:
@@ -86,7 +101,7 @@ class DecodeAttentionLayer:
         self.pool.rope_append_decode_attention(self.layer, k, v, q, attn, block_tables, ctx_lens,
                                                max_ctx_len, self.rope_dim, self.theta,
                                                scale=self.scale,
-                                               workspace=self._workspace(n, max_ctx_len),
+                                               workspace=self._workspace(n, max_ctx_len, stream),
                                                stream=stream)
         gemm_q8_0_batched([self.wo], [self.n_embd], self.q_rows, attn, n, [y],
                           workspace=self.gws, stream=stream)

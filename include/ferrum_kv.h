@@ -60,7 +60,11 @@
 extern "C" {
 #endif
 
-#define FKV_ABI_VERSION 1
+/* Revision of this ABI. 2: fkv_paged_take_fault_flags, fkv_paged_read and
+ * fkv_paged_write take a stream; fkv_prefill_attention takes a workspace. A binding
+ * checks fkv_abi_version() against the value it was written for before any other
+ * call: C symbols carry no signature, so a library of another revision still links. */
+#define FKV_ABI_VERSION 2
 
 /* Status codes; one per FerrumError variant the path can return. */
 #define FKV_OK 0
@@ -196,7 +200,8 @@ int32_t fkv_paged_get_info(const fkv_pool* pool, fkv_paged_info* out);
  * bits of every call enqueued on `stream` before this one (and of any other work
  * already finished), then synchronises that stream only. The read and the clear
  * are one atomic exchange on the device, so a bit raised meanwhile by work on
- * another stream is reported by the next call. */
+ * another stream is reported by the next call. Calls on one pool from several
+ * threads are serialised inside (each returns the bits its own exchange took). */
 int32_t fkv_paged_take_fault_flags(fkv_pool* pool, void* stream, uint32_t* flags_out);
 /* Fill every byte of device storage with `byte` (async on stream). */
 int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream);

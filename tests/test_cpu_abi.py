@@ -36,7 +36,7 @@ def test_every_declared_entry_point_is_exported_and_bound():
 
 def test_abi_version_and_device_count():
     lib = _lib.load()
-    assert lib.fkv_abi_version() == 1
+    assert lib.fkv_abi_version() == 2 == _lib.ABI_VERSION
     assert lib.fkv_device_count() >= 0
 
 
