@@ -97,6 +97,7 @@ SIGNATURES = {
     "fkv_paged_destroy": (i32, [c_void_p]),
     "fkv_paged_get_info": (i32, [c_void_p, P(PagedInfoC)]),
     "fkv_paged_take_fault_flags": (i32, [c_void_p, c_void_p, P(u32)]),
+    "fkv_paged_marked_blocks": (i32, [c_void_p, c_void_p, P(u64)]),
     "fkv_paged_fill": (i32, [c_void_p, ctypes.c_uint8, c_void_p]),
     "fkv_paged_read": (i32, [c_void_p, u64, u64, c_void_p, c_void_p]),
     "fkv_paged_write": (i32, [c_void_p, u64, u64, c_void_p, c_void_p]),

@@ -87,6 +87,7 @@ struct fkv_pool {
   uint8_t* dev = nullptr;
   uint8_t* host = nullptr;
   uint32_t* fault = nullptr;
+  uint32_t* marks = nullptr;       // device: num_blocks + num_host_blocks block marks
   uint32_t* fault_host = nullptr;  // pinned: the fault read's copy lands here
   std::mutex fault_mu;             // one fault read at a time owns fault[3] and fault_host
   std::vector<int32_t> free_list;  // stack; LIFO reuse, as a fragmented pool would see
@@ -138,7 +139,8 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
     return fail(FKV_ERR_KERNEL, "q8_0 kv needs head_dim % 64 == 0 and block_size % 16 == 0");
   if (c.f16_rounding != FKV_ROUND_NEAREST_EVEN && c.f16_rounding != FKV_ROUND_HALF_AWAY)
     return fail(FKV_ERR_INVALID, "unknown f16 rounding mode");
-  if (c.num_blocks > 0x7fffffffull) return fail(FKV_ERR_CACHE, "kv pool size overflow");
+  if (c.num_blocks > 0x7fffffffull || c.num_host_blocks > 0x7fffffffull)
+    return fail(FKV_ERR_CACHE, "kv pool size overflow");
   const uint64_t tile = fkv::tile_bytes_for(c.kv_dtype, c.block_size, c.head_dim);
   uint64_t block = 0, total = 0, host_total = 0;
   if (mul_ovf((uint64_t)c.n_layers * 2u, (uint64_t)c.n_kv_heads, &block) ||
@@ -160,18 +162,23 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
     delete p;
     return fail(FKV_ERR_UNAVAILABLE, "no device memory for kv pool");
   }
-  // Four device words: the FKV_FAULT_* bits; the sticky mark of a Q8_0 scale of 512 or
-  // more (read by the attention kernels to pick their exact instance); the sticky mark
-  // of an Inf/NaN K or V stored in an F16 pool (read by chunked prefill to pick its
-  // leak-safe instance); the staging word of fkv_paged_take_fault_flags.
+  // Four device words: the FKV_FAULT_* bits; the number of marked device blocks; one
+  // unused; the staging word of fkv_paged_take_fault_flags. Then one mark per device
+  // block and per host block (a Q8_0 scale of 512 or more, or an Inf/NaN K or V of an
+  // F16 pool, stored in the block: the attention kernels read them to pick the exact or
+  // leak-safe instance for the workgroups that read such a block).
   e = hipMalloc((void**)&p->fault, 4 * sizeof(uint32_t));
   if (e == hipSuccess) e = hipMemset(p->fault, 0, 4 * sizeof(uint32_t));
+  const uint64_t n_marks = c.num_blocks + c.num_host_blocks;
+  if (e == hipSuccess) e = hipMalloc((void**)&p->marks, n_marks * sizeof(uint32_t));
+  if (e == hipSuccess) e = hipMemset(p->marks, 0, n_marks * sizeof(uint32_t));
   if (e == hipSuccess)
     e = hipHostMalloc((void**)&p->fault_host, 64, hipHostMallocDefault);
   if (e == hipSuccess && host_total) e = hipHostMalloc((void**)&p->host, host_total, hipHostMallocDefault);
   if (e != hipSuccess) {
     (void)hipFree(p->dev);
     if (p->fault) (void)hipFree(p->fault);
+    if (p->marks) (void)hipFree(p->marks);
     if (p->fault_host) (void)hipHostFree(p->fault_host);
     delete p;
     return hip_fail(e, "pool allocation");
@@ -187,6 +194,8 @@ int32_t fkv_paged_create(const fkv_paged_config* config, fkv_pool** out) {
   p->geom.dtype = c.kv_dtype;
   p->geom.rounding = c.f16_rounding;
   p->geom.fault = p->fault;
+  p->geom.bmark = p->marks;
+  p->geom.hmark = p->marks + c.num_blocks;
   int cus = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c.device) != hipSuccess)
     cus = 0;
@@ -207,6 +216,7 @@ int32_t fkv_paged_destroy(fkv_pool* pool) {
   (void)hipDeviceSynchronize();
   if (pool->dev) (void)hipFree(pool->dev);
   if (pool->fault) (void)hipFree(pool->fault);
+  if (pool->marks) (void)hipFree(pool->marks);
   if (pool->fault_host) (void)hipHostFree(pool->fault_host);
   if (pool->host) (void)hipHostFree(pool->host);
   delete pool;
@@ -240,23 +250,37 @@ int32_t fkv_paged_take_fault_flags(fkv_pool* pool, void* stream, uint32_t* flags
   return ok();
 }
 
+int32_t fkv_paged_marked_blocks(fkv_pool* pool, void* stream, uint64_t* count_out) {
+  if (!pool || !count_out) return fail(FKV_ERR_INVALID, "null argument");
+  std::lock_guard<std::mutex> lock(pool->fault_mu);  // shares the pinned word
+  DeviceGuard dg(pool->cfg.device);
+  const hipStream_t s = (hipStream_t)stream;
+  FKV_HIP(hipMemcpyAsync(pool->fault_host, pool->fault + 1, sizeof(uint32_t),
+                         hipMemcpyDeviceToHost, s),
+          "read block marks");
+  FKV_HIP(hipStreamSynchronize(s), "synchronize");
+  *count_out = *(volatile uint32_t*)pool->fault_host;
+  return ok();
+}
+
+// Whether a value of the pool's dtype whose every byte is `byte` is one that marks its
+// block: a Q8_0 scale (byte << 8 | byte) of 512 or more (exponent bits 14 and 13), an F16
+// K or V value that is Inf or NaN (exponent bits 14 to 10).
+static uint32_t fill_marks(const fkv_pool* pool, uint8_t byte) {
+  if (pool->cfg.kv_dtype == FKV_DTYPE_Q8_0) return (byte & 0x60u) == 0x60u ? 1u : 0u;
+  if (pool->cfg.kv_dtype == FKV_DTYPE_F16) return (byte & 0x7cu) == 0x7cu ? 1u : 0u;
+  return 0u;
+}
+
 int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream) {
   if (!pool) return fail(FKV_ERR_INVALID, "null argument");
   DeviceGuard dg(pool->cfg.device);
   FKV_HIP(fkv::launch_fill(pool->dev, byte, pool->geom.block_bytes * pool->geom.num_blocks,
                            (hipStream_t)stream),
           "fill");
-  if (pool->cfg.kv_dtype == FKV_DTYPE_Q8_0) {
-    // Every scale is now (byte << 8 | byte): the pool holds a scale of 512 or more
-    // exactly when that does (exponent bits 14 and 13 set), whatever it held before.
-    const uint8_t wide = (byte & 0x60u) == 0x60u ? 1 : 0;
-    FKV_HIP(fkv::launch_fill(pool->fault + 1, wide, sizeof(uint32_t), (hipStream_t)stream), "fill");
-  } else if (pool->cfg.kv_dtype == FKV_DTYPE_F16) {
-    // Every K and V value is now (byte << 8 | byte): Inf/NaN exactly when its exponent bits are.
-    const uint8_t nonfinite = (byte & 0x7cu) == 0x7cu ? 1 : 0;
-    FKV_HIP(fkv::launch_fill(pool->fault + 2, nonfinite, sizeof(uint32_t), (hipStream_t)stream),
-            "fill");
-  }
+  // Every device block now holds the same bytes, so every mark follows the fill byte,
+  // whatever the block held before. Host blocks keep theirs (swap_in brings them back).
+  FKV_HIP(fkv::launch_marks_fill(pool->geom, fill_marks(pool, byte), (hipStream_t)stream), "fill");
   return ok();
 }
 
@@ -316,13 +340,31 @@ int32_t fkv_paged_write(fkv_pool* pool, uint64_t offset, uint64_t bytes, const v
   if (bytes)
     FKV_HIP(hipMemcpyAsync(pool->dev + offset, host_src, bytes, hipMemcpyHostToDevice, s),
             "pool write");
+  // Marks of the blocks the range touches: set where the written bytes hold a marking
+  // value, cleared where they overwrite a whole block without one, kept otherwise.
   const uint8_t* img = (const uint8_t*)host_src;
-  const int word = pool->cfg.kv_dtype == FKV_DTYPE_Q8_0 &&
-                           q8_image_has_wide_scale(pool, offset, bytes, img) ? 1
-                   : pool->cfg.kv_dtype == FKV_DTYPE_F16 &&
-                           f16_image_has_nonfinite_kv(pool, offset, bytes, img) ? 2
-                                                                                : 0;
-  if (word) FKV_HIP(fkv::launch_fill(pool->fault + word, 1, sizeof(uint32_t), s), "pool write");
+  uint8_t* ops_dev = nullptr;
+  std::vector<uint8_t> ops;
+  const uint64_t bb = pool->geom.block_bytes;
+  const bool marking = pool->cfg.kv_dtype == FKV_DTYPE_Q8_0 || pool->cfg.kv_dtype == FKV_DTYPE_F16;
+  if (bytes && marking) {
+    const uint64_t b0 = offset / bb, b1 = (offset + bytes - 1) / bb + 1;
+    ops.assign(b1 - b0, 0);
+    for (uint64_t b = b0; b < b1; b++) {
+      const uint64_t lo = std::max(offset, b * bb), hi = std::min(offset + bytes, (b + 1) * bb);
+      const uint8_t* src = img + (lo - offset);
+      const bool has = pool->cfg.kv_dtype == FKV_DTYPE_Q8_0
+                           ? q8_image_has_wide_scale(pool, lo, hi - lo, src)
+                           : f16_image_has_nonfinite_kv(pool, lo, hi - lo, src);
+      ops[b - b0] = has ? 1 : (lo == b * bb && hi == (b + 1) * bb ? 2 : 0);
+    }
+    FKV_HIP(hipMalloc((void**)&ops_dev, ops.size()), "pool write");
+    hipError_t e = hipMemcpyAsync(ops_dev, ops.data(), ops.size(), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = fkv::launch_marks_apply(pool->geom, b0, ops.size(), ops_dev, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(ops_dev);
+    if (e != hipSuccess) return hip_fail(e, "pool write");
+  }
   FKV_HIP(hipStreamSynchronize(s), "synchronize");
   return ok();
 }
@@ -466,6 +508,22 @@ static int32_t swap(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void
   }
   DeviceGuard dg(pool->cfg.device);
   const uint64_t bb = pool->geom.block_bytes;
+  // The blocks' marks travel with their bytes: swap_out copies them to the host blocks'
+  // before the bytes leave, swap_in back after the bytes arrive (stream order).
+  auto move_marks = [&]() -> hipError_t {
+    fkv::MarkPairs mp{};
+    for (uint32_t i = 0; i < n_pairs; i++) {
+      mp.dev[mp.n] = (int32_t)(out ? pairs[2 * i] : pairs[2 * i + 1]);
+      mp.host[mp.n] = (int32_t)(out ? pairs[2 * i + 1] : pairs[2 * i]);
+      if (++mp.n == fkv::kMarkPairs || i + 1 == n_pairs) {
+        const hipError_t e = fkv::launch_marks_swap(pool->geom, mp, out, (hipStream_t)stream);
+        if (e != hipSuccess) return e;
+        mp.n = 0;
+      }
+    }
+    return hipSuccess;
+  };
+  if (out) FKV_HIP(move_marks(), "swap_out");
   // Merge runs that are consecutive on both sides into one copy each.
   uint32_t i = 0;
   while (i < n_pairs) {
@@ -487,6 +545,7 @@ static int32_t swap(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void
     }
     i = j;
   }
+  if (!out) FKV_HIP(move_marks(), "swap_in");
   return ok();
 }
 

@@ -908,7 +908,7 @@ struct OrderedItem {
   int32_t seq;    // < 0: past the list
   int32_t split;
   int32_t ctx;    // ctx_lens[seq] as read (unclamped)
-  int32_t wide;   // *wide_word as thread 0 read it (0 without one)
+  int32_t marks;  // *marks_word as thread 0 read it (0 without one)
 };
 
 // Unit u of the longest-first list. Every thread of the workgroup calls this with
@@ -916,7 +916,7 @@ struct OrderedItem {
 __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_lens,
                                     uint32_t n_seqs, int32_t cap, int32_t split_tokens,
                                     uint32_t order, int32_t* s_scan, int32_t* s_key,
-                                    int32_t* s_res, const uint32_t* wide_word) {
+                                    int32_t* s_res, const uint32_t* marks_word) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int K = (int)((n_seqs + 255u) / 256u);  // <= 4
   int32_t raw[4], full[4], part[4];
@@ -956,7 +956,7 @@ __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_
   }
   if (tid == 0) {
     s_res[0] = -1;
-    s_res[3] = wide_word ? (int32_t)__atomic_load_n(wide_word, __ATOMIC_RELAXED) : 0;
+    s_res[3] = marks_word ? (int32_t)__atomic_load_n(marks_word, __ATOMIC_RELAXED) : 0;
   }
   __syncthreads();
   int32_t fpre = fin - fsum, ppre = pin - psum, F = 0, P = 0;
@@ -1017,13 +1017,15 @@ __device__ OrderedItem ordered_item(uint32_t u, const int32_t* __restrict__ ctx_
 #define FKV_MFMA_WAVES_PER_EU 3
 #endif
 
-// EXACT (Q8_0 only): the instance for pools holding scales of 512 or more. Every Q8_0
-// call launches the fast instance and then this one over the same grid; each
-// workgroup of both reads the pool's sticky word once. The fast instance computes
-// when it is clear (a workgroup whose appended token has such a scale sets it), the
-// exact one when it is set, redoing every output and partial without binary16
-// dequantised operands (qk_block_q8x, pv_block_q8x). Its own register allocation
-// keeps the fast instance's at three waves per SIMD.
+// EXACT (Q8_0 only): the instance for blocks holding scales of 512 or more. Every Q8_0
+// call launches the fast instance and then this one over the same grid. Each workgroup
+// of both reads the pool's count of marked blocks once; while it is 0 the fast one
+// computes and the exact one leaves at once. Otherwise each ORs the marks of the blocks
+// its split reads: the fast instance computes an unmarked split, the exact one a marked
+// split, without binary16 dequantised operands (qk_block_q8x, pv_block_q8x). A fast
+// workgroup whose appended token has such a scale marks that token's block, and the
+// exact instance's workgroup for the same split then recomputes its outputs. Its own
+// register allocation keeps the fast instance's at three waves per SIMD.
 template <int DT, int D, int NBUF, bool ROPE, bool EXACT>
 __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_mfma_kernel(
@@ -1042,23 +1044,23 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
   __shared__ uint8_t s_appq[2][D];                 // fused Q8_0 append: quants
   __shared__ uint16_t s_apps[2][D / 32];           // and scales
   __shared__ int32_t s_ord[2 * kAttnWaves + 4 + kOrderSortSeqs];  // work order: scans, item, keys
-  __shared__ uint32_t s_wide;  // the pool's sticky word as this workgroup read it
+  __shared__ uint32_t s_marks;  // the pool's count of marked blocks as this workgroup read it
 
   // the work list and the split clamp share this bound, so the list never holds more
   // items than the grid has workgroups
   const int32_t cap = dev::split_ctx_cap(max_blocks, B, max_splits, (uint32_t)split_tokens);
-  // The exact instance has work only over a pool marked wide; the word cannot change
-  // during its launch (only fast instances set it), so each wave reads it alone.
+  // The exact instance has work only where a block is marked; the count cannot change
+  // during its launch (only fast instances mark blocks), so each wave reads it alone.
   if constexpr (EXACT) {
-    if (!pool_has_wide_scales(g.fault)) return;
+    if (!pool_has_marks(g)) return;
   }
   const uint32_t kvh = blockIdx.x % g.n_kv_heads;
   uint32_t seq;
   int32_t split, ctx = 0;
-  // Fast Q8_0 instance: whether the pool has held a scale of 512 or more, read once
-  // per workgroup (a fast workgroup appending such a token sets the word during the
-  // launch, and the waves of one workgroup must agree before the merge barrier).
-  bool pool_wide = false;
+  // Q8_0: whether any block of the pool is marked, read once per workgroup (a fast
+  // workgroup appending a wide token marks a block during the launch, and the waves of
+  // one workgroup must agree before the barrier of blocks_marked).
+  bool any_marks = EXACT;
   if (order != kOrderGrid) {
     const OrderedItem it = ordered_item(
         blockIdx.x / g.n_kv_heads, ctx_lens, n_seqs, cap, split_tokens, order, s_ord,
@@ -1068,7 +1070,7 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
     seq = (uint32_t)it.seq;
     split = it.split;
     ctx = it.ctx;
-    pool_wide = it.wide != 0;
+    if constexpr (!EXACT) any_marks = it.marks != 0;
   } else {
     const uint32_t segs = n_seqs * g.n_kv_heads;
     seq = (blockIdx.x % segs) / g.n_kv_heads;
@@ -1099,9 +1101,9 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
   load_tab(0);
   if constexpr (DT == kDtypeQ8 && !EXACT) {
     if (order == kOrderGrid) {  // no ordering pass to carry the word: one barrier
-      if (threadIdx.x == 0) s_wide = __atomic_load_n(g.fault + 1, __ATOMIC_RELAXED);
+      if (threadIdx.x == 0) s_marks = __atomic_load_n(g.fault + 1, __ATOMIC_RELAXED);
       __syncthreads();
-      pool_wide = s_wide != 0;
+      any_marks = s_marks != 0;
     }
   }
 
@@ -1115,6 +1117,15 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
   if (split >= nsplits) return;
   const int32_t s1 = ctx - s0 < split_tokens ? ctx : s0 + split_tokens;
   const int32_t nblk = s1 > s0 ? (s1 - s0 + B - 1) / B : 0;
+  // Q8_0 with marked blocks in the pool: the split's own marks pick the instance (the
+  // fast one then only stores the appended token of a marked split).
+  bool split_marked = false;
+  if constexpr (DT == kDtypeQ8) {
+    if (any_marks) split_marked = blocks_marked(g, table, blk0, blk0 + nblk);
+    if constexpr (EXACT) {
+      if (!split_marked) return;
+    }
+  }
 
   // RoPE at the new token's position ctx - 1: the lane holds (sin, cos) of pair
   // rope_pair(lane), pos / den[p] as the reference computes it (f32 division, then
@@ -1187,30 +1198,30 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
           if ((ksc & 0x7c00u) == 0x7c00u || (vsc & 0x7c00u) == 0x7c00u)
             raise_fault(g.fault, kFaultRange);
         }
-        // A scale of 512 or more marks the pool (q8_wide_scale): the exact instance,
-        // launched after this one, then computes every output of the call.
+        // A scale of 512 or more marks the token's block (q8_wide_scale): the exact
+        // instance, launched after this one, then recomputes this split's outputs.
         if (__builtin_amdgcn_ballot_w64(q8_wide_scale(ksc) || q8_wide_scale(vsc)) != 0 &&
             ln.lane == 0)
-          mark_wide(g.fault);
+          mark_table_block(g, table, app_pos / B);
       } else {
         const uint32_t ke = encode_f16(kv, g.rounding);
         s_app[0][dd] = (uint16_t)ke;
         const uint32_t ve = encode_f16(vv, g.rounding);
         s_app[1][dd] = (uint16_t)ve;
-        // an Inf/NaN K or V marks the pool (chunked prefill's leak-safe instance)
+        // an Inf/NaN K or V marks the token's block (chunked prefill's leak-safe instance)
         if (__builtin_amdgcn_ballot_w64(f16_nonfinite(ke) || f16_nonfinite(ve)) != 0 &&
             ln.lane == 0)
-          mark_nonfinite_kv(g.fault);
+          mark_table_block(g, table, app_pos / B);
       }
     }
   };
   if constexpr (!ROPE) {
     if (app_wave) encode_app();
   }
-  // Q8_0 fast instance over a pool marked wide: the exact instance computes this
+  // Q8_0 fast instance over a marked split: the exact instance computes this
   // workgroup's outputs; only the appended token is stored here.
   bool store_only = false;
-  if constexpr (DT == kDtypeQ8 && !EXACT) store_only = pool_wide;
+  if constexpr (DT == kDtypeQ8 && !EXACT) store_only = split_marked;
 
   Accum<D> st;
   st.reset();
@@ -1350,7 +1361,7 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
       if (p >= 0 && (uint64_t)p < g.num_blocks) store_q8_token(0);
       else if (ln.lane == 0) raise_fault(g.fault, kFaultBlock);
     }
-    return;  // the whole workgroup (pool_wide is the same in all its waves)
+    return;  // the whole workgroup (split_marked is the same in all its waves)
   } else {
     for (int t = 0; t < nt; t += NBUF) {
 #pragma unroll
@@ -1578,21 +1589,21 @@ __device__ __forceinline__ bool v_nonfinite_in(const u32x2_t (&vr)[D / 16], cons
 // Storage: F16 tiles are staged as loaded except V, whose 16-byte units are
 // XOR-swizzled by row so the P.V operand reads hit distinct banks. Q8_0 tiles are
 // staged as loaded (their operand order reads conflict-free) and converted by the
-// decode kernel's BlockRegs; over a pool marked as holding scales of 512 or more
-// (the sticky word), the fast instance exits and the EXACT instance, launched after
-// it, computes with qk_block_q8x / pv_block_q8x.
+// decode kernel's BlockRegs; for a workgroup whose blocks include one marked as
+// holding a scale of 512 or more (mark_block), the fast instance exits and the EXACT
+// instance, launched after it, computes with qk_block_q8x / pv_block_q8x.
 //
 // Tokens past a column's causal end carry weight 0 in the P.V product, but an
-// Inf/NaN V there would still reach the column through 0 * NaN. F16 pools that have
-// stored a non-finite K or V carry a sticky mark (pool_has_nonfinite_kv) and run the
+// Inf/NaN V there would still reach the column through 0 * NaN. F16 blocks that hold a
+// non-finite K or V are marked (mark_block), and workgroups that read one run the
 // leak-safe instance: on a block that crosses the tile's nearest causal end, a
 // wave-uniform check for non-finite V values past that end sends the block down a
 // masked path, one P.V per query token of the tile with P restricted to that token's
 // columns and V zeroed from its end, so no column reads a position past its own (as
 // the reference's token loop never does). Q8_0 V values are finite unless a scale
-// is, and a pool holding an inf or NaN scale is marked wide, so the fast Q8_0
-// instance needs no check; the exact one masks P x scale per lane at the lane's own
-// column end.
+// is, and a block holding an inf or NaN scale is marked like a wide one, so the fast
+// Q8_0 instance needs no check; the exact one masks P x scale per lane at the lane's
+// own column end.
 template <int DT, int D>
 constexpr int prefill_tile_bytes() {
   return DT == kDtypeF16 ? B * D * 2 : B * D + B * D / 32 * 2;
@@ -1691,16 +1702,11 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   __shared__ __align__(16) uint8_t s_kv1[kStep][kBlk];
   constexpr bool EXACT = MODE == kPfExact;
 
-  if constexpr (DT == kDtypeQ8) {
-    // The word cannot change during a prefill launch (only appends set it), so every
-    // wave reads the same value and the workgroup leaves as a whole.
-    if (pool_has_wide_scales(g.fault) != EXACT) return;
-  }
-  if constexpr (DT == kDtypeF16) {
-    // Likewise the pool's mark of a stored Inf/NaN K or V (appends, fill and write set
-    // it): without one the fast instance computes, with one the leak-safe instance.
-    if (pool_has_nonfinite_kv(g.fault) != (MODE == kPfLeakSafe)) return;
-  }
+  // The pool's count of marked blocks cannot change during a prefill launch (only
+  // appends mark blocks), so every wave reads the same value. While it is 0 the fast
+  // instance computes everything; otherwise each workgroup's own blocks decide below.
+  const bool any_marks = pool_has_marks(g);
+  if (MODE != kPfFast && !any_marks) return;
   // Which sequence this workgroup takes: its grid column's, moved on by a quarter of
   // the batch per step of q(y) = (y + y / 8) % 4. The hardware deals workgroups
   // w = x + gridDim.x * y to the 8 XCDs and their 4 shader engines in rotation, so
@@ -1754,6 +1760,12 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   };
 
   const int32_t* table = tables + (uint64_t)seq * max_blocks;
+  // With marked blocks in the pool, the marks of the piece's blocks pick the instance:
+  // the exact (Q8_0: a scale of 512 or more) or leak-safe (F16: an Inf/NaN K or V) one
+  // for a marked piece, the fast one otherwise.
+  if (any_marks) {
+    if (blocks_marked(g, table, jbeg, jend) != (MODE != kPfFast)) return;
+  }
   // A table entry outside the pool raises the fault flag, stages block 0 and is
   // skipped. Blocks are staged by direct loads into LDS (dma_block_at below).
   const uint8_t* kbase = tile_ptr(g, 0, layer, 0, kvh);
@@ -2250,9 +2262,9 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
                                                         max_blocks, ctx_lens, q_lens,         \
                                                         q_offsets, max_q_len, scale,          \
                                                         split_blocks, max_splits, ws_o, ws_ml)
-  // The fast instance, then the one for pools whose marks say the fast one cannot
-  // compute them: Q8_0 the exact instance (a scale of 512 or more was stored), F16 the
-  // leak-safe one (an Inf/NaN K or V was stored). Each exits at once where the other works.
+  // The fast instance, then the one for workgroups whose blocks' marks say the fast one
+  // cannot compute them: Q8_0 the exact instance (a scale of 512 or more was stored),
+  // F16 the leak-safe one (an Inf/NaN K or V was stored). Each exits where the other works.
   const int dt = g.dtype == kDtypeQ8 ? kDtypeQ8 : kDtypeF16;
   if (dt == kDtypeQ8) {
     if (g.head_dim == 128) FKV_LAUNCH_PF(kDtypeQ8, 128, kPfFast);
@@ -2315,7 +2327,7 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
       g, layer, n_heads, G, q, out, tables, max_blocks, ctx_lens, n_seqs, max_splits, st, order, \
       scale, ws_o, ws_ml, k_new, v_new, rt)
   // Q8_0: the fast instance, then the exact one (each workgroup of which exits at once
-  // unless the pool's sticky word says it holds a scale of 512 or more).
+  // unless its split reads a block marked as holding a scale of 512 or more).
   if (g.dtype == kDtypeQ8 && roped) {
     if (g.head_dim == 128) FKV_LAUNCH_MFMA(kDtypeQ8, 128, true, false);
     else FKV_LAUNCH_MFMA(kDtypeQ8, 64, true, false);

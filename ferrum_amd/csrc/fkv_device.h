@@ -34,31 +34,50 @@ __device__ __forceinline__ void raise_fault(uint32_t* f, uint32_t bit) {
 
 // Q8_0 scales of 512 or more (binary16 exponent bits 14 and 13 set: 512 <= |s|,
 // inf, NaN): scale x quant of such a block can pass 65504, the binary16 range of the
-// fast attention operands. The pool's second fault word records, sticky, that one was
-// stored; attention over such a pool takes its exact loop.
+// fast attention operands.
 __device__ __forceinline__ bool q8_wide_scale(uint32_t bits) { return (bits & 0x6000u) == 0x6000u; }
-__device__ __forceinline__ void mark_wide(uint32_t* fault) {
-  if (__atomic_load_n(fault + 1, __ATOMIC_RELAXED) == 0u) atomicOr(fault + 1, 1u);
-}
-__device__ __forceinline__ bool pool_has_wide_scales(const uint32_t* fault) {
-  return __builtin_amdgcn_readfirstlane(__atomic_load_n(fault + 1, __ATOMIC_RELAXED)) != 0;
-}
-
-// F16 pools: the third fault word records, sticky, that an Inf or NaN K or V value
-// was stored (append, fused step, fill, write). Chunked prefill over such a pool takes
-// its leak-safe instance, which keeps such V values from queries whose causal end lies
-// before them and repairs the scores an infinite K gives (inf x 0 in the q lo part);
-// without one, the fast instance does neither.
+// F16 values the fast chunked-prefill instance cannot take: it lets 0 x NaN reach
+// queries whose causal end lies before such a V, and scores an infinite K against q's
+// lo part (inf x 0).
 __device__ __forceinline__ bool f16_nonfinite(uint32_t bits) { return (bits & 0x7c00u) == 0x7c00u; }
 // either binary16 of a packed pair
 __device__ __forceinline__ bool f16x2_nonfinite(uint32_t w) {
   return f16_nonfinite(w & 0xffffu) || f16_nonfinite(w >> 16);
 }
-__device__ __forceinline__ void mark_nonfinite_kv(uint32_t* fault) {
-  if (__atomic_load_n(fault + 2, __ATOMIC_RELAXED) == 0u) atomicOr(fault + 2, 1u);
+
+// Block marks. A store of such a value (Q8_0: a wide scale; F16: an Inf/NaN K or V)
+// marks its block; the pool's second fault word counts the marked blocks. A mark
+// stays with the block's bytes: copy_blocks copies it, swap carries it through the
+// host block's mark, fill and whole-block writes replace it; nothing else clears it.
+// Attention launches a fast instance and the exact (Q8_0) or leak-safe (F16) one
+// after it. While no block is marked (the count is 0) the fast instance computes
+// everything and the other leaves at once; otherwise every workgroup of both ORs the
+// marks of the blocks it reads, and the instance that can take them computes.
+__device__ __forceinline__ void mark_block(const Geom& g, uint64_t block) {
+  uint32_t* m = g.bmark + block;
+  if (__atomic_load_n(m, __ATOMIC_RELAXED) == 0u && atomicExch(m, 1u) == 0u)
+    atomicAdd(g.fault + 1, 1u);
 }
-__device__ __forceinline__ bool pool_has_nonfinite_kv(const uint32_t* fault) {
-  return __builtin_amdgcn_readfirstlane(__atomic_load_n(fault + 2, __ATOMIC_RELAXED)) != 0;
+// Marks the block of table entry j (the caller has checked j against the table row;
+// an entry outside the pool marks nothing: the kernels fault it).
+__device__ __forceinline__ void mark_table_block(const Geom& g, const int32_t* table, int32_t j) {
+  const int32_t p = table[j];
+  if (p >= 0 && (uint64_t)p < g.num_blocks) mark_block(g, (uint64_t)p);
+}
+__device__ __forceinline__ bool pool_has_marks(const Geom& g) {
+  return __builtin_amdgcn_readfirstlane(__atomic_load_n(g.fault + 1, __ATOMIC_RELAXED)) != 0;
+}
+// Whether any block of table entries [j0, j1) is marked (entries outside the pool are
+// skipped: the kernels fault them). Every thread of the workgroup calls it and gets
+// the same answer.
+__device__ __forceinline__ bool blocks_marked(const Geom& g, const int32_t* __restrict__ table,
+                                              int32_t j0, int32_t j1) {
+  uint32_t m = 0;
+  for (int32_t j = j0 + (int32_t)threadIdx.x; j < j1; j += (int32_t)blockDim.x) {
+    const int32_t p = table[j];
+    if (p >= 0 && (uint64_t)p < g.num_blocks) m |= g.bmark[p];
+  }
+  return __syncthreads_or(m != 0u) != 0;
 }
 
 // 16-byte load of K/V bytes that are read once per launch: the nontemporal hint

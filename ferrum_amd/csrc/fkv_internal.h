@@ -40,10 +40,12 @@ struct Geom {
   uint32_t block_size;
   int32_t dtype;     // 0 f32, 1 f16, 8 q8_0
   int32_t rounding;  // 0 nearest-even, 1 ties away
-  uint32_t* fault;   // device words: [0] FKV_FAULT_* bits; [1] nonzero once a Q8_0
-                     // scale of 512 or more was stored (sticky; q8_wide_scale);
-                     // [2] nonzero once an F16 pool stored an Inf/NaN K or V (sticky;
-                     // f16_nonfinite); [3] staging word of the fault read
+  uint32_t* fault;   // device words: [0] FKV_FAULT_* bits; [1] number of marked
+                     // blocks (bmark); [2] unused; [3] staging word of the fault read
+  uint32_t* bmark;   // per device block: 1 when a value the fast attention instances
+                     // cannot take was stored in it (Q8_0: a scale of 512 or more,
+                     // q8_wide_scale; F16: an Inf/NaN K or V, f16_nonfinite), else 0
+  uint32_t* hmark;   // per pinned host block: the mark its bytes carry
   uint32_t n_cus;    // compute units of the pool's device (read once, at creation)
 };
 
@@ -110,6 +112,20 @@ hipError_t launch_gather_tables(const Geom& g, uint32_t layer, const int32_t* ta
 hipError_t launch_copy_blocks(const Geom& g, const int64_t* pairs, uint32_t n_pairs,
                               hipStream_t s);
 hipError_t launch_fill(void* dst, uint8_t byte, uint64_t bytes, hipStream_t s);
+// Block marks (Geom::bmark). fill: every device block's mark = `mark`, the count with it.
+hipError_t launch_marks_fill(const Geom& g, uint32_t mark, hipStream_t s);
+// Up to kMarkPairs (device block, host block) pairs per launch: swap_out copies the device
+// blocks' marks to the host blocks', swap_in the other way (keeping the count).
+constexpr uint32_t kMarkPairs = 240;
+struct MarkPairs {
+  int32_t dev[kMarkPairs];
+  int32_t host[kMarkPairs];
+  uint32_t n;
+};
+hipError_t launch_marks_swap(const Geom& g, const MarkPairs& p, bool out, hipStream_t s);
+// ops[i] for device block first + i: 0 keeps the mark, 1 sets it, 2 clears it.
+hipError_t launch_marks_apply(const Geom& g, uint64_t first, uint64_t n, const uint8_t* ops,
+                              hipStream_t s);
 // fault[3] = fault[0], fault[0] = 0, atomically (fkv_paged_take_fault_flags).
 hipError_t launch_take_fault(uint32_t* fault, hipStream_t s);
 hipError_t launch_device_copy(void* dst, const void* src, uint64_t bytes, hipStream_t s);

@@ -112,7 +112,7 @@ __global__ void __launch_bounds__(256) append_f16_kernel(Geom g, uint32_t layer,
     *(uint4*)(tile + ((uint64_t)c * Bs + (uint64_t)slot % Bs) * 16u) = w;
     if (f16x2_nonfinite(w.x) || f16x2_nonfinite(w.y) || f16x2_nonfinite(w.z) ||
         f16x2_nonfinite(w.w))
-      mark_nonfinite_kv(g.fault);  // chunked prefill then takes its leak-safe instance
+      mark_block(g, (uint64_t)slot / Bs);  // chunked prefill's leak-safe instance reads it
     return;
   }
   const uint32_t dgs = D / 16;  // 16-dim groups per head
@@ -140,7 +140,7 @@ __global__ void __launch_bounds__(256) append_f16_kernel(Geom g, uint32_t layer,
   vt[2 * Bs] = (uint16_t)e2;
   vt[3 * Bs] = (uint16_t)e3;
   if (f16_nonfinite(e0) || f16_nonfinite(e1) || f16_nonfinite(e2) || f16_nonfinite(e3))
-    mark_nonfinite_kv(g.fault);  // chunked prefill then takes its leak-safe instance
+    mark_block(g, (uint64_t)slot / Bs);  // chunked prefill's leak-safe instance reads it
 }
 
 // F16 storage, block_size 16, head_dim 64 or 128, 16-byte aligned k/v: one workgroup
@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(256) append_f16_tile_kernel(Geom g, uint32_t l
               f16x2_nonfinite(kw.w);
 #pragma unroll
     for (int e = 0; e < 8; e++) nf = nf || f16_nonfinite(ve[e]);
-    if (nf) mark_nonfinite_kv(g.fault);  // chunked prefill then takes its leak-safe instance
+    if (nf) mark_block(g, (uint64_t)slot / 16u);  // chunked prefill's leak-safe instance reads it
   }
 #pragma unroll
   for (int e = 0; e < 8; e++) s_v[hl][c * 8u + e][o] = (uint16_t)ve[e];
@@ -279,7 +279,7 @@ __global__ void __launch_bounds__(256) append_scalar_kernel(Geom g, uint32_t lay
       const uint32_t e = encode_f16(x, g.rounding);
       ((uint16_t*)tile)[kv ? (uint64_t)d * g.block_size + off
                            : ((uint64_t)(d / 8) * g.block_size + off) * 8 + d % 8] = (uint16_t)e;
-      if (f16_nonfinite(e)) mark_nonfinite_kv(g.fault);
+      if (f16_nonfinite(e)) mark_block(g, (uint64_t)slot / g.block_size);
     } else
       ((float*)tile)[off * D + d] = x;
   }
@@ -335,11 +335,11 @@ __global__ void __launch_bounds__(256) append_q8_kernel(Geom g, uint32_t layer,
         tile[q8_quant_offset(1, off, c * 32u + j, D)] = (uint8_t)(q[j / 4] >> (8 * (j % 4)));
     }
     ((uint16_t*)(tile + (uint64_t)B * D))[off * cpr + c] = (uint16_t)sc;
-    // A scale of 512 or more sends later attention over the pool to its exact loop;
-    // one past the binary16 range (|x| >= 65520 * 127) is stored as +-inf, as the
-    // reference's encoder stores it, and flagged.
+    // A scale of 512 or more marks the block (attention over it takes the exact
+    // instance); one past the binary16 range (|x| >= 65520 * 127) is stored as +-inf,
+    // as the reference's encoder stores it, and flagged.
     if (q8_wide_scale(sc)) {
-      mark_wide(g.fault);
+      mark_block(g, (uint64_t)slot / B);
       if ((sc & 0x7c00u) == 0x7c00u) raise_fault(g.fault, kFaultRange);
     }
   }
@@ -400,11 +400,11 @@ __global__ void __launch_bounds__(256) append_q8_tile_kernel(Geom g, uint32_t la
         x[4 * j] = t.x; x[4 * j + 1] = t.y; x[4 * j + 2] = t.z; x[4 * j + 3] = t.w;
       }
       sc[b] = q8_quantize(x, g.rounding, q[b]);
-      // A scale of 512 or more sends later attention over the pool to its exact loop;
-      // one past the binary16 range is stored as +-inf, as the reference's encoder
-      // stores it, and flagged.
+      // A scale of 512 or more marks the block (attention over it takes the exact
+      // instance); one past the binary16 range is stored as +-inf, as the reference's
+      // encoder stores it, and flagged.
       if (q8_wide_scale(sc[b])) {
-        mark_wide(g.fault);
+        mark_block(g, (uint64_t)slot / B);
         if ((sc[b] & 0x7c00u) == 0x7c00u) raise_fault(g.fault, kFaultRange);
       }
     }
@@ -620,6 +620,11 @@ __global__ void __launch_bounds__(256) copy_blocks_kernel(Geom g, const int64_t*
       if (ch == 0 && threadIdx.x == 0) raise_fault(g.fault, kFaultBlock);
       continue;
     }
+    if (ch == 0 && threadIdx.x == 0) {  // the block's mark goes with its bytes
+      const uint32_t m = g.bmark[src] ? 1u : 0u;
+      const uint32_t old = atomicExch(g.bmark + dst, m);
+      if (m != (old ? 1u : 0u)) atomicAdd(g.fault + 1, m ? 1u : 0xffffffffu);
+    }
     const u32x4* s = (const u32x4*)(g.base + (uint64_t)src * g.block_bytes);
     u32x4* d = (u32x4*)(g.base + (uint64_t)dst * g.block_bytes);
     uint64_t i0 = ch * kCopyChunkVecs + threadIdx.x;
@@ -634,6 +639,39 @@ __global__ void __launch_bounds__(256) copy_blocks_kernel(Geom g, const int64_t*
       uint64_t i = i0 + j * 256u;
       if (i < vecs) __builtin_nontemporal_store(r[j], d + i);
     }
+  }
+}
+
+// Every device block's mark = m, and the count of marked blocks with it.
+__global__ void __launch_bounds__(256) marks_fill_kernel(Geom g, uint32_t m) {
+  for (uint64_t b = (uint64_t)blockIdx.x * 256u + threadIdx.x; b < g.num_blocks;
+       b += (uint64_t)gridDim.x * 256u)
+    g.bmark[b] = m;
+  if (blockIdx.x == 0 && threadIdx.x == 0) g.fault[1] = m ? (uint32_t)g.num_blocks : 0u;
+}
+
+// swap_out (out): host block p.host[i] takes device block p.dev[i]'s mark; swap_in: the
+// reverse, keeping the count of marked device blocks.
+__global__ void __launch_bounds__(256) marks_swap_kernel(Geom g, MarkPairs p, bool out) {
+  const uint32_t i = threadIdx.x;
+  if (i >= p.n) return;
+  if (out) {
+    g.hmark[p.host[i]] = g.bmark[p.dev[i]] ? 1u : 0u;
+  } else {
+    const uint32_t m = g.hmark[p.host[i]] ? 1u : 0u;
+    const uint32_t old = atomicExch(g.bmark + p.dev[i], m);
+    if (m != (old ? 1u : 0u)) atomicAdd(g.fault + 1, m ? 1u : 0xffffffffu);
+  }
+}
+
+__global__ void __launch_bounds__(256) marks_apply_kernel(Geom g, uint64_t first, uint64_t n,
+                                                          const uint8_t* __restrict__ ops) {
+  for (uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x; i < n;
+       i += (uint64_t)gridDim.x * 256u) {
+    if (ops[i] == 0) continue;
+    const uint32_t m = ops[i] == 1 ? 1u : 0u;
+    const uint32_t old = atomicExch(g.bmark + first + i, m);
+    if (m != (old ? 1u : 0u)) atomicAdd(g.fault + 1, m ? 1u : 0xffffffffu);
   }
 }
 
@@ -824,6 +862,25 @@ hipError_t launch_fill(void* dst, uint8_t byte, uint64_t bytes, hipStream_t s) {
   if (bytes == 0) return hipSuccess;
   uint32_t word = 0x01010101u * byte;
   fill_kernel<<<grid_for(bytes / 16 + 1, 16384), 256, 0, s>>>((uint8_t*)dst, word, bytes);
+  return hipGetLastError();
+}
+
+hipError_t launch_marks_fill(const Geom& g, uint32_t mark, hipStream_t s) {
+  marks_fill_kernel<<<grid_for(g.num_blocks, 1024), 256, 0, s>>>(g, mark ? 1u : 0u);
+  return hipGetLastError();
+}
+
+hipError_t launch_marks_swap(const Geom& g, const MarkPairs& p, bool out, hipStream_t s) {
+  if (p.n == 0) return hipSuccess;
+  if (p.n > kMarkPairs) return hipErrorInvalidValue;
+  marks_swap_kernel<<<1, 256, 0, s>>>(g, p, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_marks_apply(const Geom& g, uint64_t first, uint64_t n, const uint8_t* ops,
+                              hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  marks_apply_kernel<<<grid_for(n, 1024), 256, 0, s>>>(g, first, n, ops);
   return hipGetLastError();
 }
 

@@ -241,6 +241,14 @@ class PagedKvPool:
     def fill(self, byte: int, stream=None) -> None:
         check(self._lib.fkv_paged_fill(self._h, byte, _stream_ptr(stream)))
 
+    def marked_blocks(self, stream=None) -> int:
+        """Device blocks marked as holding a value the fast attention instances cannot
+        take (a Q8_0 scale of 512 or more, an F16 Inf/NaN K or V), after the work
+        enqueued on `stream`."""
+        n = ctypes.c_uint64()
+        check(self._lib.fkv_paged_marked_blocks(self._h, _stream_ptr(stream), ctypes.byref(n)))
+        return n.value
+
     def take_fault_flags(self, stream=None) -> int:
         """FKV_FAULT_* bits raised by the work enqueued on `stream` (default: the current
         stream) and by work already finished elsewhere; clears them."""

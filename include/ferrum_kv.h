@@ -186,7 +186,8 @@ typedef struct fkv_paged_info {
   uint64_t pool_bytes;   /* num_blocks*block_bytes */
   uint64_t free_blocks;  /* blocks with refcount 0 */
   void* device_base;     /* start of device storage */
-  void* host_base;       /* start of pinned host swap storage, or NULL */
+  void* host_base;       /* start of pinned host swap storage, or NULL (read-only for
+                            callers: see the block marks below) */
 } fkv_paged_info;
 
 typedef struct fkv_pool fkv_pool;
@@ -203,6 +204,22 @@ int32_t fkv_paged_get_info(const fkv_pool* pool, fkv_paged_info* out);
  * another stream is reported by the next call. Calls on one pool from several
  * threads are serialised inside (each returns the bits its own exchange took). */
 int32_t fkv_paged_take_fault_flags(fkv_pool* pool, void* stream, uint32_t* flags_out);
+/* Block marks. A block is marked when a value the fast attention instances cannot take
+ * is stored in it: a Q8_0 scale of 512 or more (or inf/NaN), or an Inf/NaN K or V of an
+ * F16 pool. Attention reads the marks of the blocks each workgroup covers, and only
+ * workgroups over marked blocks run the slower exact (Q8_0) or leak-safe (F16 prefill)
+ * instance. A mark stays with the block's bytes: appends and the fused step set it,
+ * fkv_copy_blocks copies it to the destination, fkv_swap_out keeps it with the host
+ * block and fkv_swap_in brings it back, fkv_paged_fill sets every device block's mark
+ * from the fill byte, fkv_paged_write sets it where the image holds such a value and
+ * clears it where the image overwrites a whole block without one. Nothing else clears
+ * it (a freed block keeps its mark until it is overwritten that way). Bytes written
+ * into host blocks through fkv_paged_info.host_base are not scanned: write pool bytes
+ * with fkv_paged_write, after fkv_swap_in where the block was swapped out.
+ * fkv_paged_marked_blocks reports how many device blocks are marked, in stream order
+ * (it synchronises `stream`). It has no counterpart in the reference, whose dense f32
+ * pool holds every value exactly. */
+int32_t fkv_paged_marked_blocks(fkv_pool* pool, void* stream, uint64_t* count_out);
 /* Fill every byte of device storage with `byte` (async on stream). */
 int32_t fkv_paged_fill(fkv_pool* pool, uint8_t byte, void* stream);
 /* Raw copies between device storage and host memory (byte offsets into the pool),
@@ -270,10 +287,10 @@ int32_t fkv_swap_in(fkv_pool* pool, const int64_t* pairs, uint32_t n_pairs, void
  * [n_seqs][max_blocks_per_seq]; ctx_lens: device int32 [n_seqs], each
  * <= max_ctx_len. Needs block_size 16, head_dim 64 or 128, and g <= 16 (F16 and
  * Q8_0, matrix cores) or g in {1,2,4,8,16} (F32). Q8_0 follows the reference's f32
- * dequantisation (kernels/src/scalar.rs:268-275) for every finite scale: while the
- * pool has never held a scale of 512 or more, operands are scale x quant in
- * binary16 (exact to one rounding); once it has (the append, fill or write that put
- * one there marks the pool), a second kernel instance takes the quants as exact
+ * dequantisation (kernels/src/scalar.rs:268-275) for every finite scale: over unmarked
+ * blocks operands are scale x quant in binary16 (exact to one rounding); a workgroup
+ * whose blocks include a marked one (a scale of 512 or more: see the block marks
+ * above) runs a second kernel instance, which takes the quants as exact
  * operands and applies the scales in f32.
  * workspace: device scratch of fkv_decode_attention_workspace_size() bytes
  * holding the split partials (running max, sum and unnormalised output per
@@ -302,7 +319,7 @@ int32_t fkv_decode_attention(fkv_pool* pool, uint32_t layer, uint32_t n_heads,
  * kernel launch: the workgroup that reads the sequence's last context split
  * encodes the token (Q8_0: quantised as fkv_append does, FKV_FAULT_VALUE_RANGE
  * included), stores it and uses its encoded values in place of what it loaded; a
- * Q8_0 token with a scale of 512 or more marks the pool, and the exact instance
+ * Q8_0 token with a scale of 512 or more marks its block, and the exact instance
  * that every Q8_0 call launches after the first recomputes the call's outputs.
  * F32 storage uses an append launch first.
  * workspace: fkv_append_decode_attention_workspace_size() bytes, same rules as
@@ -377,10 +394,11 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
  * (FKV_ERR_KERNEL otherwise). The launch holds max_q_len queries a sequence: a q_lens[s]
  * above it (or above ctx_lens[s]) raises FKV_FAULT_CTX_RANGE, and only its first
  * max_q_len queries are computed, at the positions q_lens[s] gives them. No query
- * reads a position past its own, Inf/NaN values included: an F16 pool that has
- * stored an Inf/NaN K or V runs a slower instance that keeps such V values from
- * earlier queries of the same tile and gives an infinite K's scores exactly. Q8_0 follows fkv_decode_attention's rule for scales of 512 or
- * more.
+ * reads a position past its own, Inf/NaN values included: workgroups over F16 blocks
+ * marked as holding an Inf/NaN K or V (see the block marks above) run a slower
+ * instance that keeps such V values from earlier queries of the same tile and gives an
+ * infinite K's scores exactly. Q8_0 follows fkv_decode_attention's rule for blocks
+ * marked with scales of 512 or more.
  * workspace: NULL, or device scratch of fkv_prefill_attention_workspace_size()
  * bytes (16-byte aligned; no initialisation) in which workgroups over long
  * contexts leave the partial results of pieces of their key range for a merge

@@ -6,10 +6,10 @@ and NaN positions and values elsewhere; q_len = 1 agrees with decode attention;
 output rows outside the chunk are never written. Also:
 - an Inf or NaN V inside a chunk reaches exactly the queries whose causal range holds
   it (the reference's token loop never reads a later position), through the
-  leak-safe instance that a pool which stored such a value runs, which also meets
-  the bar on finite data; an infinite K (stored by the bulk append or the fused
-  decode step) marks the pool the same way, and its +-Inf scores come out as the
-  reference's dot gives them;
+  leak-safe instance that workgroups over a block marked as holding such a value run,
+  which also meets the bar on finite data; an infinite K (stored by the bulk append or
+  the fused decode step) marks its block the same way, and its +-Inf scores come out as
+  the reference's dot gives them;
 - a sequence whose q_len exceeds the call's max_q_len (the grid holds no more) is
   clamped to it and raises FKV_FAULT_CTX_RANGE; a table entry outside the pool raises
   FKV_FAULT_BLOCK_RANGE and its block is skipped, other sequences unaffected;
@@ -217,10 +217,10 @@ def test_nonfinite_v_reaches_only_later_queries(bad, g, pieces, d, monkeypatch):
 def test_infinite_k_marks_the_pool_and_matches_the_oracle(bad, append):
     """K (V finite) holds +-Inf at dims 5 and 77 of some positions the chunks read. q is
     1.0 on dim 77, exact in f16, so q's lo part there is 0: the f16 hi + lo split gives
-    inf * 0 = NaN in the lo chain where the reference's dot gives +-Inf. Only a pool
-    marked as holding a non-finite K runs the instance that repairs it, and the store
-    must mark the pool: by the bulk append (positions inside and before the chunks) and
-    by the fused decode step (the last position of sequence 1)."""
+    inf * 0 = NaN in the lo chain where the reference's dot gives +-Inf. Only workgroups
+    over a block marked as holding a non-finite K run the instance that repairs it, and
+    the store must mark the block: by the bulk append (positions inside and before the
+    chunks) and by the fused decode step (the last position of sequence 1)."""
     import torch
     hkv, g, d = 2, 4, 128
     ctxs, qls = [60, 160], [40, 40]
@@ -255,16 +255,18 @@ def test_infinite_k_marks_the_pool_and_matches_the_oracle(bad, append):
 
 
 def test_leak_safe_instance_on_finite_data():
-    """A pool that once stored a NaN V (elsewhere) runs the leak-safe instance for every
-    later prefill: on finite chunks it meets the same bar."""
+    """Every block the chunks read holds a NaN V in layer 1 (marking it), so every
+    workgroup of a layer-0 prefill runs the leak-safe instance: on layer 0's finite
+    values it meets the same bar."""
     hkv, g, d = 8, 4, 128
     ctxs, qls = [600, 1300], [600, 256]
-    pool, layout, tab = _pool(d, hkv, ctxs, seed=41)
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=41, layers=2)
     import torch
-    spare = int(np.setdiff1d(np.arange(pool.config.num_blocks), tab.ravel())[0])
-    bad = np.full((1, hkv, d), np.nan, np.float32)
-    pool.append(0, to_dev(bad), to_dev(bad), to_dev(np.array([spare * 16], np.int64)))
+    used = np.concatenate([tab[i, :(c + 15) // 16] for i, c in enumerate(ctxs)])
+    bad = np.full((len(used), hkv, d), np.nan, np.float32)
+    pool.append(1, to_dev(bad), to_dev(bad), to_dev(used.astype(np.int64) * 16))
     torch.cuda.synchronize()
+    assert pool.marked_blocks() == len(used)
     offs = np.array([0, 600], np.int64)
     q = np.random.default_rng(5).standard_normal((856, hkv * g, d), dtype=np.float32)
     got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
@@ -323,7 +325,7 @@ def test_table_entry_outside_the_pool_is_flagged_and_skipped(dtype, pieces, monk
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("pieces", [0, 5])
 def test_q8_prefill_with_wide_values(pieces, d, monkeypatch):
-    """Q8_0 K and V with +-1e6 values (scales ~7,874): the pool is marked and the exact
+    """Q8_0 K and V with +-1e6 values (scales ~7,874): the blocks are marked and the exact
     instance computes, with whole key ranges and with 5-block pieces; q is small enough
     that the scores stay O(1); head_dim 128 and 64. With 64 dims a dim of V holds ~11
     outliers in the longer context, and with both signs they cancel in some outputs to

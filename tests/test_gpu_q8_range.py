@@ -1,17 +1,17 @@
 """GPU parity: Q8_0 decode attention past the binary16 range.
 
 The reference dequantises Q8_0 in f32, f16_to_f32(scale) * (i8 as f32)
-(crates/kernels/src/scalar.rs:268-275), exact for every finite scale. A pool that has
-held a scale of 512 or more (values beyond 512 * 127, where scale x quant can pass
-65504) runs the exact kernel instance: quants as exact binary16/bf16 operands, scales
-applied in f32. Checked against the oracle (which dequantises exactly as the
+(crates/kernels/src/scalar.rs:268-275), exact for every finite scale. Workgroups over a
+block that holds a scale of 512 or more (values beyond 512 * 127, where scale x quant
+can pass 65504; the store marks the block) run the exact kernel instance: quants as
+exact binary16/bf16 operands, scales applied in f32. Checked against the oracle (which dequantises exactly as the
 reference) at the attention bar, with no fault raised, for:
 - K and V values up to +-1e6 scattered through ordinary N(0,1) rows;
 - blocks where one token's scale is ~7,874 and its neighbours' ~0.02, with the big
   token's weight small so the ordinary tokens carry the output;
 - the fused step (and the RoPE fused step) appending such a token onto a pool that
-  held none: the step's own workgroup marks the pool and the exact instance
-  recomputes the call;
+  held none: the step's own workgroup marks the token's block and the exact instance
+  recomputes that workgroup's outputs;
 - fkv_paged_write / fkv_paged_fill putting such scales in place.
 A scale past the binary16 range itself (a 32-value run with |x| >= 65520 * 127) is
 stored as the reference's encoder stores it (+-inf) and raises FKV_FAULT_VALUE_RANGE.
@@ -116,8 +116,8 @@ def test_mixed_scales_in_one_block():
 @pytest.mark.parametrize("rope", [False, True])
 def test_fused_step_appending_a_wide_token(rope):
     """The pool holds ordinary values; the step's new token of sequence 2 has a V value
-    of 1e6. Its workgroup marks the pool during the call and the exact instance
-    launched after recomputes every output. V bytes are the oracle's append, bit for
+    of 1e6. Its workgroup marks the token's block during the call and the exact
+    instance launched after recomputes that split's outputs. V bytes are the oracle's append, bit for
     bit; K too without RoPE (with it, within one quantisation step: device sincosf)."""
     import torch
     import ferrum_amd as fa
@@ -182,7 +182,7 @@ def test_scale_past_binary16_is_stored_as_inf_and_flagged():
 
 
 @pytest.mark.parametrize("how", ["write", "fill"])
-def test_write_and_fill_mark_the_pool(how):
+def test_write_and_fill_mark_the_blocks(how):
     """A pool image with a wide scale put in place by fkv_paged_write, or every scale
     made 0x6060 (560) by fkv_paged_fill and then ordinary tokens appended over part of
     it: attention over it meets the bar against the oracle."""
