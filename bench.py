@@ -15,8 +15,11 @@ c3 continuous batching with chunked prefill in a fragmented 60%-of-HBM pool, c4
 Q8_0 KV, c5 70B long context plus copy_blocks and swap), q8gemv, the decode layer's
 Q8_0 weight projections (fkv_gemm_q8_0 over Llama-3-8B's 32 layers), gguf, the
 GGUF open + weight upload to HBM, or layer, the attention half of the decode layer
-GPU-resident (q/k/v projections, RoPE + append + attention, attn_output, C2's batch);
-each prints its own line.
+GPU-resident (q/k/v projections, RoPE + append + attention, attn_output, C2's batch),
+or gather, the block-table gather (fkv_gather_tables) on C2's shapes; each prints its
+own line. The default run adds `configs` to its line: compact results of c1, c3, c4
+(with the exact Q8_0 instance measured), c5 (with copy_blocks and swap) and gather
+(F16 and Q8_0), run after the headline in the same process (--no-configs skips them).
 
 Printed JSON line: value = algorithmic HBM bytes of the step's calls (attention +
 append) / wall time per step, timed over K steps bracketed by synchronisation.
@@ -61,7 +64,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--workload", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "c5", "q8gemv", "gguf", "layer"])
+                    choices=["c1", "c2", "c3", "c4", "c5", "q8gemv", "gguf", "layer", "gather"])
     ap.add_argument("--gguf-layers", type=int, default=4,
                     help="gguf: Llama-3-8B layers in the synthetic file (232 MB of Q8_0 each)")
     ap.add_argument("--gguf-threads", type=int, default=0, help="gguf: host threads (0 = 4, fewer on fewer CPUs)")
@@ -74,6 +77,8 @@ def parse():
                     help="q8gemv: the same groups through fkv_gemm_q8_0_batched (the matrix "
                          "cores from 8 tokens)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="default run: skip the other configs' summary after the headline")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = min(16, os.cpu_count())")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="CPU baseline budget: a third at 1 thread, the rest at --cpu-threads")
@@ -81,7 +86,7 @@ def parse():
                     help="> 0: time fkv_rope_append_decode_attention (q and k before RoPE)")
     ap.add_argument("--rope-theta", type=float, default=500000.0)
     ap.add_argument("--kv-dtype", default="f16", choices=["f16", "f32", "q8_0"],
-                    help="c2: KV storage (f32 runs the VALU attention kernel); c3: f16 "
+                    help="c2: KV storage (f32 runs the VALU attention kernel); c3, gather: f16 "
                          "(BASELINE's) or q8_0")
     ap.add_argument("--n-heads", type=int, default=32,
                     help="c2: query heads over the 8 KV heads (64: GQA group 8)")
@@ -480,7 +485,35 @@ def run_c4(args, torch, fa, lib, dev):
         L=32, n_seqs=n_seqs, hq=32, hkv=8, d=128, dtype=8, ctx0=ctx0, num_blocks=nb,
         outlier_frac=0.01, extra_cfg={"kv_dtype": "q8_0", "outliers": "1% at +-20"},
         cpu_seqs=np.arange(8))
+    res["exact_instance"] = exact_instance_leg(torch, pool, dl, args.steps, ctx)
     return res
+
+
+def exact_instance_leg(torch, pool, dl, K, ctx):
+    """The same fused decode calls after one token of every 4096-token context split of
+    every sequence was appended (layer 0) with a V value of 1e6: a Q8_0 scale of ~7,874
+    marks that block, so every workgroup of every call runs the exact instance (f32
+    scales, int8 operands) instead of the binary16 one. Same algorithmic bytes."""
+    dev = dl.q.device
+    pos = np.arange(0, ctx, 4096)
+    seqs = np.repeat(np.arange(dl.n_seqs), pos.size)
+    slots = slots_of(dl.tables, seqs, np.tile(pos, dl.n_seqs))
+    k = torch.zeros((slots.size, dl.hkv, dl.d), device=dev)
+    v = torch.zeros_like(k)
+    v[:, :, 0] = 1e6
+    pool.append(0, k, v, torch.from_numpy(slots).to(dev))
+    torch.cuda.synchronize()
+    marked = pool.marked_blocks()
+    wall, region_ms = dl.run(0, K)
+    e = elem_bytes(8)
+    call_bytes = sum(attn_bytes(dl.ctx_step[i], dl.hq, dl.hkv, dl.d, e)
+                     + append_bytes(dl.n_seqs, dl.hkv, dl.d, e, slot_bytes=0)
+                     for i in range(K)) / K
+    call_ms = region_ms / (K * dl.L)
+    gbs = call_bytes / (call_ms * 1e-3) / 1e9
+    return {"marked_blocks": int(marked), "us_per_call": round(call_ms * 1e3, 2),
+            "achieved_gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel": "attn_mfma_kernel<q8_0, exact> (qk_block_q8x / pv_block_q8x)"}
 
 
 def run_c5(args, torch, fa, lib, dev):
@@ -651,6 +684,31 @@ def run_c3(args, torch, fa, lib, dev):
     pairs = sum(int((pre_prior + (W + i) * chunk).sum()) * chunk + n_pre * chunk * (chunk + 1) // 2
                 for i in range(K)) / K
     pre_flop = 4.0 * d * hq * pairs
+    # The leak-safe instance: the same calls after position 0 of every prefill sequence
+    # (layer 0) was given a NaN V, which marks its first block, a block every workgroup
+    # of the sequence reads, so every workgroup runs the leak-safe instance. (The NaN
+    # reaches every query; the timing is the instance's, on the same bytes.)
+    if dtype == 1:
+        nan_slots = slots_of(tables[n_dec:], np.arange(n_pre), np.zeros(n_pre, np.int64))
+        kn = torch.zeros((n_pre, hkv, d), device=dev)
+        vn = torch.full((n_pre, hkv, d), float("nan"), device=dev)
+        pool.append(0, kn, vn, torch.from_numpy(nan_slots).to(dev))
+        torch.cuda.synchronize()
+        p2, p3 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        p2.record(stream)
+        for i in range(K):
+            for l in range(L):
+                prefill(W + i, l, sp)
+        p3.record(stream)
+        torch.cuda.synchronize()
+        assert pool.take_fault_flags() == 0
+        safe_us = p2.elapsed_time(p3) * 1e3 / (K * L)
+        leak_safe = {"us_per_call": round(safe_us, 2),
+                     "tflops": round(pre_flop / (safe_us * 1e-6) / 1e12, 1),
+                     "marked_blocks": int(pool.marked_blocks()),
+                     "kernel": "attn_prefill_kernel<f16, leak-safe>"}
+    else:
+        leak_safe = None
     # decode-only rate from a separate region of back-to-back fused decode calls
     dw, dms = dl.run(0, K)
     e = elem_bytes(dtype)
@@ -678,12 +736,154 @@ def run_c3(args, torch, fa, lib, dev):
         "us_per_call": round(pre_us, 2), "gflop_per_call": round(pre_flop / 1e9, 3),
         "tflops": round(pre_flop / (pre_us * 1e-6) / 1e12, 1),
         "flop_count": "4 * head_dim * n_heads per (query, key) pair",
-        "workspace_bytes": int(pre_ws_bytes)}
+        "pct_of_mfma_peak": round(100 * pre_flop / (pre_us * 1e-6) / 2.5e15, 2),
+        "workspace_bytes": int(pre_ws_bytes), "leak_safe_instance": leak_safe}
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args, pool, dl.tables, dl.ctx_step[K - 1],
                                            dl.q[L - 1].cpu().numpy(), dl.out[L - 1].cpu().numpy(),
                                            L - 1, hq, hkv, d, 1, seqs=np.arange(16))
     return res
+
+
+def gather_bytes(ctx, hkv, d, e, out_e):
+    """fkv_gather_tables of one layer: K+V of every position read once (e bytes a
+    value), written as out_e bytes a value, the block-table entries, ctx_lens and the
+    output offsets."""
+    ctx = np.asarray(ctx, np.int64)
+    n = float(ctx.sum())
+    return n * hkv * d * 2 * e + n * hkv * d * 2 * out_e + float(((ctx + 15) // 16).sum()) * 4 + \
+        ctx.size * 12
+
+
+def run_gather(args, torch, fa, lib, dev):
+    """Block-table gather (the paged KvPool::k / v, crates/kvcache/src/pool.rs:174-204) on
+    C2's shapes: 64 sequences with contexts U[128, 4096] (seed), 32 layers, 8 KV heads,
+    head_dim 128, F16 (default) or Q8_0 storage. One step = fkv_gather_tables of every
+    layer's K and V for every sequence into one contiguous output, in the raw storage
+    format (the headline) and decoded to f32."""
+    K, W = args.steps, args.warmup
+    rng = np.random.default_rng(args.seed)
+    L, hkv, d, n_seqs = 32, 8, 128, 64
+    dtype = {"f16": 1, "q8_0": 8}.get(args.kv_dtype)
+    if dtype is None:
+        raise SystemExit("gather: --kv-dtype f16 or q8_0")
+    ctx = rng.integers(128, 4097, n_seqs).astype(np.int64)
+    nblk_seq = (ctx + 15) // 16
+    pool = fa.PagedKvPool(fa.PagedConfig(n_layers=L, n_kv_heads=hkv, head_dim=d,
+                                         num_blocks=int(nblk_seq.sum()) + 64, block_size=16,
+                                         kv_dtype=dtype))
+    tables = make_tables(pool, nblk_seq, rng)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    fill_context(torch, pool, range(L), tables, ctx, hkv, d, gen, dev)
+    e = elem_bytes(dtype)
+    n_tok = int(ctx.sum())
+    tables_d = torch.from_numpy(tables).to(dev)
+    ctx_d = torch.from_numpy(ctx.astype(np.int32)).to(dev)
+    offs = np.zeros(n_seqs, np.int64)
+    offs[1:] = np.cumsum(ctx[:-1])
+    offs_d = torch.from_numpy(offs).to(dev)
+    h = ctypes.c_void_p(pool.handle)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    legs = {}
+    for fmt, name in ((1, "raw"), (0, "f32")):
+        row = (d * 2 if dtype == 1 else d // 32 * 34) if fmt == 1 else d * 4
+        out_e = row / d
+        ok = torch.empty((n_tok, hkv, row), dtype=torch.uint8, device=dev)
+        ov = torch.empty_like(ok)
+
+        def step():
+            for l in range(L):
+                rc = lib.fkv_gather_tables(h, l, tables_d.data_ptr(), tables.shape[1],
+                                           ctx_d.data_ptr(), offs_d.data_ptr(), n_seqs,
+                                           int(ctx.max()), fmt, ok.data_ptr(), ov.data_ptr(), sp)
+                if rc:
+                    fa.errors.check(rc)
+        for _ in range(W):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        for _ in range(K):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        assert pool.take_fault_flags() == 0
+        call_bytes = gather_bytes(ctx, hkv, d, e, out_e)
+        call_ms = e0.elapsed_time(e1) / (K * L)
+        legs[name] = {"gbs": round(call_bytes * K * L / wall / 1e9, 2),
+                      "kernel_gbs": round(call_bytes / (call_ms * 1e-3) / 1e9, 2),
+                      "us_per_call": round(call_ms * 1e3, 2),
+                      "bytes_per_call": int(call_bytes), "ms_per_step": round(wall * 1e3 / K, 4)}
+        if name == "raw":
+            last = (ok, ov)
+        else:
+            del ok, ov
+    copy_gbs = calibrate_copy(torch, fa, dev)
+    raw = legs["raw"]
+    res = {
+        "metric": METRIC + " [gather leg: block-table gather GB/s]",
+        "value": raw["gbs"], "unit": "GB/s", "n_gpus": 1, "steps": K, "warmup": W,
+        "ms_per_step": raw["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": {1: "f16", 8: "q8_0"}[dtype],
+        "data": "synthetic N(0,1) K/V, seeded; scattered block tables",
+        "config": {"workload": "block-table gather, C2 shapes (BASELINE configs[1])",
+                   "n_seqs": n_seqs, "n_layers": L, "n_kv_heads": hkv, "head_dim": d,
+                   "block_size": 16, "tokens": n_tok, "kv_dtype": args.kv_dtype,
+                   "format": "raw storage (f32 decode in `f32`)", "parallelism": "single GPU"},
+        "pct_of_hbm_peak": round(100 * raw["gbs"] / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "kernel": "gather_tables_tile_kernel (raw)",
+                     "achieved": raw["kernel_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(raw["kernel_gbs"] / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(os.path.join(
+                         ROOT, "profiles", f"gather_{args.kv_dtype}_llama3_8b_c2_kernel_stats_and_traffic.md")),
+                     "bytes_per_launch": raw["bytes_per_call"],
+                     "ms_per_launch": round(raw["us_per_call"] * 1e-3, 5)},
+        "f32": legs["f32"], "device_copy_gbs": round(copy_gbs, 1),
+        "raw_vs_device_copy": round(raw["kernel_gbs"] / copy_gbs, 3),
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = gather_cpu_baseline(args, pool, tables, ctx, L - 1, hkv, d, dtype,
+                                                  last, offs)
+    return res
+
+
+def gather_cpu_baseline(args, pool, tables, ctx, layer, hkv, d, dtype, gpu_out, offs):
+    """The oracle's restatement of the gather (fo_gather_tables: KvPool::k / v per
+    position, decoded to f32) on layer `layer` of 16 sequences, one thread; also counts
+    GPU raw-format bytes that differ from the oracle's on the same sample."""
+    from oracle import ref
+    seqs = np.arange(16)
+    bs = 16
+    c = np.asarray(ctx, np.int64)[seqs]
+    nb = (c + bs - 1) // bs
+    used = [int(b) for s, n in zip(seqs, nb) for b in tables[s, :n]]
+    remap = {b: i for i, b in enumerate(used)}
+    lay = ref.Layout(1, hkv, d, bs, len(used), dtype=dtype)
+    region = lay.block_bytes
+    image = np.empty(lay.pool_bytes, np.uint8)
+    for b, i in remap.items():
+        image[i * region:(i + 1) * region] = pool.read(b * pool.block_bytes + layer * region, region)
+    tab = np.zeros((len(seqs), int(nb.max())), np.int32)
+    for j, (s, n) in enumerate(zip(seqs, nb)):
+        tab[j, :n] = [remap[int(b)] for b in tables[s, :n]]
+    c32 = c.astype(np.int32)
+    t1, reps = cpu_timed(lambda: ref.gather_tables(lay, image, 0, tab, c32, 0), args.cpu_seconds / 2)
+    wk, wv, _ = ref.gather_tables(lay, image, 0, tab, c32, 1)
+    # the GPU's raw output of the last layer for these sequences (rows offs[s] ..)
+    gk = gpu_out[0][: int(c.sum())].cpu().numpy().reshape(-1)
+    gv = gpu_out[1][: int(c.sum())].cpu().numpy().reshape(-1)
+    bad = int((gk != wk.reshape(-1)).sum() + (gv != wv.reshape(-1)).sum())
+    nbytes = gather_bytes(c, hkv, d, elem_bytes(dtype), 4.0)
+    return {"value": round(nbytes / t1 / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": (f"layer {layer}, {len(seqs)} seqs ({int(c.sum())} tokens): the oracle's "
+                       f"fo_gather_tables (KvPool::k/v per position decoded to f32, "
+                       f"pool.rs:174-204), {reps} reps at 1 thread"),
+            "gpu_vs_cpu_raw_bytes_differing": bad}
 
 
 def attn_bytes_prefill(ctx_end, q_len, hq, hkv, d, e=2.0):
@@ -1154,9 +1354,71 @@ def main():
     dev = torch.device("cuda:0")
     lib = _lib.load()
     run = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5,
-           "q8gemv": run_q8gemv, "gguf": run_gguf, "layer": run_layer}[args.workload]
+           "q8gemv": run_q8gemv, "gguf": run_gguf, "layer": run_layer,
+           "gather": run_gather}[args.workload]
     result = run(args, torch, fa, lib, dev)
+    if (args.workload == "c2" and args.kv_dtype == "f16" and args.n_heads == 32
+            and not args.rope_dim and not args.no_configs):
+        result["configs"] = other_configs(args, torch, fa, lib, dev)
     print(json.dumps(result), flush=True)
+
+
+def other_configs(args, torch, fa, lib, dev):
+    """Compact results of the other BASELINE configs and the gather leg, run after the
+    headline in the same process (no CPU baselines; each leg's pool is released before
+    the next). A leg that fails records its error instead of hiding the headline."""
+    import copy
+    import gc
+
+    def pct(v):
+        return round(100 * v / HBM_PEAK_GBS, 2)
+
+    def c1(r):
+        return {"value_gbs": r["value"], "pct_of_hbm_peak": pct(r["value"]),
+                "us_per_call": round(r["roofline"]["ms_per_launch"] * 1e3, 2),
+                "frac": r["roofline"]["frac"], "note": "latency-bound: 0.58 MB a call"}
+
+    def c3(r):
+        p = r["prefill_attention"]
+        return {"value_gbs": r["value"], "pct_of_hbm_peak": r["pct_of_hbm_peak"],
+                "ms_per_step": r["ms_per_step"], "decode_only_ms_per_step": r["decode_only_ms_per_step"],
+                "decode_frac": r["roofline"]["frac"], "prefill_us_per_call": p["us_per_call"],
+                "prefill_tflops": p["tflops"], "prefill_pct_of_mfma_peak": p["pct_of_mfma_peak"],
+                "prefill_leak_safe": p["leak_safe_instance"]}
+
+    def c4(r):
+        return {"value_gbs": r["value"], "pct_of_hbm_peak": r["pct_of_hbm_peak"],
+                "ms_per_step": r["ms_per_step"], "frac": r["roofline"]["frac"],
+                "exact_instance": r["exact_instance"]}
+
+    def c5(r):
+        return {"value_gbs": r["value"], "pct_of_hbm_peak": r["pct_of_hbm_peak"],
+                "ms_per_step": r["ms_per_step"], "frac": r["roofline"]["frac"],
+                "copy_blocks_gbs": r["copy_blocks"]["gbs"],
+                "copy_blocks_pct_of_hbm_peak": r["copy_blocks"]["pct_of_hbm_peak"],
+                "swap_out_gbs": r["swap"]["out_gbs"], "swap_in_gbs": r["swap"]["in_gbs"]}
+
+    def gather(r):
+        return {"raw_gbs": r["value"], "raw_kernel_gbs": r["roofline"]["achieved"],
+                "frac": r["roofline"]["frac"], "raw_vs_device_copy": r["raw_vs_device_copy"],
+                "f32_kernel_gbs": r["f32"]["kernel_gbs"], "device_copy_gbs": r["device_copy_gbs"]}
+
+    legs = [("c1", run_c1, "f16", c1), ("c4", run_c4, "q8_0", c4), ("c5", run_c5, "f16", c5),
+            ("c3", run_c3, "f16", c3), ("gather_f16", run_gather, "f16", gather),
+            ("gather_q8_0", run_gather, "q8_0", gather)]
+    out = {}
+    for name, fn, kv, pick in legs:
+        a = copy.copy(args)
+        a.no_cpu, a.kv_dtype = True, kv
+        t0 = time.perf_counter()
+        try:
+            out[name] = pick(fn(a, torch, fa, lib, dev))
+        except Exception as ex:  # recorded in the line; the headline still prints
+            out[name] = {"error": f"{type(ex).__name__}: {ex}"[:400]}
+        out[name]["leg_seconds"] = round(time.perf_counter() - t0, 1)
+        gc.collect()
+        torch.cuda.empty_cache()
+    return out
 
 
 if __name__ == "__main__":

@@ -599,6 +599,282 @@ __global__ void __launch_bounds__(256) gather_tables_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Gather, tile path: one workgroup per 16 tokens of one 16-token block x kHpw KV heads
+// (block size 16, head_dim 64 or 128, F16 or Q8_0 storage, 16-byte aligned outputs).
+// The output rows of the 16 tokens are consecutive (row0 + o for token o), as both
+// entry points lay them out: a sequence's positions (by block table) or a window of 16
+// slots that are one whole block (by slot).
+// ---------------------------------------------------------------------------
+
+constexpr int kFmtF32 = 0;  // FKV_GATHER_F32
+constexpr int kFmtRaw = 1;  // FKV_GATHER_RAW
+
+// Heads per workgroup: F16 one 16-byte unit of each tile a thread (1 at D = 128, 2 at
+// 64); Q8_0 tiles are half the bytes and staged whole, so 4 (8) heads keep as many bytes
+// in flight per workgroup (one head a workgroup ran at 43% of a device copy).
+constexpr uint32_t gather_heads_per_wg(int dtype, uint32_t d) {
+  return dtype == kDtypeF16 ? 256u / (2u * d) : 512u / d;
+}
+
+template <int DT, int D>
+struct GatherShape {
+  static constexpr int kTph = 2 * D;            // F16 threads per (block, head) tile
+  static constexpr int kHpw = (int)gather_heads_per_wg(DT, D);
+  static constexpr int kTile = DT == kDtypeF16 ? 16 * D * 2 : 16 * D + 16 * (D / 32) * 2;
+  static constexpr int kUnits = kTile / 16;     // 16-byte units of a tile
+  static constexpr int kVRow = D + 4;           // F16 V transpose row (halves): rows 8 apart
+                                                // fall 16 banks apart
+};
+
+// LDS of the tile path: F16 the V tiles transposed to [token][dim]; Q8_0 both tiles as
+// stored.
+template <int DT, int D>
+struct __align__(16) GatherLds {  // 16-byte unit stores into q
+  using S = GatherShape<DT, D>;
+  union {
+    uint16_t v[S::kHpw][16][S::kVRow];
+    uint8_t q[S::kHpw][2][S::kTile];
+  };
+};
+
+// Stores 8 binary16 values (one 16-byte unit) as FMT requires: RAW the 16 bytes, F32
+// the 8 decoded floats (32 bytes).
+template <int FMT>
+__device__ __forceinline__ void store_f16_unit(uint8_t* dst, uint4 w) {
+  if constexpr (FMT == kFmtRaw) {
+    *(uint4*)dst = w;
+  } else {
+    ((float4*)dst)[0] = make_float4(f16_bits_to_f32(w.x & 0xffffu), f16_bits_to_f32(w.x >> 16),
+                                    f16_bits_to_f32(w.y & 0xffffu), f16_bits_to_f32(w.y >> 16));
+    ((float4*)dst)[1] = make_float4(f16_bits_to_f32(w.z & 0xffffu), f16_bits_to_f32(w.z >> 16),
+                                    f16_bits_to_f32(w.w & 0xffffu), f16_bits_to_f32(w.w >> 16));
+  }
+}
+
+// One tile group: head hl of the workgroup is KV head h (h_ok false past the last head);
+// kt / vt the head's K and V tiles (null when the block's table entry is outside the
+// pool: nothing is written); tokens o < n are written to rows row0 + o of out_k / out_v
+// (row_bytes apart; head h at h * head_bytes within a row). All 256 threads call this.
+template <int DT, int D, int FMT>
+__device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g, uint32_t layer,
+                                            int64_t blk, uint32_t h0, int32_t n,
+                                            uint8_t* out_k, uint8_t* out_v, uint64_t row0) {
+  using S = GatherShape<DT, D>;
+  constexpr uint64_t kHeadBytes = FMT == kFmtF32 ? (uint64_t)D * 4u
+                                  : DT == kDtypeF16      ? (uint64_t)D * 2u
+                                                         : (uint64_t)D / 32u * 34u;
+  const uint64_t row_bytes = (uint64_t)g.n_kv_heads * kHeadBytes;
+  const bool blk_ok = blk >= 0 && (uint64_t)blk < g.num_blocks;
+  if constexpr (DT == kDtypeF16) {
+    const uint32_t hl = threadIdx.x / S::kTph, u = threadIdx.x % S::kTph;
+    const uint32_t h = h0 + hl;
+    const bool live = blk_ok && h < g.n_kv_heads;
+    uint4 kw = make_uint4(0, 0, 0, 0), vw = make_uint4(0, 0, 0, 0);
+    if (live) {
+      // unit u of each tile: K run c = u / 16 of token u % 16; V dim u / 2, tokens 8(u % 2) ..
+      kw = *(const uint4*)(tile_ptr(g, (uint64_t)blk, layer, 0, h) + (uint64_t)u * 16u);
+      vw = *(const uint4*)(tile_ptr(g, (uint64_t)blk, layer, 1, h) + (uint64_t)u * 16u);
+    }
+    const uint32_t d = u / 2u, t8 = (u % 2u) * 8u;
+    const uint32_t vh[8] = {vw.x & 0xffffu, vw.x >> 16, vw.y & 0xffffu, vw.y >> 16,
+                            vw.z & 0xffffu, vw.z >> 16, vw.w & 0xffffu, vw.w >> 16};
+#pragma unroll
+    for (int j = 0; j < 8; j++) lds.v[hl][t8 + j][d] = (uint16_t)vh[j];
+    const uint32_t o = u % 16u, c = u / 16u;
+    if (live && (int32_t)o < n) {
+      const uint64_t off = (row0 + o) * row_bytes + (uint64_t)h * kHeadBytes;
+      constexpr uint32_t kUnitOut = FMT == kFmtF32 ? 32u : 16u;
+      store_f16_unit<FMT>(out_k + off + (uint64_t)c * kUnitOut, kw);
+    }
+    __syncthreads();
+    if (live && (int32_t)o < n) {
+      const uint16_t* r = &lds.v[hl][o][c * 8u];
+      const uint4 w = make_uint4(r[0] | ((uint32_t)r[1] << 16), r[2] | ((uint32_t)r[3] << 16),
+                                 r[4] | ((uint32_t)r[5] << 16), r[6] | ((uint32_t)r[7] << 16));
+      const uint64_t off = (row0 + o) * row_bytes + (uint64_t)h * kHeadBytes;
+      constexpr uint32_t kUnitOut = FMT == kFmtF32 ? 32u : 16u;
+      store_f16_unit<FMT>(out_v + off + (uint64_t)c * kUnitOut, w);
+    }
+    __syncthreads();  // the LDS is reused by the caller's next tile group
+  } else {
+    // Q8_0: both tiles of every head to LDS as stored, then each output unit from there.
+    for (uint32_t i = threadIdx.x; i < (uint32_t)(S::kHpw * 2 * S::kUnits); i += 256u) {
+      const uint32_t hl = i / (2u * S::kUnits), r = i % (2u * S::kUnits);
+      const uint32_t kv = r / S::kUnits, un = r % S::kUnits;
+      const uint32_t h = h0 + hl;
+      if (blk_ok && h < g.n_kv_heads)
+        *(uint4*)&lds.q[hl][kv][un * 16u] =
+            *(const uint4*)(tile_ptr(g, (uint64_t)blk, layer, kv, h) + (uint64_t)un * 16u);
+    }
+    __syncthreads();
+    if (blk_ok) {
+      if constexpr (FMT == kFmtRaw) {
+        // Ferrum's 34-byte blocks (dtype.rs:19-21: f16 scale, then 32 x i8). A step is one
+        // block b of 4 consecutive tokens 4q .. 4q + 3 of one tile: their quants come from
+        // LDS as whole dwords (K: 8 bytes of a token's run at a time; V: a dword holds the
+        // 4 tokens' bytes of one dim, transposed in registers), and each block goes out as
+        // dword stores plus one 2-byte store (the scale or the last two quants, by b's
+        // parity: blocks start 34 bytes apart).
+        constexpr uint32_t kNb = D / 32u;
+        constexpr uint32_t kPer = 2u * 4u * kNb;
+        for (uint32_t i = threadIdx.x; i < (uint32_t)S::kHpw * kPer; i += 256u) {
+          const uint32_t hl = i / kPer, r = i % kPer;
+          const uint32_t kv = r / (4u * kNb), q = (r / kNb) % 4u, b = r % kNb;
+          const uint32_t h = h0 + hl;
+          if (h >= g.n_kv_heads || (int32_t)(4u * q) >= n) continue;
+          const uint8_t* t = lds.q[hl][kv];
+          uint32_t qw[4][8];  // [token][quant dword]
+          if (kv == 0) {
+#pragma unroll
+            for (uint32_t tt = 0; tt < 4; tt++) {
+              const uint32_t o = 4u * q + tt;
+#pragma unroll
+              for (uint32_t gg = 0; gg < 4; gg++) {  // dims b*32 + gg*8 .. +7
+                const uint2 w = *(const uint2*)&t[(b / 2u) * 1024u + (gg * 16u + o) * 16u + (b % 2u) * 8u];
+                qw[tt][2 * gg] = w.x;
+                qw[tt][2 * gg + 1] = w.y;
+              }
+            }
+          } else {
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++) {  // dims b*32 + 4k .. 4k + 3: m = 2b + k/4
+              const uint32_t m = 2u * b + k / 4u, j0 = (k % 4u) * 4u;
+              uint32_t w[4];
+#pragma unroll
+              for (uint32_t jj = 0; jj < 4; jj++)
+                w[jj] = *(const uint32_t*)&t[(m / 4u) * 1024u + (q * 16u + j0 + jj) * 16u + (m % 4u) * 4u];
+#pragma unroll
+              for (uint32_t tt = 0; tt < 4; tt++)  // byte tt of each: token 4q + tt
+                qw[tt][k] = ((w[0] >> (8u * tt)) & 0xffu) | (((w[1] >> (8u * tt)) & 0xffu) << 8) |
+                            (((w[2] >> (8u * tt)) & 0xffu) << 16) | (((w[3] >> (8u * tt)) & 0xffu) << 24);
+            }
+          }
+#pragma unroll
+          for (uint32_t tt = 0; tt < 4; tt++) {
+            const uint32_t o = 4u * q + tt;
+            if ((int32_t)o >= n) break;
+            const uint32_t sc = *(const uint16_t*)&t[16u * D + (o * kNb + b) * 2u];
+            uint8_t* dst = (kv ? out_v : out_k) + (row0 + o) * row_bytes + (uint64_t)h * kHeadBytes +
+                           b * 34u;
+            if (b % 2u) {  // the block starts 2 mod 4: scale, then the quants on dword bounds
+              *(uint16_t*)dst = (uint16_t)sc;
+#pragma unroll
+              for (uint32_t k = 0; k < 8; k++) *(uint32_t*)(dst + 2 + 4 * k) = qw[tt][k];
+            } else {  // on a dword bound: scale and two quants, then quants two bytes on
+              *(uint32_t*)dst = sc | (qw[tt][0] << 16);
+#pragma unroll
+              for (uint32_t k = 1; k < 8; k++)
+                *(uint32_t*)(dst + 4 * k) = (qw[tt][k - 1] >> 16) | (qw[tt][k] << 16);
+              *(uint16_t*)(dst + 32) = (uint16_t)(qw[tt][7] >> 16);
+            }
+          }
+        }
+      } else {
+        // f16_to_f32(scale) * (i8 as f32), scalar.rs:268-275: 8 dims a step
+        constexpr uint32_t kPer = 2u * 16u * (D / 8u);
+        for (uint32_t i = threadIdx.x; i < (uint32_t)S::kHpw * kPer; i += 256u) {
+          const uint32_t hl = i / kPer, r = i % kPer;
+          const uint32_t kv = r / (16u * (D / 8u)), o = (r / (D / 8u)) % 16u, c8 = r % (D / 8u);
+          const uint32_t h = h0 + hl;
+          if (h >= g.n_kv_heads || (int32_t)o >= n) continue;
+          const uint8_t* t = lds.q[hl][kv];
+          const float sc =
+              f16_bits_to_f32(*(const uint16_t*)&t[16u * D + (o * (D / 32u) + c8 / 4u) * 2u]);
+          float x[8];
+#pragma unroll
+          for (uint32_t e = 0; e < 8; e++)
+            x[e] = sc * (float)(int8_t)t[q8_quant_offset(kv, o, c8 * 8u + e, D)];
+          float4* dst = (float4*)((kv ? out_v : out_k) + (row0 + o) * row_bytes +
+                                  (uint64_t)h * kHeadBytes + c8 * 32u);
+          dst[0] = make_float4(x[0], x[1], x[2], x[3]);
+          dst[1] = make_float4(x[4], x[5], x[6], x[7]);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// By block table: workgroup (x, y) takes sequence y, block x / head_groups of its table
+// (positions 16j .. 16j + 15, clamped to the context), head group x % head_groups.
+template <int DT, int D, int FMT>
+__global__ void __launch_bounds__(256) gather_tables_tile_kernel(
+    Geom g, uint32_t layer, const int32_t* __restrict__ tables, uint32_t max_blocks,
+    const int32_t* __restrict__ ctx_lens, const int64_t* __restrict__ out_offsets,
+    uint8_t* out_k, uint8_t* out_v) {
+  using S = GatherShape<DT, D>;
+  __shared__ GatherLds<DT, D> lds;
+  const uint32_t hgroups = (g.n_kv_heads + S::kHpw - 1) / S::kHpw;
+  const uint32_t seq = blockIdx.y, j = blockIdx.x / hgroups, hg = blockIdx.x % hgroups;
+  int32_t ctx = ctx_lens[seq];
+  const int32_t cap = (int32_t)(max_blocks * 16u);
+  if (ctx < 0 || ctx > cap) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) raise_fault(g.fault, kFaultCtx);
+    ctx = ctx < 0 ? 0 : cap;
+  }
+  const int32_t n = ctx - (int32_t)j * 16 < 16 ? ctx - (int32_t)j * 16 : 16;
+  if (n <= 0) return;  // uniform over the workgroup
+  const int32_t blk = tables[(uint64_t)seq * max_blocks + j];
+  if ((blk < 0 || (uint64_t)blk >= g.num_blocks) && hg == 0 && threadIdx.x == 0)
+    raise_fault(g.fault, kFaultBlock);
+  gather_tile<DT, D, FMT>(lds, g, layer, blk, hg * S::kHpw, n, out_k, out_v,
+                          (uint64_t)(out_offsets[seq] + (int64_t)j * 16));
+}
+
+// By slot: workgroup x takes input tokens 16w .. 16w + 15 (w = x / head_groups). When
+// they are the 16 slots of one block in order (a sequence read block by block) they go
+// through the tile path; any other window (a partial or scattered one) takes the
+// per-chunk path of gather_slots_kernel for its tokens.
+template <int DT, int D, int FMT>
+__global__ void __launch_bounds__(256) gather_slots_tile_kernel(
+    Geom g, uint32_t layer, const int64_t* __restrict__ slots, uint32_t n_tokens,
+    uint8_t* out_k, uint8_t* out_v) {
+  using S = GatherShape<DT, D>;
+  __shared__ GatherLds<DT, D> lds;
+  __shared__ int32_t s_whole;
+  const uint32_t hgroups = (g.n_kv_heads + S::kHpw - 1) / S::kHpw;
+  const uint32_t win = blockIdx.x / hgroups, hg = blockIdx.x % hgroups;
+  const uint64_t t0 = (uint64_t)win * 16u;
+  const uint64_t cap = g.num_blocks * 16u;
+  if (threadIdx.x == 0) s_whole = 1;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const uint64_t t = t0 + threadIdx.x;
+    const int64_t sl = t < n_tokens ? slots[t] : -1;
+    const int64_t s0 = t0 < n_tokens ? slots[t0] : -1;
+    if (sl < 0 || (uint64_t)sl >= cap || s0 < 0 || s0 % 16 != 0 || sl != s0 + (int64_t)threadIdx.x)
+      s_whole = 0;
+  }
+  __syncthreads();
+  if (s_whole) {
+    gather_tile<DT, D, FMT>(lds, g, layer, slots[t0] / 16, hg * S::kHpw, 16, out_k, out_v, t0);
+    return;
+  }
+  constexpr uint32_t kCv = DT == kDtypeQ8 ? 32u : 8u;  // values per chunk
+  constexpr uint32_t kCpr = D / kCv;
+  constexpr uint64_t kHeadBytes = FMT == kFmtF32 ? (uint64_t)D * 4u
+                                  : DT == kDtypeF16      ? (uint64_t)D * 2u
+                                                         : (uint64_t)D / 32u * 34u;
+  const uint32_t units = 16u * 2u * S::kHpw * kCpr;
+  for (uint32_t i = threadIdx.x; i < units; i += 256u) {
+    const uint32_t o = i / (2u * S::kHpw * kCpr), r = i % (2u * S::kHpw * kCpr);
+    const uint32_t kv = r / (S::kHpw * kCpr), hl = (r / kCpr) % S::kHpw, c = r % kCpr;
+    const uint32_t h = hg * S::kHpw + hl;
+    const uint64_t t = t0 + o;
+    if (t >= n_tokens || h >= g.n_kv_heads) continue;
+    const int64_t slot = slots[t];
+    if (slot < 0) continue;
+    if ((uint64_t)slot >= cap) {
+      if (hg == 0 && r == 0) raise_fault(g.fault, kFaultSlot);
+      continue;
+    }
+    uint8_t* row = (kv ? out_v : out_k) + (t * g.n_kv_heads + h) * kHeadBytes;
+    gather_chunk(g, layer, (uint64_t)slot / 16u, (uint32_t)((uint64_t)slot % 16u), kv, h, c, FMT,
+                 row, true);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // copy_blocks / fill / device copy
 // ---------------------------------------------------------------------------
 
@@ -741,7 +1017,7 @@ hipError_t launch_append(const Geom& g, uint32_t layer, const float* k, const fl
       append_q8_kernel<false><<<grid_for(units), 256, 0, s>>>(g, layer, k, v, slots, n_tokens);
   } else if (g.dtype == kDtypeF16 && g.block_size == 16 && (g.head_dim == 64 || g.head_dim == 128) &&
              aligned) {
-    const uint32_t hpw = g.head_dim == 128 ? 1u : 2u;
+    const uint32_t hpw = gather_heads_per_wg(g.dtype, g.head_dim);
     const uint64_t wgs = ((uint64_t)n_tokens + 15u) / 16u * ((g.n_kv_heads + hpw - 1) / hpw);
     if (wgs > 0x7fffffffull) return hipErrorInvalidValue;
     if (g.head_dim == 128)
@@ -803,10 +1079,45 @@ __global__ void __launch_bounds__(256) gather_slots_scalar_kernel(Geom g, uint32
   }
 }
 
+// The tile path's shapes: F16 or Q8_0, block size 16, head_dim 64 or 128, 16-byte
+// aligned outputs.
+static bool gather_tile_ok(const Geom& g, const void* out_k, const void* out_v) {
+  return (g.dtype == kDtypeF16 || g.dtype == kDtypeQ8) && g.block_size == 16 &&
+         (g.head_dim == 64 || g.head_dim == 128) && (uintptr_t)out_k % 16 == 0 &&
+         (uintptr_t)out_v % 16 == 0;
+}
+
+#define FKV_GATHER_TILE_DISPATCH(KERNEL, GRID, ...)                                    \
+  do {                                                                                  \
+    const bool raw = format == kFmtRaw;                                                 \
+    if (g.dtype == kDtypeF16 && g.head_dim == 128) {                                    \
+      if (raw) KERNEL<kDtypeF16, 128, kFmtRaw><<<GRID, 256, 0, s>>>(__VA_ARGS__);       \
+      else KERNEL<kDtypeF16, 128, kFmtF32><<<GRID, 256, 0, s>>>(__VA_ARGS__);           \
+    } else if (g.dtype == kDtypeF16) {                                                  \
+      if (raw) KERNEL<kDtypeF16, 64, kFmtRaw><<<GRID, 256, 0, s>>>(__VA_ARGS__);        \
+      else KERNEL<kDtypeF16, 64, kFmtF32><<<GRID, 256, 0, s>>>(__VA_ARGS__);            \
+    } else if (g.head_dim == 128) {                                                     \
+      if (raw) KERNEL<kDtypeQ8, 128, kFmtRaw><<<GRID, 256, 0, s>>>(__VA_ARGS__);        \
+      else KERNEL<kDtypeQ8, 128, kFmtF32><<<GRID, 256, 0, s>>>(__VA_ARGS__);            \
+    } else {                                                                            \
+      if (raw) KERNEL<kDtypeQ8, 64, kFmtRaw><<<GRID, 256, 0, s>>>(__VA_ARGS__);         \
+      else KERNEL<kDtypeQ8, 64, kFmtF32><<<GRID, 256, 0, s>>>(__VA_ARGS__);             \
+    }                                                                                   \
+  } while (0)
+
 hipError_t launch_gather_slots(const Geom& g, uint32_t layer, const int64_t* slots,
                                uint32_t n_tokens, int format, void* out_k, void* out_v,
                                hipStream_t s) {
   if (n_tokens == 0) return hipSuccess;
+  if (gather_tile_ok(g, out_k, out_v)) {
+    const uint32_t hpw = g.head_dim == 128 ? 1u : 2u;
+    const uint64_t wgs = ((uint64_t)n_tokens + 15u) / 16u * ((g.n_kv_heads + hpw - 1) / hpw);
+    if (wgs > 0x7fffffffull) return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)wgs);
+    FKV_GATHER_TILE_DISPATCH(gather_slots_tile_kernel, grid, g, layer, slots, n_tokens,
+                             (uint8_t*)out_k, (uint8_t*)out_v);
+    return hipGetLastError();
+  }
   if (g.dtype != kDtypeQ8 && g.head_dim % 8 != 0) {
     uint64_t units = (uint64_t)n_tokens * 2u * g.n_kv_heads * g.head_dim;
     gather_slots_scalar_kernel<<<grid_for(units), 256, 0, s>>>(
@@ -827,6 +1138,15 @@ hipError_t launch_gather_tables(const Geom& g, uint32_t layer, const int32_t* ta
                                 uint32_t max_ctx_len, int format, void* out_k, void* out_v,
                                 hipStream_t s) {
   if (n_seqs == 0 || max_ctx_len == 0) return hipSuccess;
+  if (gather_tile_ok(g, out_k, out_v)) {
+    const uint32_t hpw = gather_heads_per_wg(g.dtype, g.head_dim);
+    const uint64_t wgs = ((uint64_t)max_ctx_len + 15u) / 16u * ((g.n_kv_heads + hpw - 1) / hpw);
+    if (wgs > 0x7fffffffull) return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)wgs, n_seqs);
+    FKV_GATHER_TILE_DISPATCH(gather_tables_tile_kernel, grid, g, layer, tables, max_blocks,
+                             ctx_lens, out_offsets, (uint8_t*)out_k, (uint8_t*)out_v);
+    return hipGetLastError();
+  }
   const bool aligned = ((uintptr_t)out_k % 16 == 0) && ((uintptr_t)out_v % 16 == 0);
   uint32_t cv = g.dtype == kDtypeQ8 ? 32u : 8u;
   uint64_t units = (uint64_t)max_ctx_len * 2u * g.n_kv_heads * (g.head_dim / cv);
