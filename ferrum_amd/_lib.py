@@ -34,6 +34,11 @@ ROUND_HALF_AWAY = 1
 GATHER_F32 = 0
 GATHER_RAW = 1
 
+TUNE_ATTN_SPLIT_TOKENS = 0
+TUNE_ATTN_STREAM = 1
+TUNE_ATTN_ORDER = 2
+TUNE_PREFILL_SPLIT_BLOCKS = 3
+
 FAULT_SLOT_RANGE = 1
 FAULT_BLOCK_RANGE = 2
 FAULT_CTX_RANGE = 4
@@ -98,6 +103,7 @@ SIGNATURES = {
     "fkv_paged_get_info": (i32, [c_void_p, P(PagedInfoC)]),
     "fkv_paged_take_fault_flags": (i32, [c_void_p, c_void_p, P(u32)]),
     "fkv_paged_marked_blocks": (i32, [c_void_p, c_void_p, P(u64)]),
+    "fkv_set_tuning": (i32, [i32, i64]),
     "fkv_paged_fill": (i32, [c_void_p, ctypes.c_uint8, c_void_p]),
     "fkv_paged_read": (i32, [c_void_p, u64, u64, c_void_p, c_void_p]),
     "fkv_paged_write": (i32, [c_void_p, u64, u64, c_void_p, c_void_p]),

@@ -114,6 +114,32 @@ int32_t fkv_abi_version(void) { return FKV_ABI_VERSION; }
 
 const char* fkv_last_error(void) { return g_last_error.c_str(); }
 
+int32_t fkv_set_tuning(int32_t knob, int64_t value) {
+  fkv::Tuning& t = fkv::tuning();
+  switch (knob) {
+    case FKV_TUNE_ATTN_SPLIT_TOKENS:
+      if (value != 0 && (value < 16 || value % 16 != 0 || value > (1 << 20)))
+        return fail(FKV_ERR_INVALID, "split tokens must be 0 or a multiple of 16 up to 2^20");
+      t.split_tokens.store((int32_t)value);
+      return ok();
+    case FKV_TUNE_ATTN_STREAM:
+      if (value != 0 && value != 1) return fail(FKV_ERR_INVALID, "stream mode must be 0 or 1");
+      t.stream_mode.store((int32_t)value);
+      return ok();
+    case FKV_TUNE_ATTN_ORDER:
+      if (value < -1 || value > 2) return fail(FKV_ERR_INVALID, "order must be -1, 0, 1 or 2");
+      t.attn_order.store((int32_t)value);
+      return ok();
+    case FKV_TUNE_PREFILL_SPLIT_BLOCKS:
+      if (value < -1 || value > 0x7fffffffll)
+        return fail(FKV_ERR_INVALID, "prefill split blocks must be -1 or a block count");
+      t.prefill_split.store(value);
+      return ok();
+    default:
+      return fail(FKV_ERR_INVALID, "unknown tuning knob");
+  }
+}
+
 int32_t fkv_device_count(void) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess) return 0;

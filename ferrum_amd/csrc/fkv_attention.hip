@@ -53,24 +53,24 @@ void* static_scratch(int device) {
   return g_scratch_addr[device].load(std::memory_order_acquire);
 }
 
-const Tuning& tuning() {
-  static const Tuning t = [] {
-    Tuning r;
+Tuning& tuning() {
+  static Tuning t;
+  static std::once_flag seeded;
+  std::call_once(seeded, [] {
     if (const char* e = getenv("FKV_ATTN_SPLIT_TOKENS")) {
       const long v = strtol(e, nullptr, 10);
-      if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) r.split_tokens = (int32_t)v;
+      if (v >= 16 && v % 16 == 0 && v <= (1 << 20)) t.split_tokens = (int32_t)v;
     }
-    if (const char* e = getenv("FKV_ATTN_MODE")) r.stream_mode = strcmp(e, "stream") == 0;
+    if (const char* e = getenv("FKV_ATTN_MODE")) t.stream_mode = strcmp(e, "stream") == 0;
     if (const char* e = getenv("FKV_ATTN_ORDER")) {
       const long v = strtol(e, nullptr, 10);
-      if (v >= 0 && v <= 2) r.attn_order = (int32_t)v;
+      if (v >= 0 && v <= 2) t.attn_order = (int32_t)v;
     }
     if (const char* e = getenv("FKV_PREFILL_SPLIT_BLOCKS")) {
       const long long v = strtoll(e, nullptr, 10);
-      if (v >= 0) r.prefill_split = v;
+      if (v >= 0) t.prefill_split = v;
     }
-    return r;
-  }();
+  });
   return t;
 }
 
@@ -602,7 +602,7 @@ inline uint64_t align256(uint64_t x) { return (x + 255) / 256 * 256; }
 // 64 per head (1 x 576 tokens, 4 KV heads: 64 tokens, 9.7 us per call against
 // 13.8 us at 512). FKV_ATTN_SPLIT_TOKENS (a multiple of 16) overrides.
 uint32_t choose_split_tokens(uint32_t max_ctx_len, uint32_t n_seqs, uint32_t n_kv_heads) {
-  if (tuning().split_tokens) return (uint32_t)tuning().split_tokens;
+  if (const int32_t v = tuning().split_tokens.load(std::memory_order_relaxed)) return (uint32_t)v;
   const uint64_t segs = (uint64_t)n_seqs * (n_kv_heads ? n_kv_heads : 1);
   const uint64_t by_items = (uint64_t)max_ctx_len * segs / 2048;
   const uint64_t by_head = ((uint64_t)max_ctx_len + 63) / 64;
@@ -621,7 +621,7 @@ AttnPlan plan_attention(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32
   const uint32_t G = g.n_kv_heads ? n_heads / g.n_kv_heads : 0;
   // F16: the split kernel by default; FKV_ATTN_MODE=stream selects the persistent one.
   if (g.dtype == kDtypeF16 && G >= 1 && G <= 16 && stream_attention_supported(n_seqs) &&
-      tuning().stream_mode) {
+      tuning().stream_mode.load(std::memory_order_relaxed)) {
     p.stream_waves = stream_attention_waves(g.head_dim, n_seqs, g.n_cus);
     if (p.stream_waves > 0) {
       p.stream_path = true;

@@ -2221,8 +2221,8 @@ PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint3
   // of at least kPrefillMinPieceBlocks. FKV_PREFILL_SPLIT_BLOCKS sets the piece length
   // (0: no split).
   uint64_t split = 0;
-  if (tuning().prefill_split >= 0) {
-    split = (uint64_t)tuning().prefill_split;
+  if (const int64_t v = tuning().prefill_split.load(std::memory_order_relaxed); v >= 0) {
+    split = (uint64_t)v;
   } else {
     const uint64_t cus = g.n_cus;
     const uint64_t wgs = (uint64_t)n_seqs * g.n_kv_heads * p.tile_groups;
@@ -2314,7 +2314,7 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
   uint32_t order = n_seqs <= kOrderSortSeqs   ? kOrderLongestFirst
                    : n_seqs <= kOrderMaxSeqs ? kOrderFullFirst
                                              : kOrderGrid;
-  if (const int32_t v = tuning().attn_order; v >= 0) {
+  if (const int32_t v = tuning().attn_order.load(std::memory_order_relaxed); v >= 0) {
     if (v == 0 || (v == 1 && n_seqs <= kOrderMaxSeqs) || (v == 2 && n_seqs <= kOrderSortSeqs))
       order = (uint32_t)v;
   }

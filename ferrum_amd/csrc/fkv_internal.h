@@ -5,6 +5,7 @@
 #include <hip/hip_runtime_api.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <string>
 
 namespace fkv {
@@ -49,19 +50,20 @@ struct Geom {
   uint32_t n_cus;    // compute units of the pool's device (read once, at creation)
 };
 
-// Overrides of the launch planners for measurements, read from the environment once per
-// process (the first call that plans a launch), not per call:
+// Overrides of the launch planners for measurements and tests (fkv_set_tuning), seeded
+// from the environment once per process:
 //   FKV_ATTN_SPLIT_TOKENS   decode split length (a multiple of 16)
 //   FKV_ATTN_MODE=stream    F16 decode on the persistent kernel
 //   FKV_ATTN_ORDER          decode work order (0 grid, 1 full splits first, 2 longest first)
 //   FKV_PREFILL_SPLIT_BLOCKS  prefill key-range piece length in blocks (0: no pieces)
+// Read with relaxed loads per launch plan (no environment access per call).
 struct Tuning {
-  int32_t split_tokens = 0;      // 0: the planner's rule
-  bool stream_mode = false;
-  int32_t attn_order = -1;       // -1: the planner's rule
-  int64_t prefill_split = -1;    // -1: the planner's rule
+  std::atomic<int32_t> split_tokens{0};    // 0: the planner's rule
+  std::atomic<int32_t> stream_mode{0};
+  std::atomic<int32_t> attn_order{-1};     // -1: the planner's rule
+  std::atomic<int64_t> prefill_split{-1};  // -1: the planner's rule
 };
-const Tuning& tuning();
+Tuning& tuning();
 
 constexpr int kDtypeF32 = 0;
 constexpr int kDtypeF16 = 1;

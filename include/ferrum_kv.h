@@ -114,6 +114,24 @@ int32_t fkv_abi_version(void);
  * this read cannot clear it. */
 const char* fkv_last_error(void);
 
+/* Overrides of the launch planners, for measurements and tests; no counterpart in the
+ * reference (its CPU loops have nothing to plan). Process-wide: a launch planned while
+ * another thread changes a knob sees the old or the new value. The environment variables
+ * in brackets seed the values when the library first plans a launch.
+ *   FKV_TUNE_ATTN_SPLIT_TOKENS     decode split length, a multiple of 16 up to 2^20;
+ *                                  0: the planner's rule [FKV_ATTN_SPLIT_TOKENS]
+ *   FKV_TUNE_ATTN_STREAM           1: F16 decode on the persistent kernel [FKV_ATTN_MODE=stream]
+ *   FKV_TUNE_ATTN_ORDER            decode work order 0 grid, 1 full splits first, 2 longest
+ *                                  first; -1: the planner's rule [FKV_ATTN_ORDER]
+ *   FKV_TUNE_PREFILL_SPLIT_BLOCKS  prefill key-range piece length in blocks, 0 no pieces;
+ *                                  -1: the planner's rule [FKV_PREFILL_SPLIT_BLOCKS]
+ * Out-of-range values: FKV_ERR_INVALID, nothing changed. */
+#define FKV_TUNE_ATTN_SPLIT_TOKENS 0
+#define FKV_TUNE_ATTN_STREAM 1
+#define FKV_TUNE_ATTN_ORDER 2
+#define FKV_TUNE_PREFILL_SPLIT_BLOCKS 3
+int32_t fkv_set_tuning(int32_t knob, int64_t value);
+
 /* Number of visible HIP devices (0 when no GPU); never fails. */
 int32_t fkv_device_count(void);
 

@@ -24,3 +24,24 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture
+def tune():
+    """Planner overrides through fkv_set_tuning for one test: tune(attn_order=0,
+    attn_stream=1, attn_split_tokens=..., prefill_split_blocks=...); every knob the test
+    set goes back to the planner's own rule afterwards."""
+    import ferrum_amd as fa
+    knobs = {"attn_split_tokens": (fa.TUNE_ATTN_SPLIT_TOKENS, 0),
+             "attn_stream": (fa.TUNE_ATTN_STREAM, 0),
+             "attn_order": (fa.TUNE_ATTN_ORDER, -1),
+             "prefill_split_blocks": (fa.TUNE_PREFILL_SPLIT_BLOCKS, -1)}
+    touched = set()
+
+    def set_knobs(**kw):
+        for name, value in kw.items():
+            fa.set_tuning(knobs[name][0], int(value))
+            touched.add(name)
+    yield set_knobs
+    for name in touched:
+        fa.set_tuning(*knobs[name])

@@ -114,3 +114,18 @@ def test_static_scratch_size_matches_the_header():
     m = re.search(r"#define FKV_STATIC_SCRATCH_BYTES \((\d+)ull << (\d+)\)", text)
     assert m, "FKV_STATIC_SCRATCH_BYTES missing from ferrum_kv.h"
     assert int(m.group(1)) << int(m.group(2)) == _lib.STATIC_SCRATCH_BYTES
+
+
+def test_set_tuning_checks_its_arguments():
+    lib = _lib.load()
+    assert lib.fkv_set_tuning(99, 0) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_set_tuning(_lib.TUNE_ATTN_SPLIT_TOKENS, 24) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_set_tuning(_lib.TUNE_ATTN_ORDER, 3) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_set_tuning(_lib.TUNE_ATTN_STREAM, 2) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_set_tuning(_lib.TUNE_PREFILL_SPLIT_BLOCKS, -2) == _lib.FKV_ERR_INVALID
+    for knob, value, default in ((_lib.TUNE_ATTN_SPLIT_TOKENS, 512, 0),
+                                 (_lib.TUNE_ATTN_ORDER, 1, -1),
+                                 (_lib.TUNE_ATTN_STREAM, 1, 0),
+                                 (_lib.TUNE_PREFILL_SPLIT_BLOCKS, 7, -1)):
+        assert lib.fkv_set_tuning(knob, value) == _lib.FKV_OK
+        assert lib.fkv_set_tuning(knob, default) == _lib.FKV_OK

@@ -55,13 +55,13 @@ SHAPES = [(1, 128, 4), (1, 128, 8), (1, 64, 8), (1, 128, 1), (1, 64, 2), (1, 128
 
 
 @pytest.fixture(params=["split", "stream"])
-def f16_schedule(request, monkeypatch):
-    """F16 runs on the MFMA split kernel by default; FKV_ATTN_MODE=stream selects
-    the persistent schedule. Both must meet the same bar."""
+def f16_schedule(request, tune):
+    """F16 runs on the MFMA split kernel by default; the stream knob of fkv_set_tuning
+    selects the persistent schedule. Both must meet the same bar."""
     if request.param == "stream":
-        monkeypatch.setenv("FKV_ATTN_MODE", "stream")
+        tune(attn_stream=1)
     else:
-        monkeypatch.delenv("FKV_ATTN_MODE", raising=False)
+        tune(attn_stream=0)
     return request.param
 
 
@@ -107,9 +107,9 @@ ORDER_CTXS = [0, 1, 511, 512, 513, 1024, 1500, 3000, 17, 4100, 0, 2048, 700]
 
 
 @pytest.mark.parametrize("dtype", [1, 8])
-def test_work_orders_are_bit_identical(dtype, monkeypatch):
+def test_work_orders_are_bit_identical(dtype, tune):
     """The split kernel's workgroups take the (sequence, KV head, split) items in
-    grid order, full-first order or longest-first order (FKV_ATTN_ORDER=0/1/2).
+    grid order, full-first order or longest-first order (fkv_set_tuning order 0/1/2).
     An item is computed the same way whichever workgroup takes it, so the three
     outputs agree bit for bit; empty contexts, contexts of whole splits and a
     9-split context are in the batch."""
@@ -120,7 +120,7 @@ def test_work_orders_are_bit_identical(dtype, monkeypatch):
     q = np.random.default_rng(8).standard_normal((len(ORDER_CTXS), hkv * g, d), dtype=np.float32)
     outs = []
     for order in ("0", "1", "2"):
-        monkeypatch.setenv("FKV_ATTN_ORDER", order)
+        tune(attn_order=order)
         outs.append(_run(pool, 0, q, tab, ORDER_CTXS))
     assert pool.take_fault_flags() == 0
     assert np.all(outs[0][0] == 0.0) and np.all(outs[0][10] == 0.0)
@@ -132,13 +132,13 @@ def test_work_orders_are_bit_identical(dtype, monkeypatch):
 
 
 @pytest.mark.parametrize("order", ["0", "1", "2"])
-def test_context_outside_the_table_is_flagged(order, monkeypatch):
+def test_context_outside_the_table_is_flagged(order, tune):
     """A context length past the table row (or negative) raises FKV_FAULT_CTX_RANGE in
     every work order; the sequence is read up to the row's end (or not at all, with
     a zero output) and the other sequences are unaffected."""
     import ferrum_amd as fa
     from oracle import ref
-    monkeypatch.setenv("FKV_ATTN_ORDER", order)
+    tune(attn_order=order)
     ctxs = [40, 1100, 600]
     pool, layout, tab = _build(1, 128, 2, ctxs, seed=6, layers=1)
     cap = tab.shape[1] * 16
@@ -158,7 +158,7 @@ def test_context_outside_the_table_is_flagged(order, monkeypatch):
 
 
 @pytest.mark.parametrize("dtype,order", [(1, "0"), (1, "1"), (1, "2"), (8, "2"), (0, "2")])
-def test_context_past_max_ctx_len_is_flagged(dtype, order, monkeypatch):
+def test_context_past_max_ctx_len_is_flagged(dtype, order, tune):
     """A device context longer than the call's max_ctx_len (but inside the table row)
     is clamped to what the launch's splits hold (512 here for every path: 64-token
     splits on the matrix cores, 256-token partitions on F32) and raises
@@ -167,7 +167,7 @@ def test_context_past_max_ctx_len_is_flagged(dtype, order, monkeypatch):
     other sequences are unaffected."""
     import ferrum_amd as fa
     from oracle import ref
-    monkeypatch.setenv("FKV_ATTN_ORDER", order)
+    tune(attn_order=order)
     ctxs = [40, 300, 1100]
     pool, layout, tab = _build(dtype, 128, 2, ctxs, seed=11, layers=1)
     q = np.random.default_rng(3).standard_normal((3, 8, 128), dtype=np.float32)
@@ -184,7 +184,7 @@ def test_context_past_max_ctx_len_is_flagged(dtype, order, monkeypatch):
 
 
 @pytest.mark.parametrize("n_seqs", [300, 1100])
-def test_large_batches_match_oracle(n_seqs, monkeypatch):
+def test_large_batches_match_oracle(n_seqs, tune):
     """300 sequences take the full-first order (three or fewer per thread of the
     ranking), 1,100 the grid order; both against the oracle and the grid order."""
     import ferrum_amd as fa
@@ -193,9 +193,9 @@ def test_large_batches_match_oracle(n_seqs, monkeypatch):
     ctxs = [int(c) for c in np.random.default_rng(n_seqs).integers(0, 1100, n_seqs)]
     pool, layout, tab = _build(1, d, hkv, ctxs, seed=2, layers=1)
     q = np.random.default_rng(4).standard_normal((n_seqs, hkv * g, d), dtype=np.float32)
-    monkeypatch.delenv("FKV_ATTN_ORDER", raising=False)
+    tune(attn_order=-1)
     got = _run(pool, 0, q, tab, ctxs)
-    monkeypatch.setenv("FKV_ATTN_ORDER", "0")
+    tune(attn_order="0")
     grid = _run(pool, 0, q, tab, ctxs)
     assert pool.take_fault_flags() == 0
     assert np.array_equal(got.view(np.uint32), grid.view(np.uint32))

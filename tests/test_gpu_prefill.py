@@ -15,7 +15,7 @@ output rows outside the chunk are never written. Also:
   FKV_FAULT_BLOCK_RANGE and its block is skipped, other sequences unaffected;
 - Q8_0 pools, with ordinary values and with values up to +-1e6 (the exact instance);
 - key ranges cut into pieces (the workspace path, down to one-block pieces through
-  FKV_PREFILL_SPLIT_BLOCKS) and read whole (no workspace): both meet the bar, every
+  fkv_set_tuning's prefill piece knob) and read whole (no workspace): both meet the bar, every
   instance.
 """
 import numpy as np
@@ -124,11 +124,11 @@ def test_prefill_with_one_query_is_decode():
 
 @pytest.mark.parametrize("pieces", [1, 3, 7])
 @pytest.mark.parametrize("dtype,g", [(1, 4), (8, 4), (1, 16), (1, 1)])
-def test_prefill_small_pieces(dtype, g, pieces, monkeypatch):
+def test_prefill_small_pieces(dtype, g, pieces, tune):
     """Key ranges cut into pieces of `pieces` blocks (at most 32 a workgroup, so longer
     ranges get longer pieces): odd and one-block pieces, pieces past a wave's own
     causal end, ranges shorter than one piece; against the oracle."""
-    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
+    tune(prefill_split_blocks=pieces)
     hkv, d = 2, 128
     ctxs = [3, 16, 33, 190, 520, 1029]
     qls = [3, 9, 33, 61, 200, 17]
@@ -183,13 +183,13 @@ def test_prefill_c3_chunk_shape(dtype):
 @pytest.mark.parametrize("pieces", [0, 1, 2])
 @pytest.mark.parametrize("g", [4, 1, 16])
 @pytest.mark.parametrize("bad", [np.nan, np.inf, -np.inf])
-def test_nonfinite_v_reaches_only_later_queries(bad, g, pieces, d, monkeypatch):
+def test_nonfinite_v_reaches_only_later_queries(bad, g, pieces, d, tune):
     """V of position p0 + 9 of a fresh 40-token chunk (and of position 3 of a chunk after
     100 tokens of history) holds an Inf/NaN in a few dims: queries before it must be
     finite, the ones at or after it what the oracle gives; with whole key ranges (0)
     and with pieces of 1 and 2 blocks; head_dim 128 and 64 (the staged V tiles' chunks
     fall differently over the two staging slots)."""
-    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
+    tune(prefill_split_blocks=pieces)
     hkv = 2
     ctxs, qls = [40, 140], [40, 40]
     marks = [(0, 9), (1, 100 + 3)]
@@ -276,12 +276,12 @@ def test_leak_safe_instance_on_finite_data():
 
 
 @pytest.mark.parametrize("pieces", [0, 3])
-def test_q_len_past_max_q_len_is_clamped_and_flagged(pieces, monkeypatch):
+def test_q_len_past_max_q_len_is_clamped_and_flagged(pieces, tune):
     """Sequence 1 says 300 queries but the call's max_q_len is 200: its first 200 rows are
     computed, the rest untouched, FKV_FAULT_CTX_RANGE raised; sequence 0 is unaffected
     (whole key ranges, and 3-block pieces merged under the same clamp)."""
     import ferrum_amd as fa
-    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
+    tune(prefill_split_blocks=pieces)
     hkv, g, d = 2, 4, 128
     ctxs, qls = [150, 500], [150, 300]
     pool, layout, tab = _pool(d, hkv, ctxs, seed=51)
@@ -296,13 +296,13 @@ def test_q_len_past_max_q_len_is_clamped_and_flagged(pieces, monkeypatch):
 
 @pytest.mark.parametrize("dtype", [1, 8])
 @pytest.mark.parametrize("pieces", [0, 3])
-def test_table_entry_outside_the_pool_is_flagged_and_skipped(dtype, pieces, monkeypatch):
+def test_table_entry_outside_the_pool_is_flagged_and_skipped(dtype, pieces, tune):
     """Two of sequence 1's table entries point outside the pool (-1 and past the last
     block): FKV_FAULT_BLOCK_RANGE is raised, those blocks are skipped (no read outside the
     pool; the rows stay finite), sequence 0 still matches the oracle, and rows outside the
     chunks are untouched. F16 and Q8_0, whole key ranges and 3-block pieces."""
     import ferrum_amd as fa
-    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
+    tune(prefill_split_blocks=pieces)
     hkv, g, d = 2, 4, 128
     ctxs, qls = [100, 70], [20, 30]
     pool, layout, tab = _pool(d, hkv, ctxs, seed=61, dtype=dtype)
@@ -322,17 +322,46 @@ def test_table_entry_outside_the_pool_is_flagged_and_skipped(dtype, pieces, monk
     assert np.all(got[0] == 5.0) and np.all(got[rows - 1] == 5.0)
 
 
+def _term_sums(layout, image, q, tab, ctxs, qls, offs, scale):
+    """sum_p |w_p * V[p][d]| per output value, in f64 from the pool's decoded K/V (the
+    reference's f32 dequantisation, scalar.rs:268-275) and f64 softmax weights: the size
+    of the terms an output is the sum of, which bounds what rounding the terms can do."""
+    from oracle import ref
+    ctx = np.array(ctxs, np.int32)
+    kk, vv, koffs = ref.gather_tables(layout, image, 0, tab, ctx, 0)
+    hq, d = q.shape[1], q.shape[2]
+    g = hq // layout.n_kv_heads
+    out = np.zeros(q.shape, np.float64)
+    for s, (c, ql, o) in enumerate(zip(ctxs, qls, offs)):
+        ks = kk[koffs[s]:koffs[s] + c].astype(np.float64)
+        vs = np.abs(vv[koffs[s]:koffs[s] + c].astype(np.float64))
+        for h in range(hq):
+            qq = q[o:o + ql, h].astype(np.float64)            # [ql, d]
+            sc = qq @ ks[:, h // g].T * scale                  # [ql, c]
+            pos = c - ql + np.arange(ql)
+            sc[np.arange(c)[None, :] > pos[:, None]] = -np.inf
+            w = np.exp(sc - sc.max(1, keepdims=True))
+            w /= w.sum(1, keepdims=True)
+            out[o:o + ql, h] = w @ vs[:, h // g]
+    return out
+
+
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("pieces", [0, 5])
-def test_q8_prefill_with_wide_values(pieces, d, monkeypatch):
-    """Q8_0 K and V with +-1e6 values (scales ~7,874): the blocks are marked and the exact
-    instance computes, with whole key ranges and with 5-block pieces; q is small enough
-    that the scores stay O(1); head_dim 128 and 64. With 64 dims a dim of V holds ~11
-    outliers in the longer context, and with both signs they cancel in some outputs to
-    ~1e-6 of their own size: there a difference of an f32 rounding in the weights (1e-7
-    of 1e6) exceeds the elementwise 1e-2 bar whatever computes it, so at head_dim 64
-    the V outliers are positive (K's keep both signs)."""
-    monkeypatch.setenv("FKV_PREFILL_SPLIT_BLOCKS", str(pieces))
+def test_q8_prefill_with_wide_values(pieces, d, tune):
+    """Q8_0 K and V with +-1e6 values of both signs (scales ~7,874): the blocks are
+    marked and the exact instance computes, with whole key ranges and with 5-block
+    pieces; q is small enough that the scores stay O(1); head_dim 128 and 64.
+
+    The exact instance forms each weight x V scale in f32 and carries it as bf16 hi + lo
+    (16 significant bits) against the int8 V, so every term of an output is exact to
+    2^-16 of itself. With 64 dims a dim of V holds ~11 outliers in the longer context,
+    and outliers of both signs cancel some outputs to ~1e-6 of their terms, below any
+    bar relative to the output alone. The bar is the elementwise one plus 2^-16 of the
+    sum of the terms' magnitudes (sum_p |w_p V_p|, computed in f64 from the decoded
+    K/V), the rounding the terms are allowed."""
+    tune(prefill_split_blocks=pieces)
+    import ferrum_amd as fa
     hkv, g = 2, 4
     ctxs, qls = [300, 700], [300, 200]
 
@@ -342,8 +371,6 @@ def test_q8_prefill_with_wide_values(pieces, d, monkeypatch):
         for x in (k, v):
             idx = rng.integers(0, d, size=(n, hkv))
             big = rng.choice([-1e6, 1e6], size=(n, hkv, 1))
-            if x is v and d < 128:
-                big = np.abs(big)
             np.put_along_axis(x, idx[..., None], big, -1)
         return k, v
     pool, layout, tab = _pool(d, hkv, ctxs, seed=61, dtype=8, kv=kv)
@@ -353,7 +380,14 @@ def test_q8_prefill_with_wide_values(pieces, d, monkeypatch):
     assert pool.take_fault_flags() == 0
     want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
     assert np.abs(want).max() > 1e3
-    assert_close(got, want, what="q8 wide prefill")
+    terms = _term_sums(layout, pool.read(), q, tab, ctxs, qls, offs, fa.default_scale(d))
+    err = np.abs(got.astype(np.float64) - want)
+    lim = 2e-3 + 1e-2 * np.abs(want) + 2.0 ** -16 * terms
+    assert np.all(err <= lim), (f"q8 wide prefill: {(err > lim).sum()} values out of tolerance, "
+                                f"max err/lim {np.max(err / lim):.3f}")
+    # the outliers cancel in some outputs: the elementwise bar alone would not hold there
+    cancel = np.abs(want) < 1e-3 * terms
+    assert cancel.any()
 
 
 def test_prefill_rejects_f32_pools():
