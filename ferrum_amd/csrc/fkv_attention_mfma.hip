@@ -1610,37 +1610,24 @@ constexpr int prefill_tile_bytes() {
 }
 
 enum : int { kPfFast = 0, kPfExact = 1, kPfLeakSafe = 2 };
-// F16 V tiles of a prefill step in LDS: the step's two blocks interleaved by 16-dim
-// chunks of 512 bytes, chunk m of block b at byte ((m % NMH) * 2 + b) * 512 of the V area
-// of staging slot m / NMH (NMH = D/32 chunks a slot). So the 8 bytes a lane takes from
-// each block for the paired P.V operand are 512 bytes apart, the pair a
-// ds_read2st64_b64 gives. In a chunk, dim 16m + col has 32 bytes (16 tokens) whose four
-// 8-byte slots (token groups) are permuted by bits 2-3 of col: the LDS serves a 64-bit
-// read 16 lanes a clock over 32 banks, the lanes of one token group read cols 0..15,
-// 4 to 128 bytes, and the permutation puts cols c, c+4, c+8 and c+12 on different
-// slots. Byte offset of (chunk m, block b, col, token group grp) from the first slot's
-// V area:
-template <int NMH, int KBLK>
-__device__ __forceinline__ uint32_t pf_vi_off(uint32_t m, uint32_t b, uint32_t col, uint32_t grp) {
-  return (m / NMH) * KBLK + ((m % NMH) * 2u + b) * 512u + col * 32u +
-         ((grp ^ ((col >> 2) & 3u)) * 8u);
+// F16 tiles of a prefill step in LDS, both loaded 16 bytes a lane (a block is 4 K and
+// 4 V load instructions at head_dim 128):
+// - K: the stored [D/8][B][8] layout with the 16 token rows of each 8-dim run permuted,
+//   token t at row pf_k_row(t, b) for the step's block b (bits 2 and 3 of t swapped, then
+//   bit 3 flipped for the second block). Rows 0-7 of a run then hold tokens 0-3 and
+//   8-11 of the first block, and the score MFMAs read their K operands as runs of 8
+//   consecutive rows (below).
+// - V: the stored [D][B] layout as 16-byte halves (dim n, tokens 8h .. 8h + 7), half
+//   (n, h) at unit pf_v_unit(n, h) = 2n + (h ^ x) with x = bit 2 ^ bit 3 of n. The P.V
+//   operand of lane (col, grp) is one half (dim 16m + col, h = grp % 2) of block grp / 2;
+//   the swap puts the 8 (or 16) lanes an LDS read serves a clock on distinct banks.
+__device__ __forceinline__ uint32_t pf_swap23(uint32_t t) {
+  return (t & 3u) | ((t & 4u) << 1) | ((t & 8u) >> 1);
 }
-// Block b's V direct loads of wave w, k < K: 4 bytes a lane, instruction k = dims
-// 8(4k + w) .. +7, i.e. half w % 2 of chunk 2k + w/2, from source offset voff + k*1024.
-// The instruction's immediate offset (a constant, hence the recursion) is added to the
-// LDS address as well, so the LDS base handed over is the destination less k*1024.
-template <int K, int NMH, int KBLK>
-__device__ __forceinline__ void pf_v_dma(__amdgpu_buffer_rsrc_t rs, uint8_t* varea0, uint32_t b,
-                                         uint32_t w, uint32_t voff) {
-  if constexpr (K > 0) {
-    pf_v_dma<K - 1, NMH, KBLK>(rs, varea0, b, w, voff);
-    constexpr uint32_t k = K - 1;
-    const uint32_t m = 2u * k + w / 2u;
-    uint8_t* lds = varea0 + (m / NMH) * KBLK + ((m % NMH) * 2u + b) * 512u + (w % 2u) * 256u -
-                   k * 1024u;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)lds, 4,
-                                             voff, 0, (int)(k * 1024u), 0);
-  }
+__device__ __forceinline__ uint32_t pf_k_row(uint32_t t, uint32_t b) { return pf_swap23(t) ^ (b * 8u); }
+__device__ __forceinline__ uint32_t pf_k_token(uint32_t r, uint32_t b) { return pf_swap23(r ^ (b * 8u)); }
+__device__ __forceinline__ uint32_t pf_v_unit(uint32_t n, uint32_t h) {
+  return 2u * n + (h ^ (((n >> 2) ^ (n >> 3)) & 1u));
 }
 template <int N>
 struct PfBuf {  // a staging buffer index as a type
@@ -1688,7 +1675,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ q_lens,
     const int64_t* __restrict__ q_offsets, uint32_t max_q_len, float scale,
     uint32_t split_blocks, uint32_t max_splits, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml) {
+    float* __restrict__ ws_ml, uint32_t prio_blocks) {
   constexpr int NC = D / 32, NM = D / 16;
   constexpr int kStep = 2;  // blocks per softmax step
   constexpr int kTile = prefill_tile_bytes<DT, D>();
@@ -1770,20 +1757,21 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   // skipped. Blocks are staged by direct loads into LDS (dma_block_at below).
   const uint8_t* kbase = tile_ptr(g, 0, layer, 0, kvh);
   // F16 stages with loads straight into LDS: no staging registers, and a block's data
-  // lands while the step computes. An instruction writes 64 lanes' data contiguously;
-  // the lanes' sources give the layout: K as stored (16 bytes a lane, instruction n
-  // of the block = bytes n*1024 ..), V in pf_vi_off's order (4 bytes a lane,
-  // instruction n = dims 8n .. 8n + 7). Wave w issues instructions w, w + 4, ...; its
-  // lanes' V sources differ between them by a constant, as the slot permutation of
-  // dims 8(w + 4k) + l/8 does not depend on k.
-  constexpr int kKIns = kTile / 1024, kVIns = kTile / 256;
-  uint32_t dma_k = 0, dma_v = 0;
+  // lands while the step computes. An instruction writes 64 lanes' 16 bytes
+  // contiguously (1 KiB); the lanes' sources give the layout (pf_k_row, pf_v_unit):
+  // instruction n of the K tile fills runs 4n .. 4n + 3, lane l row l % 16 of run
+  // 4n + l / 16; instruction n of the V tile fills units 64n + l. The K tile's
+  // instructions come first, then the V tile's, and wave w issues w, w + 4, ... A lane's
+  // source offset within its instruction's KiB is the same for every n (the K rows'
+  // permutation depends on the block's place b in the step: two offsets).
+  constexpr int kKIns = kTile / 1024, kFIns = 2 * kKIns;
+  uint32_t dma_k0 = 0, dma_k1 = 0, dma_v = 0;
   if constexpr (DT == kDtypeF16) {
-    const uint32_t l = ln.lane, w = (uint32_t)wave;
-    dma_k = (w * 64u + l) * 16u;
-    const uint32_t sl = (l % 8u) / 2u, perm = (2u * w + (l >> 5)) & 3u;
-    dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + w * 256u + (l >> 3) * 32u +
-            (sl ^ perm) * 8u + (l % 2u) * 4u;
+    const uint32_t l = ln.lane;
+    dma_k0 = ((l >> 4) * B + pf_k_token(l & 15u, 0u)) * 16u;
+    dma_k1 = ((l >> 4) * B + pf_k_token(l & 15u, 1u)) * 16u;
+    const uint32_t n = l >> 1, u = pf_v_unit(n, 0u) ^ (l & 1u);  // unit 64n' + l's half
+    dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + n * 32u + (u & 1u) * 16u;
   }
   // The pool's block count clamped to 2^31: one unsigned compare tests p >= 0 and
   // p < num_blocks for any int32 p. A block's bytes fit 32 bits (the API checks), so
@@ -1811,12 +1799,16 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         __builtin_amdgcn_make_buffer_rsrc((void*)kt, (short)0, 0x7fffffff, 0x00020000);
     if constexpr (DT == kDtypeF16) {
 #pragma unroll
-      for (int k = 0; k < (kKIns + 3) / 4; k++)
-        if (kKIns % 4 == 0 || k * 4 + wave < kKIns)
+      for (int k = 0; k < (kFIns + 3) / 4; k++) {
+        const int i = wave + 4 * k;  // wave-uniform
+        if (kFIns % 4 == 0 || i < kFIns) {
+          const bool isv = i >= kKIns;
+          const uint32_t n = (uint32_t)(isv ? i - kKIns : i);
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              rs, (__attribute__((address_space(3))) void*)(dst + (k * 4 + wave) * 1024), 16,
-              dma_k + k * 4096u, 0, 0, 0);
-      pf_v_dma<kVIns / 4, NM / 2, kBlk>(rs, buf[0] + kTile, (uint32_t)b, (uint32_t)wave, dma_v);
+              rs, (__attribute__((address_space(3))) void*)(dst + (isv ? kTile : 0) + n * 1024u),
+              16, (isv ? dma_v : (b == 0 ? dma_k0 : dma_k1)) + n * 1024u, 0, 0, 0);
+        }
+      }
     } else {
       // Q8_0 tiles as stored, K to dst and V to dst + kTile: 16-byte units, instruction
       // i of the block (wave w takes i = w, w + 4, ...) = 64 units of the K tile (i' = i)
@@ -1865,6 +1857,14 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   __syncthreads();
 
   int32_t j0 = jbeg;
+  // Issue priority by work left: a wave whose workgroup has more than 1/2, 1/4, 1/8 of
+  // the longest range of the launch (prio_blocks) left issues ahead of the other waves
+  // on its SIMD (workgroups of other sequences and tiles). The hardware otherwise
+  // favours the oldest wave: workgroups drift apart, and the launch ends with laggards
+  // alone on their SIMDs, where one wave reaches well under half the SIMD's rate.
+  // prio_blocks 0 (launches cut into pieces, whose later pieces queue for slots): off.
+  const int32_t prio3 = (int32_t)(prio_blocks / 2u), prio2 = (int32_t)(prio_blocks / 4u),
+                prio1 = (int32_t)(prio_blocks / 8u);
   // One step: blocks j0, j0 + 1 from buffer BUF; the next step's go to the other.
   auto step = [&](auto bufc) __attribute__((always_inline)) {
     constexpr int BUF = decltype(bufc)::value;
@@ -1876,36 +1876,48 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     // ended the last step), and the table entries of the step after
     if (more) nlv[0] = dma_block_at(pn[0], nxt, 0);
     if (more2) nlv[1] = dma_block_at(pn[1], nxt, 1);
+    if (prio_blocks != 0) {
+      const int32_t left = jend - j0;  // wave-uniform
+      if (left > prio3) __builtin_amdgcn_s_setprio(3);
+      else if (left > prio2) __builtin_amdgcn_s_setprio(2);
+      else if (left > prio1) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
+    }
     float sc[kStep][4];
     if constexpr (DT == kDtypeF16 && MODE == kPfFast) {
-      // Both blocks' QK chains issued back to back (the second block's LDS reads and
-      // MFMAs overlap the first's latency), then the scores: one wave-uniform test for
-      // the causal mask of the step.
+      // The step's 32 tokens as two score MFMAs X = 0, 1 whose rows mix the blocks: row
+      // r of X is token 8 * (r / 4 % 2) + 4X + r % 4 of block r / 8, K row r ^ 8X of that
+      // block (pf_k_row). Lane (col, grp) then holds the scores of tokens 8 * (grp % 2)
+      // + 4X + 0..3 of block grp / 2: its 8 weights are 8 consecutive tokens of one
+      // block, whose V is one 16-byte half-row (pf_v_unit) for the paired P.V below.
+      // Both chains are issued back to back, then one wave-uniform test for the causal
+      // mask of the step.
       f32x4 a[kStep];
 #pragma unroll
-      for (int bb = 0; bb < kStep; bb++) {
-        const uint8_t* ks = cur[bb];
+      for (int x = 0; x < kStep; x++) {
+        const uint8_t* ks = cur[0] + (ln.col >> 3) * kBlk;
         uint4 kr[NC];
 #pragma unroll
         for (int c = 0; c < NC; c++)
-          kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
-        a[bb] = qk_mfma_pf1<D>(kr, qh, qlo);
+          kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + (ln.col ^ (8 * x))) * 16);
+        a[x] = qk_mfma_pf1<D>(kr, qh, qlo);
       }
       // a block past a column's causal end (or past the wave's tile, or not in the
       // pool) is masked; the step's blocks both lie before every end in the common case
       const bool full2 = lv[0] & lv[1] & ((j0 + kStep) * B <= end_min);
 #pragma unroll
-      for (int bb = 0; bb < kStep; bb++)
+      for (int x = 0; x < kStep; x++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) sc[bb][r] = a[bb][r];
+        for (int r = 0; r < 4; r++) sc[x][r] = a[x][r];
       if (!full2) {
+        const bool lvb = (ln.grp >> 1) ? lv[1] : lv[0];
+        const int32_t tb = (j0 + (ln.grp >> 1)) * B + (ln.grp & 1) * 8;
 #pragma unroll
-        for (int bb = 0; bb < kStep; bb++) {
-          const int32_t t0 = (j0 + bb) * B;
+        for (int x = 0; x < kStep; x++) {
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            const bool ok = ln.real && lv[bb] && t0 + ln.grp * 4 + r < end_col;
-            sc[bb][r] = ok ? sc[bb][r] : -__builtin_inff();
+            const bool ok = ln.real && lvb && tb + 4 * x + r < end_col;
+            sc[x][r] = ok ? sc[x][r] : -__builtin_inff();
           }
         }
       }
@@ -1922,10 +1934,11 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       // operand conversion for such a block would spill inside the loop).
       if (DT == kDtypeF16 || j < jw_end) {  // wave-uniform
         if constexpr (DT == kDtypeF16) {
-          uint4 kr[NC];
+          uint4 kr[NC];  // token col's K row (pf_k_row): the scores in token order
+          const uint32_t kro = pf_k_row((uint32_t)ln.col, (uint32_t)bb);
 #pragma unroll
           for (int c = 0; c < NC; c++)
-            kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + ln.col) * 16);
+            kr[c] = *(const uint4*)(ks + ((c * 4 + ln.grp) * B + kro) * 16);
           qk_block_pf<D, MODE != kPfFast>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0,
                                           end_col, sc[bb]);
         } else {
@@ -1951,17 +1964,18 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     float ef[kStep][4];
     softmax_step_pf<D, kStep>(sc, hscale, ln, st, pw, ef);
     if constexpr (kPair) {
-      // P.V of both blocks: one 16x16x32 MFMA per 16 dims, k-slots grp*8 .. +3 the first
-      // block's tokens grp*4 .. +3 and grp*8 + 4 .. +7 the second's, in P (the lane's own
-      // weights) and in V (8 bytes from each block's tile, 512 bytes apart in pf_vi_off's
-      // layout: one ds_read2st64_b64) alike. The pool holds no Inf/NaN here, so V needs
-      // zeroing only where P's zeros could meet unwritten bytes: tokens at or past the
-      // wave's furthest causal end, and a block not in the pool or not staged (a slot
-      // not staged this step holds an earlier block's bytes, or nothing written yet).
+      // P.V of both blocks: one 16x16x32 MFMA per 16 dims. Lane (col, grp)'s 8 weights
+      // (score MFMAs 0 then 1) are tokens 8 * (grp % 2) + 0..7 of block grp / 2, and so
+      // is its V operand: half grp % 2 of dim 16m + col of that block, one 16-byte read
+      // (pf_v_unit). The pool holds no Inf/NaN here, so V needs zeroing only where P's
+      // zeros could meet unwritten bytes: tokens at or past the wave's furthest causal
+      // end, and a block not in the pool or not staged (a slot not staged this step
+      // holds an earlier block's bytes, or nothing written yet).
       if (j0 < jw_end) {  // wave-uniform
         const f16x8 pa = {pw[0][0], pw[0][1], pw[0][2], pw[0][3],
                           pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
-        const uint8_t* vc = cur[0] + kTile;
+        const uint8_t* vc = cur[0] + (ln.grp >> 1) * kBlk + kTile +
+                            pf_v_unit((uint32_t)ln.col, (uint32_t)(ln.grp & 1)) * 16u;
         // Masks (wave-uniform branch) change only the V operands: MFMAs in common code
         // keep the accumulators in place (MFMAs on both sides of a branch made the
         // compiler move them between registers, and spill). Operands half at a time.
@@ -1970,19 +1984,15 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         for (int h = 0; h < 2; h++) {
           uint4 v[NM / 2];
 #pragma unroll
-          for (int i = 0; i < NM / 2; i++) {
-            const uint32_t vo = pf_vi_off<NM / 2, kBlk>((uint32_t)(h * (NM / 2) + i), 0u,
-                                                        (uint32_t)ln.col, (uint32_t)ln.grp);
-            const u32x2_t a = *(const u32x2_t*)(vc + vo), b = *(const u32x2_t*)(vc + vo + 512u);
-            v[i] = uint4{a.x, a.y, b.x, b.y};
-          }
+          for (int i = 0; i < NM / 2; i++)
+            v[i] = *(const uint4*)(vc + (h * (NM / 2) + i) * 512);
           if (vmask) {
-            const int32_t t0 = j0 * B + ln.grp * 4;
-            const int32_t n0 = lv[0] ? end_max - t0 : 0, n1 = lv[1] ? end_max - t0 - B : 0;
-            const uint32_t k0 = n0 >= 2 ? ~0u : (n0 == 1 ? 0xffffu : 0u);
-            const uint32_t k1 = n0 >= 4 ? ~0u : (n0 == 3 ? 0xffffu : 0u);
-            const uint32_t k2 = n1 >= 2 ? ~0u : (n1 == 1 ? 0xffffu : 0u);
-            const uint32_t k3 = n1 >= 4 ? ~0u : (n1 == 3 ? 0xffffu : 0u);
+            const int32_t t0 = (j0 + (ln.grp >> 1)) * B + (ln.grp & 1) * 8;
+            const int32_t n = ((ln.grp >> 1) ? lv[1] : lv[0]) ? end_max - t0 : 0;
+            const uint32_t k0 = n >= 2 ? ~0u : (n == 1 ? 0xffffu : 0u);
+            const uint32_t k1 = n >= 4 ? ~0u : (n == 3 ? 0xffffu : 0u);
+            const uint32_t k2 = n >= 6 ? ~0u : (n == 5 ? 0xffffu : 0u);
+            const uint32_t k3 = n >= 8 ? ~0u : (n == 7 ? 0xffffu : 0u);
 #pragma unroll
             for (int i = 0; i < NM / 2; i++) {
               v[i].x &= k0;
@@ -2003,15 +2013,14 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
       if (j < jw_end && lv[bb]) {
-        const uint8_t* vs = cur[bb] + kTile;  // (Q8_0; F16 V is interleaved: vi0)
-        const uint8_t* vi0 = cur[0] + kTile;
+        const uint8_t* vs = cur[bb] + kTile;
         if constexpr (DT == kDtypeF16) {
+          // tokens grp*4 .. +3 of dim 16m + col: 8 bytes of half grp / 2 (pf_v_unit)
+          const uint8_t* vl = vs + pf_v_unit((uint32_t)ln.col, (uint32_t)(ln.grp >> 1)) * 16u +
+                              (ln.grp & 1) * 8;
           u32x2_t vr[NM];
 #pragma unroll
-          for (int m = 0; m < NM; m++) {
-            vr[m] = *(const u32x2_t*)(vi0 + pf_vi_off<NM / 2, kBlk>((uint32_t)m, (uint32_t)bb,
-                                                                    (uint32_t)ln.col, (uint32_t)ln.grp));
-          }
+          for (int m = 0; m < NM; m++) vr[m] = *(const u32x2_t*)(vl + m * 512);
           // Leak-safe instance: a block where a non-finite V lies past the tile's
           // nearest causal end takes one P.V per query token jt of the tile, V cut at
           // that token's causal end, into a zeroed temporary; only the rows (columns)
@@ -2027,10 +2036,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
           } else if constexpr (MODE == kPfLeakSafe) {
             for (int32_t jt = 0; jt < T; jt++) {
 #pragma unroll
-              for (int m = 0; m < NM; m++) {
-                vr[m] = *(const u32x2_t*)(vi0 + pf_vi_off<NM / 2, kBlk>((uint32_t)m, (uint32_t)bb,
-                                                                        (uint32_t)ln.col, (uint32_t)ln.grp));
-              }
+              for (int m = 0; m < NM; m++) vr[m] = *(const u32x2_t*)(vl + m * 512);
               mask_v_tail<D>(vr, ln, t0, p0 + tile * T + jt + 1);
 #pragma unroll
               for (int m = 0; m < NM; m++) {
@@ -2231,11 +2237,13 @@ PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint3
       split = std::max<uint64_t>(kPrefillMinPieceBlocks, (max_nblk + want - 1) / want);
     }
   }
+  p.prio_blocks = (uint32_t)max_nblk;
   if (split == 0 || max_nblk <= split) return p;  // one piece per workgroup
   split = std::max<uint64_t>(split, (max_nblk + kPrefillMaxSplits - 1) / kPrefillMaxSplits);
   if (max_nblk <= split) return p;
   p.split_blocks = (uint32_t)split;
   p.max_splits = (uint32_t)((max_nblk + split - 1) / split);
+  p.prio_blocks = 0;  // pieces queue for slots: issue priority measured slower there
   const uint64_t slots = (uint64_t)n_seqs * g.n_kv_heads * p.tile_groups * p.max_splits *
                          (uint64_t)(kAttnWaves * 16);
   p.ws_o_floats = slots * g.head_dim;
@@ -2261,7 +2269,8 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
   attn_prefill_kernel<DT_, D_, X_><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
                                                         max_blocks, ctx_lens, q_lens,         \
                                                         q_offsets, max_q_len, scale,          \
-                                                        split_blocks, max_splits, ws_o, ws_ml)
+                                                        split_blocks, max_splits, ws_o, ws_ml, \
+                                                        plan.prio_blocks)
   // The fast instance, then the one for workgroups whose blocks' marks say the fast one
   // cannot compute them: Q8_0 the exact instance (a scale of 512 or more was stored),
   // F16 the leak-safe one (an Inf/NaN K or V was stored). Each exits where the other works.

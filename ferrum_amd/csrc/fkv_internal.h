@@ -176,6 +176,7 @@ struct PrefillPlan {
   uint32_t max_splits;
   uint64_t ws_o_floats;   // partial outputs, then (max, sum) pairs
   uint64_t ws_bytes;
+  uint32_t prio_blocks;   // longest key range in blocks (issue-priority scale; 0: off)
 };
 PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_q_len,
                          uint32_t max_ctx_len);
