@@ -1629,6 +1629,88 @@ __device__ __forceinline__ uint32_t pf_k_token(uint32_t r, uint32_t b) { return 
 __device__ __forceinline__ uint32_t pf_v_unit(uint32_t n, uint32_t h) {
   return 2u * n + (h ^ (((n >> 2) ^ (n >> 3)) & 1u));
 }
+
+// Fast Q8_0 prefill: a step's two staged Q8_0 blocks (raw: block b's K tile at
+// raw + 2b * kTileQ, its V tile after it, both as stored: q8_quant_offset's order, then
+// the f16 scales [B][D/32]) dequantised into binary16 tiles in the F16 staging layout
+// above (block b's K tile at f16 + 2b * kTileF, its V tile after it), once per
+// workgroup. Thread tid converts 16-byte unit u = tid % UB of each block's K tile and of
+// its V tile (head_dim 128: UB = 256, both; head_dim 64: UB = 128, the K tile for
+// tid < 128, the V tile otherwise). A unit is 8 values: int8 -> binary16 exactly, times
+// the scale with one rounding (v_pk_mul_f16), the operand the decode kernel's
+// BlockRegs<Q8_0> forms in registers. No value overflows: blocks holding a scale of 512
+// or more are computed by the exact instance.
+// The lane's byte offsets within the tiles, worked out once (block 1's K row of a
+// unit holds token t ^ 4 where block 0's holds t: its offsets differ by one bit).
+struct PfQ8Lane {
+  uint32_t kq, ks, vq, vs, o;  // K quants, K scale, V quants, V scales (block 0), unit
+};
+template <int D>
+__device__ __forceinline__ PfQ8Lane pf_q8_lane(uint32_t tid) {
+  constexpr uint32_t NG = D / 32, UB = B * D * 2 / 16;
+  const uint32_t u = tid % UB;
+  PfQ8Lane l;
+  {  // K row u % 16 of run r = u / 16: token pf_k_token, dims 8r .. 8r + 7, scale group r / 4
+    const uint32_t r = u >> 4, t = pf_k_token(u & 15u, 0u), c = r >> 2;
+    l.kq = (c >> 1) * 1024u + ((r & 3u) * 16u + t) * 16u + (c & 1u) * 8u;
+    l.ks = B * D + (t * NG + c) * 2u;
+  }
+  {  // V unit u: half h (tokens 8h .. 8h + 7) of dim n; token t's scale of group c is
+     // half c % 2 of the dword at (t * NG + c - c % 2) * 2
+    const uint32_t n = u >> 1, h = (u & 1u) ^ (((n >> 2) ^ (n >> 3)) & 1u);
+    const uint32_t m = n >> 4, c = n >> 5;
+    l.vq = (m >> 2) * 1024u + (2u * h * 16u + (n & 15u)) * 16u + (m & 3u) * 4u;
+    l.vs = (B * D + (8u * h * NG + (c & ~1u)) * 2u) | ((c & 1u) << 31);  // bit 31: odd group
+  }
+  l.o = u * 16u;
+  // opaque from here: the per-step code adds only constants (tile and buffer offsets)
+  asm volatile("" : "+v"(l.kq), "+v"(l.ks), "+v"(l.vq), "+v"(l.vs), "+v"(l.o));
+  return l;
+}
+template <int D>
+__device__ __forceinline__ void pf_q8_to_f16(const uint8_t* raw, uint8_t* f16, const PfQ8Lane& l,
+                                             uint32_t wave) {
+  constexpr uint32_t NG = D / 32, kTileQ = B * D + B * NG * 2, kTileF = B * D * 2;
+  constexpr uint32_t UB = kTileF / 16;
+  constexpr uint32_t kKsFlip = 4u * NG * 2u;  // t ^ 4 in the scale offset (t * NG * 2)
+#pragma unroll
+  for (uint32_t b = 0; b < 2; b++) {
+#pragma unroll
+    for (uint32_t isv = 0; isv < 2; isv++) {
+      if (UB == 128 && (wave >> 1) != isv) continue;  // head_dim 64: waves 0-1 K, 2-3 V
+      const uint8_t* rt = raw + (2u * b + isv) * kTileQ;
+      uint4 o;
+      if (!isv) {
+        const u32x2_t q = *(const u32x2_t*)(rt + (l.kq ^ (b * 64u)));
+        const uint32_t sw = *(const uint16_t*)(rt + (l.ks ^ (b * kKsFlip)));
+        const f16x2 s2 = __builtin_bit_cast(f16x2, sw | (sw << 16));
+        const uint32_t w0 = q.x ^ 0x80808080u, w1 = q.y ^ 0x80808080u;
+        o = make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelLo) * s2),
+                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelHi) * s2),
+                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelLo) * s2),
+                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelHi) * s2));
+      } else {
+        const uint8_t* qp = rt + l.vq;
+        const uint32_t qa = *(const uint32_t*)qp ^ 0x80808080u;          // tokens 8h .. +3
+        const uint32_t qb = *(const uint32_t*)(qp + 256) ^ 0x80808080u;  // tokens 8h + 4 .. +7
+        const uint8_t* sp = rt + (l.vs & 0x7fffffffu);
+        const uint32_t sel = (l.vs >> 31) ? 0x07060302u : 0x05040100u;
+        f16x2 sc[4];
+#pragma unroll
+        for (int pr = 0; pr < 4; pr++)
+          sc[pr] = __builtin_bit_cast(
+              f16x2, __builtin_amdgcn_perm(*(const uint32_t*)(sp + (2 * pr + 1) * NG * 2),
+                                           *(const uint32_t*)(sp + 2 * pr * NG * 2), sel));
+        o = make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelLo) * sc[0]),
+                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelHi) * sc[1]),
+                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelLo) * sc[2]),
+                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelHi) * sc[3]));
+      }
+      *(uint4*)(f16 + (2u * b + isv) * kTileF + l.o) = o;
+      __builtin_amdgcn_sched_barrier(0);  // one unit's registers live at a time
+    }
+  }
+}
 template <int N>
 struct PfBuf {  // a staging buffer index as a type
   static constexpr int value = N;
@@ -1688,6 +1770,12 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   __shared__ __align__(16) uint8_t s_kv0[kStep][kBlk];
   __shared__ __align__(16) uint8_t s_kv1[kStep][kBlk];
   constexpr bool EXACT = MODE == kPfExact;
+  // The fast instances compute from binary16 tiles in the F16 staging layout: F16 from
+  // the staged blocks themselves, Q8_0 from s_f16, into which each step's staged blocks
+  // are dequantised once per workgroup (pf_q8_to_f16).
+  constexpr bool kQ8F = DT == kDtypeQ8 && MODE == kPfFast;
+  constexpr int kTileF = B * D * 2, kBlkF = 2 * kTileF;
+  __shared__ __align__(16) uint8_t s_f16[kQ8F ? kStep : 1][kQ8F ? kBlkF : 16];
 
   // The pool's count of marked blocks cannot change during a prefill launch (only
   // appends mark blocks), so every wave reads the same value. While it is 0 the fast
@@ -1833,8 +1921,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     }
     return ok;
   };
-  // Fast F16 instance: P.V of a step's two blocks in one MFMA (below).
-  constexpr bool kPair = DT == kDtypeF16 && MODE == kPfFast;
+  // Fast instances: scores from mixed-block rows and P.V of a step's two blocks in one
+  // MFMA, over binary16 tiles in the F16 layout (below).
+  constexpr bool kPair = MODE == kPfFast;
   // every load this wave issued has landed (vmcnt 0; expcnt and lgkmcnt left alone)
   auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
 
@@ -1857,6 +1946,8 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   __syncthreads();
 
   int32_t j0 = jbeg;
+  PfQ8Lane q8l{};
+  if constexpr (kQ8F) q8l = pf_q8_lane<D>(threadIdx.x);
   // Issue priority by work left: a wave whose workgroup has more than 1/2, 1/4, 1/8 of
   // the longest range of the launch (prio_blocks) left issues ahead of the other waves
   // on its SIMD (workgroups of other sequences and tiles). The hardware otherwise
@@ -1883,8 +1974,16 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       else if (left > prio1) __builtin_amdgcn_s_setprio(1);
       else __builtin_amdgcn_s_setprio(0);
     }
+    // the tiles the fast instances compute from: F16 as staged; Q8_0 dequantised into
+    // s_f16 (every thread a share, then a barrier; the barrier that ended the last step
+    // follows every wave's reads of s_f16)
+    const uint8_t* const cf = kQ8F ? &s_f16[0][0] : &cur[0][0];
+    if constexpr (kQ8F) {
+      pf_q8_to_f16<D>(&cur[0][0], &s_f16[0][0], q8l, (uint32_t)wave);
+      __syncthreads();
+    }
     float sc[kStep][4];
-    if constexpr (DT == kDtypeF16 && MODE == kPfFast) {
+    if constexpr (kPair) {
       // The step's 32 tokens as two score MFMAs X = 0, 1 whose rows mix the blocks: row
       // r of X is token 8 * (r / 4 % 2) + 4X + r % 4 of block r / 8, K row r ^ 8X of that
       // block (pf_k_row). Lane (col, grp) then holds the scores of tokens 8 * (grp % 2)
@@ -1895,7 +1994,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       f32x4 a[kStep];
 #pragma unroll
       for (int x = 0; x < kStep; x++) {
-        const uint8_t* ks = cur[0] + (ln.col >> 3) * kBlk;
+        const uint8_t* ks = cf + (ln.col >> 3) * kBlkF;
         uint4 kr[NC];
 #pragma unroll
         for (int c = 0; c < NC; c++)
@@ -1927,11 +2026,10 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       const int32_t j = j0 + bb;
       const int32_t t0 = j * B;
       const uint8_t* ks = cur[bb];
-      // F16: every wave scores both blocks. One past the wave's tile (at most the last of
-      // the workgroup's range, or a slot holding an earlier step's block) lies past every
-      // column's causal end, so the causal mask gives it -inf throughout; skipping it
-      // instead cost a -inf store of the four scores on every step. Q8_0 skips it (its
-      // operand conversion for such a block would spill inside the loop).
+      // F16 (leak-safe): every wave scores both blocks. One past the wave's tile (at most
+      // the last of the workgroup's range, or a slot holding an earlier step's block)
+      // lies past every column's causal end, so the causal mask gives it -inf
+      // throughout. Q8_0 (exact) skips it.
       if (DT == kDtypeF16 || j < jw_end) {  // wave-uniform
         if constexpr (DT == kDtypeF16) {
           uint4 kr[NC];  // token col's K row (pf_k_row): the scores in token order
@@ -1942,24 +2040,17 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
           qk_block_pf<D, MODE != kPfFast>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0,
                                           end_col, sc[bb]);
         } else {
+          static_assert(DT == kDtypeF16 || EXACT, "fast Q8_0 takes the paired path");
           BlockRegs<kDtypeQ8, D> rg;
           rg.template load_k_tile<true>(ks, ln);
-          if constexpr (EXACT) {
-            qk_block_q8x<D>(rg, qh, qlo, 1.0f, ln, lv[bb], t0, end_col, sc[bb]);
-          } else {
-            uint4 kr[NC];
-            rg.k_operand(kr);
-            // (the repair kept: without it the register allocation spills 12 bytes)
-            qk_block_pf<D, true>(kr, qh, qlo, ln, lv[bb], t0 + B <= end_min, t0, end_col,
-                                 sc[bb]);
-          }
+          qk_block_q8x<D>(rg, qh, qlo, 1.0f, ln, lv[bb], t0, end_col, sc[bb]);
         }
       } else {
 #pragma unroll
         for (int r = 0; r < 4; r++) sc[bb][r] = -__builtin_inff();
       }
     }
-    }  // DT != kDtypeF16 || MODE != kPfFast
+    }  // !kPair
     f16x4 pw[kStep];
     float ef[kStep][4];
     softmax_step_pf<D, kStep>(sc, hscale, ln, st, pw, ef);
@@ -1974,7 +2065,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       if (j0 < jw_end) {  // wave-uniform
         const f16x8 pa = {pw[0][0], pw[0][1], pw[0][2], pw[0][3],
                           pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
-        const uint8_t* vc = cur[0] + (ln.grp >> 1) * kBlk + kTile +
+        const uint8_t* vc = cf + (ln.grp >> 1) * kBlkF + kTileF +
                             pf_v_unit((uint32_t)ln.col, (uint32_t)(ln.grp & 1)) * 16u;
         // Masks (wave-uniform branch) change only the V operands: MFMAs in common code
         // keep the accumulators in place (MFMAs on both sides of a branch made the
@@ -2051,13 +2142,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         } else {
           BlockRegs<kDtypeQ8, D> rg;
           rg.template load_v_tile<true>(vs, ln);
-          if constexpr (EXACT) {
-            pv_block_q8x<D>(rg, ef[bb], ln, t0, end_col, st);
-          } else {
-            u32x2_t vr[NM];
-            rg.v_operand(vr);
-            pv_block<D>(vr, pw[bb], ln, t0, end_max, st);
-          }
+          pv_block_q8x<D>(rg, ef[bb], ln, t0, end_col, st);
         }
       }
     }
