@@ -1617,17 +1617,22 @@ enum : int { kPfFast = 0, kPfExact = 1, kPfLeakSafe = 2 };
 //   bit 3 flipped for the second block). Rows 0-7 of a run then hold tokens 0-3 and
 //   8-11 of the first block, and the score MFMAs read their K operands as runs of 8
 //   consecutive rows (below).
-// - V: the stored [D][B] layout as 16-byte halves (dim n, tokens 8h .. 8h + 7), half
-//   (n, h) at unit pf_v_unit(n, h) = 2n + (h ^ x) with x = bit 2 ^ bit 3 of n. The P.V
-//   operand of lane (col, grp) is one half (dim 16m + col, h = grp % 2) of block grp / 2;
-//   the swap puts the 8 (or 16) lanes an LDS read serves a clock on distinct banks.
+// - V: the stored [D][B] layout of 16-byte halves (dim n, tokens 8h .. 8h + 7), half (n, h)
+//   at unit pf_v_unit<SW>(n, h) = 2n + (h ^ (SW ? bit 3 of n : 0)). The fast instances'
+//   P.V operand of lane (col, grp) is one half (dim 16m + col, h = grp % 2) of block
+//   grp / 2; the leak-safe instance reads 8 bytes, tokens grp*4 .. +3 (half grp / 2). An
+//   LDS probe of the two patterns (SQ_LDS_BANK_CONFLICT) found the 16-byte reads free of
+//   bank conflicts as stored and 2-way conflicted with the swap, the 8-byte reads the
+//   other way round: the leak-safe instance stages V with the swap (SW), the fast ones
+//   without.
 __device__ __forceinline__ uint32_t pf_swap23(uint32_t t) {
   return (t & 3u) | ((t & 4u) << 1) | ((t & 8u) >> 1);
 }
 __device__ __forceinline__ uint32_t pf_k_row(uint32_t t, uint32_t b) { return pf_swap23(t) ^ (b * 8u); }
 __device__ __forceinline__ uint32_t pf_k_token(uint32_t r, uint32_t b) { return pf_swap23(r ^ (b * 8u)); }
+template <bool SW>
 __device__ __forceinline__ uint32_t pf_v_unit(uint32_t n, uint32_t h) {
-  return 2u * n + (h ^ (((n >> 2) ^ (n >> 3)) & 1u));
+  return 2u * n + (h ^ (SW ? (n >> 3) & 1u : 0u));
 }
 
 // Fast Q8_0 prefill: a step's two staged Q8_0 blocks (raw: block b's K tile at
@@ -1657,7 +1662,7 @@ __device__ __forceinline__ PfQ8Lane pf_q8_lane(uint32_t tid) {
   }
   {  // V unit u: half h (tokens 8h .. 8h + 7) of dim n; token t's scale of group c is
      // half c % 2 of the dword at (t * NG + c - c % 2) * 2
-    const uint32_t n = u >> 1, h = (u & 1u) ^ (((n >> 2) ^ (n >> 3)) & 1u);
+    const uint32_t n = u >> 1, h = u & 1u;  // (pf_v_unit<false>)
     const uint32_t m = n >> 4, c = n >> 5;
     l.vq = (m >> 2) * 1024u + (2u * h * 16u + (n & 15u)) * 16u + (m & 3u) * 4u;
     l.vs = (B * D + (8u * h * NG + (c & ~1u)) * 2u) | ((c & 1u) << 31);  // bit 31: odd group
@@ -1858,8 +1863,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
     const uint32_t l = ln.lane;
     dma_k0 = ((l >> 4) * B + pf_k_token(l & 15u, 0u)) * 16u;
     dma_k1 = ((l >> 4) * B + pf_k_token(l & 15u, 1u)) * 16u;
-    const uint32_t n = l >> 1, u = pf_v_unit(n, 0u) ^ (l & 1u);  // unit 64n' + l's half
-    dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + n * 32u + (u & 1u) * 16u;
+    // unit 64n' + l: half (l / 2 + 32n', l % 2 ^ swap) of the stored tile (pf_v_unit)
+    const uint32_t n = l >> 1, h = (l & 1u) ^ (MODE == kPfLeakSafe ? (n >> 3) & 1u : 0u);
+    dma_v = (uint32_t)(g.n_kv_heads * g.tile_bytes) + n * 32u + h * 16u;
   }
   // The pool's block count clamped to 2^31: one unsigned compare tests p >= 0 and
   // p < num_blocks for any int32 p. A block's bytes fit 32 bits (the API checks), so
@@ -2066,7 +2072,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
         const f16x8 pa = {pw[0][0], pw[0][1], pw[0][2], pw[0][3],
                           pw[1][0], pw[1][1], pw[1][2], pw[1][3]};
         const uint8_t* vc = cf + (ln.grp >> 1) * kBlkF + kTileF +
-                            pf_v_unit((uint32_t)ln.col, (uint32_t)(ln.grp & 1)) * 16u;
+                            pf_v_unit<false>((uint32_t)ln.col, (uint32_t)(ln.grp & 1)) * 16u;
         // Masks (wave-uniform branch) change only the V operands: MFMAs in common code
         // keep the accumulators in place (MFMAs on both sides of a branch made the
         // compiler move them between registers, and spill). Operands half at a time.
@@ -2106,9 +2112,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
       if (j < jw_end && lv[bb]) {
         const uint8_t* vs = cur[bb] + kTile;
         if constexpr (DT == kDtypeF16) {
-          // tokens grp*4 .. +3 of dim 16m + col: 8 bytes of half grp / 2 (pf_v_unit)
-          const uint8_t* vl = vs + pf_v_unit((uint32_t)ln.col, (uint32_t)(ln.grp >> 1)) * 16u +
-                              (ln.grp & 1) * 8;
+          // tokens grp*4 .. +3 of dim 16m + col: 8 bytes of half grp / 2 (pf_v_unit<true>)
+          const uint8_t* vl =
+              vs + pf_v_unit<true>((uint32_t)ln.col, (uint32_t)(ln.grp >> 1)) * 16u + (ln.grp & 1) * 8;
           u32x2_t vr[NM];
 #pragma unroll
           for (int m = 0; m < NM; m++) vr[m] = *(const u32x2_t*)(vl + m * 512);
