@@ -1639,80 +1639,109 @@ __device__ __forceinline__ uint32_t pf_v_unit(uint32_t n, uint32_t h) {
 // raw + 2b * kTileQ, its V tile after it, both as stored: q8_quant_offset's order, then
 // the f16 scales [B][D/32]) dequantised into binary16 tiles in the F16 staging layout
 // above (block b's K tile at f16 + 2b * kTileF, its V tile after it), once per
-// workgroup. Thread tid converts 16-byte unit u = tid % UB of each block's K tile and of
-// its V tile (head_dim 128: UB = 256, both; head_dim 64: UB = 128, the K tile for
-// tid < 128, the V tile otherwise). A unit is 8 values: int8 -> binary16 exactly, times
-// the scale with one rounding (v_pk_mul_f16), the operand the decode kernel's
-// BlockRegs<Q8_0> forms in registers. No value overflows: blocks holding a scale of 512
-// or more are computed by the exact instance.
-// The lane's byte offsets within the tiles, worked out once (block 1's K row of a
-// unit holds token t ^ 4 where block 0's holds t: its offsets differ by one bit).
+// workgroup. The work is wave tasks of 64 lanes (dealt to the waves in pf_q8_to_f16):
+// - K task (b, p): lane (g = l / 16, s = l % 16) reads the 16-byte unit holding runs
+//   4(2p) + g and 4(2p + 1) + g of token t = pf_k_token(s, b) (the two 32-dim chunks
+//   2p, 2p + 1 share a unit) and writes K rows s of both runs;
+// - V task (b, P, hh): lane l writes V unit 128P + 64hh + l, i.e. half h = l % 2 (tokens
+//   8h .. 8h + 7) of dim n = 64P + 32hh + l / 2, from two dwords of the stored tile
+//   (tokens 8h .. 8h + 3 and 8h + 4 .. 8h + 7, 256 bytes apart); all its dims share the
+//   scale group 2P + hh.
+// The K task's reads and both tasks' writes cover contiguous 1 KiB spans (strided 16-byte
+// writes measured 2-way bank conflicts in an LDS probe; contiguous ones none); the V
+// dword reads of the two halves meet on the same banks, at one extra clock an
+// instruction. A value is int8 -> binary16 exactly, times the scale with
+// one rounding (v_pk_mul_f16): the operand the decode kernel's BlockRegs<Q8_0> forms in
+// registers. No value overflows: blocks holding a scale of 512 or more are computed by
+// the exact instance.
+// The lane's offsets (three registers at 128 VGPRs): kq0 the K unit of block 0 (block 1's
+// token is t ^ 4: kq0 ^ 64), l16 = 16 × lane (the K row offset (g·16 + s)·16 and the V
+// unit offset within a task), and vq the V dword of dim l / 2's unit group, half l % 2
+// (its scale row offset is bit 9 of vq, times 16·NG).
 struct PfQ8Lane {
-  uint32_t kq, ks, vq, vs, o;  // K quants, K scale, V quants, V scales (block 0), unit
+  uint32_t kq0, l16, vq;
 };
 template <int D>
-__device__ __forceinline__ PfQ8Lane pf_q8_lane(uint32_t tid) {
-  constexpr uint32_t NG = D / 32, UB = B * D * 2 / 16;
-  const uint32_t u = tid % UB;
+__device__ __forceinline__ PfQ8Lane pf_q8_lane(uint32_t lane) {
+  const uint32_t g = lane >> 4, s = lane & 15u;
   PfQ8Lane l;
-  {  // K row u % 16 of run r = u / 16: token pf_k_token, dims 8r .. 8r + 7, scale group r / 4
-    const uint32_t r = u >> 4, t = pf_k_token(u & 15u, 0u), c = r >> 2;
-    l.kq = (c >> 1) * 1024u + ((r & 3u) * 16u + t) * 16u + (c & 1u) * 8u;
-    l.ks = B * D + (t * NG + c) * 2u;
-  }
-  {  // V unit u: half h (tokens 8h .. 8h + 7) of dim n; token t's scale of group c is
-     // half c % 2 of the dword at (t * NG + c - c % 2) * 2
-    const uint32_t n = u >> 1, h = u & 1u;  // (pf_v_unit<false>)
-    const uint32_t m = n >> 4, c = n >> 5;
-    l.vq = (m >> 2) * 1024u + (2u * h * 16u + (n & 15u)) * 16u + (m & 3u) * 4u;
-    l.vs = (B * D + (8u * h * NG + (c & ~1u)) * 2u) | ((c & 1u) << 31);  // bit 31: odd group
-  }
-  l.o = u * 16u;
-  // opaque from here: the per-step code adds only constants (tile and buffer offsets)
-  asm volatile("" : "+v"(l.kq), "+v"(l.ks), "+v"(l.vq), "+v"(l.vs), "+v"(l.o));
+  l.kq0 = (g * 16u + pf_k_token(s, 0u)) * 16u;
+  l.l16 = lane * 16u;
+  // dim 32hh + lane / 2 of unit group P: j = (lane / 2) % 16, m % 4 = 2hh + lane / 32
+  l.vq = (lane & 1u) * 512u + ((lane >> 1) & 15u) * 16u + (lane >> 5) * 4u;
+  // opaque from here: the per-step code adds only constants (task and buffer offsets)
+  asm volatile("" : "+v"(l.kq0), "+v"(l.l16), "+v"(l.vq));
   return l;
 }
+// One K task (block b, chunk pair p) and one V task (block b, unit group P, half h).
+template <int D>
+__device__ __forceinline__ void pf_q8_k_task(const uint8_t* raw, uint8_t* f16, const PfQ8Lane& l,
+                                             uint32_t b, uint32_t p) {
+  constexpr uint32_t NG = D / 32, kTileQ = B * D + B * NG * 2, kTileF = B * D * 2;
+  const uint8_t* rt = raw + 2u * b * kTileQ;
+  const uint32_t kq = l.kq0 ^ (b * 64u);  // token t ^ 4 for block 1 (pf_k_token)
+  const uint4 q = *(const uint4*)(rt + p * 1024u + kq);
+  const uint32_t t = (kq / 16u) & 15u;
+  // scales of chunks 2p, 2p + 1 of token t: one dword
+  const uint32_t sw = *(const uint32_t*)(rt + B * D + (t * NG + 2u * p) * 2u);
+  uint8_t* kf = f16 + 2u * b * kTileF + l.l16;  // run g of chunk 0, row s
+#pragma unroll
+  for (uint32_t h = 0; h < 2; h++) {
+    const f16x2 s2 = __builtin_bit_cast(
+        f16x2, __builtin_amdgcn_perm(sw, sw, h ? 0x03020302u : 0x01000100u));
+    const uint32_t w0 = (h ? q.z : q.x) ^ 0x80808080u, w1 = (h ? q.w : q.y) ^ 0x80808080u;
+    *(uint4*)(kf + (2u * p + h) * 1024u) =  // run 4(2p + h) + g
+        make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelLo) * s2),
+                   __builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelHi) * s2),
+                   __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelLo) * s2),
+                   __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelHi) * s2));
+  }
+}
+template <int D>
+__device__ __forceinline__ void pf_q8_v_task(const uint8_t* raw, uint8_t* f16, const PfQ8Lane& l,
+                                             uint32_t b, uint32_t P, uint32_t hh) {
+  constexpr uint32_t NG = D / 32, kTileQ = B * D + B * NG * 2, kTileF = B * D * 2;
+  const uint8_t* rt = raw + (2u * b + 1u) * kTileQ;
+  const uint8_t* qp = rt + P * 1024u + hh * 8u + l.vq;
+  const uint32_t qa = *(const uint32_t*)qp ^ 0x80808080u;          // tokens 8h .. +3
+  const uint32_t qb = *(const uint32_t*)(qp + 256) ^ 0x80808080u;  // tokens 8h + 4 .. +7
+  // tokens 8h .. 8h + 7 (h = lane % 2, bit 9 of vq), groups 2P and 2P + 1: a dword a token
+  const uint8_t* sp = rt + B * D + 4u * P + ((l.vq >> 9) & 1u) * 16u * NG;
+  const uint32_t sel = hh ? 0x07060302u : 0x05040100u;  // group 2P + hh: wave-uniform
+  f16x2 sc[4];
+#pragma unroll
+  for (int pr = 0; pr < 4; pr++)
+    sc[pr] = __builtin_bit_cast(
+        f16x2, __builtin_amdgcn_perm(*(const uint32_t*)(sp + (2 * pr + 1) * NG * 2),
+                                     *(const uint32_t*)(sp + 2 * pr * NG * 2), sel));
+  // unit pf_v_unit(64P + 32hh + l / 2, l % 2) = 128P + 64hh + l
+  *(uint4*)(f16 + (2u * b + 1u) * kTileF + (128u * P + 64u * hh) * 16u + l.l16) =
+      make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelLo) * sc[0]),
+                 __builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelHi) * sc[1]),
+                 __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelLo) * sc[2]),
+                 __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelHi) * sc[3]));
+}
+// A step's 2 (K tasks a block + V tasks a block) tasks over the 4 waves. head_dim 128:
+// wave w the K task (w / 2, w % 2) and the V tasks (0 and 1, P = w / 2, hh = w % 2), 3
+// each; head_dim 64: tasks K(0), K(1), V(0, 0, 0), V(0, 0, 1), V(1, 0, 0), V(1, 0, 1)
+// dealt w, w + 4.
 template <int D>
 __device__ __forceinline__ void pf_q8_to_f16(const uint8_t* raw, uint8_t* f16, const PfQ8Lane& l,
                                              uint32_t wave) {
-  constexpr uint32_t NG = D / 32, kTileQ = B * D + B * NG * 2, kTileF = B * D * 2;
-  constexpr uint32_t UB = kTileF / 16;
-  constexpr uint32_t kKsFlip = 4u * NG * 2u;  // t ^ 4 in the scale offset (t * NG * 2)
-#pragma unroll
-  for (uint32_t b = 0; b < 2; b++) {
-#pragma unroll
-    for (uint32_t isv = 0; isv < 2; isv++) {
-      if (UB == 128 && (wave >> 1) != isv) continue;  // head_dim 64: waves 0-1 K, 2-3 V
-      const uint8_t* rt = raw + (2u * b + isv) * kTileQ;
-      uint4 o;
-      if (!isv) {
-        const u32x2_t q = *(const u32x2_t*)(rt + (l.kq ^ (b * 64u)));
-        const uint32_t sw = *(const uint16_t*)(rt + (l.ks ^ (b * kKsFlip)));
-        const f16x2 s2 = __builtin_bit_cast(f16x2, sw | (sw << 16));
-        const uint32_t w0 = q.x ^ 0x80808080u, w1 = q.y ^ 0x80808080u;
-        o = make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelLo) * s2),
-                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelHi) * s2),
-                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelLo) * s2),
-                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelHi) * s2));
-      } else {
-        const uint8_t* qp = rt + l.vq;
-        const uint32_t qa = *(const uint32_t*)qp ^ 0x80808080u;          // tokens 8h .. +3
-        const uint32_t qb = *(const uint32_t*)(qp + 256) ^ 0x80808080u;  // tokens 8h + 4 .. +7
-        const uint8_t* sp = rt + (l.vs & 0x7fffffffu);
-        const uint32_t sel = (l.vs >> 31) ? 0x07060302u : 0x05040100u;
-        f16x2 sc[4];
-#pragma unroll
-        for (int pr = 0; pr < 4; pr++)
-          sc[pr] = __builtin_bit_cast(
-              f16x2, __builtin_amdgcn_perm(*(const uint32_t*)(sp + (2 * pr + 1) * NG * 2),
-                                           *(const uint32_t*)(sp + 2 * pr * NG * 2), sel));
-        o = make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelLo) * sc[0]),
-                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelHi) * sc[1]),
-                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelLo) * sc[2]),
-                       __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelHi) * sc[3]));
-      }
-      *(uint4*)(f16 + (2u * b + isv) * kTileF + l.o) = o;
-      __builtin_amdgcn_sched_barrier(0);  // one unit's registers live at a time
+  static_assert(D == 128 || D == 64, "head_dim 64 or 128");
+  if constexpr (D == 128) {
+    pf_q8_k_task<D>(raw, f16, l, wave >> 1, wave & 1u);
+    __builtin_amdgcn_sched_barrier(0);  // one task's registers live at a time
+    pf_q8_v_task<D>(raw, f16, l, 0u, wave >> 1, wave & 1u);
+    __builtin_amdgcn_sched_barrier(0);
+    pf_q8_v_task<D>(raw, f16, l, 1u, wave >> 1, wave & 1u);
+  } else {
+    if (wave < 2u) {
+      pf_q8_k_task<D>(raw, f16, l, wave, 0u);
+      __builtin_amdgcn_sched_barrier(0);
+      pf_q8_v_task<D>(raw, f16, l, 1u, 0u, wave);
+    } else {
+      pf_q8_v_task<D>(raw, f16, l, 0u, 0u, wave - 2u);
     }
   }
 }
@@ -1953,7 +1982,7 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
 
   int32_t j0 = jbeg;
   PfQ8Lane q8l{};
-  if constexpr (kQ8F) q8l = pf_q8_lane<D>(threadIdx.x);
+  if constexpr (kQ8F) q8l = pf_q8_lane<D>(ln.lane);
   // Issue priority by work left: a wave whose workgroup has more than 1/2, 1/4, 1/8 of
   // the longest range of the launch (prio_blocks) left issues ahead of the other waves
   // on its SIMD (workgroups of other sequences and tiles). The hardware otherwise
