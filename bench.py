@@ -88,6 +88,9 @@ def parse():
     ap.add_argument("--kv-dtype", default="f16", choices=["f16", "f32", "q8_0"],
                     help="c2: KV storage (f32 runs the VALU attention kernel); c3, gather: f16 "
                          "(BASELINE's) or q8_0")
+    ap.add_argument("--attn-engine", default="mfma", choices=["mfma", "valu"],
+                    help="F16 decode arithmetic: matrix cores (default) or the VALU partition "
+                         "kernel (fkv_set_tuning FKV_TUNE_ATTN_ENGINE), to measure the choice")
     ap.add_argument("--n-heads", type=int, default=32,
                     help="c2: query heads over the 8 KV heads (64: GQA group 8)")
     return ap.parse_args()
@@ -1353,12 +1356,20 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     dev = torch.device("cuda:0")
     lib = _lib.load()
+    if args.attn_engine == "valu":
+        fa.set_tuning(fa.TUNE_ATTN_ENGINE, 1)
     run = {"c1": run_c1, "c2": run_c2, "c3": run_c3, "c4": run_c4, "c5": run_c5,
            "q8gemv": run_q8gemv, "gguf": run_gguf, "layer": run_layer,
            "gather": run_gather}[args.workload]
     result = run(args, torch, fa, lib, dev)
+    if args.attn_engine == "valu":
+        # a measurement of the alternative engine: the committed traffic figure belongs
+        # to the matrix-core kernel
+        result["attn_engine"] = "valu (attn_partition_kernel on F16 storage)"
+        if isinstance(result.get("roofline"), dict):
+            result["roofline"]["traffic"] = None
     if (args.workload == "c2" and args.kv_dtype == "f16" and args.n_heads == 32
-            and not args.rope_dim and not args.no_configs):
+            and not args.rope_dim and not args.no_configs and args.attn_engine == "mfma"):
         result["configs"] = other_configs(args, torch, fa, lib, dev)
     print(json.dumps(result), flush=True)
 

@@ -135,6 +135,10 @@ int32_t fkv_set_tuning(int32_t knob, int64_t value) {
         return fail(FKV_ERR_INVALID, "prefill split blocks must be -1 or a block count");
       t.prefill_split.store(value);
       return ok();
+    case FKV_TUNE_ATTN_ENGINE:
+      if (value != 0 && value != 1) return fail(FKV_ERR_INVALID, "engine must be 0 or 1");
+      t.attn_engine.store((int32_t)value);
+      return ok();
     default:
       return fail(FKV_ERR_INVALID, "unknown tuning knob");
   }

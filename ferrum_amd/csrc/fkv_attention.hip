@@ -70,6 +70,7 @@ Tuning& tuning() {
       const long long v = strtoll(e, nullptr, 10);
       if (v >= 0) t.prefill_split = v;
     }
+    if (const char* e = getenv("FKV_ATTN_ENGINE")) t.attn_engine = strcmp(e, "valu") == 0;
   });
   return t;
 }
@@ -93,11 +94,16 @@ using namespace dev;
 //   phase 3  acc[g][d] = sum_t e[g][t] * V_t[d]; rows and waves reduced via LDS
 // With one partition the output is acc / l; otherwise (m, l, acc) go to the
 // workspace and attn_combine_kernel merges partitions (log-sum-exp).
+// F32 storage: K and V tiles [token][D]. F16 storage (the matrix-core operand order the
+// pool keeps, read here only when FKV_TUNE_ATTN_ENGINE selects this kernel, to measure
+// the choice): K [D/8][16][8], a 16-byte unit = 8 dims of one token, so a lane's unit
+// of token row r is run c; V [D][16], a unit = 8 tokens of one dim, so phase 3 runs
+// per (dim, 8 tokens) unit instead of per token row (pv_f16 below).
 
 template <int DT, int D>
 struct AttnShape {
-  static_assert(DT == kDtypeF32, "the VALU partition kernel reads F32 storage");
-  static constexpr int E = 4;
+  static_assert(DT == kDtypeF32 || DT == kDtypeF16, "the VALU partition kernel reads F32 or F16");
+  static constexpr int E = DT == kDtypeF32 ? 4 : 2;
   static constexpr int EPL = 16 / E;            // values per lane per 16-byte load
   static constexpr int LPR = D / EPL;           // lanes per token row
   static constexpr int RPP = 64 / LPR;          // token rows per load instruction
@@ -106,11 +112,26 @@ struct AttnShape {
   static_assert(LPR >= 1 && LPR <= 32 && RPP * LPR == 64 && PASSES * RPP == kAttnBlock, "shape");
 };
 
-// One 16-byte load of F32 storage as 4 floats.
+// One 16-byte load of storage as floats: F32 4, F16 8 (binary16 -> binary32 is exact).
 template <int DT, int EPL>
 __device__ __forceinline__ void decode16(const uint4& w, float (&f)[EPL]) {
-  f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y);
-  f[2] = __uint_as_float(w.z); f[3] = __uint_as_float(w.w);
+  if constexpr (DT == kDtypeF32) {
+    f[0] = __uint_as_float(w.x); f[1] = __uint_as_float(w.y);
+    f[2] = __uint_as_float(w.z); f[3] = __uint_as_float(w.w);
+  } else {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      f[2 * i] = f16_bits_to_f32(u[i] & 0xffffu);
+      f[2 * i + 1] = f16_bits_to_f32(u[i] >> 16);
+    }
+  }
+}
+// Byte offset of lane (row r, column c)'s 16-byte unit of a K tile.
+template <int DT>
+__device__ __forceinline__ uint64_t k_unit_off(int row, int c, uint64_t row_bytes) {
+  return DT == kDtypeF32 ? (uint64_t)row * row_bytes + (uint64_t)c * 16u
+                         : ((uint64_t)c * kAttnBlock + (uint64_t)row) * 16u;
 }
 
 template <int DT, int D, int G>
@@ -192,20 +213,27 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 #pragma unroll
       for (int ps = 0; ps < PASSES; ps++) {
         int row = ps * RPP + r;
-        kreg[j][ps] = load_stream16(kt + row * row_bytes + c * 16);
+        kreg[j][ps] = load_stream16(kt + k_unit_off<DT>(row, c, row_bytes));
       }
     }
   }
-  uint4 vreg[S::kPrefetchV ? NB : 1][PASSES];
+  // F16 V: D / 32 units of 16 bytes a lane (unit ps * 64 + lane: dim (ps * 64 + lane) / 2,
+  // tokens 8 (lane % 2) .. + 7), 1 KiB of consecutive bytes an instruction.
+  constexpr int PV = DT == kDtypeF16 ? D / 32 : PASSES;
+  uint4 vreg[S::kPrefetchV ? NB : 1][PV];
   if constexpr (S::kPrefetchV) {
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       if (live[j]) {
         const uint8_t* vt = tile_ptr(g, (uint64_t)phys[j], layer, 1, kvh);
 #pragma unroll
-        for (int ps = 0; ps < PASSES; ps++) {
-          int row = ps * RPP + r;
-          vreg[j][ps] = load_stream16(vt + row * row_bytes + c * 16);
+        for (int ps = 0; ps < PV; ps++) {
+          if constexpr (DT == kDtypeF16) {
+            vreg[j][ps] = load_stream16(vt + (uint64_t)(ps * 64 + lane) * 16u);
+          } else {
+            int row = ps * RPP + r;
+            vreg[j][ps] = load_stream16(vt + row * row_bytes + c * 16);
+          }
         }
       }
     }
@@ -265,6 +293,50 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
   __syncthreads();
 
   // Phase 3: weighted V.
+  if constexpr (DT == kDtypeF16) {
+    // per unit: dim n = (ps * 64 + lane) / 2, its 8 tokens of half lane % 2; the two
+    // halves of a dim (lanes l, l ^ 1) are summed at the end
+    float acc3[PV][G];
+#pragma unroll
+    for (int ps = 0; ps < PV; ps++)
+#pragma unroll
+      for (int gg = 0; gg < G; gg++) acc3[ps][gg] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      if (!live[j]) continue;
+      float vf[PV][8];
+#pragma unroll
+      for (int ps = 0; ps < PV; ps++) {
+        const uint4 w = S::kPrefetchV ? vreg[j][ps]
+                                      : load_stream16(tile_ptr(g, (uint64_t)phys[j], layer, 1, kvh) +
+                                                      (uint64_t)(ps * 64 + lane) * 16u);
+        decode16<DT, 8>(w, vf[ps]);
+      }
+      const int32_t tb = (wave * NB + j) * kAttnBlock + (lane & 1) * 8;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        if (tb + i < n_valid) {  // tokens past the context: no term (V there may be NaN)
+          float pw[G];
+#pragma unroll
+          for (int gg = 0; gg < G; gg++) pw[gg] = s_p[tb + i][gg];
+#pragma unroll
+          for (int ps = 0; ps < PV; ps++)
+#pragma unroll
+            for (int gg = 0; gg < G; gg++) acc3[ps][gg] = __builtin_fmaf(pw[gg], vf[ps][i], acc3[ps][gg]);
+        }
+      }
+    }
+#pragma unroll
+    for (int ps = 0; ps < PV; ps++)
+#pragma unroll
+      for (int gg = 0; gg < G; gg++) acc3[ps][gg] += __shfl_xor(acc3[ps][gg], 1);
+    if ((lane & 1) == 0) {
+#pragma unroll
+      for (int ps = 0; ps < PV; ps++)
+#pragma unroll
+        for (int gg = 0; gg < G; gg++) s_acc[wave][gg][(ps * 64 + lane) / 2] = acc3[ps][gg];
+    }
+  } else {
   float acc[G][EPL];
 #pragma unroll
   for (int gg = 0; gg < G; gg++)
@@ -319,6 +391,7 @@ __global__ void __launch_bounds__(256) attn_partition_kernel(
 #pragma unroll
       for (int i = 0; i < EPL; i++) s_acc[wave][gg][c * EPL + i] = acc[gg][i];
   }
+  }  // F32
   __syncthreads();
 
   for (int e = threadIdx.x; e < G * D; e += 256) {
@@ -516,7 +589,7 @@ hipError_t launch_attn_t(const Geom& g, uint32_t layer, uint32_t n_heads, const 
                                   kAttnPartTokens, ws_o, ws_ml, out, s);
 }
 
-template <int D>
+template <int DT, int D>
 hipError_t dispatch_group(uint32_t G, const Geom& g, uint32_t layer, uint32_t n_heads,
                           const float* q, float* out, const int32_t* tables,
                           uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
@@ -524,7 +597,7 @@ hipError_t dispatch_group(uint32_t G, const Geom& g, uint32_t layer, uint32_t n_
                           hipStream_t s) {
 #define FKV_G(N)                                                                             \
   case N:                                                                                    \
-    return launch_attn_t<kDtypeF32, D, N>(g, layer, n_heads, q, out, tables, max_blocks,     \
+    return launch_attn_t<DT, D, N>(g, layer, n_heads, q, out, tables, max_blocks,            \
                                           ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
   switch (G) {
     FKV_G(1)
@@ -634,6 +707,10 @@ AttnPlan plan_attention(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32
     }
   }
   p.mfma_path = (g.dtype == kDtypeF16 || g.dtype == kDtypeQ8) && G >= 1 && G <= 16;
+  // FKV_TUNE_ATTN_ENGINE = 1: F16 on the VALU partition kernel where it has an instance
+  if (p.mfma_path && g.dtype == kDtypeF16 && tuning().attn_engine.load(std::memory_order_relaxed) &&
+      (G == 1 || G == 2 || G == 4 || G == 8 || G == 16))
+    p.mfma_path = false;
   p.split_tokens = p.mfma_path ? choose_split_tokens(max_ctx_len, n_seqs, g.n_kv_heads)
                                                     : kAttnPartTokens;
   p.max_splits = max_ctx_len ? (max_ctx_len + p.split_tokens - 1) / p.split_tokens : 1;
@@ -793,11 +870,18 @@ hipError_t launch_decode_attention(const Geom& g, uint32_t layer, uint32_t n_hea
   const uint32_t max_parts = p.max_splits;
   float* ws_o = ws ? (float*)(ws + p.o_off) : nullptr;
   float* ws_ml = ws ? (float*)(ws + p.ml_off) : nullptr;
-  // F16 and Q8_0 never get here (mfma_path covers every supported group size).
+  // Q8_0 never gets here, F16 only when FKV_TUNE_ATTN_ENGINE selects the VALU kernel.
+  if (g.dtype == kDtypeF16) {
+    if (g.head_dim == 128)
+      return dispatch_group<kDtypeF16, 128>(G, g, layer, n_heads, q, out, tables, max_blocks,
+                                            ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
+    return dispatch_group<kDtypeF16, 64>(G, g, layer, n_heads, q, out, tables, max_blocks,
+                                         ctx_lens, n_seqs, max_parts, scale, ws_o, ws_ml, s);
+  }
   if (g.head_dim == 128)
-    return dispatch_group<128>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
+    return dispatch_group<kDtypeF32, 128>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens,
                                n_seqs, max_parts, scale, ws_o, ws_ml, s);
-  return dispatch_group<64>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens, n_seqs,
+  return dispatch_group<kDtypeF32, 64>(G, g, layer, n_heads, q, out, tables, max_blocks, ctx_lens, n_seqs,
                             max_parts, scale, ws_o, ws_ml, s);
 }
 

@@ -125,11 +125,16 @@ const char* fkv_last_error(void);
  *                                  first; -1: the planner's rule [FKV_ATTN_ORDER]
  *   FKV_TUNE_PREFILL_SPLIT_BLOCKS  prefill key-range piece length in blocks, 0 no pieces;
  *                                  -1: the planner's rule [FKV_PREFILL_SPLIT_BLOCKS]
+ *   FKV_TUNE_ATTN_ENGINE           F16 decode arithmetic: 0 the matrix cores (default),
+ *                                  1 the VALU partition kernel (group sizes 1, 2, 4, 8, 16;
+ *                                  others stay on the matrix cores), kept to measure the
+ *                                  choice [FKV_ATTN_ENGINE=valu]
  * Out-of-range values: FKV_ERR_INVALID, nothing changed. */
 #define FKV_TUNE_ATTN_SPLIT_TOKENS 0
 #define FKV_TUNE_ATTN_STREAM 1
 #define FKV_TUNE_ATTN_ORDER 2
 #define FKV_TUNE_PREFILL_SPLIT_BLOCKS 3
+#define FKV_TUNE_ATTN_ENGINE 4
 int32_t fkv_set_tuning(int32_t knob, int64_t value);
 
 /* Number of visible HIP devices (0 when no GPU); never fails. */

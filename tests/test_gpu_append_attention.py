@@ -91,6 +91,34 @@ def test_fused_step_matches_append_then_attention(dtype, d, hkv, g, rounding):
     pool.close()
 
 
+@pytest.mark.parametrize("d,hkv,g", [(128, 8, 4), (64, 4, 8), (128, 2, 16)])
+def test_fused_step_on_the_valu_engine(d, hkv, g, tune):
+    """F16 with FKV_TUNE_ATTN_ENGINE = 1: the step appends through fkv_append's kernel and
+    attends on the VALU partition kernel; the same pool bytes and the same bar."""
+    import torch
+    import ferrum_amd as fa
+    from oracle import ref
+    tune(attn_engine=1)
+    layer = 1
+    pool, layout, tab, knew, vnew = _setup(1, d, hkv, CTXS, 0, seed=d + g + 1)
+    before = pool.read()
+    q = np.random.default_rng(4).standard_normal((len(CTXS), hkv * g, d), dtype=np.float32)
+    ctx = np.array(CTXS, np.int32)
+    out = torch.full(q.shape, 7.0, dtype=torch.float32, device="cuda")
+    pool.append_decode_attention(layer, to_dev(knew), to_dev(vnew), to_dev(q), out, to_dev(tab),
+                                 to_dev(ctx), int(ctx.max()))
+    torch.cuda.synchronize()
+    assert pool.take_fault_flags() == 0
+    image = pool.read()
+    want_image = before.copy()
+    tail = np.array([slots_for(tab[i], c)[-1] for i, c in enumerate(CTXS)], np.int64)
+    ref.append(layout, want_image, layer, knew, vnew, tail)
+    assert np.array_equal(image, want_image), "append is not bit-exact"
+    want = ref.attention(layout, image, layer, q, tab, ctx, fa.default_scale(d))
+    assert_close(out.cpu().numpy(), want)
+    pool.close()
+
+
 def test_fused_step_empty_context_and_bad_table_entry():
     import torch
     pool, layout, tab, knew, vnew = _setup(1, 128, 2, [0, 40], seed=5, layers=1)

@@ -54,12 +54,15 @@ SHAPES = [(1, 128, 4), (1, 128, 8), (1, 64, 8), (1, 128, 1), (1, 64, 2), (1, 128
           (8, 64, 3), (8, 128, 1)]
 
 
-@pytest.fixture(params=["split", "stream"])
+@pytest.fixture(params=["split", "stream", "valu"])
 def f16_schedule(request, tune):
     """F16 runs on the MFMA split kernel by default; the stream knob of fkv_set_tuning
-    selects the persistent schedule. Both must meet the same bar."""
+    selects the persistent schedule, the engine knob the VALU partition kernel (group
+    sizes 1, 2, 4, 8, 16; others stay on the matrix cores). All meet the same bar."""
     if request.param == "stream":
         tune(attn_stream=1)
+    elif request.param == "valu":
+        tune(attn_stream=0, attn_engine=1)
     else:
         tune(attn_stream=0)
     return request.param
@@ -67,8 +70,8 @@ def f16_schedule(request, tune):
 
 @pytest.mark.parametrize("dtype,d,g", SHAPES)
 def test_attention_matches_oracle(dtype, d, g, f16_schedule):
-    if dtype != 1 and f16_schedule == "stream":
-        pytest.skip("the schedule switch only applies to F16 storage")
+    if dtype != 1 and f16_schedule != "split":
+        pytest.skip("the schedule and engine switches only apply to F16 storage")
     import ferrum_amd as fa
     from oracle import ref
     hkv = 2
@@ -226,15 +229,17 @@ def test_attention_zero_context_gives_zeros():
     assert np.all(np.isfinite(o[1])) and np.any(o[1] != 0.0)
 
 
-@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("dtype,engine", [(0, 0), (1, 0), (1, 1)])
 @pytest.mark.parametrize("ctx", [40, 600])
-def test_attention_non_finite_scores(ctx, dtype):
+def test_attention_non_finite_scores(ctx, dtype, engine, tune):
     """One K row is (+inf, 0, ..., 0). Head 0 (q0 > 0) scores it +inf: a non-finite
     max gives zeros (scalar.rs:127-130). Head 1 (q0 < 0) scores it -inf: the token
     only drops out. Head 2 (q0 == 0) scores it 0*inf = NaN with a finite max: the
-    output is NaN. A second pool where every score of a head is -inf gives zeros."""
+    output is NaN. A second pool where every score of a head is -inf gives zeros.
+    engine 1: F16 on the VALU partition kernel."""
     import ferrum_amd as fa
     from oracle import ref
+    tune(attn_engine=engine)
     d, hkv, g = 64, 1, 4
     nb = (ctx + 15) // 16
     pool, layout = make_pools(1, hkv, d, nb + 2, dtype=dtype)
@@ -265,16 +270,17 @@ def test_attention_non_finite_scores(ctx, dtype):
     assert np.all(got2 == 0.0)
 
 
-@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("dtype,engine", [(0, 0), (1, 0), (1, 1)])
 @pytest.mark.parametrize("bad", [np.inf, -np.inf])
-def test_attention_infinite_k_with_any_q(bad, dtype):
+def test_attention_infinite_k_with_any_q(bad, dtype, engine, tune):
     """One K row holds +-Inf at two dims; 16 query heads see it with random q there. On
     the matrix cores q is split into f16 hi + lo parts after a scaling, so the lo part
     at those dims is zero or of either sign: the score must still be the reference's
     dot (+-Inf, or NaN where the two infinities meet with opposite signs), giving zeros,
-    a dropped token or NaN as the oracle does."""
+    a dropped token or NaN as the oracle does. engine 1: F16 on the VALU partition kernel."""
     import ferrum_amd as fa
     from oracle import ref
+    tune(attn_engine=engine)
     d, hkv, g, ctx = 128, 1, 16, 300
     nb = (ctx + 15) // 16
     pool, layout = make_pools(1, hkv, d, nb + 2, dtype=dtype)
