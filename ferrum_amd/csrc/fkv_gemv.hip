@@ -470,7 +470,7 @@ struct MmB {
   uint4 s[kMmChunk / 4];  // scales of 4 blocks
 };
 
-__global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const GemvBatch bat, uint32_t cols,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void gemm_q8_mfma_kernel(const GemvBatch bat, uint32_t cols,
                                                            uint32_t n_tokens, uint32_t n_tiles,
                                                            const uint8_t* __restrict__ ws) {
   uint32_t mi = 0;
@@ -529,19 +529,26 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const GemvBatch bat, 
   // B operands and x scales of chunk k for this wave's token tile.
   const uint8_t* bq = ws + (((uint64_t)ttc * (nb / 2u)) * 64u + lane) * 16u;
   const uint8_t* bs = ws + mm_quant_bytes(n_tiles, nb) + (((uint64_t)ttc * (nb / 4u)) * 16u + c) * 16u;
+  auto bq_load = [&](uint32_t k, int p) {
+    return *(const uint4*)(bq + ((uint64_t)k * (kMmChunk / 2u) + (uint32_t)p) * 1024u);
+  };
+  auto bs_load = [&](uint32_t k, int u) {
+    return *(const uint4*)(bs + ((uint64_t)k * (kMmChunk / 4u) + (uint32_t)u) * 256u);
+  };
   auto b_load = [&](uint32_t k, MmB& o) {
 #pragma unroll
-    for (int p = 0; p < (int)kMmChunk / 2; ++p)
-      o.q[p] = *(const uint4*)(bq + ((uint64_t)k * (kMmChunk / 2u) + p) * 1024u);
+    for (int p = 0; p < (int)kMmChunk / 2; ++p) o.q[p] = bq_load(k, p);
 #pragma unroll
-    for (int u = 0; u < (int)kMmChunk / 4; ++u)
-      o.s[u] = *(const uint4*)(bs + ((uint64_t)k * (kMmChunk / 4u) + u) * 256u);
+    for (int u = 0; u < (int)kMmChunk / 4; ++u) o.s[u] = bs_load(k, u);
   };
 
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   // Chunk k from LDS buffer `buf` with B operands o. Four blocks' integer dots are
-  // issued before their epilogues, which then run in block order.
-  auto compute = [&](uint32_t buf, const MmB& o) {
+  // issued before their epilogues, which then run in block order. Each register of o
+  // is reloaded with chunk kn's operand once its last use has issued, so one set of
+  // registers holds chunk k and receives chunk kn (one chunk ahead, as a second set
+  // would, in half the registers).
+  auto compute = [&](uint32_t buf, MmB& o, uint32_t kn) {
     const uint8_t* wl = &s_w[buf][c * kMmRowStride + grp * 8u];
 #pragma unroll
     for (int b0 = 0; b0 < (int)kMmChunk; b0 += 4) {
@@ -567,7 +574,13 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const GemvBatch bat, 
         const v4i zero = {0, 0, 0, 0};
         si[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
       }
+      // the reloads stay after the dots that read the registers they overwrite
+      __builtin_amdgcn_sched_barrier(0);
+      o.q[b0 / 2] = bq_load(kn, b0 / 2);
+      o.q[b0 / 2 + 1] = bq_load(kn, b0 / 2 + 1);
       const uint4 s4 = o.s[b0 / 4];
+      o.s[b0 / 4] = bs_load(kn, b0 / 4);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int b = b0 + i;
@@ -582,23 +595,21 @@ __global__ __launch_bounds__(256) void gemm_q8_mfma_kernel(const GemvBatch bat, 
   };
 
   const uint32_t nc = nb / kMmChunk;  // even
-  MmB b0, b1;
-  if (on) b_load(0, b0);
+  MmB bo;
+  if (on) b_load(0, bo);
   stage_load(0);
   stage_store(0);
   __syncthreads();
   for (uint32_t k = 0; k < nc; k += 2) {
-    // chunk k (buffer 0, b0) while chunk k + 1 loads; then chunk k + 1 (buffer 1, b1)
-    if (on) b_load(k + 1, b1);
+    // chunk k (buffer 0) while chunk k + 1's weights and B operands load; then chunk
+    // k + 1 (buffer 1)
     stage_load(k + 1);
-    if (on) compute(0, b0);
+    if (on) compute(0, bo, k + 1);
     stage_store(1);
     __syncthreads();
-    if (k + 2 < nc) {
-      if (on) b_load(k + 2, b0);
-      stage_load(k + 2);
-    }
-    if (on) compute(1, b1);
+    if (k + 2 < nc) stage_load(k + 2);
+    // past the last chunk the reloads read it again (in bounds, never used): no branch
+    if (on) compute(1, bo, k + 2 < nc ? k + 2 : nc - 1);
     if (k + 2 < nc) stage_store(0);
     __syncthreads();
   }
