@@ -1788,10 +1788,10 @@ __global__ void __launch_bounds__(256)
 __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_kernel(
     Geom g, uint32_t layer, uint32_t n_heads, uint32_t G, const float* __restrict__ q,
     float* __restrict__ out, const int32_t* __restrict__ tables, uint32_t max_blocks,
-    const int32_t* __restrict__ ctx_lens, const int32_t* __restrict__ q_lens,
-    const int64_t* __restrict__ q_offsets, uint32_t max_q_len, float scale,
-    uint32_t split_blocks, uint32_t max_splits, float* __restrict__ ws_o,
-    float* __restrict__ ws_ml, uint32_t prio_blocks) {
+    uint32_t cap_blocks, const int32_t* __restrict__ ctx_lens,
+    const int32_t* __restrict__ q_lens, const int64_t* __restrict__ q_offsets,
+    uint32_t max_q_len, float scale, uint32_t split_blocks, uint32_t max_splits,
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, uint32_t prio_blocks) {
   constexpr int NC = D / 32, NM = D / 16;
   constexpr int kStep = 2;  // blocks per softmax step
   constexpr int kTile = prefill_tile_bytes<DT, D>();
@@ -1831,7 +1831,9 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   const uint32_t seq = sk / g.n_kv_heads, kvh = sk % g.n_kv_heads;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int32_t T = 16 / (int32_t)G;  // query tokens per wave tile
-  const PfSeq sq = pf_seq(ctx_lens, q_lens, seq, (int32_t)(max_blocks * B), max_q_len);
+  // contexts are clamped to cap_blocks (the table row, or the staged blocks of a Q8_0
+  // call through pf_stage_q8_kernel, whose instances must agree on every piece)
+  const PfSeq sq = pf_seq(ctx_lens, q_lens, seq, (int32_t)(cap_blocks * B), max_q_len);
   // The grid holds max_q_len queries a sequence: past that the first max_q_len are
   // computed, at the positions the caller gave them, and the fault is raised.
   if (sq.clamped && blockIdx.y == 0 && blockIdx.z == 0 && threadIdx.x == 0 && kvh == 0)
@@ -2238,6 +2240,79 @@ __attribute__((amdgpu_waves_per_eu(MODE == kPfFast ? 4 : 2, 8))) attn_prefill_ke
   }
 }
 
+// Q8_0 prefill through a staging area: the blocks of the calling sequences dequantised
+// once per call into binary16 tiles in the F16 pool layout (K [D/8][B][8], V [D][B]),
+// staged block s * nblk + j holding block j of sequence s (contexts clamped to nblk
+// blocks) in a one-layer staging pool. The staging table maps (s, j) to it (-1 where the
+// pool's entry lies outside the pool: the prefill kernel faults and skips it) and the
+// staging marks copy the pool block's mark. A value is f16(scale x quant) with one
+// rounding (v_pk_mul_f16): the operand the fast Q8_0 instance forms in LDS from the
+// same bytes, so the F16 fast instance over the staging computes what it would. In
+// the fast Q8_0 instance every workgroup dequantises every block it stages, and up to
+// max_q_len / 16 workgroups of a (sequence, KV head) stage the same block; here each
+// block is converted once. Marked blocks (scales of 512 or more, whose products can
+// overflow binary16) are computed by the exact instance from the pool itself.
+// Grid (n_seqs * nblk, n_kv_heads); thread t writes K unit t (run t / 16, token t %
+// 16) and V unit t (dim t / 2, tokens 8 (t % 2) .. + 7), twice at head_dim 128.
+template <int D>
+__global__ void __launch_bounds__(256) pf_stage_q8_kernel(
+    Geom g, uint32_t layer, const int32_t* __restrict__ tables, uint32_t max_blocks,
+    const int32_t* __restrict__ ctx_lens, uint32_t nblk, uint8_t* __restrict__ stage,
+    int32_t* __restrict__ stab, uint32_t* __restrict__ smark) {
+  constexpr uint32_t NG = D / 32, kTileF = B * D * 2;
+  const uint32_t sj = blockIdx.x, h = blockIdx.y;
+  const uint32_t sq = sj / nblk, j = sj % nblk;
+  int32_t c = ctx_lens[sq];
+  const int32_t cap = (int32_t)(nblk * B);
+  c = c < 0 ? 0 : (c > cap ? cap : c);
+  if ((int32_t)(j * B) >= c) return;  // past the context: never read
+  const int32_t p = tables[(uint64_t)sq * max_blocks + j];
+  const bool ok = p >= 0 && (uint64_t)p < g.num_blocks;
+  if (h == 0 && threadIdx.x == 0) {
+    stab[sj] = ok ? (int32_t)sj : -1;
+    smark[sj] = ok ? g.bmark[p] : 0u;
+  }
+  if (!ok) return;
+  const uint8_t* kq = tile_ptr(g, (uint64_t)p, layer, 0, h);
+  const uint8_t* vq = tile_ptr(g, (uint64_t)p, layer, 1, h);
+  uint8_t* kf = stage + (uint64_t)sj * (2u * g.n_kv_heads * kTileF) + (uint64_t)h * kTileF;
+  uint8_t* vf = kf + (uint64_t)g.n_kv_heads * kTileF;
+  // K units: dims 8r .. 8r + 7 of token tt (q8_quant_offset: chunk cc, group gg)
+  for (uint32_t u = threadIdx.x; u < (uint32_t)D / 8u * 16u; u += 256u) {
+    {
+      const uint32_t r = u / 16u, tt = u % 16u, cc = r / 4u, gg = r % 4u;
+      const uint2 qq = *(const uint2*)(kq + (cc / 2u) * 1024u + (gg * 16u + tt) * 16u + (cc % 2u) * 8u);
+      const uint32_t sb = *(const uint16_t*)(kq + B * D + (tt * NG + cc) * 2u);
+      const f16x2 s2 = __builtin_bit_cast(f16x2, sb | (sb << 16));
+      const uint32_t w0 = qq.x ^ 0x80808080u, w1 = qq.y ^ 0x80808080u;
+      *(uint4*)(kf + (r * 16u + tt) * 16u) =
+          make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelLo) * s2),
+                     __builtin_bit_cast(uint32_t, i8_pair_to_f16(w0, kSelHi) * s2),
+                     __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelLo) * s2),
+                     __builtin_bit_cast(uint32_t, i8_pair_to_f16(w1, kSelHi) * s2));
+    }
+  }
+  // V units: tokens 8hh .. 8hh + 7 of dim n, each with its token's scale of group n / 32
+  for (uint32_t u = threadIdx.x; u < (uint32_t)D * 2u; u += 256u) {
+    {
+      const uint32_t n = u / 2u, hh = u % 2u, m = n / 16u, jj = n % 16u;
+      const uint8_t* src = vq + (m / 4u) * 1024u + (2u * hh * 16u + jj) * 16u + (m % 4u) * 4u;
+      const uint32_t qa = *(const uint32_t*)src ^ 0x80808080u;          // tokens 8hh .. +3
+      const uint32_t qb = *(const uint32_t*)(src + 256) ^ 0x80808080u;  // tokens 8hh + 4 .. +7
+      const uint8_t* sp = vq + B * D + ((8u * hh) * NG + n / 32u) * 2u;
+      uint32_t sc[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) sc[i] = *(const uint16_t*)(sp + i * NG * 2u);
+      auto pr = [&](int i) { return __builtin_bit_cast(f16x2, sc[i] | (sc[i + 1] << 16)); };
+      *(uint4*)(vf + n * 32u + hh * 16u) =
+          make_uint4(__builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelLo) * pr(0)),
+                     __builtin_bit_cast(uint32_t, i8_pair_to_f16(qa, kSelHi) * pr(2)),
+                     __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelLo) * pr(4)),
+                     __builtin_bit_cast(uint32_t, i8_pair_to_f16(qb, kSelHi) * pr(6)));
+    }
+  }
+}
+
 // Merges the key-range pieces of every prefill workgroup cut into more than one:
 // out = sum_z 2^(m_z - M) o_z / sum_z 2^(m_z - M) l_z with M = max_z m_z (0 where M is
 // not finite, as the single-piece path writes). Grid (n_seqs * n_kv_heads, tile
@@ -2334,8 +2409,9 @@ hipError_t launch_attention_stream(const Geom& g, uint32_t layer, uint32_t n_hea
   return hipGetLastError();
 }
 
-PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_q_len,
-                         uint32_t max_ctx_len) {
+namespace {
+PrefillPlan prefill_plan_pieces(const Geom& g, uint32_t n_heads, uint32_t n_seqs,
+                                uint32_t max_q_len, uint32_t max_ctx_len) {
   PrefillPlan p{};
   const uint32_t G = n_heads / g.n_kv_heads;
   const uint32_t T = 16 / G;
@@ -2370,6 +2446,27 @@ PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint3
   p.ws_bytes = (p.ws_o_floats + slots * 2) * sizeof(float);
   return p;
 }
+}  // namespace
+
+// The key-range pieces, then for Q8_0 pools the staging area of pf_stage_q8_kernel after
+// the partials: n_seqs x ceil(max_ctx_len / 16) blocks of binary16 K and V tiles of every
+// KV head (one layer), the staging table and the staging marks.
+PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_q_len,
+                         uint32_t max_ctx_len) {
+  PrefillPlan p = prefill_plan_pieces(g, n_heads, n_seqs, max_q_len, max_ctx_len);
+  const uint64_t nblk = ((uint64_t)max_ctx_len + B - 1) / B;
+  p.cap_blocks = (uint32_t)nblk;
+  if (g.dtype != kDtypeQ8) return p;
+  const uint64_t n = (uint64_t)n_seqs * nblk;
+  if (nblk == 0 || n > 0x7fffffffull) return p;
+  auto al = [](uint64_t x) { return (x + 255) / 256 * 256; };
+  p.stage_nblk = (uint32_t)nblk;
+  p.stage_off = al(p.ws_bytes);
+  p.stage_tab_off = p.stage_off + al(n * 2u * g.n_kv_heads * B * g.head_dim * 2u);
+  p.stage_mark_off = p.stage_tab_off + al(n * 4u);
+  p.ws_bytes = p.stage_mark_off + al(n * 4u);
+  return p;
+}
 
 hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_heads,
                                     const float* q, float* out, const int32_t* tables,
@@ -2385,17 +2482,57 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
   float* ws_o = split ? (float*)workspace : nullptr;
   float* ws_ml = split ? ws_o + plan.ws_o_floats : nullptr;
   dim3 grid(n_seqs * g.n_kv_heads, plan.tile_groups, max_splits);
+  // Contexts past max_ctx_len (whole blocks) are clamped to it with FKV_FAULT_CTX_RANGE
+  // by every kernel of the call. Q8_0 with a workspace: the calling sequences' blocks
+  // dequantised once into the staging area (which holds that many blocks a sequence),
+  // the F16 fast instance over it, the exact instance over the pool for marked blocks.
+  const uint32_t cap_blocks =
+      plan.cap_blocks != 0 && plan.cap_blocks < max_blocks ? plan.cap_blocks : max_blocks;
+  const bool staged = g.dtype == kDtypeQ8 && workspace != nullptr && plan.stage_nblk != 0 &&
+                      plan.stage_nblk == cap_blocks;
+  Geom gs = g;
+  int32_t* stab = nullptr;
+  if (staged) {
+    uint8_t* wsb = (uint8_t*)workspace;
+    stab = (int32_t*)(wsb + plan.stage_tab_off);
+    gs.base = wsb + plan.stage_off;
+    gs.tile_bytes = (uint64_t)B * g.head_dim * 2u;
+    gs.block_bytes = 2u * g.n_kv_heads * gs.tile_bytes;
+    gs.num_blocks = (uint64_t)n_seqs * plan.stage_nblk;
+    gs.n_layers = 1;
+    gs.dtype = kDtypeF16;
+    gs.bmark = (uint32_t*)(wsb + plan.stage_mark_off);
+    gs.hmark = nullptr;
+    const dim3 sgrid(n_seqs * plan.stage_nblk, g.n_kv_heads);
+    if (g.head_dim == 128)
+      pf_stage_q8_kernel<128><<<sgrid, 256, 0, s>>>(g, layer, tables, max_blocks, ctx_lens,
+                                                    plan.stage_nblk, gs.base, stab, gs.bmark);
+    else
+      pf_stage_q8_kernel<64><<<sgrid, 256, 0, s>>>(g, layer, tables, max_blocks, ctx_lens,
+                                                   plan.stage_nblk, gs.base, stab, gs.bmark);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
 #define FKV_LAUNCH_PF(DT_, D_, X_)                                                          \
   attn_prefill_kernel<DT_, D_, X_><<<grid, 256, 0, s>>>(g, layer, n_heads, G, q, out, tables, \
-                                                        max_blocks, ctx_lens, q_lens,         \
-                                                        q_offsets, max_q_len, scale,          \
+                                                        max_blocks, cap_blocks, ctx_lens,     \
+                                                        q_lens, q_offsets, max_q_len, scale,  \
                                                         split_blocks, max_splits, ws_o, ws_ml, \
                                                         plan.prio_blocks)
   // The fast instance, then the one for workgroups whose blocks' marks say the fast one
   // cannot compute them: Q8_0 the exact instance (a scale of 512 or more was stored),
   // F16 the leak-safe one (an Inf/NaN K or V was stored). Each exits where the other works.
   const int dt = g.dtype == kDtypeQ8 ? kDtypeQ8 : kDtypeF16;
-  if (dt == kDtypeQ8) {
+  if (staged) {
+    if (g.head_dim == 128)
+      attn_prefill_kernel<kDtypeF16, 128, kPfFast><<<grid, 256, 0, s>>>(
+          gs, 0, n_heads, G, q, out, stab, plan.stage_nblk, cap_blocks, ctx_lens, q_lens,
+          q_offsets, max_q_len, scale, split_blocks, max_splits, ws_o, ws_ml, plan.prio_blocks);
+    else
+      attn_prefill_kernel<kDtypeF16, 64, kPfFast><<<grid, 256, 0, s>>>(
+          gs, 0, n_heads, G, q, out, stab, plan.stage_nblk, cap_blocks, ctx_lens, q_lens,
+          q_offsets, max_q_len, scale, split_blocks, max_splits, ws_o, ws_ml, plan.prio_blocks);
+  } else if (dt == kDtypeQ8) {
     if (g.head_dim == 128) FKV_LAUNCH_PF(kDtypeQ8, 128, kPfFast);
     else FKV_LAUNCH_PF(kDtypeQ8, 64, kPfFast);
   } else {
@@ -2414,14 +2551,15 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
 #undef FKV_LAUNCH_PF
   e = hipGetLastError();
   if (e != hipSuccess || !split) return e;
+  // the combine reads the table width only as the context cap
   const dim3 cgrid(n_seqs * g.n_kv_heads, plan.tile_groups);
   if (g.head_dim == 128)
-    attn_prefill_combine_kernel<128><<<cgrid, 256, 0, s>>>(g.n_kv_heads, n_heads, G, max_blocks,
+    attn_prefill_combine_kernel<128><<<cgrid, 256, 0, s>>>(g.n_kv_heads, n_heads, G, cap_blocks,
                                                            ctx_lens, q_lens, q_offsets, max_q_len,
                                                            split_blocks, max_splits, ws_o, ws_ml,
                                                            out);
   else
-    attn_prefill_combine_kernel<64><<<cgrid, 256, 0, s>>>(g.n_kv_heads, n_heads, G, max_blocks,
+    attn_prefill_combine_kernel<64><<<cgrid, 256, 0, s>>>(g.n_kv_heads, n_heads, G, cap_blocks,
                                                           ctx_lens, q_lens, q_offsets, max_q_len,
                                                           split_blocks, max_splits, ws_o, ws_ml,
                                                           out);

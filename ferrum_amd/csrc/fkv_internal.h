@@ -179,6 +179,11 @@ struct PrefillPlan {
   uint64_t ws_o_floats;   // partial outputs, then (max, sum) pairs
   uint64_t ws_bytes;
   uint32_t prio_blocks;   // longest key range in blocks (issue-priority scale; 0: off)
+  uint32_t cap_blocks;    // ceil(max_ctx_len / 16): longer contexts are clamped (fault)
+  // Q8_0 pools: blocks a sequence stages (ceil(max_ctx_len / 16); 0: no staging), and
+  // the workspace offsets of the binary16 tiles, the staging table and staging marks
+  uint32_t stage_nblk;
+  uint64_t stage_off, stage_tab_off, stage_mark_off;
 };
 PrefillPlan prefill_plan(const Geom& g, uint32_t n_heads, uint32_t n_seqs, uint32_t max_q_len,
                          uint32_t max_ctx_len);

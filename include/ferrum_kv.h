@@ -416,7 +416,9 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
  * 64 or 128, g <= 16, and a pool block (all layers' K and V) under 4 GiB
  * (FKV_ERR_KERNEL otherwise). The launch holds max_q_len queries a sequence: a q_lens[s]
  * above it (or above ctx_lens[s]) raises FKV_FAULT_CTX_RANGE, and only its first
- * max_q_len queries are computed, at the positions q_lens[s] gives them. No query
+ * max_q_len queries are computed, at the positions q_lens[s] gives them. A ctx_lens[s]
+ * past max_ctx_len rounded up to whole blocks raises FKV_FAULT_CTX_RANGE and is
+ * clamped to it (the sequence's queries then end at the clamped context). No query
  * reads a position past its own, Inf/NaN values included: workgroups over F16 blocks
  * marked as holding an Inf/NaN K or V (see the block marks above) run a slower
  * instance that keeps such V values from earlier queries of the same tile and gives an
@@ -425,9 +427,12 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
  * workspace: NULL, or device scratch of fkv_prefill_attention_workspace_size()
  * bytes (16-byte aligned; no initialisation) in which workgroups over long
  * contexts leave the partial results of pieces of their key range for a merge
- * pass. With NULL every workgroup reads its whole key range itself (same results
- * within the attention tolerance; slower when contexts differ in length). Calls
- * that share one workspace must not overlap. */
+ * pass, and (Q8_0 pools) the call's blocks are dequantised once to binary16 for
+ * every workgroup that reads them: n_seqs x ceil(max_ctx_len / 16) blocks of K and V
+ * tiles of every KV head, 2 x n_kv_heads x 16 x head_dim x 2 bytes each. With NULL
+ * every workgroup reads its whole key range itself and Q8_0 workgroups dequantise
+ * what they read (same results within the attention tolerance; slower). Calls that
+ * share one workspace must not overlap. */
 int32_t fkv_prefill_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
                                              uint32_t n_seqs, uint32_t max_q_len,
                                              uint32_t max_ctx_len, uint64_t* bytes_out);

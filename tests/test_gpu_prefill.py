@@ -49,12 +49,14 @@ def _pool(d, hkv, ctxs, seed, layers=1, dtype=1, kv=None):
     return pool, layout, tab
 
 
-def _prefill(pool, layer, q, tab, ctxs, qls, offs, fill=5.0, max_q_len=None, split=True):
+def _prefill(pool, layer, q, tab, ctxs, qls, offs, fill=5.0, max_q_len=None, split=True,
+             max_ctx_len=None):
     import torch
     out = torch.full(q.shape, fill, dtype=torch.float32, device="cuda")
     pool.prefill_attention(layer, to_dev(q), out, to_dev(tab), to_dev(np.array(ctxs, np.int32)),
                            to_dev(np.array(qls, np.int32)), to_dev(offs),
-                           max(qls) if max_q_len is None else max_q_len, max(ctxs), split=split)
+                           max(qls) if max_q_len is None else max_q_len,
+                           max(ctxs) if max_ctx_len is None else max_ctx_len, split=split)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
@@ -320,6 +322,60 @@ def test_table_entry_outside_the_pool_is_flagged_and_skipped(dtype, pieces, tune
     s1 = slice(1 + qls[0], 1 + qls[0] + qls[1])
     assert np.all(np.isfinite(got[s1]))
     assert np.all(got[0] == 5.0) and np.all(got[rows - 1] == 5.0)
+
+
+@pytest.mark.parametrize("d,g", [(128, 4), (64, 8), (128, 1), (64, 16)])
+def test_q8_staged_prefill_is_bit_identical_to_in_kernel_dequant(d, g, tune):
+    """With a workspace, a Q8_0 call dequantises its blocks once into binary16 staging
+    tiles (the F16 pool layout) and runs the F16 fast instance over them; without one,
+    every workgroup dequantises what it stages into LDS. Both form f16(scale x quant)
+    with one rounding and run the same score/P.V code, so with whole key ranges (no
+    pieces on either side) the outputs agree bit for bit, including a sequence whose
+    history holds a block marked for a wide scale (computed by the exact instance in
+    both) and contexts that end mid-block; and both meet the oracle's bar."""
+    tune(prefill_split_blocks=0)
+    hkv = 2
+    ctxs, qls = [300, 17, 1000, 520], [300, 17, 100, 33]
+
+    def kv(rng, n):
+        k = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        v = rng.standard_normal((n, hkv, d), dtype=np.float32)
+        k[317 + 5, 1, 3] = 3e5  # sequence 2's block 0 (its rows start at 300 + 17)
+        return k, v
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=71, dtype=8, kv=kv)
+    assert pool.marked_blocks() == 1
+    offs = np.array([0, 300, 317, 417], np.int64)
+    q = np.random.default_rng(8).standard_normal((450, hkv * g, d), dtype=np.float32)
+    staged = _prefill(pool, 0, q, tab, ctxs, qls, offs, split=True)
+    assert pool.take_fault_flags() == 0
+    direct = _prefill(pool, 0, q, tab, ctxs, qls, offs, split=False)
+    assert pool.take_fault_flags() == 0
+    assert np.array_equal(staged.view(np.uint32), direct.view(np.uint32))
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    rows = _used(450, offs, qls)
+    assert_close(staged[rows], want[rows], what="staged q8 prefill")
+    assert np.all(staged[~rows] == 5.0)
+
+
+@pytest.mark.parametrize("dtype,split", [(1, True), (1, False), (8, True), (8, False)])
+def test_context_past_max_ctx_len_is_clamped_and_flagged(dtype, split, tune):
+    """A context longer than the call's max_ctx_len (300 here: 19 blocks, 304 tokens) is
+    clamped to 304 tokens with FKV_FAULT_CTX_RANGE, by every kernel of the call alike
+    (the staged Q8_0 path holds no more): the sequence's queries end at position 303, as
+    the oracle gives them for a 304-token context; the other sequence is unaffected.
+    F16 and Q8_0, with a workspace (key-range pieces of 4 blocks; Q8_0 staged) and
+    without."""
+    import ferrum_amd as fa
+    tune(prefill_split_blocks=4)
+    hkv, g, d = 2, 4, 128
+    ctxs, qls = [120, 400], [40, 50]
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=81, dtype=dtype)
+    offs = np.array([0, 40], np.int64)
+    q = np.random.default_rng(9).standard_normal((90, hkv * g, d), dtype=np.float32)
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs, split=split, max_ctx_len=300)
+    assert pool.take_fault_flags() == fa.FAULT_CTX_RANGE
+    want = _want(pool, layout, q, tab, [120, 304], qls, offs, d)
+    assert_close(got, want, what="prefill past max_ctx_len")
 
 
 def _term_sums(layout, image, q, tab, ctxs, qls, offs, scale):
