@@ -606,9 +606,6 @@ __global__ void __launch_bounds__(256) gather_tables_kernel(
 // slots that are one whole block (by slot).
 // ---------------------------------------------------------------------------
 
-constexpr int kFmtF32 = 0;  // FKV_GATHER_F32
-constexpr int kFmtRaw = 1;  // FKV_GATHER_RAW
-
 // Heads per workgroup: F16 one 16-byte unit of each tile a thread (1 at D = 128, 2 at
 // 64); Q8_0 tiles are half the bytes and staged whole, so 4 (8) heads keep as many bytes
 // in flight per workgroup (one head a workgroup ran at 43% of a device copy).
@@ -626,15 +623,49 @@ struct GatherShape {
                                                 // fall 16 banks apart
 };
 
+// Bytes of a Q8_0 workgroup's heads in one output row: kHpw heads of D / 32 34-byte
+// blocks, 16 x 34 at head_dim 64 and 128 alike.
+constexpr uint32_t kGatherQ8Span = 16u * 34u;
+
 // LDS of the tile path: F16 the V tiles transposed to [token][dim]; Q8_0 both tiles as
-// stored.
-template <int DT, int D>
+// stored, and for the raw format the workgroup's output records [kv][token][span].
+constexpr int kFmtF32 = 0;  // FKV_GATHER_F32
+constexpr int kFmtRaw = 1;  // FKV_GATHER_RAW
+
+// Q8_0 tiles in LDS: head hl's K tile, then its V tile. For the raw format 16 bytes of
+// padding follow every 256 bytes of a tile and heads start 32 banks apart: the record
+// pass's dword reads of one instruction (lanes of other token groups, blocks and heads,
+// at multiples of 256 bytes in the stored tile) then fall on distinct banks (unpadded:
+// 8 V lanes a bank).
+template <int D, int FMT>
+struct GatherQ8Lds {
+  static constexpr uint32_t kTile = 16u * D + 16u * (D / 32u) * 2u;
+  static constexpr bool kPad = FMT == kFmtRaw;
+  static constexpr uint32_t kTileP = kPad ? kTile + (kTile + 255u) / 256u * 16u : kTile;
+  static constexpr uint32_t kHead = kPad ? (2u * kTileP + 127u) / 256u * 256u + 128u : 2u * kTileP;
+  // byte b of head hl's tile kv
+  __device__ static uint32_t off(uint32_t hl, uint32_t kv, uint32_t b) {
+    return hl * kHead + kv * kTileP + (kPad ? b + (b >> 8) * 16u : b);
+  }
+};
+
+template <int DT, int D, int FMT>
 struct __align__(16) GatherLds {  // 16-byte unit stores into q
   using S = GatherShape<DT, D>;
+  using Q = GatherQ8Lds<D, FMT>;
+  static constexpr bool kRec = DT == kDtypeQ8 && FMT == kFmtRaw;
   union {
     uint16_t v[S::kHpw][16][S::kVRow];
-    uint8_t q[S::kHpw][2][S::kTile];
+    uint8_t q[DT == kDtypeQ8 ? S::kHpw * Q::kHead : 16];
   };
+  // records: token rows 560 bytes apart, V's 16 bytes past a whole number of K's (the
+  // record pass's stores of one instruction then meet at most 2 to a bank, against 4)
+  static constexpr uint32_t kRecRow = kGatherQ8Span + 16u;
+  static constexpr uint32_t kRecKv = 16u * kRecRow + 16u;
+  uint8_t rec[kRec ? 2u * kRecKv : 16u];
+  __device__ uint8_t* rec_at(uint32_t kv, uint32_t o, uint32_t b) {
+    return rec + kv * kRecKv + o * kRecRow + b;
+  }
 };
 
 // Stores 8 binary16 values (one 16-byte unit) as FMT requires: RAW the 16 bytes, F32
@@ -656,7 +687,7 @@ __device__ __forceinline__ void store_f16_unit(uint8_t* dst, uint4 w) {
 // pool: nothing is written); tokens o < n are written to rows row0 + o of out_k / out_v
 // (row_bytes apart; head h at h * head_bytes within a row). All 256 threads call this.
 template <int DT, int D, int FMT>
-__device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g, uint32_t layer,
+__device__ __forceinline__ void gather_tile(GatherLds<DT, D, FMT>& lds, const Geom& g, uint32_t layer,
                                             int64_t blk, uint32_t h0, int32_t n,
                                             uint8_t* out_k, uint8_t* out_v, uint64_t row0) {
   using S = GatherShape<DT, D>;
@@ -703,18 +734,22 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g
       const uint32_t kv = r / S::kUnits, un = r % S::kUnits;
       const uint32_t h = h0 + hl;
       if (blk_ok && h < g.n_kv_heads)
-        *(uint4*)&lds.q[hl][kv][un * 16u] =
+        *(uint4*)&lds.q[GatherQ8Lds<D, FMT>::off(hl, kv, un * 16u)] =
             *(const uint4*)(tile_ptr(g, (uint64_t)blk, layer, kv, h) + (uint64_t)un * 16u);
     }
     __syncthreads();
     if (blk_ok) {
       if constexpr (FMT == kFmtRaw) {
-        // Ferrum's 34-byte blocks (dtype.rs:19-21: f16 scale, then 32 x i8). A step is one
-        // block b of 4 consecutive tokens 4q .. 4q + 3 of one tile: their quants come from
-        // LDS as whole dwords (K: 8 bytes of a token's run at a time; V: a dword holds the
-        // 4 tokens' bytes of one dim, transposed in registers), and each block goes out as
-        // dword stores plus one 2-byte store (the scale or the last two quants, by b's
-        // parity: blocks start 34 bytes apart).
+        // Ferrum's 34-byte blocks (dtype.rs:19-21: f16 scale, then 32 x i8), in two
+        // passes. First each output record is built in LDS: a step is one block b of 4
+        // consecutive tokens 4q .. 4q + 3 of one tile, whose quants come from the staged
+        // tile as whole dwords (K: 8 bytes of a token's run at a time; V: a dword holds
+        // the 4 tokens' bytes of one dim, transposed by byte permutes), written as dwords
+        // plus one 2-byte store (the scale or the last two quants, by b's parity: blocks
+        // start 34 bytes apart, records 4-byte aligned). Then the records go out as
+        // whole 16-byte units: a token's heads of the workgroup are one contiguous span
+        // of its output row (written directly, the 4-byte stores of 64 lanes fell on as
+        // many scattered blocks).
         constexpr uint32_t kNb = D / 32u;
         constexpr uint32_t kPer = 2u * 4u * kNb;
         for (uint32_t i = threadIdx.x; i < (uint32_t)S::kHpw * kPer; i += 256u) {
@@ -722,7 +757,11 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g
           const uint32_t kv = r / (4u * kNb), q = (r / kNb) % 4u, b = r % kNb;
           const uint32_t h = h0 + hl;
           if (h >= g.n_kv_heads || (int32_t)(4u * q) >= n) continue;
-          const uint8_t* t = lds.q[hl][kv];
+          using Q = GatherQ8Lds<D, FMT>;
+          const uint8_t* t = lds.q + Q::off(hl, kv, 0u);
+          // byte b of the tile (the padding is inserted between 256-byte spans, and no
+          // read below crosses one)
+          auto tb = [](uint32_t b) { return Q::kPad ? b + (b >> 8) * 16u : b; };
           uint32_t qw[4][8];  // [token][quant dword]
           if (kv == 0) {
 #pragma unroll
@@ -730,7 +769,7 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g
               const uint32_t o = 4u * q + tt;
 #pragma unroll
               for (uint32_t gg = 0; gg < 4; gg++) {  // dims b*32 + gg*8 .. +7
-                const uint2 w = *(const uint2*)&t[(b / 2u) * 1024u + (gg * 16u + o) * 16u + (b % 2u) * 8u];
+                const uint2 w = *(const uint2*)&t[tb((b / 2u) * 1024u + (gg * 16u + o) * 16u + (b % 2u) * 8u)];
                 qw[tt][2 * gg] = w.x;
                 qw[tt][2 * gg + 1] = w.y;
               }
@@ -742,20 +781,24 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g
               uint32_t w[4];
 #pragma unroll
               for (uint32_t jj = 0; jj < 4; jj++)
-                w[jj] = *(const uint32_t*)&t[(m / 4u) * 1024u + (q * 16u + j0 + jj) * 16u + (m % 4u) * 4u];
-#pragma unroll
-              for (uint32_t tt = 0; tt < 4; tt++)  // byte tt of each: token 4q + tt
-                qw[tt][k] = ((w[0] >> (8u * tt)) & 0xffu) | (((w[1] >> (8u * tt)) & 0xffu) << 8) |
-                            (((w[2] >> (8u * tt)) & 0xffu) << 16) | (((w[3] >> (8u * tt)) & 0xffu) << 24);
+                w[jj] = *(const uint32_t*)&t[tb((m / 4u) * 1024u + (q * 16u + j0 + jj) * 16u + (m % 4u) * 4u)];
+              // 4 x 4 byte transpose: token tt's bytes of dims 4k .. 4k + 3
+              const uint32_t lo01 = __builtin_amdgcn_perm(w[1], w[0], 0x05010400u);
+              const uint32_t hi01 = __builtin_amdgcn_perm(w[1], w[0], 0x07030602u);
+              const uint32_t lo23 = __builtin_amdgcn_perm(w[3], w[2], 0x05010400u);
+              const uint32_t hi23 = __builtin_amdgcn_perm(w[3], w[2], 0x07030602u);
+              qw[0][k] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u);
+              qw[1][k] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u);
+              qw[2][k] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
+              qw[3][k] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
             }
           }
 #pragma unroll
           for (uint32_t tt = 0; tt < 4; tt++) {
             const uint32_t o = 4u * q + tt;
             if ((int32_t)o >= n) break;
-            const uint32_t sc = *(const uint16_t*)&t[16u * D + (o * kNb + b) * 2u];
-            uint8_t* dst = (kv ? out_v : out_k) + (row0 + o) * row_bytes + (uint64_t)h * kHeadBytes +
-                           b * 34u;
+            const uint32_t sc = *(const uint16_t*)&t[tb(16u * D + (o * kNb + b) * 2u)];
+            uint8_t* dst = lds.rec_at(kv, o, hl * (uint32_t)kHeadBytes + b * 34u);
             if (b % 2u) {  // the block starts 2 mod 4: scale, then the quants on dword bounds
               *(uint16_t*)dst = (uint16_t)sc;
 #pragma unroll
@@ -769,6 +812,30 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g
             }
           }
         }
+        __syncthreads();
+        // The span of the group's heads that exist, at h0 * kHeadBytes = a multiple of 544
+        // bytes into the row: whole 16-byte units where the rows keep that alignment,
+        // dwords otherwise (records are dword multiples).
+        const uint32_t nh = g.n_kv_heads - h0 < (uint32_t)S::kHpw ? g.n_kv_heads - h0 : (uint32_t)S::kHpw;
+        const uint32_t span = nh * (uint32_t)kHeadBytes;
+        const uint64_t col0 = (uint64_t)h0 * kHeadBytes;
+        if (span % 16u == 0 && row_bytes % 16u == 0) {
+          const uint32_t per = span / 16u;
+          for (uint32_t i = threadIdx.x; i < 2u * (uint32_t)n * per; i += 256u) {
+            const uint32_t kv = i / ((uint32_t)n * per), r = i % ((uint32_t)n * per);
+            const uint32_t o = r / per, u = r % per;
+            *(uint4*)((kv ? out_v : out_k) + (row0 + o) * row_bytes + col0 + u * 16u) =
+                *(const uint4*)lds.rec_at(kv, o, u * 16u);
+          }
+        } else {
+          const uint32_t per = span / 4u;
+          for (uint32_t i = threadIdx.x; i < 2u * (uint32_t)n * per; i += 256u) {
+            const uint32_t kv = i / ((uint32_t)n * per), r = i % ((uint32_t)n * per);
+            const uint32_t o = r / per, u = r % per;
+            *(uint32_t*)((kv ? out_v : out_k) + (row0 + o) * row_bytes + col0 + u * 4u) =
+                *(const uint32_t*)lds.rec_at(kv, o, u * 4u);
+          }
+        }
       } else {
         // f16_to_f32(scale) * (i8 as f32), scalar.rs:268-275: 8 dims a step
         constexpr uint32_t kPer = 2u * 16u * (D / 8u);
@@ -777,7 +844,7 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D>& lds, const Geom& g
           const uint32_t kv = r / (16u * (D / 8u)), o = (r / (D / 8u)) % 16u, c8 = r % (D / 8u);
           const uint32_t h = h0 + hl;
           if (h >= g.n_kv_heads || (int32_t)o >= n) continue;
-          const uint8_t* t = lds.q[hl][kv];
+          const uint8_t* t = lds.q + GatherQ8Lds<D, FMT>::off(hl, kv, 0u);  // unpadded
           const float sc =
               f16_bits_to_f32(*(const uint16_t*)&t[16u * D + (o * (D / 32u) + c8 / 4u) * 2u]);
           float x[8];
@@ -803,7 +870,7 @@ __global__ void __launch_bounds__(256) gather_tables_tile_kernel(
     const int32_t* __restrict__ ctx_lens, const int64_t* __restrict__ out_offsets,
     uint8_t* out_k, uint8_t* out_v) {
   using S = GatherShape<DT, D>;
-  __shared__ GatherLds<DT, D> lds;
+  __shared__ GatherLds<DT, D, FMT> lds;
   const uint32_t hgroups = (g.n_kv_heads + S::kHpw - 1) / S::kHpw;
   const uint32_t seq = blockIdx.y, j = blockIdx.x / hgroups, hg = blockIdx.x % hgroups;
   int32_t ctx = ctx_lens[seq];
@@ -830,7 +897,7 @@ __global__ void __launch_bounds__(256) gather_slots_tile_kernel(
     Geom g, uint32_t layer, const int64_t* __restrict__ slots, uint32_t n_tokens,
     uint8_t* out_k, uint8_t* out_v) {
   using S = GatherShape<DT, D>;
-  __shared__ GatherLds<DT, D> lds;
+  __shared__ GatherLds<DT, D, FMT> lds;
   __shared__ int32_t s_whole;
   const uint32_t hgroups = (g.n_kv_heads + S::kHpw - 1) / S::kHpw;
   const uint32_t win = blockIdx.x / hgroups, hg = blockIdx.x % hgroups;
@@ -1110,7 +1177,7 @@ hipError_t launch_gather_slots(const Geom& g, uint32_t layer, const int64_t* slo
                                hipStream_t s) {
   if (n_tokens == 0) return hipSuccess;
   if (gather_tile_ok(g, out_k, out_v)) {
-    const uint32_t hpw = g.head_dim == 128 ? 1u : 2u;
+    const uint32_t hpw = gather_heads_per_wg(g.dtype, g.head_dim);
     const uint64_t wgs = ((uint64_t)n_tokens + 15u) / 16u * ((g.n_kv_heads + hpw - 1) / hpw);
     if (wgs > 0x7fffffffull) return hipErrorInvalidValue;
     const dim3 grid((uint32_t)wgs);
