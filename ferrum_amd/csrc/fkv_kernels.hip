@@ -750,31 +750,38 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D, FMT>& lds, const Ge
         // whole 16-byte units: a token's heads of the workgroup are one contiguous span
         // of its output row (written directly, the 4-byte stores of 64 lanes fell on as
         // many scattered blocks).
+        // Wave 0 takes the V blocks (64 items: head, token quad, block; a quad's 4 tokens
+        // share each dword read), waves 1-3 the K blocks (256 items: head, token, block),
+        // so no wave runs both paths and all four work (kHpw x kNb = 16 at head_dim 64
+        // and 128 alike).
         constexpr uint32_t kNb = D / 32u;
-        constexpr uint32_t kPer = 2u * 4u * kNb;
-        for (uint32_t i = threadIdx.x; i < (uint32_t)S::kHpw * kPer; i += 256u) {
-          const uint32_t hl = i / kPer, r = i % kPer;
-          const uint32_t kv = r / (4u * kNb), q = (r / kNb) % 4u, b = r % kNb;
-          const uint32_t h = h0 + hl;
-          if (h >= g.n_kv_heads || (int32_t)(4u * q) >= n) continue;
-          using Q = GatherQ8Lds<D, FMT>;
-          const uint8_t* t = lds.q + Q::off(hl, kv, 0u);
-          // byte b of the tile (the padding is inserted between 256-byte spans, and no
-          // read below crosses one)
-          auto tb = [](uint32_t b) { return Q::kPad ? b + (b >> 8) * 16u : b; };
-          uint32_t qw[4][8];  // [token][quant dword]
-          if (kv == 0) {
+        static_assert(S::kHpw * kNb == 16, "64 V and 256 K items");
+        using Q = GatherQ8Lds<D, FMT>;
+        // byte b of a tile (the padding is inserted between 256-byte spans, and no read
+        // below crosses one)
+        auto tb = [](uint32_t b) { return Q::kPad ? b + (b >> 8) * 16u : b; };
+        // one 34-byte block of token o from its quant dwords qw and its scale
+        auto put = [&](uint32_t kv, uint32_t o, uint32_t hl, uint32_t b, const uint32_t (&qw)[8],
+                       uint32_t sc) {
+          uint8_t* dst = lds.rec_at(kv, o, hl * (uint32_t)kHeadBytes + b * 34u);
+          if (b % 2u) {  // the block starts 2 mod 4: scale, then the quants on dword bounds
+            *(uint16_t*)dst = (uint16_t)sc;
 #pragma unroll
-            for (uint32_t tt = 0; tt < 4; tt++) {
-              const uint32_t o = 4u * q + tt;
+            for (uint32_t k = 0; k < 8; k++) *(uint32_t*)(dst + 2 + 4 * k) = qw[k];
+          } else {  // on a dword bound: scale and two quants, then quants two bytes on
+            *(uint32_t*)dst = sc | (qw[0] << 16);
 #pragma unroll
-              for (uint32_t gg = 0; gg < 4; gg++) {  // dims b*32 + gg*8 .. +7
-                const uint2 w = *(const uint2*)&t[tb((b / 2u) * 1024u + (gg * 16u + o) * 16u + (b % 2u) * 8u)];
-                qw[tt][2 * gg] = w.x;
-                qw[tt][2 * gg + 1] = w.y;
-              }
-            }
-          } else {
+            for (uint32_t k = 1; k < 8; k++)
+              *(uint32_t*)(dst + 4 * k) = (qw[k - 1] >> 16) | (qw[k] << 16);
+            *(uint16_t*)(dst + 32) = (uint16_t)(qw[7] >> 16);
+          }
+        };
+        if (threadIdx.x < 64u) {
+          const uint32_t hl = threadIdx.x / (4u * kNb), q = (threadIdx.x / kNb) % 4u,
+                         b = threadIdx.x % kNb;
+          if (h0 + hl < g.n_kv_heads && (int32_t)(4u * q) < n) {
+            const uint8_t* t = lds.q + Q::off(hl, 1u, 0u);
+            uint32_t qw[4][8];  // [token][quant dword]
 #pragma unroll
             for (uint32_t k = 0; k < 8; k++) {  // dims b*32 + 4k .. 4k + 3: m = 2b + k/4
               const uint32_t m = 2u * b + k / 4u, j0 = (k % 4u) * 4u;
@@ -792,24 +799,26 @@ __device__ __forceinline__ void gather_tile(GatherLds<DT, D, FMT>& lds, const Ge
               qw[2][k] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u);
               qw[3][k] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u);
             }
-          }
 #pragma unroll
-          for (uint32_t tt = 0; tt < 4; tt++) {
-            const uint32_t o = 4u * q + tt;
-            if ((int32_t)o >= n) break;
-            const uint32_t sc = *(const uint16_t*)&t[tb(16u * D + (o * kNb + b) * 2u)];
-            uint8_t* dst = lds.rec_at(kv, o, hl * (uint32_t)kHeadBytes + b * 34u);
-            if (b % 2u) {  // the block starts 2 mod 4: scale, then the quants on dword bounds
-              *(uint16_t*)dst = (uint16_t)sc;
-#pragma unroll
-              for (uint32_t k = 0; k < 8; k++) *(uint32_t*)(dst + 2 + 4 * k) = qw[tt][k];
-            } else {  // on a dword bound: scale and two quants, then quants two bytes on
-              *(uint32_t*)dst = sc | (qw[tt][0] << 16);
-#pragma unroll
-              for (uint32_t k = 1; k < 8; k++)
-                *(uint32_t*)(dst + 4 * k) = (qw[tt][k - 1] >> 16) | (qw[tt][k] << 16);
-              *(uint16_t*)(dst + 32) = (uint16_t)(qw[tt][7] >> 16);
+            for (uint32_t tt = 0; tt < 4; tt++) {
+              const uint32_t o = 4u * q + tt;
+              if ((int32_t)o >= n) break;
+              put(1u, o, hl, b, qw[tt], *(const uint16_t*)&t[tb(16u * D + (o * kNb + b) * 2u)]);
             }
+          }
+        } else {
+          for (uint32_t i = threadIdx.x - 64u; i < 16u * 16u; i += 192u) {
+            const uint32_t hl = i / (16u * kNb), o = (i / kNb) % 16u, b = i % kNb;
+            if (h0 + hl >= g.n_kv_heads || (int32_t)o >= n) continue;
+            const uint8_t* t = lds.q + Q::off(hl, 0u, 0u);
+            uint32_t qw[8];
+#pragma unroll
+            for (uint32_t gg = 0; gg < 4; gg++) {  // dims b*32 + gg*8 .. +7
+              const uint2 w = *(const uint2*)&t[tb((b / 2u) * 1024u + (gg * 16u + o) * 16u + (b % 2u) * 8u)];
+              qw[2 * gg] = w.x;
+              qw[2 * gg + 1] = w.y;
+            }
+            put(0u, o, hl, b, qw, *(const uint16_t*)&t[tb(16u * D + (o * kNb + b) * 2u)]);
           }
         }
         __syncthreads();
