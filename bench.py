@@ -93,6 +93,10 @@ def parse():
                          "kernel (fkv_set_tuning FKV_TUNE_ATTN_ENGINE), to measure the choice")
     ap.add_argument("--n-heads", type=int, default=32,
                     help="c2: query heads over the 8 KV heads (64: GQA group 8)")
+    ap.add_argument("--c3-streams", type=int, default=2, choices=[1, 2],
+                    help="c3: 2 (default) issues each layer's chunk append + prefill attention on "
+                         "a second stream beside its decode call (independent sequences); 1 "
+                         "serialises them on one stream")
     return ap.parse_args()
 
 
@@ -648,6 +652,14 @@ def run_c3(args, torch, fa, lib, dev):
             n_pre, chunk, max_pre_ctx, scale, pre_ws.data_ptr() if pre_ws_bytes else None,
             pre_ws_bytes, sp))
 
+    # --c3-streams 2: a layer's prefill chunk (append, then prefill attention) goes to a
+    # second stream of default priority; the decode sequences and the prefill sequences
+    # share no block, so the two streams need no ordering inside the step
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    stream_b = torch.cuda.Stream() if args.c3_streams == 2 else stream
+    spb = stream_b.cuda_stream
+
     def step(t, sp):
         cl = dl.ctx_step_d[t].data_ptr()
         for l in range(L):
@@ -656,19 +668,22 @@ def run_c3(args, torch, fa, lib, dev):
                 h, l, hq, k_, v_, q_, o_, dl.tables_d.data_ptr(), dl.max_blocks, cl, n_dec,
                 dl.max_ctx, scale, dl.ws.data_ptr(), dl.ws_bytes, sp))
             fa.errors.check(lib.fkv_append(h, l, kp[l].data_ptr(), vp[l].data_ptr(),
-                                           pre_slots[t].data_ptr(), n_pre * chunk, sp))
-            prefill(t, l, sp)
+                                           pre_slots[t].data_ptr(), n_pre * chunk, spb))
+            prefill(t, l, spb)
 
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
     for t in range(W):
         step(t, sp)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record(stream)
+    stream_b.wait_event(e0)
     for i in range(K):
         step(W + i, sp)
+    if stream_b is not stream:  # the timed region ends when both streams have drained
+        done_b = torch.cuda.Event()
+        done_b.record(stream_b)
+        stream.wait_event(done_b)
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -724,6 +739,7 @@ def run_c3(args, torch, fa, lib, dev):
                         "(BASELINE configs[2])",
                         {"kv_dtype": args.kv_dtype, "ctx": "log-normal median 2048 sigma 1.0 cap 32768",
                          "prefill": f"{n_pre} x {chunk}-token chunks",
+                         "streams": args.c3_streams,
                          "pool_blocks": num_blocks, "pool_gb": round(pool.pool_bytes / 1e9, 1),
                          "fragmented_by": "10000 seeded alloc/free cycles"},
                         "fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)",
@@ -1395,7 +1411,8 @@ def other_configs(args, torch, fa, lib, dev):
                 "ms_per_step": r["ms_per_step"], "decode_only_ms_per_step": r["decode_only_ms_per_step"],
                 "decode_frac": r["roofline"]["frac"], "prefill_us_per_call": p["us_per_call"],
                 "prefill_tflops": p["tflops"], "prefill_pct_of_mfma_peak": p["pct_of_mfma_peak"],
-                "prefill_leak_safe": p["leak_safe_instance"]}
+                "prefill_leak_safe": p["leak_safe_instance"],
+                "streams": r["config"].get("streams", 1)}
 
     def c4(r):
         return {"value_gbs": r["value"], "pct_of_hbm_peak": r["pct_of_hbm_peak"],
