@@ -93,6 +93,14 @@ struct fkv_pool {
   std::vector<int32_t> free_list;  // stack; LIFO reuse, as a fragmented pool would see
   std::vector<uint32_t> refcount;
   std::vector<fkv_seqs*> managers;  // detached when the pool is destroyed
+  // RoPE (sin, cos) table of the last (rope_dim, theta) used (RopeTable::sc): rope_pos
+  // positions; a table outgrown or replaced stays allocated until the pool is destroyed
+  // (calls in flight may still read it)
+  std::mutex rope_mu;
+  float* rope_sc = nullptr;
+  uint32_t rope_pos = 0, rope_dim = 0;
+  float rope_theta = 0.0f;
+  std::vector<float*> rope_old;
 };
 
 static void detach_manager(fkv_seqs* m);
@@ -249,6 +257,8 @@ int32_t fkv_paged_destroy(fkv_pool* pool) {
   if (pool->marks) (void)hipFree(pool->marks);
   if (pool->fault_host) (void)hipHostFree(pool->fault_host);
   if (pool->host) (void)hipHostFree(pool->host);
+  if (pool->rope_sc) (void)hipFree(pool->rope_sc);
+  for (float* t : pool->rope_old) (void)hipFree(t);
   delete pool;
   return ok();
 }
@@ -712,6 +722,52 @@ static int32_t rope_table(const fkv_pool* pool, uint32_t rope_dim, float theta,
   return FKV_OK;
 }
 
+// The pool's (sin, cos) table for rope_dim and theta covering positions [0, n_pos):
+// sinf and cosf of f = pos / den[i] (the f32 division of math.rs:31-34) from the C
+// library, as the reference's f32::sin_cos gives them, so the device rotates with the
+// reference's values (the device sincosf can differ from them in the last bit, which
+// moves a stored binary16 K across a rounding boundary now and then). Built on the host
+// when the (rope_dim, theta) pair changes or n_pos outgrows it (doubling), uploaded with
+// a blocking copy; 16 MiB at rope_dim 128 and 32,768 positions.
+static int32_t rope_cache(fkv_pool* pool, fkv::RopeTable* t, float theta, uint32_t n_pos) {
+  const uint32_t np = (uint32_t)t->rope_dim / 2u;
+  if (np == 0 || n_pos == 0) return FKV_OK;
+  // positions past 2^24 are not exact in f32: they keep the device sincosf
+  constexpr uint64_t kMaxPos = 1ull << 24;
+  std::lock_guard<std::mutex> lock(pool->rope_mu);
+  const bool match = pool->rope_sc != nullptr && pool->rope_dim == (uint32_t)t->rope_dim &&
+                     memcmp(&pool->rope_theta, &theta, sizeof(float)) == 0;
+  if (!match || (pool->rope_pos < n_pos && pool->rope_pos < kMaxPos)) {
+    uint64_t want = 4096;
+    while (want < n_pos && want < kMaxPos) want *= 2;
+    if (match && want < 2ull * pool->rope_pos) want = 2ull * pool->rope_pos;
+    if (want > kMaxPos) want = kMaxPos;
+    std::vector<float> h(want * np * 2u);
+    for (uint64_t pos = 0; pos < want; pos++)
+      for (uint32_t i = 0; i < np; i++) {
+        const float f = (float)pos / t->den[i];  // math.rs:33, f32
+        h[(pos * np + i) * 2u] = sinf(f);
+        h[(pos * np + i) * 2u + 1u] = cosf(f);
+      }
+    float* d = nullptr;
+    hipError_t e = hipMalloc((void**)&d, h.size() * sizeof(float));
+    if (e != hipSuccess) return fail(FKV_ERR_INTERNAL, std::string("rope table: ") + hipGetErrorString(e));
+    e = hipMemcpy(d, h.data(), h.size() * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(d);
+      return fail(FKV_ERR_INTERNAL, std::string("rope table: ") + hipGetErrorString(e));
+    }
+    if (pool->rope_sc) pool->rope_old.push_back(pool->rope_sc);
+    pool->rope_sc = d;
+    pool->rope_pos = (uint32_t)want;
+    pool->rope_dim = (uint32_t)t->rope_dim;
+    pool->rope_theta = theta;
+  }
+  t->sc = pool->rope_sc;
+  t->sc_pos = pool->rope_pos;
+  return FKV_OK;
+}
+
 int32_t fkv_rope_append_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
                                                         uint32_t n_seqs, uint32_t max_ctx_len,
                                                         uint64_t* bytes_out) {
@@ -735,6 +791,11 @@ int32_t fkv_rope_append_decode_attention(fkv_pool* pool, uint32_t layer, uint32_
   int32_t st = rope_table(pool, rope_dim, theta, &rope);
   if (st) return st;
   if (n_seqs && (!k_new || !v_new)) return fail(FKV_ERR_INVALID, "null argument");
+  if (n_seqs) {
+    DeviceGuard dg(pool->cfg.device);
+    st = rope_cache(pool, &rope, theta, max_ctx_len);
+    if (st) return st;
+  }
   return decode_attention(pool, layer, n_heads, k_new, v_new, q, out, block_tables,
                           max_blocks_per_seq, ctx_lens, n_seqs, max_ctx_len, scale, workspace,
                           workspace_bytes, stream, &rope);

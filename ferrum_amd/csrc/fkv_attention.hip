@@ -771,9 +771,14 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(RopeTable rope, const in
   if ((int32_t)(2 * pr) < rope.rope_dim) {
     int32_t c = ctx_lens[s];
     c = c < 0 ? 0 : (c > cap ? cap : c);
-    const float freq = (float)(c > 0 ? c - 1 : 0) / rope.den[pr];
+    const uint32_t pos = (uint32_t)(c > 0 ? c - 1 : 0);
     float sn, cs;
-    sincosf(freq, &sn, &cs);
+    if (rope.sc != nullptr && pos < rope.sc_pos) {
+      sn = rope.sc[((uint64_t)pos * (uint32_t)(rope.rope_dim / 2) + pr) * 2u];
+      cs = rope.sc[((uint64_t)pos * (uint32_t)(rope.rope_dim / 2) + pr) * 2u + 1u];
+    } else {
+      sincosf((float)pos / rope.den[pr], &sn, &cs);
+    }
     const float a2 = a * cs - b * sn, b2 = a * sn + b * cs;
     a = a2;
     b = b2;

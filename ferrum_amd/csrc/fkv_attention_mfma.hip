@@ -1135,8 +1135,14 @@ __attribute__((amdgpu_waves_per_eu(EXACT ? 2 : FKV_MFMA_WAVES_PER_EU, 8))) attn_
   auto rope_angles = [&]() {
     const int pr = rope_pair(ln.lane);
     if (2 * pr < rope.rope_dim) {
-      const float freq = (float)(ctx > 0 ? ctx - 1 : 0) / rope.den[pr];
-      sincosf(freq, &rsin, &rcos);
+      const uint32_t pos = (uint32_t)(ctx > 0 ? ctx - 1 : 0);
+      if (rope.sc != nullptr && pos < rope.sc_pos) {
+        const float2 v = *(const float2*)(rope.sc + ((uint64_t)pos * (uint32_t)(rope.rope_dim / 2) + pr) * 2u);
+        rsin = v.x;
+        rcos = v.y;
+      } else {
+        sincosf((float)pos / rope.den[pr], &rsin, &rcos);
+      }
     }
   };
 

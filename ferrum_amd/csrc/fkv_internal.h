@@ -78,6 +78,11 @@ constexpr int kDtypeQ8 = 8;
 struct RopeTable {
   int32_t rope_dim;  // even, <= head_dim <= 128
   float den[64];
+  // (sin, cos) of pair p at position pos: sc[(pos * rope_dim / 2 + p) * 2 + {0, 1}], for
+  // pos < sc_pos (the pool's table, built on the host with the C library's sinf and
+  // cosf as the reference's f32::sin_cos); past it, or with sc null, the device sincosf
+  const float* sc;
+  uint32_t sc_pos;
 };
 
 constexpr uint32_t kFaultSlot = 1u;

@@ -5,8 +5,8 @@ fo_q8_gemm for attn_q/attn_k/attn_v, fo_rope at the token's position, the append
 attention loop, fo_q8_gemm for attn_output. Each stage is pinned on the GPU's own
 intermediates:
 - q, k, v (before RoPE) bit for bit against fo_q8_gemm of the normed rows;
-- the appended V bytes bit for bit; K within one storage rounding step of the oracle's
-  rotation (device sincosf, as in the RoPE step's own tests);
+- the appended V and K bytes bit for bit against the oracle's rotation (the pool's
+  host-built sin/cos table, as in the RoPE step's own tests);
 - the attention rows at the attention bar against the oracle's attention over the GPU's
   pool with the oracle-rotated q;
 - attn_output bit for bit against fo_q8_gemm of the GPU's attention rows.
@@ -78,7 +78,7 @@ def test_decode_layer_matches_the_oracle_chain(dtype, n_embd, hq, hkv, d, rope_d
     v_o = ref.q8_gemm(wv, hkv * d, n_embd, x).reshape(n, hkv, d)
     for got, want in ((q_g, q_o), (k_g, k_o), (v_g, v_o)):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-    # RoPE + append: V exact, K within one storage step
+    # RoPE + append: V and K exact
     qr, kr = ref.rope_step(q_o, k_o, ctx, rope_dim, theta)
     tail = np.array([slots_for(tab[i], c)[-1] for i, c in enumerate(ctxs)], np.int64)
     want_image = before.copy()

@@ -117,8 +117,8 @@ def test_mixed_scales_in_one_block():
 def test_fused_step_appending_a_wide_token(rope):
     """The pool holds ordinary values; the step's new token of sequence 2 has a V value
     of 1e6. Its workgroup marks the token's block during the call and the exact
-    instance launched after recomputes that split's outputs. V bytes are the oracle's append, bit for
-    bit; K too without RoPE (with it, within one quantisation step: device sincosf)."""
+    instance launched after recomputes that split's outputs. V and K bytes are the oracle's
+    append, bit for bit, with and without RoPE."""
     import torch
     import ferrum_amd as fa
     from oracle import ref
