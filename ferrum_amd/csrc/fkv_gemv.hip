@@ -482,8 +482,9 @@ struct MmB {
   uint4 s[kMmSub / 4];  // scales of 4 blocks
 };
 
-template <uint32_t CH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(CH == 16 ? 4 : 1, 8)))
+template <uint32_t CH, bool PF, bool PROD>
+__global__ __launch_bounds__(PROD ? 320 : 256)
+__attribute__((amdgpu_waves_per_eu(CH == 16 ? 4 : 1, 8)))
 void gemm_q8_mfma_kernel(const GemvBatch bat, uint32_t cols, uint32_t n_tokens,
                          uint32_t n_tiles, const uint8_t* __restrict__ ws) {
   using S = MmShape<CH>;
@@ -551,65 +552,164 @@ void gemm_q8_mfma_kernel(const GemvBatch bat, uint32_t cols, uint32_t n_tokens,
 
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t nsub = nb / kMmSub;
-  // Chunk k from LDS buffer `buf`, its sub-chunks in order with B operands o. Four
-  // blocks' integer dots are issued before their epilogues, which then run in block
-  // order. Each register of o is reloaded with the next sub-chunk's operand once its
-  // last use has issued (one set of registers, a sub-chunk ahead); past the last
-  // sub-chunk the reloads read it again (in bounds, never used), so the loop has no
-  // branch.
+  // One block's epilogue for this lane's 4 outputs: the reference's
+  // acc + f32(sumi) * (w_scale * x_scale), no fused multiply-add.
+  auto epilogue = [&](const v4i& si, const float4& w4, float xs) {
+    acc[0] = acc[0] + (float)si[0] * (w4.x * xs);
+    acc[1] = acc[1] + (float)si[1] * (w4.y * xs);
+    acc[2] = acc[2] + (float)si[2] * (w4.z * xs);
+    acc[3] = acc[3] + (float)si[3] * (w4.w * xs);
+  };
+  // Chunk k from LDS buffer `buf`, in groups of 4 blocks with B operands o. A group's
+  // four integer dots are issued before its epilogues, which then run in block order.
+  // Each register of o is reloaded with the next sub-chunk's operand
+  // once its last use has issued (one set of registers, a sub-chunk ahead); past the
+  // last sub-chunk the reloads read it again (in bounds, never used), so the loop has no
+  // branch. With PF the next group's A operands and weight scales are read from LDS
+  // before this group's dots, so their latency passes under the epilogues (a lone
+  // wave on its SIMD has nothing else to cover it); without PF each group reads its own
+  // just before use (fewer registers, for launches where several waves share a SIMD).
   auto compute = [&](uint32_t buf, MmB& o, uint32_t k) {
+    constexpr int kGroups = (int)CH / 4;
+    const uint8_t* wl = &s_w[buf][c * S::kStride + grp * 8u];
+    uint32_t ra[2][4][3];  // a group's A operand dwords as stored (3 at 2 mod 4, else 2)
+    float4 rw[2][4];       // its weight scales of rows grp*4 .. +3
+    auto group_read = [&](int g, int slot) {
 #pragma unroll
-    for (uint32_t sub = 0; sub < CH / kMmSub; ++sub) {
+      for (int i = 0; i < 4; ++i) {
+        const int b = 4 * g + i;  // the block's parity is its parity in the chunk
+        if (b % 2 == 0) {         // quants at 34b + 2 + 8grp: 2 mod 4
+          const uint32_t* p = (const uint32_t*)(wl + 34 * b);
+          ra[slot][i][0] = p[0];
+          ra[slot][i][1] = p[1];
+          ra[slot][i][2] = p[2];
+        } else {  // 0 mod 4
+          const uint32_t* p = (const uint32_t*)(wl + 34 * b + 2);
+          ra[slot][i][0] = p[0];
+          ra[slot][i][1] = p[1];
+        }
+        if (PF) rw[slot][i] = *(const float4*)&s_ws[buf][b][grp * 4u];
+      }
+    };
+    if (PF) group_read(0, 0);
+#pragma unroll
+    for (int g = 0; g < kGroups; ++g) {
+      const int cur = PF ? (g & 1) : 0;
+      const uint32_t sub = (uint32_t)g / 4u;
+      const int b0 = (4 * g) % (int)kMmSub;  // first block of the group in its sub-chunk
       const uint32_t gn = k * (CH / kMmSub) + sub + 1u;
       const uint32_t kn = gn < nsub ? gn : nsub - 1u;
-      const uint8_t* wl = &s_w[buf][c * S::kStride + grp * 8u + sub * kMmSub * kQ8Bytes];
+      if (!PF) group_read(g, cur);
+      long av[4];
 #pragma unroll
-      for (int b0 = 0; b0 < (int)kMmSub; b0 += 4) {
-        v4i si[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int b = b0 + i;  // the block's parity is its parity in the chunk
-          uint32_t lo, hi;
-          if (b % 2 == 0) {  // quants at 34b + 2 + 8grp: 2 mod 4
-            const uint32_t* p = (const uint32_t*)(wl + 34 * b);
-            const uint32_t d0 = p[0], d1 = p[1], d2 = p[2];
-            lo = __builtin_amdgcn_alignbit(d1, d0, 16);
-            hi = __builtin_amdgcn_alignbit(d2, d1, 16);
-          } else {  // 0 mod 4
-            const uint32_t* p = (const uint32_t*)(wl + 34 * b + 2);
-            lo = p[0];
-            hi = p[1];
-          }
-          const uint4 u = o.q[b / 2];
-          const long av = (long)(((uint64_t)hi << 32) | lo);
-          const long bv = (b % 2 == 0) ? (long)(((uint64_t)u.y << 32) | u.x)
-                                       : (long)(((uint64_t)u.w << 32) | u.z);
-          const v4i zero = {0, 0, 0, 0};
-          si[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, zero, 0, 0, 0);
+      for (int i = 0; i < 4; ++i) {
+        const int b = b0 + i;
+        uint32_t lo, hi;
+        if (b % 2 == 0) {
+          lo = __builtin_amdgcn_alignbit(ra[cur][i][1], ra[cur][i][0], 16);
+          hi = __builtin_amdgcn_alignbit(ra[cur][i][2], ra[cur][i][1], 16);
+        } else {
+          lo = ra[cur][i][0];
+          hi = ra[cur][i][1];
         }
-        // the reloads stay after the dots that read the registers they overwrite
-        __builtin_amdgcn_sched_barrier(0);
-        o.q[b0 / 2] = bq_load(kn, b0 / 2);
-        o.q[b0 / 2 + 1] = bq_load(kn, b0 / 2 + 1);
-        const uint4 s4 = o.s[b0 / 4];
-        o.s[b0 / 4] = bs_load(kn, b0 / 4);
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t bl = sub * kMmSub + (uint32_t)(b0 + i);
-          const float4 w4 = *(const float4*)&s_ws[buf][bl][grp * 4u];
-          const float xs = __uint_as_float(i == 0 ? s4.x : i == 1 ? s4.y : i == 2 ? s4.z : s4.w);
-          acc[0] = acc[0] + (float)si[i][0] * (w4.x * xs);
-          acc[1] = acc[1] + (float)si[i][1] * (w4.y * xs);
-          acc[2] = acc[2] + (float)si[i][2] * (w4.z * xs);
-          acc[3] = acc[3] + (float)si[i][3] * (w4.w * xs);
-        }
+        av[i] = (long)(((uint64_t)hi << 32) | lo);
       }
+      // the next group's reads go out before this group's dots and epilogues
+      if (PF && g + 1 < kGroups) group_read(g + 1, cur ^ 1);
+      v4i si[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int b = b0 + i;
+        const uint4 u = o.q[b / 2];
+        const long bv = (b % 2 == 0) ? (long)(((uint64_t)u.y << 32) | u.x)
+                                     : (long)(((uint64_t)u.w << 32) | u.z);
+        const v4i zero = {0, 0, 0, 0};
+        si[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(av[i], bv, zero, 0, 0, 0);
+      }
+      // the reloads stay after the dots that read the registers they overwrite
+      __builtin_amdgcn_sched_barrier(0);
+      o.q[b0 / 2] = bq_load(kn, b0 / 2);
+      o.q[b0 / 2 + 1] = bq_load(kn, b0 / 2 + 1);
+      const uint4 s4 = o.s[b0 / 4];
+      o.s[b0 / 4] = bs_load(kn, b0 / 4);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        epilogue(si[i], PF ? rw[cur][i] : *(const float4*)&s_ws[buf][4 * g + i][grp * 4u],
+                 __uint_as_float(i == 0 ? s4.x : i == 1 ? s4.y : i == 2 ? s4.z : s4.w));
     }
   };
 
   const uint32_t nc = nb / CH;  // even (launch_gemm_q8_mfma picks CH so)
   MmB bo;
+  if (PROD) {
+    // A fifth wave stages the weights: two chunks in flight in its registers, one chunk
+    // into the LDS buffer the four computing waves read next, their scales converted
+    // from there. Its waits on HBM are its own: the computing waves' load counters hold
+    // only their B operands, which a weight load issued before them would otherwise
+    // hold back (loads retire in issue order).
+    // Lane l stages units (l % 4) + 4j of row l / 4; it converts the scales of row l % 16,
+    // blocks l / 16 + 4i.
+    constexpr uint32_t kPer = (S::kRowUnits + 3u) / 4u;
+    constexpr uint32_t kSc = CH / 4u;
+    if (wave == 4u) {
+      const uint32_t pr = lane / 4u, pu = lane % 4u;
+      const uint8_t* psrc =
+          M.w + (uint64_t)(row0 + pr < rows ? row0 + pr : rows - 1u) * row_bytes + pu * 16u;
+      uint4 pst[2][kPer];
+      auto p_load = [&](uint32_t k, int set) {
+        const uint8_t* p = psrc + (uint64_t)k * S::kRowBytes;
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+          if (S::kRowUnits % 4u == 0u || pu + 4u * j < S::kRowUnits)
+            pst[set][j] = *(const uint4*)(p + 64u * j);
+      };
+      auto p_store = [&](int set, uint32_t buf) {
+        uint8_t* d = &s_w[buf][pr * S::kStride + pu * 16u];
+#pragma unroll
+        for (uint32_t j = 0; j < kPer; ++j)
+          if (S::kRowUnits % 4u == 0u || pu + 4u * j < S::kRowUnits) {
+            uint2* dst = (uint2*)(d + 64u * j);  // 8-byte aligned rows
+            dst[0] = make_uint2(pst[set][j].x, pst[set][j].y);
+            dst[1] = make_uint2(pst[set][j].z, pst[set][j].w);
+          }
+        const uint32_t sr = lane % 16u, sb0 = lane / 16u;
+        uint32_t sb[kSc];
+#pragma unroll
+        for (uint32_t i = 0; i < kSc; ++i)
+          sb[i] = *(const uint16_t*)&s_w[buf][sr * S::kStride + (sb0 + 4u * i) * kQ8Bytes];
+#pragma unroll
+        for (uint32_t i = 0; i < kSc; ++i) s_ws[buf][sb0 + 4u * i][sr] = dev::f16_bits_to_f32(sb[i]);
+      };
+      // Loads past the last chunk read the last chunk again (in bounds, never stored),
+      // so every iteration issues set 1's loads before set 0's and the wait before a
+      // set's stores leaves the other set in flight.
+      const uint32_t last = nc - 1u;
+      p_load(0, 0);
+      p_load(1, 1);  // nc >= 2
+      p_store(0, 0);
+      p_load(2u < last ? 2u : last, 0);
+      __syncthreads();  // buffer 0 holds chunk 0
+      for (uint32_t k = 0; k < nc; k += 2) {
+        // set 1 holds chunk k + 1, set 0 chunk k + 2
+        p_store(1, 1);
+        p_load(k + 3u < last ? k + 3u : last, 1);
+        __syncthreads();
+        if (k + 2u < nc) p_store(0, 0);
+        p_load(k + 4u < last ? k + 4u : last, 0);
+        __syncthreads();
+      }
+      return;  // after the last barrier
+    }
+    if (on) b_load(0, bo);
+    __syncthreads();
+    for (uint32_t k = 0; k < nc; k += 2) {
+      if (on) compute(0, bo, k);
+      __syncthreads();
+      if (on) compute(1, bo, k + 1);
+      __syncthreads();
+    }
+  } else {
   if (on) b_load(0, bo);
   stage_load(0);
   stage_store(0);
@@ -624,6 +724,7 @@ void gemm_q8_mfma_kernel(const GemvBatch bat, uint32_t cols, uint32_t n_tokens,
     if (on) compute(1, bo, k + 1);
     if (k + 2 < nc) stage_store(0);
     __syncthreads();
+  }
   }
 
   if (!on) return;
@@ -651,12 +752,12 @@ uint64_t gemm_mfma_workspace_bytes(uint32_t cols, uint32_t n_tokens) {
   return mm_quant_bytes(n_tiles, nb) + (uint64_t)n_tiles * nb * 16u * 4u;
 }
 
-// Batched launches of at most this many workgroups (two a CU on 256 CUs) stage longer
-// chunks of weights (gemm_q8_mfma_kernel).
-#ifndef FKV_GEMM_LONG_CHUNK_WGS
-#define FKV_GEMM_LONG_CHUNK_WGS 512
+// Batched launches of at most this many workgroups (one a CU on MI355X's 256 CUs) stage
+// their weights by a fifth wave (gemm_q8_mfma_kernel with PROD).
+#ifndef FKV_GEMM_PRODUCER_WGS
+#define FKV_GEMM_PRODUCER_WGS 256
 #endif
-constexpr uint32_t kGemmLongChunkWgs = FKV_GEMM_LONG_CHUNK_WGS;
+constexpr uint32_t kGemmProducerWgs = FKV_GEMM_PRODUCER_WGS;
 
 hipError_t launch_gemm_q8_mfma(GemvBatch b, uint32_t cols, const float* x, uint32_t n_tokens,
                                void* workspace, hipStream_t s) {
@@ -672,20 +773,22 @@ hipError_t launch_gemm_q8_mfma(GemvBatch b, uint32_t cols, const float* x, uint3
                                                                    (uint8_t*)workspace);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // Chunk length: 16 blocks where the launch holds more than kGemmLongChunkWgs
-  // workgroups (several waves share each SIMD and hide each other's load latency),
-  // otherwise 32 where that gives an even chunk count (16 always does: cols is a
-  // multiple of 1024). Measured at 64 tokens (Llama-3-8B projections, one box): 16
-  // everywhere 1,840 GB/s, 32 on the small launches 1,888, 64 where it divides 1,865.
+  // 32-block chunks with the A operands and weight scales read a group ahead wherever
+  // the chunk count is even (columns a multiple of 2048), staged by a producer wave
+  // where the launch leaves one workgroup a CU; otherwise 16-block chunks. Measured at
+  // 64 tokens (Llama-3-8B projections, one box, us a call): q/k/v 18.0 (producer 20.7,
+  // 16-block chunks 21.1), attn_output 12.2, gate/up 56.9 (16-block chunks 60.0,
+  // producer 72.1), down 32.0 (no producer 33.6).
   const uint32_t nb = cols / 32u;
   const dim3 grid(n_wg, (n_tiles + 3u) / 4u);
-  const bool few = (uint64_t)grid.x * grid.y <= kGemmLongChunkWgs;
-  if (few && nb % 64u == 0u)
-    gemm_q8_mfma_kernel<32><<<grid, 256, 0, s>>>(b, cols, n_tokens, n_tiles,
-                                                 (const uint8_t*)workspace);
+  const bool one_a_cu = (uint64_t)grid.x * grid.y <= kGemmProducerWgs;
+  const uint8_t* wsp = (const uint8_t*)workspace;
+  if (nb % 64u != 0u)
+    gemm_q8_mfma_kernel<16, false, false><<<grid, 256, 0, s>>>(b, cols, n_tokens, n_tiles, wsp);
+  else if (one_a_cu)
+    gemm_q8_mfma_kernel<32, true, true><<<grid, 320, 0, s>>>(b, cols, n_tokens, n_tiles, wsp);
   else
-    gemm_q8_mfma_kernel<16><<<grid, 256, 0, s>>>(b, cols, n_tokens, n_tiles,
-                                                 (const uint8_t*)workspace);
+    gemm_q8_mfma_kernel<32, true, false><<<grid, 256, 0, s>>>(b, cols, n_tokens, n_tiles, wsp);
   return hipGetLastError();
 }
 
