@@ -51,6 +51,7 @@ def _gemv(w, rows, cols, x):
 @pytest.mark.parametrize("rows,cols,n_tokens", [
     (16, 1024, 8), (16, 1024, 16), (33, 1024, 17), (48, 2048, 63), (40, 1024, 64),
     (17, 3072, 65), (64, 2048, 200), (1, 1024, 8), (40, 4096, 37), (4100, 2048, 50),
+    (16400, 2048, 40),
 ])
 def test_matches_oracle_and_gemv(rows, cols, n_tokens):
     rng = np.random.default_rng(rows * 131 + cols + n_tokens)
