@@ -93,6 +93,10 @@ def parse():
                          "kernel (fkv_set_tuning FKV_TUNE_ATTN_ENGINE), to measure the choice")
     ap.add_argument("--n-heads", type=int, default=32,
                     help="c2: query heads over the 8 KV heads (64: GQA group 8)")
+    ap.add_argument("--c3-decode-wgs-per-cu", type=int, default=-1, choices=[-1, 0, 2, 3],
+                    help="c3: cap the decode call at this many workgroups a CU "
+                         "(FKV_TUNE_ATTN_WGS_PER_CU; 0: no cap) so the prefill stream runs "
+                         "beside it; -1: 2 for f16 KV, none for q8_0 (measured)")
     ap.add_argument("--c3-streams", type=int, default=2, choices=[1, 2],
                     help="c3: 2 (default) issues each layer's chunk append + prefill attention on "
                          "a second stream beside its decode call (independent sequences); 1 "
@@ -671,6 +675,16 @@ def run_c3(args, torch, fa, lib, dev):
                                            pre_slots[t].data_ptr(), n_pre * chunk, spb))
             prefill(t, l, spb)
 
+    # The cap leaves room on each CU for the prefill stream (one stream has nothing to run
+    # beside the decode call). Measured on the mixed step: f16 KV 4,500 -> 4,875 GB/s with
+    # 2 decode workgroups a CU; q8_0 KV 3,249 -> 3,055 (its prefill, with the staging pass,
+    # is the larger share of the step), so q8_0 runs uncapped by default.
+    cap = args.c3_decode_wgs_per_cu
+    if cap < 0:
+        cap = 2 if dtype == 1 else 0
+    if stream_b is stream:
+        cap = 0
+    fa.set_tuning(fa.TUNE_ATTN_WGS_PER_CU, cap)
     for t in range(W):
         step(t, sp)
     torch.cuda.synchronize()
@@ -687,6 +701,7 @@ def run_c3(args, torch, fa, lib, dev):
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    fa.set_tuning(fa.TUNE_ATTN_WGS_PER_CU, 0)
     assert pool.take_fault_flags() == 0
     # chunked-prefill attention alone over the timed steps' chunks (it reads the pool
     # only, so the calls can run again): 4 * D * Hq flops per (query, key) pair
@@ -740,6 +755,7 @@ def run_c3(args, torch, fa, lib, dev):
                         {"kv_dtype": args.kv_dtype, "ctx": "log-normal median 2048 sigma 1.0 cap 32768",
                          "prefill": f"{n_pre} x {chunk}-token chunks",
                          "streams": args.c3_streams,
+                         "decode_wgs_per_cu": cap or None,
                          "pool_blocks": num_blocks, "pool_gb": round(pool.pool_bytes / 1e9, 1),
                          "fragmented_by": "10000 seeded alloc/free cycles"},
                         "fkv_append_decode_attention (attn_mfma_kernel + attn_combine_kernel)",
@@ -1412,7 +1428,8 @@ def other_configs(args, torch, fa, lib, dev):
                 "decode_frac": r["roofline"]["frac"], "prefill_us_per_call": p["us_per_call"],
                 "prefill_tflops": p["tflops"], "prefill_pct_of_mfma_peak": p["pct_of_mfma_peak"],
                 "prefill_leak_safe": p["leak_safe_instance"],
-                "streams": r["config"].get("streams", 1)}
+                "streams": r["config"].get("streams", 1),
+                "decode_wgs_per_cu": r["config"].get("decode_wgs_per_cu")}
 
     def c4(r):
         return {"value_gbs": r["value"], "pct_of_hbm_peak": r["pct_of_hbm_peak"],

@@ -8,7 +8,8 @@ from . import _lib
 from ._lib import (DTYPE_F16, DTYPE_F32, DTYPE_Q8_0, FAULT_BLOCK_RANGE, FAULT_CTX_RANGE,
                    FAULT_SLOT_RANGE, FAULT_VALUE_RANGE, GATHER_F32, GATHER_RAW, ROUND_HALF_AWAY,
                    ROUND_NEAREST_EVEN, STATIC_SCRATCH_BYTES, TUNE_ATTN_ENGINE, TUNE_ATTN_ORDER,
-                   TUNE_ATTN_SPLIT_TOKENS, TUNE_ATTN_STREAM, TUNE_PREFILL_SPLIT_BLOCKS)
+                   TUNE_ATTN_SPLIT_TOKENS, TUNE_ATTN_STREAM, TUNE_ATTN_WGS_PER_CU,
+                   TUNE_PREFILL_SPLIT_BLOCKS)
 from .errors import (CacheError, FerrumError, GgufError, InternalError, InvalidRequest,
                      KernelError, Unavailable)
 from .gguf import GgufFile
@@ -27,7 +28,8 @@ __all__ = [
     "PreallocatedKvPool", "SequenceManager", "default_scale", "device_copy", "gemm_q8_0", "gemm_q8_0_batched",
     "gemm_q8_0_batched_workspace_bytes", "gemm_q8_0_multi",
     "gemv_q8_0", "load_library", "q8_0_row_bytes", "set_tuning", "TUNE_ATTN_ENGINE", "TUNE_ATTN_ORDER",
-    "TUNE_ATTN_SPLIT_TOKENS", "TUNE_ATTN_STREAM", "TUNE_PREFILL_SPLIT_BLOCKS",
+    "TUNE_ATTN_SPLIT_TOKENS", "TUNE_ATTN_STREAM", "TUNE_ATTN_WGS_PER_CU",
+    "TUNE_PREFILL_SPLIT_BLOCKS",
 ]
 
 

@@ -39,6 +39,7 @@ TUNE_ATTN_STREAM = 1
 TUNE_ATTN_ORDER = 2
 TUNE_PREFILL_SPLIT_BLOCKS = 3
 TUNE_ATTN_ENGINE = 4
+TUNE_ATTN_WGS_PER_CU = 5
 
 FAULT_SLOT_RANGE = 1
 FAULT_BLOCK_RANGE = 2

@@ -147,6 +147,11 @@ int32_t fkv_set_tuning(int32_t knob, int64_t value) {
       if (value != 0 && value != 1) return fail(FKV_ERR_INVALID, "engine must be 0 or 1");
       t.attn_engine.store((int32_t)value);
       return ok();
+    case FKV_TUNE_ATTN_WGS_PER_CU:
+      if (value != 0 && value != 2 && value != 3)
+        return fail(FKV_ERR_INVALID, "decode workgroups per CU must be 0, 2 or 3");
+      t.attn_wgs_per_cu.store((int32_t)value);
+      return ok();
     default:
       return fail(FKV_ERR_INVALID, "unknown tuning knob");
   }

@@ -71,6 +71,10 @@ Tuning& tuning() {
       if (v >= 0) t.prefill_split = v;
     }
     if (const char* e = getenv("FKV_ATTN_ENGINE")) t.attn_engine = strcmp(e, "valu") == 0;
+    if (const char* e = getenv("FKV_ATTN_WGS_PER_CU")) {
+      const int v = atoi(e);
+      if (v == 2 || v == 3) t.attn_wgs_per_cu = v;
+    }
   });
   return t;
 }

@@ -2572,6 +2572,19 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
   return hipGetLastError();
 }
 
+// Dynamic LDS that holds a decode launch to at most tuning().attn_wgs_per_cu workgroups
+// a CU (0: none asked for): more than a (cap + 1)-th of the CU's 160 KiB in all, at most
+// a cap-th.
+static size_t decode_lds_pad(const void* fn) {
+  const int32_t cap = tuning().attn_wgs_per_cu.load(std::memory_order_relaxed);
+  if (cap <= 0) return 0;
+  hipFuncAttributes a;
+  if (hipFuncGetAttributes(&a, fn) != hipSuccess) return 0;
+  constexpr size_t kCuLds = 160u * 1024u;
+  const size_t want = kCuLds / (size_t)(cap + 1) + 1u;
+  return want > a.sharedSizeBytes ? want - a.sharedSizeBytes : 0u;
+}
+
 hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads,
                                  const float* q, float* out, const int32_t* tables,
                                  uint32_t max_blocks, const int32_t* ctx_lens, uint32_t n_seqs,
@@ -2596,9 +2609,10 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
   RopeTable rt{};
   if (roped) rt = *rope;
 #define FKV_LAUNCH_MFMA(DT_, D_, R_, X_)                                                         \
-  attn_mfma_kernel<DT_, D_, NBUF, R_, X_><<<grid, 256, 0, s>>>(                                  \
-      g, layer, n_heads, G, q, out, tables, max_blocks, ctx_lens, n_seqs, max_splits, st, order, \
-      scale, ws_o, ws_ml, k_new, v_new, rt)
+  attn_mfma_kernel<DT_, D_, NBUF, R_, X_>                                                        \
+      <<<grid, 256, decode_lds_pad((const void*)&attn_mfma_kernel<DT_, D_, NBUF, R_, X_>), s>>>( \
+          g, layer, n_heads, G, q, out, tables, max_blocks, ctx_lens, n_seqs, max_splits, st,   \
+          order, scale, ws_o, ws_ml, k_new, v_new, rt)
   // Q8_0: the fast instance, then the exact one (each workgroup of which exits at once
   // unless its split reads a block marked as holding a scale of 512 or more).
   if (g.dtype == kDtypeQ8 && roped) {

@@ -57,6 +57,7 @@ struct Geom {
 //   FKV_ATTN_ORDER          decode work order (0 grid, 1 full splits first, 2 longest first)
 //   FKV_PREFILL_SPLIT_BLOCKS  prefill key-range piece length in blocks (0: no pieces)
 //   FKV_ATTN_ENGINE=valu    F16 decode on the VALU partition kernel
+//   FKV_ATTN_WGS_PER_CU     decode workgroups a CU at most (2 or 3; 0: no cap)
 // Read with relaxed loads per launch plan (no environment access per call).
 struct Tuning {
   std::atomic<int32_t> split_tokens{0};    // 0: the planner's rule
@@ -64,6 +65,7 @@ struct Tuning {
   std::atomic<int32_t> attn_order{-1};     // -1: the planner's rule
   std::atomic<int64_t> prefill_split{-1};  // -1: the planner's rule
   std::atomic<int32_t> attn_engine{0};     // 1: F16 decode on the VALU partition kernel
+  std::atomic<int32_t> attn_wgs_per_cu{0}; // 2 or 3: decode workgroups a CU at most; 0: no cap
 };
 Tuning& tuning();
 

@@ -129,12 +129,17 @@ const char* fkv_last_error(void);
  *                                  1 the VALU partition kernel (group sizes 1, 2, 4, 8, 16;
  *                                  others stay on the matrix cores), kept to measure the
  *                                  choice [FKV_ATTN_ENGINE=valu]
+ *   FKV_TUNE_ATTN_WGS_PER_CU       at most this many decode-attention workgroups on a CU
+ *                                  (2 or 3; 0: no cap), by the LDS each one asks for: room
+ *                                  for prefill work on another stream to run beside the
+ *                                  decode call [FKV_ATTN_WGS_PER_CU]
  * Out-of-range values: FKV_ERR_INVALID, nothing changed. */
 #define FKV_TUNE_ATTN_SPLIT_TOKENS 0
 #define FKV_TUNE_ATTN_STREAM 1
 #define FKV_TUNE_ATTN_ORDER 2
 #define FKV_TUNE_PREFILL_SPLIT_BLOCKS 3
 #define FKV_TUNE_ATTN_ENGINE 4
+#define FKV_TUNE_ATTN_WGS_PER_CU 5
 int32_t fkv_set_tuning(int32_t knob, int64_t value);
 
 /* Number of visible HIP devices (0 when no GPU); never fails. */

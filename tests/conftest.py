@@ -29,14 +29,16 @@ def pytest_collection_modifyitems(config, items):
 @pytest.fixture
 def tune():
     """Planner overrides through fkv_set_tuning for one test: tune(attn_order=0,
-    attn_stream=1, attn_split_tokens=..., prefill_split_blocks=..., attn_engine=1); every knob the test
+    attn_stream=1, attn_split_tokens=..., prefill_split_blocks=..., attn_engine=1,
+    attn_wgs_per_cu=2); every knob the test
     set goes back to the planner's own rule afterwards."""
     import ferrum_amd as fa
     knobs = {"attn_split_tokens": (fa.TUNE_ATTN_SPLIT_TOKENS, 0),
              "attn_stream": (fa.TUNE_ATTN_STREAM, 0),
              "attn_order": (fa.TUNE_ATTN_ORDER, -1),
              "prefill_split_blocks": (fa.TUNE_PREFILL_SPLIT_BLOCKS, -1),
-             "attn_engine": (fa.TUNE_ATTN_ENGINE, 0)}
+             "attn_engine": (fa.TUNE_ATTN_ENGINE, 0),
+             "attn_wgs_per_cu": (fa.TUNE_ATTN_WGS_PER_CU, 0)}
     touched = set()
 
     def set_knobs(**kw):

@@ -124,10 +124,13 @@ def test_set_tuning_checks_its_arguments():
     assert lib.fkv_set_tuning(_lib.TUNE_ATTN_STREAM, 2) == _lib.FKV_ERR_INVALID
     assert lib.fkv_set_tuning(_lib.TUNE_PREFILL_SPLIT_BLOCKS, -2) == _lib.FKV_ERR_INVALID
     assert lib.fkv_set_tuning(_lib.TUNE_ATTN_ENGINE, 2) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_set_tuning(_lib.TUNE_ATTN_WGS_PER_CU, 1) == _lib.FKV_ERR_INVALID
+    assert lib.fkv_set_tuning(_lib.TUNE_ATTN_WGS_PER_CU, 4) == _lib.FKV_ERR_INVALID
     for knob, value, default in ((_lib.TUNE_ATTN_SPLIT_TOKENS, 512, 0),
                                  (_lib.TUNE_ATTN_ORDER, 1, -1),
                                  (_lib.TUNE_ATTN_STREAM, 1, 0),
                                  (_lib.TUNE_PREFILL_SPLIT_BLOCKS, 7, -1),
-                                 (_lib.TUNE_ATTN_ENGINE, 1, 0)):
+                                 (_lib.TUNE_ATTN_ENGINE, 1, 0),
+                                 (_lib.TUNE_ATTN_WGS_PER_CU, 2, 0)):
         assert lib.fkv_set_tuning(knob, value) == _lib.FKV_OK
         assert lib.fkv_set_tuning(knob, default) == _lib.FKV_OK

@@ -95,6 +95,22 @@ def test_attention_matches_oracle(dtype, d, g, f16_schedule):
     print(f"max abs err vs oracle {err:.2e}")
 
 
+@pytest.mark.parametrize("dtype,d,g", [(1, 128, 4), (8, 128, 8), (1, 64, 16)])
+def test_workgroups_per_cu_cap_changes_nothing_but_occupancy(dtype, d, g, tune):
+    """FKV_TUNE_ATTN_WGS_PER_CU only enlarges each decode workgroup's LDS request: the
+    outputs with a cap of 2 or 3 are the uncapped call's, bit for bit."""
+    hkv = 2
+    pool, layout, tab = _build(dtype, d, hkv, CTXS, seed=31 + d + g)
+    q = np.random.default_rng(5).standard_normal((len(CTXS), hkv * g, d), dtype=np.float32)
+    tune(attn_stream=0)
+    want = _run(pool, 1, q, tab, CTXS)
+    for cap in (2, 3):
+        tune(attn_wgs_per_cu=cap)
+        got = _run(pool, 1, q, tab, CTXS)
+        assert pool.take_fault_flags() == 0
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), cap
+
+
 def test_attention_long_context_uses_combine(f16_schedule):
     import ferrum_amd as fa
     from oracle import ref
