@@ -737,8 +737,9 @@ static int32_t rope_table(const fkv_pool* pool, uint32_t rope_dim, float theta,
 static int32_t rope_cache(fkv_pool* pool, fkv::RopeTable* t, float theta, uint32_t n_pos) {
   const uint32_t np = (uint32_t)t->rope_dim / 2u;
   if (np == 0 || n_pos == 0) return FKV_OK;
-  // positions past 2^24 are not exact in f32: they keep the device sincosf
-  constexpr uint64_t kMaxPos = 1ull << 24;
+  // At most 2^20 positions (512 MiB at rope_dim 128, built once on the host); positions
+  // past the table keep the device sincosf.
+  constexpr uint64_t kMaxPos = 1ull << 20;
   std::lock_guard<std::mutex> lock(pool->rope_mu);
   const bool match = pool->rope_sc != nullptr && pool->rope_dim == (uint32_t)t->rope_dim &&
                      memcmp(&pool->rope_theta, &theta, sizeof(float)) == 0;

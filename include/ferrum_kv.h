@@ -399,10 +399,11 @@ int32_t fkv_append_decode_attention_noalloc(fkv_pool* pool, uint32_t layer, uint
  * come from a table the pool builds on the host on the first call for a (rope_dim,
  * theta) pair, and again when max_ctx_len outgrows it (doubling): the C library's
  * sinf and cosf of f for every position below max_ctx_len (rounded up to a power of
- * two, at least 4,096, at most 2^24), as the reference's f32::sin_cos gives them, so
+ * two, at least 4,096, at most 2^20), as the reference's f32::sin_cos gives them, so
  * the stored K is the reference's rotation bit for bit. That call blocks while the
- * table is built and uploaded (16 MiB at rope_dim 128 and 32,768 positions, held until
- * fkv_paged_destroy); positions past the table rotate with the device's sincosf.
+ * table is built and uploaded (16 MiB at rope_dim 128 and 32,768 positions, 512 MiB at
+ * 2^20; held until fkv_paged_destroy). Positions past 2^20 rotate with the device's
+ * sincosf, which can differ from the C library's by an ulp (one f16 step in stored K).
  * workspace: fkv_rope_append_decode_attention_workspace_size() bytes. */
 int32_t fkv_rope_append_decode_attention_workspace_size(const fkv_pool* pool, uint32_t n_heads,
                                                         uint32_t n_seqs, uint32_t max_ctx_len,
