@@ -685,23 +685,25 @@ def run_c3(args, torch, fa, lib, dev):
     if stream_b is stream:
         cap = 0
     fa.set_tuning(fa.TUNE_ATTN_WGS_PER_CU, cap)
-    for t in range(W):
-        step(t, sp)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record(stream)
-    stream_b.wait_event(e0)
-    for i in range(K):
-        step(W + i, sp)
-    if stream_b is not stream:  # the timed region ends when both streams have drained
-        done_b = torch.cuda.Event()
-        done_b.record(stream_b)
-        stream.wait_event(done_b)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    fa.set_tuning(fa.TUNE_ATTN_WGS_PER_CU, 0)
+    try:  # the knob is process-wide: the later legs run uncapped whatever happens here
+        for t in range(W):
+            step(t, sp)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record(stream)
+        stream_b.wait_event(e0)
+        for i in range(K):
+            step(W + i, sp)
+        if stream_b is not stream:  # the timed region ends when both streams have drained
+            done_b = torch.cuda.Event()
+            done_b.record(stream_b)
+            stream.wait_event(done_b)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        fa.set_tuning(fa.TUNE_ATTN_WGS_PER_CU, 0)
     assert pool.take_fault_flags() == 0
     # chunked-prefill attention alone over the timed steps' chunks (it reads the pool
     # only, so the calls can run again): 4 * D * Hq flops per (query, key) pair

@@ -2574,15 +2574,23 @@ hipError_t launch_prefill_attention(const Geom& g, uint32_t layer, uint32_t n_he
 
 // Dynamic LDS that holds a decode launch to at most tuning().attn_wgs_per_cu workgroups
 // a CU (0: none asked for): more than a (cap + 1)-th of the CU's 160 KiB in all, at most
-// a cap-th.
-static size_t decode_lds_pad(const void* fn) {
+// a cap-th. The instance's static LDS is read once per instance (on the first capped
+// launch of the first device that runs it; the instance's static LDS is the same on
+// every gfx950 device).
+template <int DT, int D, int NB, bool R, bool X>
+size_t decode_lds_pad() {
   const int32_t cap = tuning().attn_wgs_per_cu.load(std::memory_order_relaxed);
   if (cap <= 0) return 0;
-  hipFuncAttributes a;
-  if (hipFuncGetAttributes(&a, fn) != hipSuccess) return 0;
+  static const size_t fixed = [] {
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, (const void*)&attn_mfma_kernel<DT, D, NB, R, X>) ==
+                   hipSuccess
+               ? (size_t)a.sharedSizeBytes
+               : (size_t)0;
+  }();
   constexpr size_t kCuLds = 160u * 1024u;
   const size_t want = kCuLds / (size_t)(cap + 1) + 1u;
-  return want > a.sharedSizeBytes ? want - a.sharedSizeBytes : 0u;
+  return want > fixed ? want - fixed : 0u;
 }
 
 hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads,
@@ -2610,7 +2618,7 @@ hipError_t launch_attention_mfma(const Geom& g, uint32_t layer, uint32_t n_heads
   if (roped) rt = *rope;
 #define FKV_LAUNCH_MFMA(DT_, D_, R_, X_)                                                         \
   attn_mfma_kernel<DT_, D_, NBUF, R_, X_>                                                        \
-      <<<grid, 256, decode_lds_pad((const void*)&attn_mfma_kernel<DT_, D_, NBUF, R_, X_>), s>>>( \
+      <<<grid, 256, decode_lds_pad<DT_, D_, NBUF, R_, X_>(), s>>>(                              \
           g, layer, n_heads, G, q, out, tables, max_blocks, ctx_lens, n_seqs, max_splits, st,   \
           order, scale, ws_o, ws_ml, k_new, v_new, rt)
   // Q8_0: the fast instance, then the exact one (each workgroup of which exits at once
