@@ -478,10 +478,11 @@ __global__ __launch_bounds__(kActThreads) void q8_act_kernel(const float* __rest
 // tile blockIdx.y * 4 + w). The 16 rows' Q8_0 bytes are staged chunk by chunk (CH
 // blocks) into LDS as stored, with their scales as f32 [block][row]; a lane (c, grp)
 // reads its A operand, quants grp*8 .. +7 of row c, from there (one 16-bit realignment
-// for blocks at 2 mod 4). Chunk k + 1's weights load while chunk k is computed, and the
-// B operands one 16-block sub-chunk ahead. A chunk of 16 blocks computes in about half
-// the latency of its weight loads: enough where 4 waves share each SIMD, not where a
-// launch leaves one wave per SIMD, which takes chunks of 32 blocks instead.
+// for blocks at 2 mod 4). The B operands load one 16-block sub-chunk ahead. The weights:
+// chunk k + 1 loads while chunk k is computed, staged by the four computing waves
+// (without PROD), or by a fifth wave two chunks ahead (PROD: launches that leave one
+// workgroup a CU, where a chunk's weight loads would otherwise hold up the computing
+// waves' B-operand waits). Chunks are 32 blocks wherever the chunk count is even, else 16.
 struct MmB {
   uint4 q[kMmSub / 2];  // block pairs
   uint4 s[kMmSub / 4];  // scales of 4 blocks
