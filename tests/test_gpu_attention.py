@@ -349,3 +349,33 @@ def test_fused_step_past_max_ctx_len_stores_no_token(dtype):
                          fa.default_scale(128))
     assert_close(out.cpu().numpy(), want)
     pool.close()
+
+
+EDGE_CTXS = [0, 1, 15, 16, 17, 31, 255, 256, 257, 1023, 1024, 1025]
+
+
+@pytest.mark.parametrize("case", range(40))
+def test_attention_randomized_shapes_against_oracle(case, tune):
+    """Seeded random cases: storage type, head_dim, group size, batch size, contexts drawn
+    from split and block edges (0, 1, 15-17, 31, 255-257, 1023-1025) and random lengths,
+    and the split length (the planner's, or 16, 256 or 1,024 tokens forced), each against
+    the oracle at the attention bar."""
+    import ferrum_amd as fa
+    from oracle import ref
+    rng = np.random.default_rng(1000 + case)
+    dtype = [1, 8, 0][case % 3]
+    d = [64, 128][(case // 3) % 2]
+    groups = [1, 2, 4, 8, 16] if dtype == 0 else [1, 2, 3, 4, 5, 8, 12, 16]
+    g = int(rng.choice(groups))
+    hkv = int(rng.choice([1, 2, 4]))
+    n = int(rng.integers(1, 10))
+    ctxs = [int(rng.choice(EDGE_CTXS)) if rng.random() < 0.6 else int(rng.integers(1, 2100))
+            for _ in range(n)]
+    split = [0, 16, 256, 1024][int(rng.integers(0, 4))]
+    tune(attn_split_tokens=split, attn_stream=0)
+    pool, layout, tab = _build(dtype, d, hkv, ctxs, seed=case, layers=1)
+    q = (rng.standard_normal((n, hkv * g, d)) * rng.choice([0.1, 1.0, 4.0])).astype(np.float32)
+    got = _run(pool, 0, q, tab, ctxs)
+    assert pool.take_fault_flags() == 0
+    want = ref.attention(layout, pool.read(), 0, q, tab, np.array(ctxs), fa.default_scale(d))
+    assert_close(got, want, what=f"case {case}: dtype {dtype} d {d} g {g} hkv {hkv} split {split} ctxs {ctxs}")
