@@ -458,3 +458,43 @@ def test_prefill_rejects_f32_pools():
                                                             device="cuda"),
                                z + 1, z + 1, torch.zeros(1, dtype=torch.int64, device="cuda"), 1,
                                1)
+
+
+@pytest.mark.parametrize("case", range(24))
+def test_prefill_randomized_shapes_against_oracle(case, tune):
+    """Seeded random cases: F16 or Q8_0, head_dim, group size, sequences with random
+    histories and chunk lengths (q_len <= context, block and tile edges among them, rows
+    in a shuffled order with gaps between them), whole key ranges or pieces of 1 to 40
+    blocks; against the oracle at the attention bar, rows outside every chunk untouched."""
+    rng = np.random.default_rng(2000 + case)
+    dtype = [1, 8][case % 2]
+    d = [64, 128][(case // 2) % 2]
+    g = int(rng.choice([1, 2, 3, 4, 5, 8, 16]))
+    hkv = int(rng.choice([1, 2]))
+    n = int(rng.integers(1, 6))
+    edges = [1, 4, 15, 16, 17, 31, 32, 33, 64, 65]
+    ctxs, qls = [], []
+    for _ in range(n):
+        ql = int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(1, 200))
+        hist = int(rng.choice([0, 1, 16, 17])) if rng.random() < 0.4 else int(rng.integers(0, 900))
+        ctxs.append(hist + ql)
+        qls.append(ql)
+    pieces = int(rng.choice([-1, 0, 1, 3, 40]))
+    tune(prefill_split_blocks=pieces)
+    pool, layout, tab = _pool(d, hkv, ctxs, seed=case, dtype=dtype)
+    order = rng.permutation(n)
+    gaps = rng.integers(0, 3, n)
+    offs = np.zeros(n, np.int64)
+    row = int(rng.integers(0, 3))
+    for i in order:  # chunks placed in a shuffled order with gaps
+        offs[i] = row
+        row += qls[i] + int(gaps[i])
+    rows = row + 1
+    q = (rng.standard_normal((rows, hkv * g, d)) * rng.choice([0.3, 1.0, 3.0])).astype(np.float32)
+    got = _prefill(pool, 0, q, tab, ctxs, qls, offs)
+    assert pool.take_fault_flags() == 0
+    want = _want(pool, layout, q, tab, ctxs, qls, offs, d)
+    used = _used(rows, offs, qls)
+    assert_close(got[used], want[used], what=f"case {case}: dtype {dtype} d {d} g {g} hkv {hkv} "
+                 f"pieces {pieces} ctxs {ctxs} qls {qls}")
+    assert np.all(got[~used] == 5.0)
