@@ -142,3 +142,46 @@ def test_rope_errors_in_reference_order():
         assert str(e.value) == msg
     assert np.array_equal(pool.read(), before), "a rejected call wrote to the pool"
     pool.close()
+
+
+@pytest.mark.parametrize("case", range(30))
+def test_rope_step_randomized_against_oracle(case, tune):
+    """Seeded random cases of the fused step: storage (F16 in either rounding, Q8_0, F32),
+    head_dim, group size, batch, contexts from 1 through block and split edges, rope_dim
+    (even, 0 to head_dim), theta and the split length; stored V and K bit for bit and the
+    output at the attention bar against the oracle."""
+    import ferrum_amd as fa
+    from oracle import ref
+    rng = np.random.default_rng(3000 + case)
+    dtype = [1, 8, 0][case % 3]
+    rounding = int(rng.integers(0, 2)) if dtype == 1 else 0
+    d = [64, 128][(case // 3) % 2]
+    g = int(rng.choice([1, 2, 4, 8, 16] if dtype == 0 else [1, 2, 3, 4, 6, 8, 16]))
+    hkv = int(rng.choice([1, 2, 4]))
+    n = int(rng.integers(1, 8))
+    edges = [1, 2, 15, 16, 17, 256, 257, 1024, 1025]
+    ctxs = [int(rng.choice(edges)) if rng.random() < 0.5 else int(rng.integers(1, 3000))
+            for _ in range(n)]
+    rope_dim = int(rng.choice([0, 2, 32, d // 2, d - 2, d]))
+    theta = float(rng.choice([10000.0, 500000.0, 1000000.0]))
+    tune(attn_split_tokens=[0, 256, 1024][int(rng.integers(0, 3))], attn_stream=0)
+    pool, layout, tab, knew, vnew = _setup(dtype, d, hkv, ctxs, rounding=rounding, seed=case,
+                                           layers=1)
+    before = pool.read()
+    q = rng.standard_normal((n, hkv * g, d)).astype(np.float32)
+    got = _run_rope(pool, 0, knew, vnew, q, tab, ctxs, rope_dim, theta)
+    assert pool.take_fault_flags() == 0
+    image = pool.read()
+    qr, kr = ref.rope_step(q, knew, ctxs, rope_dim, theta)
+    tail = np.array([slots_for(tab[i], c)[-1] for i, c in enumerate(ctxs)], np.int64)
+    want_image = before.copy()
+    ref.append(layout, want_image, 0, kr, vnew, tail)
+    kg, vg = ref.gather_slots(layout, image, 0, tail, 0)
+    kw, vw = ref.gather_slots(layout, want_image, 0, tail, 0)
+    what = (f"case {case}: dtype {dtype} rounding {rounding} d {d} g {g} hkv {hkv} "
+            f"rope_dim {rope_dim} theta {theta} ctxs {ctxs}")
+    assert np.array_equal(vg.view(np.uint32), vw.view(np.uint32)), what
+    _check_k(dtype, kg, kw, kr)
+    want = ref.attention(layout, image, 0, qr, tab, np.array(ctxs), fa.default_scale(d))
+    assert_close(got, want, what=what)
+    pool.close()
