@@ -140,3 +140,31 @@ def test_workspace_size_and_rejection():
         fa.gemm_q8_0_batched([w], [16], 4096, x, 64, [y], workspace=small)
     torch.cuda.synchronize()
     assert np.all(y.cpu().numpy() == 5.0)
+
+
+@pytest.mark.parametrize("case", range(20))
+def test_randomized_batches_against_oracle_and_gemv(case):
+    """Seeded random launches: 1 to 4 matrices (an empty one possible) sharing an
+    activation, row counts from 1 to ~5,000 (all three kernel instances: 16-block chunks,
+    32-block chunks with and without the producer wave), columns 1,024 to 6,144, 8 to 150
+    tokens with activation rows of widely different scales; every output against the GEMV
+    bit for bit and a sample of rows against the oracle bit for bit."""
+    rng = np.random.default_rng(4000 + case)
+    cols = int(rng.choice([1024, 2048, 3072, 4096, 6144]))
+    n_tokens = int(rng.integers(8, 151))
+    nm = int(rng.integers(1, 5))
+    rows = [int(rng.choice([0, 1, 15, 16, 17, int(rng.integers(1, 300)), int(rng.integers(300, 5000))]))
+            for _ in range(nm)]
+    if not any(rows):
+        rows[0] = 33
+    ws = [_weights(rng, r, cols) if r else np.zeros(0, np.uint8) for r in rows]
+    x = (rng.standard_normal((n_tokens, cols)) *
+         rng.choice([1e-3, 1.0, 50.0], (n_tokens, 1))).astype(np.float32)
+    ys = _batched(ws, rows, cols, x)
+    for r, w, y in zip(rows, ws, ys):
+        if not r:
+            continue
+        _same(y, _gemv(w, r, cols, x))
+        sel = np.unique(rng.integers(0, r, min(r, 24)))
+        wr = w.reshape(r, -1)[sel].reshape(-1)
+        _same(y[:, sel], ref.q8_gemm(wr, sel.size, cols, x))
