@@ -232,3 +232,88 @@ def test_destroying_the_pool_detaches_its_manager():
     with pytest.raises(fa.errors.CacheError):
         mgr.length(s)
     mgr.close()
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_random_scheduler_operations_match_the_model(seed):
+    """Seeded random admissions, appends, forks, truncations, swaps and frees on a small
+    pool (some refused with Unavailable, which must change nothing). After every step each
+    resident sequence's K/V, read through its slots, is the f16 encoding of its own token
+    history bit for bit; every 20 steps the attention over all resident sequences matches
+    the oracle's."""
+    import ferrum_amd as fa
+    from oracle import ref
+    rng = np.random.default_rng(6000 + seed)
+    pool, layout, mgr = _setup(24, num_host_blocks=40)
+    model = {}  # seq -> (k rows, v rows, swapped)
+    done = {}
+    for step in range(100):
+        live = sorted(model)
+        resident = [q for q in live if not model[q][2]]
+        op = rng.choice(["add", "append", "append", "fork", "truncate", "swap_out",
+                         "swap_in", "free"])
+        free_before = pool.free_block_count()
+        try:
+            if op == "add" or not live:
+                seq = mgr.add(int(rng.integers(0, 160)))
+                model[seq] = (np.zeros((0, HKV, D), np.float32), np.zeros((0, HKV, D), np.float32), False)
+            elif op == "append" and resident:
+                seq = int(rng.choice(resident))
+                n = int(rng.integers(1, 40))
+                k = rng.standard_normal((n, HKV, D)).astype(np.float32)
+                v = rng.standard_normal((n, HKV, D)).astype(np.float32)
+                _append(pool, mgr, seq, k, v)
+                mk, mv, _ = model[seq]
+                model[seq] = (np.concatenate([mk, k]), np.concatenate([mv, v]), False)
+            elif op == "fork" and resident:
+                parent = int(rng.choice(resident))
+                child = mgr.fork(parent)
+                mk, mv, _ = model[parent]
+                model[child] = (mk.copy(), mv.copy(), False)
+            elif op == "truncate" and resident:
+                seq = int(rng.choice(resident))
+                mk, mv, _ = model[seq]
+                m = int(rng.integers(0, mk.shape[0] + 1))
+                mgr.truncate(seq, m)
+                model[seq] = (mk[:m], mv[:m], False)
+            elif op == "swap_out" and resident:
+                seq = int(rng.choice(resident))
+                mgr.swap_out(seq)
+                mk, mv, _ = model[seq]
+                model[seq] = (mk, mv, True)
+            elif op == "swap_in":
+                swapped = [q for q in live if model[q][2]]
+                if swapped:
+                    seq = int(rng.choice(swapped))
+                    mgr.swap_in(seq)
+                    mk, mv, _ = model[seq]
+                    model[seq] = (mk, mv, False)
+            elif op == "free" and live:
+                seq = int(rng.choice(live))
+                mgr.free(seq)
+                del model[seq]
+            done[op] = done.get(op, 0) + 1
+        except fa.Unavailable:
+            assert pool.free_block_count() == free_before, (step, op)
+            done["unavailable"] = done.get("unavailable", 0) + 1
+        import torch
+        torch.cuda.synchronize()
+        for seq, (mk, mv, swapped) in model.items():
+            assert mgr.length(seq) == (mk.shape[0], swapped), (step, op, seq)
+            if swapped or mk.shape[0] == 0:
+                continue
+            gk, gv = _rows_of(pool, layout, mgr, seq)
+            assert np.array_equal(gk.view(np.uint32), _enc(mk).view(np.uint32)), (step, op, seq)
+            assert np.array_equal(gv.view(np.uint32), _enc(mv).view(np.uint32)), (step, op, seq)
+        resident = [q for q in sorted(model) if not model[q][2] and model[q][0].shape[0] > 0]
+        if step % 20 == 19 and resident:
+            q = rng.standard_normal((len(resident), HKV * G, D)).astype(np.float32)
+            got, tab, ctx = _attend(pool, mgr, resident, q)
+            want = ref.attention(layout, pool.read(), 0, q, tab, ctx, fa.default_scale(D))
+            assert_close(got, want, what=f"step {step}")
+            done["attention"] = done.get("attention", 0) + 1
+    assert pool.take_fault_flags() == 0
+    # the walk must have reached every kind of step, a refusal and the attention check
+    for kind in ("add", "append", "fork", "truncate", "swap_out", "swap_in", "free",
+                 "unavailable", "attention"):
+        assert done.get(kind, 0) > 0, (kind, done)
