@@ -134,3 +134,13 @@ def test_set_tuning_checks_its_arguments():
                                  (_lib.TUNE_ATTN_WGS_PER_CU, 2, 0)):
         assert lib.fkv_set_tuning(knob, value) == _lib.FKV_OK
         assert lib.fkv_set_tuning(knob, default) == _lib.FKV_OK
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """Without the built library every product call raises; nothing falls back to the CPU."""
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libferrum_kv.so"))
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="is missing: .*no CPU fallback"):
+        _lib.load()
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        fa.PagedKvPool(fa.PagedConfig(n_layers=1, n_kv_heads=2, head_dim=64, num_blocks=16))
