@@ -234,17 +234,23 @@ def test_destroying_the_pool_detaches_its_manager():
     mgr.close()
 
 
+@pytest.mark.parametrize("dtype", [1, 8])
 @pytest.mark.parametrize("seed", range(3))
-def test_random_scheduler_operations_match_the_model(seed):
+def test_random_scheduler_operations_match_the_model(seed, dtype):
     """Seeded random admissions, appends, forks, truncations, swaps and frees on a small
     pool (some refused with Unavailable, which must change nothing). After every step each
-    resident sequence's K/V, read through its slots, is the f16 encoding of its own token
-    history bit for bit; every 20 steps the attention over all resident sequences matches
-    the oracle's."""
+    resident sequence's K/V, read through its slots, is its own token history through the
+    storage's encoding (binary16, or Q8_0 blocks of 32 along each head) bit for bit; every
+    20 steps the attention over all resident sequences matches the oracle's."""
     import ferrum_amd as fa
     from oracle import ref
-    rng = np.random.default_rng(6000 + seed)
-    pool, layout, mgr = _setup(24, num_host_blocks=40)
+    rng = np.random.default_rng(6000 + 10 * dtype + seed)
+    pool, layout, mgr = _setup(24, num_host_blocks=40, dtype=dtype)
+    if dtype == 1:
+        enc = _enc
+    else:
+        def enc(rows):
+            return ref.q8_dequant(ref.q8_quantize_row(rows), rows.size).reshape(rows.shape)
     model = {}  # seq -> (k rows, v rows, swapped)
     done = {}
     for step in range(100):
@@ -303,8 +309,8 @@ def test_random_scheduler_operations_match_the_model(seed):
             if swapped or mk.shape[0] == 0:
                 continue
             gk, gv = _rows_of(pool, layout, mgr, seq)
-            assert np.array_equal(gk.view(np.uint32), _enc(mk).view(np.uint32)), (step, op, seq)
-            assert np.array_equal(gv.view(np.uint32), _enc(mv).view(np.uint32)), (step, op, seq)
+            assert np.array_equal(gk.view(np.uint32), enc(mk).view(np.uint32)), (step, op, seq)
+            assert np.array_equal(gv.view(np.uint32), enc(mv).view(np.uint32)), (step, op, seq)
         resident = [q for q in sorted(model) if not model[q][2] and model[q][0].shape[0] > 0]
         if step % 20 == 19 and resident:
             q = rng.standard_normal((len(resident), HKV * G, D)).astype(np.float32)
